@@ -1,0 +1,131 @@
+// Device helpers shared by the gfx950 kernels: element conversions with
+// explicit rounding, MFMA operand types, and launch-side declarations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../../include/qk_abi.h"
+
+namespace qk {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- conversions
+// fp16 -> fp32 is exact; bf16 -> fp32 is a shift.
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+    return (float)v;
+}
+
+// fp32 -> bf16 with round-to-nearest-even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// fp32 -> fp16 with round-to-nearest-even (hardware conversion, default mode).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16)f;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float load_half_bits(uint32_t bits, int dtype) {
+    return dtype == QK_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+}
+
+__device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype) {
+    switch (dtype) {
+    case QK_F16: return f16_bits_to_f32(((const uint16_t*)p)[i]);
+    case QK_BF16: return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+    case QK_F32: return ((const float*)p)[i];
+    default: return 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------- W8A8 epilogue
+// Applied to the exact int32 accumulator of one output element.  The float
+// operations (and their order) are part of the op contract:
+//   v = float(acc [+ int32 bias]); v *= pertoken[m] (if any);
+//   v = fmaf(v, scale[n], float bias[n] or +0); cast with RNE.
+// int8 output: clamp(rint(fmaf(float(acc), scale[n], offset[n]))).
+struct QmmEpilogue {
+    const float* scale;
+    const float* offset;
+    const float* pertoken;
+    const void* bias;
+    void* out;
+    int64_t ldo;
+    int scale_per_ch;
+    int offset_per_ch;
+    int bias_dtype;   // 0 = none
+    int out_dtype;
+};
+
+__device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64_t n, int32_t acc) {
+    float bf = 0.0f;
+    if (e.bias_dtype == QK_I32) acc = (int32_t)((uint32_t)acc + (uint32_t)((const int32_t*)e.bias)[n]);
+    else if (e.bias_dtype) bf = load_scalar(e.bias, n, e.bias_dtype);
+    int64_t o = m * e.ldo + n;
+    if (e.out_dtype == QK_I32) { ((int32_t*)e.out)[o] = acc; return; }
+    float s = e.scale[e.scale_per_ch ? n : 0];
+    float v = (float)acc;
+    if (e.out_dtype == QK_I8) {
+        float off = e.offset ? e.offset[e.offset_per_ch ? n : 0] : 0.0f;
+        float t = __builtin_rintf(__builtin_fmaf(v, s, off));
+        t = fminf(fmaxf(t, -128.0f), 127.0f);
+        ((int8_t*)e.out)[o] = (int8_t)(int)t;
+        return;
+    }
+    if (e.pertoken) v = v * e.pertoken[m];
+    v = __builtin_fmaf(v, s, bf);
+    if (e.out_dtype == QK_BF16) ((uint16_t*)e.out)[o] = (uint16_t)f32_to_bf16_bits(v);
+    else if (e.out_dtype == QK_F16) ((uint16_t*)e.out)[o] = (uint16_t)f32_to_f16_bits(v);
+    else ((float*)e.out)[o] = v;
+}
+
+// ---------------------------------------------------------------- launchers
+// Host-side entry points of each kernel file (validated arguments only).
+hipError_t launch_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t K,
+                                const float* smooth, int8_t* y, float* scale, hipStream_t stream);
+
+struct QmmArgs {
+    const int8_t* a;
+    int64_t lda;
+    const int8_t* b;
+    int64_t sbk, sbn;     // x2 strides (one of them is 1)
+    int64_t M, N, K;
+    QmmEpilogue epi;
+};
+hipError_t launch_quant_matmul(const QmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
+size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K);
+
+struct WqbmmArgs {
+    const void* x;
+    int x_dtype;
+    const void* w;
+    int w_dtype;          // QK_I32 (int4 packed) or QK_I8
+    const void* scale;
+    const void* offset;
+    int s_dtype;
+    int64_t M, N, K, group;  // group == 0: per channel (one group of K)
+    const void* bias;
+    int bias_dtype;       // 0 = none
+    void* out;
+    int out_dtype;
+};
+hipError_t launch_weight_quant_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
+size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group);
+
+hipError_t launch_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed,
+                            hipStream_t stream);
+
+}  // namespace qk

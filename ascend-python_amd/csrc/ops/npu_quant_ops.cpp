@@ -1,0 +1,336 @@
+// torch.ops.npu.* registration of the quantized-inference hot path.
+//
+// Mirrors the reference's op_api layer: a custom schema per op
+// (op_plugin/config/v2r2/op_plugin_functions.yaml:1904 "custom:" section,
+// impl_ns op_api), a host function that checks shapes and dtypes with
+// TORCH_CHECK, allocates every output on the input's device
+// (apply_tensor_without_format, op_plugin/ops/base_ops/opapi/MmKernelNpuOpApi.cpp:27-30),
+// asks for the workspace size, allocates the workspace from the caching
+// allocator (op_plugin/utils/op_api_common.h:547-551), and launches through
+// the C ABI on the current stream (op_plugin/utils/op_api_common.h:530).
+// A non-zero ABI return becomes a TORCH_CHECK failure carrying
+// qk_last_error(), as EXEC_NPU_CMD does with aclGetRecentErrMsg()
+// (op_plugin/utils/op_api_common.h:546, 555).
+//
+// Registered for the CUDA dispatch key (HIP tensors on PyTorch-ROCm) and for
+// Meta (shape inference; runs the same checks without launching).
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <optional>
+#include <tuple>
+
+#include "../../../include/qk_abi.h"
+
+namespace {
+
+int qk_dtype_of(at::ScalarType t) {
+    switch (t) {
+    case at::kHalf: return QK_F16;
+    case at::kBFloat16: return QK_BF16;
+    case at::kFloat: return QK_F32;
+    case at::kChar: return QK_I8;
+    case at::kInt: return QK_I32;
+    default: return 0;
+    }
+}
+
+qk_stream_t current_stream(const at::Tensor& t) {
+    return reinterpret_cast<qk_stream_t>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+void check_rc(int rc, const char* op) {
+    TORCH_CHECK(rc == QK_OK, "call ", op, " failed, detail:", qk_last_error());
+}
+
+at::Tensor workspace_for(const at::Tensor& like, size_t bytes) {
+    return at::empty({(int64_t)bytes}, like.options().dtype(at::kByte));
+}
+
+// ---------------------------------------------------------------- npu_dynamic_quant
+
+std::tuple<at::Tensor, at::Tensor> dynamic_quant_shapes(const at::Tensor& x, const std::optional<at::Tensor>& smooth) {
+    TORCH_CHECK(x.scalar_type() == at::kHalf || x.scalar_type() == at::kBFloat16,
+                "npu_dynamic_quant: input must be float16 or bfloat16, got ", x.scalar_type());
+    TORCH_CHECK(x.dim() >= 1, "npu_dynamic_quant: input must have at least one dimension");
+    const int64_t K = x.size(-1);
+    if (smooth.has_value()) {
+        TORCH_CHECK(smooth->scalar_type() == at::kFloat, "npu_dynamic_quant: smooth_scales must be float32");
+        TORCH_CHECK(smooth->dim() == 1 && smooth->size(0) == K, "npu_dynamic_quant: smooth_scales must be [", K,
+                    "], got ", smooth->sizes());
+    }
+    auto y = at::empty(x.sizes(), x.options().dtype(at::kChar));
+    auto s = at::empty(x.sizes().slice(0, x.dim() - 1), x.options().dtype(at::kFloat));
+    return {y, s};
+}
+
+std::tuple<at::Tensor, at::Tensor> npu_dynamic_quant(const at::Tensor& input,
+                                                     const std::optional<at::Tensor>& smooth_scales) {
+    auto [y, s] = dynamic_quant_shapes(input, smooth_scales);
+    const c10::DeviceGuard guard(input.device());
+    auto x = input.contiguous();
+    const int64_t K = x.size(-1);
+    const int64_t rows = K == 0 ? 0 : x.numel() / K;
+    at::Tensor sm;
+    if (smooth_scales.has_value()) sm = smooth_scales->contiguous();
+    const int rc = qk_dynamic_quant(x.data_ptr(), qk_dtype_of(x.scalar_type()), K == 0 ? s.numel() : rows, K,
+                                    sm.defined() ? sm.data_ptr<float>() : nullptr, y.data_ptr<int8_t>(),
+                                    s.data_ptr<float>(), current_stream(x));
+    check_rc(rc, "npu_dynamic_quant");
+    return {y, s};
+}
+
+std::tuple<at::Tensor, at::Tensor> npu_dynamic_quant_meta(const at::Tensor& input,
+                                                          const std::optional<at::Tensor>& smooth_scales) {
+    return dynamic_quant_shapes(input, smooth_scales);
+}
+
+// ---------------------------------------------------------------- npu_quant_matmul
+
+struct QmmPlan {
+    int64_t M, N, K;
+    at::ScalarType out_type;
+    std::vector<int64_t> out_shape;
+};
+
+QmmPlan quant_matmul_plan(const at::Tensor& x1, const at::Tensor& x2, const at::Tensor& scale,
+                          const std::optional<at::Tensor>& offset, const std::optional<at::Tensor>& pertoken_scale,
+                          const std::optional<at::Tensor>& bias, std::optional<at::ScalarType> output_dtype) {
+    const char* op = "npu_quant_matmul";
+    TORCH_CHECK(x1.scalar_type() == at::kChar && x2.scalar_type() == at::kChar, op,
+                ": x1 and x2 must be int8, got ", x1.scalar_type(), " and ", x2.scalar_type());
+    TORCH_CHECK(x1.dim() >= 2 && x1.dim() <= 6, op, ": x1 must have 2 to 6 dimensions, got ", x1.dim());
+    TORCH_CHECK(x2.dim() == 2, op, ": x2 must be 2-D [K, N], got ", x2.dim(), " dimensions");
+    const int64_t K = x1.size(-1);
+    TORCH_CHECK(x2.size(0) == K, op, ": x1 last dim (", K, ") must equal x2 first dim (", x2.size(0), ")");
+    const int64_t N = x2.size(1);
+    const int64_t M = K == 0 ? x1.numel() / std::max<int64_t>(1, x1.size(-1)) : x1.numel() / K;
+    const at::ScalarType out_type = output_dtype.value_or(at::kChar);
+    TORCH_CHECK(out_type == at::kBFloat16 || out_type == at::kHalf || out_type == at::kChar ||
+                    out_type == at::kInt || out_type == at::kFloat,
+                op, ": output_dtype must be bfloat16, float16, float32, int8 or int32, got ", out_type);
+    TORCH_CHECK(scale.scalar_type() == at::kFloat || scale.scalar_type() == at::kBFloat16, op,
+                ": scale must be float32 or bfloat16, got ", scale.scalar_type());
+    TORCH_CHECK(scale.dim() == 1 && (scale.size(0) == 1 || scale.size(0) == N), op, ": scale must be [1] or [", N,
+                "], got ", scale.sizes());
+    if (offset.has_value()) {
+        TORCH_CHECK(out_type == at::kChar, op, ": offset is only supported with an int8 output");
+        TORCH_CHECK(offset->scalar_type() == at::kFloat, op, ": offset must be float32");
+        TORCH_CHECK(offset->dim() == 1 && (offset->size(0) == 1 || offset->size(0) == N), op,
+                    ": offset must be [1] or [", N, "]");
+    }
+    if (pertoken_scale.has_value()) {
+        TORCH_CHECK(out_type == at::kBFloat16 || out_type == at::kHalf || out_type == at::kFloat, op,
+                    ": pertoken_scale needs output_dtype bfloat16, float16 or float32");
+        TORCH_CHECK(pertoken_scale->scalar_type() == at::kFloat, op, ": pertoken_scale must be float32");
+        TORCH_CHECK(pertoken_scale->numel() == M, op, ": pertoken_scale must have M=", M, " elements, got ",
+                    pertoken_scale->numel());
+    }
+    if (bias.has_value()) {
+        const auto bt = bias->scalar_type();
+        TORCH_CHECK(bt == at::kInt || bt == at::kBFloat16 || bt == at::kHalf || bt == at::kFloat, op,
+                    ": bias must be int32, bfloat16, float16 or float32, got ", bt);
+        TORCH_CHECK(bias->numel() == N && (bias->dim() == 1 || (bias->dim() == 2 && bias->size(0) == 1)), op,
+                    ": bias must be [", N, "], got ", bias->sizes());
+        TORCH_CHECK(bt == at::kInt || !(out_type == at::kChar || out_type == at::kInt), op,
+                    ": int8/int32 outputs take an int32 bias");
+    }
+    std::vector<int64_t> shape(x1.sizes().begin(), x1.sizes().end());
+    shape.back() = N;
+    return {M, N, K, out_type, shape};
+}
+
+at::Tensor npu_quant_matmul(const at::Tensor& x1_in, const at::Tensor& x2_in, const at::Tensor& scale_in,
+                            const std::optional<at::Tensor>& offset, const std::optional<at::Tensor>& pertoken_scale,
+                            const std::optional<at::Tensor>& bias, std::optional<at::ScalarType> output_dtype) {
+    QmmPlan pl = quant_matmul_plan(x1_in, x2_in, scale_in, offset, pertoken_scale, bias, output_dtype);
+    const c10::DeviceGuard guard(x1_in.device());
+    auto out = at::empty(pl.out_shape, x1_in.options().dtype(pl.out_type));
+    if (pl.M == 0 || pl.N == 0) return out;
+    auto x1 = x1_in.contiguous();
+    // Transposed view of an [N,K] weight is read in place, as the reference
+    // flags mat2 instead of copying it (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:40-53).
+    at::Tensor x2 = x2_in;
+    const bool kn = x2.stride(1) == 1 && x2.stride(0) >= std::max<int64_t>(1, pl.N);
+    const bool nk = x2.stride(0) == 1 && x2.stride(1) >= std::max<int64_t>(1, pl.K);
+    if (!kn && !nk) x2 = x2.contiguous();
+    const int64_t sbk = kn || (!nk) ? x2.stride(0) : 1;
+    const int64_t sbn = kn || (!nk) ? 1 : x2.stride(1);
+    auto scale = scale_in.scalar_type() == at::kFloat ? scale_in.contiguous() : scale_in.to(at::kFloat);
+    at::Tensor off, pt, b;
+    if (offset.has_value()) off = offset->contiguous();
+    if (pertoken_scale.has_value()) pt = pertoken_scale->contiguous();
+    if (bias.has_value()) b = bias->contiguous();
+    size_t ws_bytes = 0;
+    check_rc(qk_quant_matmul_workspace_size(pl.M, pl.N, pl.K, qk_dtype_of(pl.out_type), &ws_bytes),
+             "npu_quant_matmul");
+    at::Tensor ws = ws_bytes ? workspace_for(x1, ws_bytes) : at::Tensor();
+    const int rc = qk_quant_matmul(
+        x1.data_ptr<int8_t>(), pl.K, x2.data_ptr<int8_t>(), sbk, sbn, pl.M, pl.N, pl.K, scale.data_ptr<float>(),
+        scale.numel(), off.defined() ? off.data_ptr<float>() : nullptr, off.defined() ? off.numel() : 0,
+        pt.defined() ? pt.data_ptr<float>() : nullptr, b.defined() ? b.data_ptr() : nullptr,
+        b.defined() ? qk_dtype_of(b.scalar_type()) : 0, out.data_ptr(), qk_dtype_of(pl.out_type),
+        ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(x1));
+    check_rc(rc, "npu_quant_matmul");
+    return out;
+}
+
+at::Tensor npu_quant_matmul_meta(const at::Tensor& x1, const at::Tensor& x2, const at::Tensor& scale,
+                                 const std::optional<at::Tensor>& offset,
+                                 const std::optional<at::Tensor>& pertoken_scale, const std::optional<at::Tensor>& bias,
+                                 std::optional<at::ScalarType> output_dtype) {
+    QmmPlan pl = quant_matmul_plan(x1, x2, scale, offset, pertoken_scale, bias, output_dtype);
+    return at::empty(pl.out_shape, x1.options().dtype(pl.out_type));
+}
+
+// ---------------------------------------------------------------- npu_weight_quant_batchmatmul
+
+struct WqPlan {
+    int64_t M, N, K, group;
+    bool int4;
+    std::vector<int64_t> out_shape;
+};
+
+WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at::Tensor& antiquant_scale,
+                         const std::optional<at::Tensor>& antiquant_offset,
+                         const std::optional<at::Tensor>& quant_scale, const std::optional<at::Tensor>& quant_offset,
+                         const std::optional<at::Tensor>& bias, int64_t group) {
+    const char* op = "npu_weight_quant_batchmatmul";
+    TORCH_CHECK(x.scalar_type() == at::kHalf || x.scalar_type() == at::kBFloat16, op,
+                ": x must be float16 or bfloat16, got ", x.scalar_type());
+    TORCH_CHECK(x.dim() >= 2, op, ": x must be at least 2-D, got ", x.dim());
+    TORCH_CHECK(weight.dim() == 2, op, ": weight must be 2-D, got ", weight.dim());
+    TORCH_CHECK(weight.scalar_type() == at::kInt || weight.scalar_type() == at::kChar, op,
+                ": weight must be int32 (int4 packed 8 per element) or int8, got ", weight.scalar_type());
+    TORCH_CHECK(!quant_scale.has_value() && !quant_offset.has_value(), op,
+                ": quant_scale/quant_offset (int8 output) are not supported by this build");
+    const bool int4 = weight.scalar_type() == at::kInt;
+    const int64_t K = x.size(-1);
+    TORCH_CHECK(weight.size(0) == K, op, ": x last dim (", K, ") must equal weight first dim (", weight.size(0), ")");
+    const int64_t N = int4 ? weight.size(1) * 8 : weight.size(1);
+    TORCH_CHECK(group >= 0, op, ": antiquant_group_size must be >= 0");
+    TORCH_CHECK(group == 0 || K % group == 0, op, ": K=", K, " must be a multiple of antiquant_group_size=", group);
+    const auto st = antiquant_scale.scalar_type();
+    TORCH_CHECK(st == at::kHalf || st == at::kBFloat16, op, ": antiquant_scale must be float16 or bfloat16");
+    const int64_t ng = group > 0 ? K / group : 1;
+    const bool per_ch_ok = group == 0 && antiquant_scale.numel() == N &&
+                           (antiquant_scale.dim() == 1 || (antiquant_scale.dim() == 2 && antiquant_scale.size(0) == 1));
+    const bool grouped_ok = group > 0 && antiquant_scale.dim() == 2 && antiquant_scale.size(0) == ng &&
+                            antiquant_scale.size(1) == N;
+    TORCH_CHECK(per_ch_ok || grouped_ok, op, ": antiquant_scale must be ", group > 0 ? "[K/group, N] = [" : "[N] = [",
+                group > 0 ? ng : N, group > 0 ? ", " : "", group > 0 ? std::to_string(N) : std::string(""),
+                "], got ", antiquant_scale.sizes());
+    if (antiquant_offset.has_value()) {
+        TORCH_CHECK(antiquant_offset->scalar_type() == st, op, ": antiquant_offset must match antiquant_scale's dtype");
+        TORCH_CHECK(antiquant_offset->sizes() == antiquant_scale.sizes(), op,
+                    ": antiquant_offset must have antiquant_scale's shape");
+    }
+    if (bias.has_value()) {
+        const auto bt = bias->scalar_type();
+        TORCH_CHECK(bt == at::kHalf || bt == at::kBFloat16 || bt == at::kFloat, op, ": bias must be a float type");
+        TORCH_CHECK(bias->numel() == N, op, ": bias must have N=", N, " elements");
+    }
+    std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
+    shape.back() = N;
+    const int64_t M = K == 0 ? 0 : x.numel() / K;
+    return {M, N, K, group, int4, shape};
+}
+
+at::Tensor npu_weight_quant_batchmatmul(const at::Tensor& x_in, const at::Tensor& weight_in,
+                                        const at::Tensor& antiquant_scale,
+                                        const std::optional<at::Tensor>& antiquant_offset,
+                                        const std::optional<at::Tensor>& quant_scale,
+                                        const std::optional<at::Tensor>& quant_offset,
+                                        const std::optional<at::Tensor>& bias, int64_t antiquant_group_size) {
+    WqPlan pl = weight_quant_plan(x_in, weight_in, antiquant_scale, antiquant_offset, quant_scale, quant_offset, bias,
+                                  antiquant_group_size);
+    const c10::DeviceGuard guard(x_in.device());
+    auto out = at::empty(pl.out_shape, x_in.options());
+    if (pl.M == 0 || pl.N == 0) return out;
+    auto x = x_in.contiguous();
+    auto w = weight_in.contiguous();
+    auto sc = antiquant_scale.contiguous();
+    at::Tensor off, b;
+    if (antiquant_offset.has_value()) off = antiquant_offset->contiguous();
+    if (bias.has_value()) b = bias->contiguous();
+    const int wdt = pl.int4 ? QK_I32 : QK_I8;
+    size_t ws_bytes = 0;
+    check_rc(qk_weight_quant_bmm_workspace_size(pl.M, pl.N, pl.K, wdt, pl.group, &ws_bytes),
+             "npu_weight_quant_batchmatmul");
+    at::Tensor ws = ws_bytes ? workspace_for(x, ws_bytes) : at::Tensor();
+    const int rc = qk_weight_quant_bmm(x.data_ptr(), qk_dtype_of(x.scalar_type()), w.data_ptr(), wdt, sc.data_ptr(),
+                                       off.defined() ? off.data_ptr() : nullptr, qk_dtype_of(sc.scalar_type()), pl.M,
+                                       pl.N, pl.K, pl.group, b.defined() ? b.data_ptr() : nullptr,
+                                       b.defined() ? qk_dtype_of(b.scalar_type()) : 0, out.data_ptr(),
+                                       qk_dtype_of(out.scalar_type()), ws.defined() ? ws.data_ptr() : nullptr,
+                                       ws_bytes, current_stream(x));
+    check_rc(rc, "npu_weight_quant_batchmatmul");
+    return out;
+}
+
+at::Tensor npu_weight_quant_batchmatmul_meta(const at::Tensor& x, const at::Tensor& weight,
+                                             const at::Tensor& antiquant_scale,
+                                             const std::optional<at::Tensor>& antiquant_offset,
+                                             const std::optional<at::Tensor>& quant_scale,
+                                             const std::optional<at::Tensor>& quant_offset,
+                                             const std::optional<at::Tensor>& bias, int64_t antiquant_group_size) {
+    WqPlan pl = weight_quant_plan(x, weight, antiquant_scale, antiquant_offset, quant_scale, quant_offset, bias,
+                                  antiquant_group_size);
+    return at::empty(pl.out_shape, x.options());
+}
+
+// ---------------------------------------------------------------- npu_convert_weight_to_int4pack
+
+std::vector<int64_t> int4pack_shape(const at::Tensor& w) {
+    const char* op = "npu_convert_weight_to_int4pack";
+    TORCH_CHECK(w.scalar_type() == at::kInt || w.scalar_type() == at::kChar, op, ": weight must be int32 or int8");
+    TORCH_CHECK(w.dim() == 2, op, ": weight must be 2-D [K, N]");
+    TORCH_CHECK(w.size(1) % 8 == 0, op, ": N=", w.size(1), " must be a multiple of 8");
+    return {w.size(0), w.size(1) / 8};
+}
+
+at::Tensor npu_convert_weight_to_int4pack(const at::Tensor& weight, int64_t inner_k_tiles) {
+    (void)inner_k_tiles;
+    auto shape = int4pack_shape(weight);
+    const c10::DeviceGuard guard(weight.device());
+    auto w = weight.contiguous();
+    auto out = at::empty(shape, w.options().dtype(at::kInt));
+    check_rc(qk_int4_pack(w.data_ptr(), qk_dtype_of(w.scalar_type()), w.size(0), w.size(1), out.data_ptr<int32_t>(),
+                          current_stream(w)),
+             "npu_convert_weight_to_int4pack");
+    return out;
+}
+
+at::Tensor npu_convert_weight_to_int4pack_meta(const at::Tensor& weight, int64_t inner_k_tiles) {
+    (void)inner_k_tiles;
+    return at::empty(int4pack_shape(weight), weight.options().dtype(at::kInt));
+}
+
+}  // namespace
+
+TORCH_LIBRARY(npu, m) {
+    m.def("npu_dynamic_quant(Tensor input, *, Tensor? smooth_scales=None) -> (Tensor, Tensor)");
+    m.def(
+        "npu_quant_matmul(Tensor x1, Tensor x2, Tensor scale, *, Tensor? offset=None, Tensor? pertoken_scale=None, "
+        "Tensor? bias=None, ScalarType? output_dtype=None) -> Tensor");
+    m.def(
+        "npu_weight_quant_batchmatmul(Tensor x, Tensor weight, Tensor antiquant_scale, Tensor? antiquant_offset=None, "
+        "Tensor? quant_scale=None, Tensor? quant_offset=None, Tensor? bias=None, int antiquant_group_size=0) -> Tensor");
+    m.def("npu_convert_weight_to_int4pack(Tensor weight, int inner_k_tiles=0) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(npu, CUDA, m) {
+    m.impl("npu_dynamic_quant", &npu_dynamic_quant);
+    m.impl("npu_quant_matmul", &npu_quant_matmul);
+    m.impl("npu_weight_quant_batchmatmul", &npu_weight_quant_batchmatmul);
+    m.impl("npu_convert_weight_to_int4pack", &npu_convert_weight_to_int4pack);
+}
+
+TORCH_LIBRARY_IMPL(npu, Meta, m) {
+    m.impl("npu_dynamic_quant", &npu_dynamic_quant_meta);
+    m.impl("npu_quant_matmul", &npu_quant_matmul_meta);
+    m.impl("npu_weight_quant_batchmatmul", &npu_weight_quant_batchmatmul_meta);
+    m.impl("npu_convert_weight_to_int4pack", &npu_convert_weight_to_int4pack_meta);
+}

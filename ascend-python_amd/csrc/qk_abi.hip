@@ -1,0 +1,187 @@
+// extern "C" entry points of libqk_hip.so (declared in include/qk_abi.h).
+//
+// Each entry validates its plain-pointer arguments, turns a failure into a
+// negative return code plus a thread-local message (the role
+// aclGetRecentErrMsg() plays behind EXEC_NPU_CMD,
+// op_plugin/utils/op_api_common.h:544-555), and enqueues the kernels on the
+// caller's stream.  Nothing here allocates or synchronises.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "kernels/common.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int launched(hipError_t e, const char* op) {
+    if (e != hipSuccess) return fail(QK_ERR_LAUNCH, "%s: kernel launch failed: %s", op, hipGetErrorString(e));
+    return QK_OK;
+}
+
+bool is_half(int dt) { return dt == QK_F16 || dt == QK_BF16; }
+bool is_float_out(int dt) { return dt == QK_F16 || dt == QK_BF16 || dt == QK_F32; }
+
+constexpr int64_t kMaxGrid = (int64_t)1 << 31;  // gridDim.x limit
+constexpr int64_t kMaxExactK = 131071;           // 131071 * 128 * 128 < 2^31
+
+}  // namespace
+
+extern "C" {
+
+const char* qk_last_error(void) { return g_last_error.c_str(); }
+
+int qk_abi_version(void) { return 1; }
+
+int qk_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t K, const float* smooth_scales, int8_t* y,
+                     float* scale, qk_stream_t stream) {
+    g_last_error.clear();
+    if (!is_half(x_dtype)) return fail(QK_ERR_ARG, "npu_dynamic_quant: x must be float16 or bfloat16 (got dtype %d)", x_dtype);
+    if (rows < 0 || K < 0) return fail(QK_ERR_ARG, "npu_dynamic_quant: negative size rows=%lld K=%lld", (long long)rows, (long long)K);
+    if (rows == 0) return QK_OK;
+    if (!scale || (K > 0 && (!x || !y))) return fail(QK_ERR_ARG, "npu_dynamic_quant: null pointer");
+    if (rows >= kMaxGrid) return fail(QK_ERR_UNSUPPORTED, "npu_dynamic_quant: %lld rows exceed the launch limit", (long long)rows);
+    return launched(qk::launch_dynamic_quant(x, x_dtype, rows, K, smooth_scales, y, scale, (hipStream_t)stream),
+                    "npu_dynamic_quant");
+}
+
+int qk_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int out_dtype, size_t* bytes) {
+    g_last_error.clear();
+    (void)out_dtype;
+    if (!bytes) return fail(QK_ERR_ARG, "npu_quant_matmul: bytes is null");
+    if (M < 0 || N < 0 || K < 0) return fail(QK_ERR_ARG, "npu_quant_matmul: negative size");
+    *bytes = qk::quant_matmul_workspace(M, N, K);
+    return QK_OK;
+}
+
+int qk_quant_matmul(const int8_t* x1, int64_t ldx1, const int8_t* x2, int64_t x2_stride_k, int64_t x2_stride_n,
+                    int64_t M, int64_t N, int64_t K, const float* scale, int64_t scale_len, const float* offset,
+                    int64_t offset_len, const float* pertoken_scale, const void* bias, int bias_dtype, void* out,
+                    int out_dtype, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_quant_matmul";
+    if (M < 0 || N < 0 || K < 0) return fail(QK_ERR_ARG, "%s: negative size M=%lld N=%lld K=%lld", op, (long long)M, (long long)N, (long long)K);
+    if (!(is_float_out(out_dtype) || out_dtype == QK_I8 || out_dtype == QK_I32))
+        return fail(QK_ERR_ARG, "%s: unsupported output dtype %d", op, out_dtype);
+    if (K > kMaxExactK) return fail(QK_ERR_UNSUPPORTED, "%s: K=%lld exceeds %lld, the int32-exact bound", op, (long long)K, (long long)kMaxExactK);
+    if (M == 0 || N == 0) return QK_OK;
+    if (!out || (K > 0 && (!x1 || !x2))) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    if (ldx1 < K) return fail(QK_ERR_ARG, "%s: ldx1=%lld < K=%lld", op, (long long)ldx1, (long long)K);
+    if (!(x2_stride_k == 1 || x2_stride_n == 1))
+        return fail(QK_ERR_ARG, "%s: x2 must be [K,N]-contiguous or a transposed view of [N,K] (strides %lld,%lld)", op,
+                    (long long)x2_stride_k, (long long)x2_stride_n);
+    if (out_dtype != QK_I32) {
+        if (!scale) return fail(QK_ERR_ARG, "%s: scale is required for output dtype %d", op, out_dtype);
+        if (scale_len != 1 && scale_len != N)
+            return fail(QK_ERR_ARG, "%s: scale must have 1 or N=%lld elements (got %lld)", op, (long long)N, (long long)scale_len);
+    }
+    if (offset) {
+        if (out_dtype != QK_I8) return fail(QK_ERR_ARG, "%s: offset is only valid with an int8 output", op);
+        if (offset_len != 1 && offset_len != N)
+            return fail(QK_ERR_ARG, "%s: offset must have 1 or N elements (got %lld)", op, (long long)offset_len);
+    }
+    if (pertoken_scale && !is_float_out(out_dtype))
+        return fail(QK_ERR_ARG, "%s: pertoken_scale needs a float16/bfloat16/float32 output", op);
+    if (bias) {
+        if (!(bias_dtype == QK_I32 || is_half(bias_dtype) || bias_dtype == QK_F32))
+            return fail(QK_ERR_ARG, "%s: bias dtype %d unsupported", op, bias_dtype);
+        if (bias_dtype != QK_I32 && !is_float_out(out_dtype))
+            return fail(QK_ERR_ARG, "%s: a float bias needs a float output (int8/int32 outputs take an int32 bias)", op);
+    }
+    const size_t need = qk::quant_matmul_workspace(M, N, K);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(QK_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, workspace_bytes);
+
+    qk::QmmArgs p;
+    p.a = x1;
+    p.lda = ldx1;
+    p.b = x2;
+    p.sbk = x2_stride_k;
+    p.sbn = x2_stride_n;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.epi.scale = scale;
+    p.epi.scale_per_ch = scale_len != 1;
+    p.epi.offset = offset;
+    p.epi.offset_per_ch = offset_len != 1;
+    p.epi.pertoken = pertoken_scale;
+    p.epi.bias = bias;
+    p.epi.bias_dtype = bias ? bias_dtype : 0;
+    p.epi.out = out;
+    p.epi.ldo = N;
+    p.epi.out_dtype = out_dtype;
+    return launched(qk::launch_quant_matmul(p, workspace, workspace_bytes, (hipStream_t)stream), op);
+}
+
+int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weight_dtype, int64_t group_size,
+                                       size_t* bytes) {
+    g_last_error.clear();
+    if (!bytes) return fail(QK_ERR_ARG, "npu_weight_quant_batchmatmul: bytes is null");
+    if (M < 0 || N < 0 || K < 0 || group_size < 0) return fail(QK_ERR_ARG, "npu_weight_quant_batchmatmul: negative size");
+    *bytes = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size);
+    return QK_OK;
+}
+
+int qk_weight_quant_bmm(const void* x, int x_dtype, const void* weight, int weight_dtype, const void* antiquant_scale,
+                        const void* antiquant_offset, int scale_dtype, int64_t M, int64_t N, int64_t K,
+                        int64_t group_size, const void* bias, int bias_dtype, void* out, int out_dtype,
+                        void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_weight_quant_batchmatmul";
+    if (!is_half(x_dtype)) return fail(QK_ERR_ARG, "%s: x must be float16 or bfloat16", op);
+    if (weight_dtype != QK_I32 && weight_dtype != QK_I8)
+        return fail(QK_ERR_ARG, "%s: weight must be int32 (packed int4) or int8", op);
+    if (!is_half(scale_dtype)) return fail(QK_ERR_ARG, "%s: antiquant_scale must be float16 or bfloat16", op);
+    if (!is_half(out_dtype)) return fail(QK_ERR_ARG, "%s: output must be float16 or bfloat16", op);
+    if (M < 0 || N < 0 || K < 0 || group_size < 0) return fail(QK_ERR_ARG, "%s: negative size", op);
+    if (weight_dtype == QK_I32 && N % 8 != 0) return fail(QK_ERR_ARG, "%s: int4 packing needs N %% 8 == 0 (N=%lld)", op, (long long)N);
+    if (group_size > 0 && K % group_size != 0)
+        return fail(QK_ERR_ARG, "%s: K=%lld is not a multiple of antiquant_group_size=%lld", op, (long long)K, (long long)group_size);
+    if (bias && !(is_half(bias_dtype) || bias_dtype == QK_F32)) return fail(QK_ERR_ARG, "%s: bias dtype %d unsupported", op, bias_dtype);
+    if (M == 0 || N == 0) return QK_OK;
+    if (!out || (K > 0 && (!x || !weight || !antiquant_scale))) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    const size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(QK_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, workspace_bytes);
+    qk::WqbmmArgs p;
+    p.x = x;
+    p.x_dtype = x_dtype;
+    p.w = weight;
+    p.w_dtype = weight_dtype;
+    p.scale = antiquant_scale;
+    p.offset = antiquant_offset;
+    p.s_dtype = scale_dtype;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.group = group_size;
+    p.bias = bias;
+    p.bias_dtype = bias ? bias_dtype : 0;
+    p.out = out;
+    p.out_dtype = out_dtype;
+    return launched(qk::launch_weight_quant_bmm(p, workspace, workspace_bytes, (hipStream_t)stream), op);
+}
+
+int qk_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_convert_weight_to_int4pack";
+    if (w_dtype != QK_I8 && w_dtype != QK_I32) return fail(QK_ERR_ARG, "%s: weight must be int8 or int32", op);
+    if (K < 0 || N < 0 || N % 8 != 0) return fail(QK_ERR_ARG, "%s: need K >= 0 and N %% 8 == 0 (N=%lld)", op, (long long)N);
+    if (K * N == 0) return QK_OK;
+    if (!w || !packed) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    return launched(qk::launch_int4_pack(w, w_dtype, K, N, packed, (hipStream_t)stream), op);
+}
+
+}  // extern "C"

@@ -1,0 +1,85 @@
+"""op_plugin_amd -- MI355X (gfx950) quantized-inference ops behind the torch_npu op names.
+
+Importing this package loads ``_npu_ops.so``, which registers
+
+* ``torch.ops.npu.npu_dynamic_quant(input, *, smooth_scales=None) -> (int8 y, fp32 scale)``
+* ``torch.ops.npu.npu_quant_matmul(x1, x2, scale, *, offset=None, pertoken_scale=None,
+  bias=None, output_dtype=None) -> Tensor``  (W8A8)
+* ``torch.ops.npu.npu_weight_quant_batchmatmul(x, weight, antiquant_scale,
+  antiquant_offset=None, quant_scale=None, quant_offset=None, bias=None,
+  antiquant_group_size=0) -> Tensor``  (W4A16 / W8A16)
+* ``torch.ops.npu.npu_convert_weight_to_int4pack(weight, inner_k_tiles=0) -> Tensor``
+
+and exposes the same callables here, so code written as
+``torch_npu.npu_quant_matmul(...)`` runs as ``op_plugin_amd.npu_quant_matmul(...)``
+(the reference tests call ops this way, e.g.
+test/test_custom_ops/test_npu_rms_norm.py:20).  The kernels are the HIP code of
+``libqk_hip.so``; there is no fallback: if the native library is missing, the
+import fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqk_hip.so")
+OPS_PATH = os.path.join(_HERE, "_npu_ops.so")
+
+if not (os.path.exists(LIB_PATH) and os.path.exists(OPS_PATH)):
+    raise ImportError(
+        "op_plugin_amd: native libraries are not built (expected "
+        f"{LIB_PATH} and {OPS_PATH}); run `python ascend-python_amd/build.py` or "
+        "`__graft_entry__.build()` first")
+
+if not hasattr(torch.ops.npu, "npu_quant_matmul"):
+    torch.ops.load_library(OPS_PATH)
+
+npu_dynamic_quant = torch.ops.npu.npu_dynamic_quant
+npu_quant_matmul = torch.ops.npu.npu_quant_matmul
+npu_weight_quant_batchmatmul = torch.ops.npu.npu_weight_quant_batchmatmul
+npu_convert_weight_to_int4pack = torch.ops.npu.npu_convert_weight_to_int4pack
+
+# qk_abi.h constants
+QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32 = 1, 2, 3, 4, 5
+QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, -2, -3, -4
+
+ABI_SYMBOLS = (
+    "qk_last_error", "qk_abi_version", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",
+    "qk_quant_matmul", "qk_weight_quant_bmm_workspace_size", "qk_weight_quant_bmm", "qk_int4_pack",
+)
+
+_abi = None
+
+
+def abi() -> ctypes.CDLL:
+    """ctypes handle on libqk_hip.so with argtypes set (the C ABI of include/qk_abi.h)."""
+    global _abi
+    if _abi is None:
+        L = ctypes.CDLL(LIB_PATH)
+        P, I64, I, SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+        L.qk_last_error.restype = ctypes.c_char_p
+        L.qk_last_error.argtypes = []
+        L.qk_abi_version.restype = I
+        L.qk_dynamic_quant.argtypes = [P, I, I64, I64, P, P, P, P]
+        L.qk_quant_matmul_workspace_size.argtypes = [I64, I64, I64, I, ctypes.POINTER(SZ)]
+        L.qk_quant_matmul.argtypes = [P, I64, P, I64, I64, I64, I64, I64, P, I64, P, I64, P, P, I, P, I, P, SZ, P]
+        L.qk_weight_quant_bmm_workspace_size.argtypes = [I64, I64, I64, I, I64, ctypes.POINTER(SZ)]
+        L.qk_weight_quant_bmm.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P, SZ, P]
+        L.qk_int4_pack.argtypes = [P, I, I64, I64, P, P]
+        for name in ABI_SYMBOLS:
+            getattr(L, name).restype = I if name != "qk_last_error" else ctypes.c_char_p
+        _abi = L
+    return _abi
+
+
+def last_error() -> str:
+    return abi().qk_last_error().decode()
+
+
+__all__ = [
+    "npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
+    "npu_convert_weight_to_int4pack", "abi", "last_error", "LIB_PATH", "OPS_PATH",
+]

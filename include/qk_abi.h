@@ -1,0 +1,150 @@
+/*
+ * qk_abi.h -- C ABI of libqk_hip.so, the MI355X (gfx950) kernels of the
+ * quantized-inference hot path: npu_dynamic_quant, npu_quant_matmul (W8A8)
+ * and npu_weight_quant_batchmatmul (W4A16 / W8A16).
+ *
+ * This is the layer the reference reaches through EXEC_NPU_CMD
+ * (op_plugin/utils/op_api_common.h:520-570): a two-phase C call,
+ * "<op>GetWorkspaceSize" then "<op>(workspace, size, executor, stream)",
+ * resolved by dlsym from libcust_opapi.so / libopapi.so
+ * (op_plugin/utils/op_api_common.h:80-123).  Here the two phases are
+ * qk_*_workspace_size() and the op call itself; operands are plain device
+ * pointers, sizes and strides instead of aclTensor descriptors, so no torch
+ * or vendor type appears in a signature.
+ *
+ * Contract, as in the reference boundary:
+ *   - the caller allocates every output and the workspace
+ *     (op_plugin/ops/base_ops/opapi/MmKernelNpuOpApi.cpp:27-30,
+ *      op_plugin/utils/op_api_common.h:547-551); the library allocates nothing;
+ *   - work is enqueued on `stream` and never synchronised
+ *     (op_plugin/utils/op_api_common.h:530, 563-566);
+ *   - a non-zero return is an error and qk_last_error() gives a thread-local
+ *     message (the reference's aclGetRecentErrMsg(),
+ *     op_plugin/utils/op_api_common.h:546, 555).
+ * All functions are thread-safe; calls on one stream execute in order.
+ */
+#ifndef QK_ABI_H
+#define QK_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as hipStream_t; NULL is the default (null) stream. */
+typedef struct ihipStream_t* qk_stream_t;
+
+/* Element types.  F16 = IEEE binary16, BF16 = bfloat16. */
+typedef enum {
+    QK_F16 = 1,
+    QK_BF16 = 2,
+    QK_F32 = 3,
+    QK_I8 = 4,
+    QK_I32 = 5
+} qk_dtype;
+
+/* Return codes. */
+enum {
+    QK_OK = 0,
+    QK_ERR_ARG = -1,          /* invalid argument (shape, dtype, pointer, alignment) */
+    QK_ERR_UNSUPPORTED = -2,  /* valid request this build does not implement */
+    QK_ERR_WORKSPACE = -3,    /* workspace missing or smaller than *_workspace_size() */
+    QK_ERR_LAUNCH = -4        /* the HIP runtime refused a launch */
+};
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* qk_last_error(void);
+
+/* ABI revision; bumped on any incompatible signature change. */
+int qk_abi_version(void);
+
+/*
+ * npu_dynamic_quant -- replaces aclnnDynamicQuant behind EXEC_NPU_CMD
+ * (op_plugin/utils/op_api_common.h:520-570); the nearest reference op is the
+ * static quantize_per_channel (op_plugin/ops/base_ops/aclops/QuantizePerChannelKernelNpu.cpp:69-92).
+ * x: [rows, K] fp16/bf16, row-major.  smooth_scales: [K] fp32 or NULL.
+ * y: [rows, K] int8.  scale: [rows] fp32.
+ * Per row: s = max|x*smooth| / 127 (fp32 division), y = clamp(rint(x*smooth / s)),
+ * ties to even; an all-zero row gives s = 0, y = 0.  No workspace.
+ */
+int qk_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t K,
+                     const float* smooth_scales, int8_t* y, float* scale, qk_stream_t stream);
+
+/*
+ * npu_quant_matmul (W8A8), phase 1 -- replaces aclnnQuantMatmul*GetWorkspaceSize
+ * (op_plugin/utils/op_api_common.h:543-546).  Writes the workspace bytes the
+ * call with the same shape needs (0 when none) to *bytes.
+ */
+int qk_quant_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int out_dtype, size_t* bytes);
+
+/*
+ * npu_quant_matmul (W8A8), phase 2 -- replaces aclnnQuantMatmul* behind
+ * EXEC_NPU_CMD (op_plugin/utils/op_api_common.h:552-566); shape/bias rules
+ * follow mm / addmm (op_plugin/ops/base_ops/opapi/MmKernelNpuOpApi.cpp:24-32,
+ * op_plugin/ops/base_ops/opapi/AddmmKernelNpuOpApi.cpp:24-55).
+ * x1: int8 [M,K], row stride ldx1.  x2: int8 [K,N] addressed as
+ * x2[k*x2_stride_k + n*x2_stride_n]; exactly one stride must be 1
+ * ([K,N]-contiguous: (N',1); transposed view of [N,K]: (1,K')), as the
+ * reference flags a transposed mat2 instead of copying it
+ * (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:40-53).
+ * acc = sum_k x1*x2 in int32, exact: K above 131071 is refused (QK_ERR_UNSUPPORTED).
+ * scale: fp32 [scale_len], scale_len 1 or N.  offset (int8 output only): fp32 [1|N] or NULL.
+ * pertoken_scale: fp32 [M] or NULL.  bias: [N] of bias_dtype
+ * (QK_I32: added to acc; QK_BF16/QK_F16/QK_F32: added after scaling) or NULL.
+ * out: [M,N] row-major of out_dtype:
+ *   QK_BF16/QK_F16: cast(fmaf(float(acc) [* pertoken[m]], scale[n], bias[n]))
+ *   QK_I8:          clamp(rint(fmaf(float(acc), scale[n], offset[n])))
+ *   QK_I32:         acc (+ int32 bias)
+ */
+int qk_quant_matmul(const int8_t* x1, int64_t ldx1,
+                    const int8_t* x2, int64_t x2_stride_k, int64_t x2_stride_n,
+                    int64_t M, int64_t N, int64_t K,
+                    const float* scale, int64_t scale_len,
+                    const float* offset, int64_t offset_len,
+                    const float* pertoken_scale,
+                    const void* bias, int bias_dtype,
+                    void* out, int out_dtype,
+                    void* workspace, size_t workspace_bytes, qk_stream_t stream);
+
+/*
+ * npu_weight_quant_batchmatmul, phase 1 (see qk_quant_matmul_workspace_size).
+ */
+int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weight_dtype,
+                                       int64_t group_size, size_t* bytes);
+
+/*
+ * npu_weight_quant_batchmatmul (W4A16 / W8A16), phase 2 -- replaces
+ * aclnnWeightQuantBatchMatmul* behind EXEC_NPU_CMD; the nearest reference op
+ * is bmm (op_plugin/ops/base_ops/opapi/BmmKernelNpuOpApi.cpp:24-52).
+ * x: [M,K] fp16/bf16 row-major.  weight: QK_I32 -> int4 packed [K, N/8]
+ * (nibble i of word j is column 8j+i, two's complement); QK_I8 -> int8 [K,N].
+ * antiquant_scale / antiquant_offset: [K/group, N] (group_size > 0) or [N]
+ * (group_size == 0, per channel), of scale_dtype (fp16/bf16); offset may be NULL.
+ * bias: [N] or NULL.  out: [M,N] of out_dtype (fp16/bf16).
+ * out = sum_k x[m,k] * (w[k,n] + offset[g,n]) * scale[g,n] + bias[n], g = k/group,
+ * with fp32 accumulation; the dequantized weight is never rounded to 16 bits.
+ */
+int qk_weight_quant_bmm(const void* x, int x_dtype,
+                        const void* weight, int weight_dtype,
+                        const void* antiquant_scale, const void* antiquant_offset, int scale_dtype,
+                        int64_t M, int64_t N, int64_t K, int64_t group_size,
+                        const void* bias, int bias_dtype,
+                        void* out, int out_dtype,
+                        void* workspace, size_t workspace_bytes, qk_stream_t stream);
+
+/*
+ * npu_convert_weight_to_int4pack -- packs int4 values held one per element
+ * (int8 or int32 [K,N], values in [-8,7]) into int32 [K, N/8] in the layout
+ * qk_weight_quant_bmm reads.  No counterpart exists in the reference snapshot
+ * (int4 is disabled there: op_plugin/third_party/acl/inc/graph/types.h:57).
+ */
+int qk_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed,
+                 qk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QK_ABI_H */

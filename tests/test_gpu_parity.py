@@ -1,0 +1,366 @@
+"""GPU parity: the HIP kernels against the CPU oracle on the same seeded inputs.
+
+Bar: int8 quantized activations, their scales and int32 accumulators
+bit-exact; W8A8 bf16/fp16 outputs bit-exact as well (the epilogue's float32
+operations are fixed by the op contract) and, as the stated bar, within
+rtol 1e-2 / atol 1e-2; W4A16 outputs within rtol 1e-2 / atol 1e-2 of the
+float64 oracle.  Full-size shapes the oracle cannot finish in seconds are
+checked on a row subset plus exact checksums of the whole int32 output.
+"""
+import numpy as np
+import pytest
+import torch
+
+from op_plugin_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, F32, I8, I32 = 1, 2, 3, 4, 5
+CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32, torch.int8: I8, torch.int32: I32}
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import op_plugin_amd
+    return op_plugin_amd
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def to_bits(t):
+    return W.bits(t.cpu())
+
+
+def bf16_close(got_bits, ref_bits, dtype=torch.bfloat16, rtol=1e-2, atol=1e-2):
+    g = W.from_bits(got_bits, dtype).float()
+    r = W.from_bits(ref_bits, dtype).float()
+    torch.testing.assert_close(g, r, rtol=rtol, atol=atol)
+
+
+# ----------------------------------------------------------------------------- npu_dynamic_quant
+
+DQ_CASES = [
+    ("cfg1", W.CFG1, None),
+    ("cfg2_m16", W.CFG2[2], None),
+    ("cfg4", W.CFG4, None),
+]
+
+
+@pytest.mark.parametrize("name,case,_", DQ_CASES)
+def test_dynamic_quant_configs(ops, oracle, name, case, _):
+    say(f"dynamic_quant {name} {case.M}x{case.K}")
+    x = W.w8a8_inputs(case)["x"]
+    y, s = ops.npu_dynamic_quant(x.to(DEV))
+    torch.cuda.synchronize()
+    ry, rs = oracle.dynamic_quant(W.bits(x), CODE[x.dtype])
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(y.cpu().numpy(), ry)
+
+
+@pytest.mark.parametrize("K", [4096, 14336])
+def test_dynamic_quant_cfg5_bf16(ops, oracle, K):
+    say(f"dynamic_quant cfg5 bf16 512x{K}")
+    g = torch.Generator().manual_seed(K)
+    x = torch.randn((512, K), generator=g).to(torch.bfloat16)
+    y, s = ops.npu_dynamic_quant(x.to(DEV))
+    ry, rs = oracle.dynamic_quant(W.bits(x), BF16)
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(y.cpu().numpy(), ry)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K", [1, 7, 8, 24, 1000, 2056, 40000])
+def test_dynamic_quant_edge_cases(ops, oracle, dtype, K):
+    say(f"dynamic_quant edge {dtype} K={K}")
+    g = torch.Generator().manual_seed(K)
+    x = torch.randn((6, K), generator=g)
+    x[1] = 0.0                                   # zero row
+    x[2] = 0.0
+    x[2, K // 2] = -3.0                          # single nonzero
+    x[3] = x[3] * 1e-30 if dtype == torch.bfloat16 else x[3] * 1e-6   # tiny (subnormal range)
+    if K >= 8:                                   # exact ties around scale 1.0
+        x[4, :8] = torch.tensor([127.0, 0.5, 1.5, 2.5, -2.5, 3.5, 126.5, -126.5])
+        x[4, 8:] = 0.0
+    x = x.to(dtype)
+    y, s = ops.npu_dynamic_quant(x.to(DEV))
+    ry, rs = oracle.dynamic_quant(W.bits(x), CODE[dtype])
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(y.cpu().numpy(), ry)
+
+
+def test_dynamic_quant_smooth_and_batch_dims(ops, oracle):
+    say("dynamic_quant smooth scales, 3-D input")
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((2, 3, 512), generator=g).to(torch.float16)
+    sm = 0.5 + torch.rand(512, generator=g)
+    y, s = ops.npu_dynamic_quant(x.to(DEV), smooth_scales=sm.to(DEV))
+    assert y.shape == (2, 3, 512) and s.shape == (2, 3)
+    ry, rs = oracle.dynamic_quant(W.bits(x), F16, sm.numpy())
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(y.cpu().numpy(), ry)
+
+
+def test_dynamic_quant_empty(ops):
+    say("dynamic_quant empty")
+    y, s = ops.npu_dynamic_quant(torch.empty((0, 64), dtype=torch.float16, device=DEV))
+    assert y.shape == (0, 64) and s.shape == (0,)
+
+
+# ----------------------------------------------------------------------------- npu_quant_matmul
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (4, 256, 128), (16, 96, 512), (33, 200, 1024),
+                                   (128, 384, 4096), (257, 136, 192), (64, 8, 16), (5, 7, 13)])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_quant_matmul_int32_exact(ops, oracle, M, N, K, transposed):
+    say(f"quant_matmul int32 M={M} N={N} K={K} transposed={transposed}")
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    wd = w.to(DEV)
+    if transposed:
+        wd = w.t().contiguous().to(DEV).t()      # [K,N] view of an [N,K] tensor
+    one = torch.ones(1, device=DEV)
+    out = ops.npu_quant_matmul(a.to(DEV), wd, one, output_dtype=torch.int32)
+    ref = oracle.w8a8_acc(a.numpy(), w.numpy())
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
+def _w8a8_full_path(ops, oracle, case, rows=None, seed=0):
+    d = W.w8a8_inputs(case, seed)
+    x, w, ws, b = d["x"], d["w"], d["w_scale"], d["bias"]
+    xq, xs = ops.npu_dynamic_quant(x.to(DEV))
+    out = ops.npu_quant_matmul(xq, w.to(DEV), ws.to(DEV), pertoken_scale=xs,
+                               bias=None if b is None else b.to(DEV), output_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    sel = slice(None) if rows is None else rows
+    rq, rs = oracle.dynamic_quant(W.bits(x[sel]), CODE[x.dtype])
+    assert np.array_equal(xq.cpu().numpy()[sel], rq)
+    assert np.array_equal(xs.cpu().numpy()[sel], rs)
+    ref = oracle.quant_matmul(rq, w.numpy(), ws.numpy(), pertoken=rs,
+                              bias=None if b is None else W.bits(b), bias_dtype=BF16, out_dtype=BF16)
+    got = to_bits(out)[sel]
+    bf16_close(got, ref)
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} bf16 outputs differ in bits"
+    return xq, w
+
+
+def test_quant_matmul_cfg1(ops, oracle):
+    say("quant_matmul cfg1 full path 128x4096x4096")
+    _w8a8_full_path(ops, oracle, W.CFG1)
+
+
+@pytest.mark.parametrize("idx", [0, 1, 2])
+def test_quant_matmul_cfg2_decode(ops, oracle, idx):
+    c = W.CFG2[idx]
+    say(f"quant_matmul cfg2 M={c.M} 8192x28672")
+    _w8a8_full_path(ops, oracle, c)
+
+
+def test_quant_matmul_cfg4_prefill(ops, oracle):
+    """Full 4096x8192x8192: rows 0..31, 2048..2079 and the last 16 against the oracle,
+    and every int32 accumulator through exact row and column checksums."""
+    c = W.CFG4
+    say("quant_matmul cfg4 prefill 4096x8192x8192")
+    rows = np.r_[0:32, 2048:2080, 4080:4096]
+    xq, w = _w8a8_full_path(ops, oracle, c, rows=rows)
+    acc = ops.npu_quant_matmul(xq, w.to(DEV), torch.ones(1, device=DEV), output_dtype=torch.int32)
+    a64 = xq.cpu().to(torch.int64)
+    w64 = w.to(torch.int64)
+    acc64 = acc.cpu().to(torch.int64)
+    # column sums: 1^T (A W) = (1^T A) W ; row sums: (A W) 1 = A (W 1)
+    assert torch.equal(acc64.sum(0), a64.sum(0) @ w64)
+    assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32, torch.int32])
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_quant_matmul_epilogue_variants(ops, oracle, out_dtype, bias_dtype, per_tensor):
+    say(f"quant_matmul epilogue out={out_dtype} bias={bias_dtype} per_tensor={per_tensor}")
+    g = torch.Generator().manual_seed(3)
+    M, N, K = 48, 160, 320
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    s = 1e-3 + 9e-3 * torch.rand(1 if per_tensor else N, generator=g)
+    pt = 1e-2 * torch.rand(M, generator=g)
+    b = None
+    if bias_dtype is torch.int32:
+        b = torch.randint(-1000, 1000, (N,), generator=g, dtype=torch.int32)
+    elif bias_dtype is not None:
+        b = torch.randn(N, generator=g).to(bias_dtype)
+    out = ops.npu_quant_matmul(a.to(DEV), w.to(DEV), s.to(DEV), pertoken_scale=pt.to(DEV),
+                               bias=None if b is None else b.to(DEV), output_dtype=out_dtype)
+    bias_np = None if b is None else (b.numpy() if b.dtype in (torch.int32, torch.float32) else W.bits(b))
+    ref = oracle.quant_matmul(a.numpy(), w.numpy(), s.numpy(), pertoken=pt.numpy(), bias=bias_np,
+                              bias_dtype=CODE[b.dtype] if b is not None else BF16, out_dtype=CODE[out_dtype])
+    got = out.cpu()
+    got_np = got.numpy() if out_dtype == torch.float32 else W.bits(got)
+    assert np.array_equal(got_np, ref)
+
+
+def test_quant_matmul_int8_output(ops, oracle):
+    say("quant_matmul int8 output with offset and int32 bias")
+    g = torch.Generator().manual_seed(4)
+    M, N, K = 20, 64, 256
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    s = 1e-4 + 1e-3 * torch.rand(N, generator=g)
+    off = torch.randn(N, generator=g)
+    b = torch.randint(-500, 500, (N,), generator=g, dtype=torch.int32)
+    out = ops.npu_quant_matmul(a.to(DEV), w.to(DEV), s.to(DEV), offset=off.to(DEV), bias=b.to(DEV),
+                               output_dtype=torch.int8)
+    ref = oracle.quant_matmul(a.numpy(), w.numpy(), s.numpy(), offset=off.numpy(), bias=b.numpy(),
+                              bias_dtype=I32, out_dtype=I8)
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
+def test_quant_matmul_batched_x1_and_transposed_weight(ops, oracle):
+    say("quant_matmul 3-D x1, nn.Linear-layout weight")
+    g = torch.Generator().manual_seed(5)
+    a = torch.randint(-127, 128, (2, 24, 256), generator=g, dtype=torch.int8)
+    w_nk = torch.randint(-127, 128, (192, 256), generator=g, dtype=torch.int8)
+    s = 1e-3 + 9e-3 * torch.rand(192, generator=g)
+    out = ops.npu_quant_matmul(a.to(DEV), w_nk.to(DEV).t(), s.to(DEV), output_dtype=torch.bfloat16)
+    assert out.shape == (2, 24, 192)
+    ref = oracle.quant_matmul(a.reshape(48, 256).numpy(), w_nk.t().numpy(), s.numpy(), out_dtype=BF16)
+    assert np.array_equal(to_bits(out).reshape(48, 192), ref)
+
+
+def test_quant_matmul_errors(ops):
+    say("quant_matmul argument errors")
+    a = torch.zeros((4, 64), dtype=torch.int8, device=DEV)
+    w = torch.zeros((64, 32), dtype=torch.int8, device=DEV)
+    with pytest.raises(RuntimeError, match="must equal"):
+        ops.npu_quant_matmul(a, w[:32], torch.ones(32, device=DEV), output_dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="scale must be"):
+        ops.npu_quant_matmul(a, w, torch.ones(7, device=DEV), output_dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="int8"):
+        ops.npu_quant_matmul(a.float(), w, torch.ones(32, device=DEV))
+
+
+# ----------------------------------------------------------------------------- npu_weight_quant_batchmatmul
+
+def _w4_ref(oracle, d, group, bias=None, x_dtype=torch.bfloat16, s_dtype=torch.float16):
+    return oracle.weight_quant_bmm(W.bits(d["x"]), CODE[x_dtype], d["w_packed"].numpy(), W.bits(d["scale"]),
+                                   None if d["offset"] is None else W.bits(d["offset"]), CODE[s_dtype], group,
+                                   bias=None if bias is None else W.bits(bias), bias_dtype=CODE.get(
+                                       None if bias is None else bias.dtype, BF16),
+                                   out_dtype=CODE[x_dtype])
+
+
+def _w4_run(ops, d, group, bias=None):
+    return ops.npu_weight_quant_batchmatmul(
+        d["x"].to(DEV), d["w_packed"].to(DEV), d["scale"].to(DEV),
+        None if d["offset"] is None else d["offset"].to(DEV), bias=None if bias is None else bias.to(DEV),
+        antiquant_group_size=group)
+
+
+def test_w4a16_cfg3_decode(ops, oracle):
+    c = W.CFG3[0]
+    say(f"w4a16 cfg3 M={c.M} 4096x11008")
+    d = W.w4a16_inputs(c)
+    out = _w4_run(ops, d, 128)
+    bf16_close(to_bits(out), _w4_ref(oracle, d, 128))
+
+
+def test_w4a16_cfg3_prefill(ops, oracle):
+    c = W.CFG3[1]
+    say(f"w4a16 cfg3 M={c.M} 4096x11008 (rows subset)")
+    d = W.w4a16_inputs(c)
+    out = _w4_run(ops, d, 128)
+    rows = np.r_[0:16, 1000:1016, 2032:2048]
+    sub = dict(d, x=d["x"][rows])
+    bf16_close(to_bits(out)[rows], _w4_ref(oracle, sub, 128))
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype", [
+    (1, 64, 128, 128, True, torch.bfloat16),
+    (3, 136, 256, 32, True, torch.bfloat16),
+    (16, 256, 512, 64, False, torch.bfloat16),
+    (17, 128, 384, 128, True, torch.float16),
+    (40, 200, 256, 0, True, torch.bfloat16),
+    (5, 24, 96, 0, False, torch.float16),
+    (2, 16, 100, 0, True, torch.bfloat16),       # K % 32 != 0: generic kernel
+])
+def test_w4a16_shapes(ops, oracle, M, N, K, group, offset, x_dtype):
+    say(f"w4a16 M={M} N={N} K={K} group={group} offset={offset} {x_dtype}")
+    case = W.W4A16Case(M=M, N=N, K=K, group=group, x_dtype=x_dtype, offset=offset)
+    d = W.w4a16_inputs(case, seed=M + N + K)
+    if x_dtype == torch.float16:
+        d = dict(d, scale=d["scale"], offset=d["offset"])
+    if group == 0:
+        d = dict(d, scale=d["scale"].reshape(-1), offset=None if d["offset"] is None else d["offset"].reshape(-1))
+    b = torch.randn(N).to(x_dtype)
+    out = _w4_run(ops, d, group, bias=b)
+    ref = _w4_ref(oracle, d, group, bias=b, x_dtype=x_dtype)
+    bf16_close(to_bits(out), ref, dtype=x_dtype)
+
+
+def test_int4_pack_device(ops, oracle):
+    say("npu_convert_weight_to_int4pack")
+    g = torch.Generator().manual_seed(8)
+    w = torch.randint(-8, 8, (64, 96), generator=g, dtype=torch.int32)
+    p = ops.npu_convert_weight_to_int4pack(w.to(DEV))
+    assert np.array_equal(p.cpu().numpy(), oracle.int4_pack(w.numpy().astype(np.int8)))
+
+
+# ----------------------------------------------------------------------------- through the C ABI
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def test_abi_quant_matmul_matches_op(ops, oracle):
+    """Drive qk_quant_matmul directly with device pointers (the drop-in boundary)."""
+    say("ABI qk_quant_matmul")
+    L = ops.abi()
+    g = torch.Generator().manual_seed(12)
+    M, N, K = 32, 256, 512
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(DEV)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8).to(DEV)
+    s = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(DEV)
+    pt = (1e-2 * torch.rand(M, generator=g)).to(DEV)
+    b = torch.randn(N, generator=g).to(torch.bfloat16).to(DEV)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    import ctypes
+    ws = ctypes.c_size_t(0)
+    assert L.qk_quant_matmul_workspace_size(M, N, K, BF16, ctypes.byref(ws)) == 0
+    wsbuf = torch.empty(max(1, ws.value), dtype=torch.uint8, device=DEV)
+    rc = L.qk_quant_matmul(a.data_ptr(), K, w.data_ptr(), N, 1, M, N, K, s.data_ptr(), N, None, 0, pt.data_ptr(),
+                           b.data_ptr(), BF16, out.data_ptr(), BF16, wsbuf.data_ptr(), ws.value, _stream())
+    assert rc == 0, ops.last_error()
+    ref = ops.npu_quant_matmul(a, w, s, pertoken_scale=pt, bias=b, output_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    # a bad stride pair is refused with a message, nothing launched
+    rc = L.qk_quant_matmul(a.data_ptr(), K, w.data_ptr(), 2, 2, M, N, K, s.data_ptr(), N, None, 0, None, None, 0,
+                           out.data_ptr(), BF16, None, 0, _stream())
+    assert rc == -1 and "transposed view" in ops.last_error()
+
+
+def test_abi_dynamic_quant_and_w4a16(ops, oracle):
+    say("ABI qk_dynamic_quant / qk_weight_quant_bmm")
+    L = ops.abi()
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn((8, 1024), generator=g).to(torch.float16).to(DEV)
+    y = torch.empty((8, 1024), dtype=torch.int8, device=DEV)
+    s = torch.empty(8, dtype=torch.float32, device=DEV)
+    assert L.qk_dynamic_quant(x.data_ptr(), F16, 8, 1024, None, y.data_ptr(), s.data_ptr(), _stream()) == 0
+    torch.cuda.synchronize()
+    ry, rs = oracle.dynamic_quant(W.bits(x.cpu()), F16)
+    assert np.array_equal(y.cpu().numpy(), ry) and np.array_equal(s.cpu().numpy(), rs)
+
+    case = W.W4A16Case(M=4, N=128, K=256)
+    d = W.w4a16_inputs(case, seed=1)
+    xd, wd, sd, od = (d[k].to(DEV) for k in ("x", "w_packed", "scale", "offset"))
+    out = torch.empty((4, 128), dtype=torch.bfloat16, device=DEV)
+    rc = L.qk_weight_quant_bmm(xd.data_ptr(), BF16, wd.data_ptr(), I32, sd.data_ptr(), od.data_ptr(), F16, 4, 128,
+                               256, 128, None, 0, out.data_ptr(), BF16, None, 0, _stream())
+    assert rc == 0, ops.last_error()
+    torch.cuda.synchronize()
+    bf16_close(to_bits(out), _w4_ref(oracle, d, 128))

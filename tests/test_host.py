@@ -1,0 +1,120 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every
+symbol include/qk_abi.h declares, invalid arguments are refused before any
+launch, and the torch.ops.npu schemas infer shapes and raise the documented
+errors (Meta tensors run the same checks as the GPU implementations)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import op_plugin_amd as q
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+F16, BF16, F32, I8, I32 = 1, 2, 3, 4, 5
+
+
+def _declared_functions():
+    src = open(os.path.join(ROOT, "include", "qk_abi.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(qk_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_abi_exports_every_declared_symbol():
+    names = _declared_functions()
+    assert len(names) >= 8
+    L = ctypes.CDLL(q.LIB_PATH)
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in qk_abi.h but not exported"
+    assert set(names) == set(q.ABI_SYMBOLS)
+    assert q.abi().qk_abi_version() == 1
+
+
+def test_abi_refuses_bad_arguments_without_launch():
+    L = q.abi()
+    assert L.qk_dynamic_quant(None, 9, 4, 16, None, None, None, None) == q.QK_ERR_ARG
+    assert "float16 or bfloat16" in q.last_error()
+    assert L.qk_dynamic_quant(None, F16, 4, 16, None, None, None, None) == q.QK_ERR_ARG
+    assert "null pointer" in q.last_error()
+    assert L.qk_dynamic_quant(None, F16, 0, 16, None, None, None, None) == q.QK_OK
+    assert q.last_error() == ""
+    fake = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    rc = L.qk_quant_matmul(fake, 64, fake, 2, 2, 4, 32, 64, fake, 32, None, 0, None, None, 0, fake, BF16, None, 0, None)
+    assert rc == q.QK_ERR_ARG and "transposed view" in q.last_error()
+    rc = L.qk_quant_matmul(fake, 64, fake, 32, 1, 4, 32, 64, fake, 7, None, 0, None, None, 0, fake, BF16, None, 0, None)
+    assert rc == q.QK_ERR_ARG and "scale" in q.last_error()
+    rc = L.qk_quant_matmul(fake, 200000, fake, 32, 1, 4, 32, 200000, fake, 32, None, 0, None, None, 0, fake, BF16,
+                           None, 0, None)
+    assert rc == q.QK_ERR_UNSUPPORTED and "int32-exact" in q.last_error()
+    rc = L.qk_quant_matmul(fake, 64, fake, 32, 1, 4, 32, 64, fake, 32, fake, 32, None, None, 0, fake, BF16, None, 0,
+                           None)
+    assert rc == q.QK_ERR_ARG and "offset" in q.last_error()
+    rc = L.qk_weight_quant_bmm(fake, BF16, fake, I32, fake, None, F16, 4, 12, 128, 128, None, 0, fake, BF16, None, 0,
+                               None)
+    assert rc == q.QK_ERR_ARG and "N % 8" in q.last_error()
+    rc = L.qk_weight_quant_bmm(fake, BF16, fake, I32, fake, None, F16, 4, 16, 100, 128, None, 0, fake, BF16, None, 0,
+                               None)
+    assert rc == q.QK_ERR_ARG and "multiple of antiquant_group_size" in q.last_error()
+    ws = ctypes.c_size_t(123)
+    assert L.qk_weight_quant_bmm_workspace_size(16, 11008, 4096, I32, 128, ctypes.byref(ws)) == 0
+    assert L.qk_int4_pack(fake, I8, 4, 12, fake, None) == q.QK_ERR_ARG
+
+
+def _m(shape, dtype):
+    return torch.empty(shape, dtype=dtype, device="meta")
+
+
+def test_schemas_registered():
+    for name in ("npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
+                 "npu_convert_weight_to_int4pack"):
+        assert hasattr(torch.ops.npu, name)
+    s = str(torch.ops.npu.npu_quant_matmul.default._schema)
+    assert "pertoken_scale" in s and "ScalarType? output_dtype" in s
+
+
+def test_meta_shapes():
+    y, s = q.npu_dynamic_quant(_m((2, 3, 64), torch.bfloat16))
+    assert y.shape == (2, 3, 64) and y.dtype == torch.int8 and s.shape == (2, 3) and s.dtype == torch.float32
+    out = q.npu_quant_matmul(_m((2, 5, 64), torch.int8), _m((64, 48), torch.int8), _m((48,), torch.float32),
+                             pertoken_scale=_m((10,), torch.float32), bias=_m((48,), torch.bfloat16),
+                             output_dtype=torch.bfloat16)
+    assert out.shape == (2, 5, 48) and out.dtype == torch.bfloat16
+    assert q.npu_quant_matmul(_m((4, 64), torch.int8), _m((64, 8), torch.int8), _m((1,), torch.float32)).dtype \
+        == torch.int8
+    out = q.npu_weight_quant_batchmatmul(_m((16, 4096), torch.bfloat16), _m((4096, 1376), torch.int32),
+                                         _m((32, 11008), torch.float16), _m((32, 11008), torch.float16),
+                                         antiquant_group_size=128)
+    assert out.shape == (16, 11008) and out.dtype == torch.bfloat16
+    assert q.npu_convert_weight_to_int4pack(_m((64, 96), torch.int32)).shape == (64, 12)
+
+
+@pytest.mark.parametrize("call,msg", [
+    (lambda: q.npu_dynamic_quant(_m((4, 8), torch.float32)), "float16 or bfloat16"),
+    (lambda: q.npu_dynamic_quant(_m((4, 8), torch.float16), smooth_scales=_m((7,), torch.float32)), "smooth_scales"),
+    (lambda: q.npu_quant_matmul(_m((4, 64), torch.int8), _m((32, 8), torch.int8), _m((8,), torch.float32)),
+     "must equal"),
+    (lambda: q.npu_quant_matmul(_m((4, 64), torch.int8), _m((64, 8), torch.int8), _m((8,), torch.float32),
+                                pertoken_scale=_m((3,), torch.float32), output_dtype=torch.bfloat16), "pertoken_scale"),
+    (lambda: q.npu_quant_matmul(_m((4, 64), torch.int8), _m((64, 8), torch.int8), _m((8,), torch.float32),
+                                pertoken_scale=_m((4,), torch.float32)), "pertoken_scale needs"),
+    (lambda: q.npu_quant_matmul(_m((4, 64), torch.int8), _m((64, 8), torch.int8), _m((8,), torch.float32),
+                                bias=_m((8,), torch.bfloat16), output_dtype=torch.int32), "int32 bias"),
+    (lambda: q.npu_weight_quant_batchmatmul(_m((2, 100), torch.bfloat16), _m((100, 2), torch.int32),
+                                            _m((1, 16), torch.float16), antiquant_group_size=64), "multiple"),
+    (lambda: q.npu_weight_quant_batchmatmul(_m((2, 128), torch.bfloat16), _m((128, 2), torch.int32),
+                                            _m((2, 16), torch.float16), antiquant_group_size=128), "antiquant_scale"),
+    (lambda: q.npu_weight_quant_batchmatmul(_m((2, 128), torch.bfloat16), _m((128, 2), torch.int32),
+                                            _m((1, 16), torch.float16), quant_scale=_m((16,), torch.float32),
+                                            antiquant_group_size=128), "not supported"),
+    (lambda: q.npu_convert_weight_to_int4pack(_m((4, 12), torch.int32)), "multiple of 8"),
+])
+def test_meta_errors(call, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        call()
+
+
+def test_product_path_has_no_cpu_kernel():
+    """The ops have no CPU implementation: a CPU tensor is refused, never computed on the host."""
+    with pytest.raises(NotImplementedError):
+        q.npu_dynamic_quant(torch.zeros((2, 8), dtype=torch.float16))
