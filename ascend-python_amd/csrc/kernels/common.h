@@ -51,6 +51,17 @@ __device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype
     }
 }
 
+// ---------------------------------------------------------------- XCD-aware ids
+// The dispatcher hands consecutive workgroup ids to the 8 XCDs round-robin,
+// and each XCD has its own L2.  Renumbering so that the ids one XCD receives
+// are consecutive logical ids keeps neighbouring tiles (which share cache
+// lines of A, B or a packed weight row) inside one L2.  Bijective on [0, nblk).
+__device__ __forceinline__ int xcd_swizzle(int bid, int nblk) {
+    const int full = nblk & ~7;
+    if (bid >= full) return bid;
+    return (bid & 7) * (full >> 3) + (bid >> 3);
+}
+
 // ---------------------------------------------------------------- W8A8 epilogue
 // Applied to the exact int32 accumulator of one output element.  The float
 // operations (and their order) are part of the op contract:

@@ -181,6 +181,198 @@ __global__ __launch_bounds__(kThreads) void qmm_tiled(QmmArgs p) {
             }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill kernel: 256x256 output tile per 256-thread workgroup (wave tile
+// 128x128 = 8x8 MFMA tiles, 256 int32 accumulators per lane), K in 64-byte
+// steps, two LDS stages (64 KB) so one barrier per step, next step's global
+// loads in flight during the current step's MFMAs.
+//
+// LDS layouts (16-byte chunks XOR-swizzled so fragment reads and tile writes
+// are bank-conflict free):
+//   A and [N,K] B : [row][64 k-bytes], chunk c of row r at r*64 + 16*(c ^ ((r>>2)&3))
+//   [K,N] B       : [k][256 n-bytes],  chunk c of row k at k*256 + 16*(c ^ h(k)),
+//                   h(k) = (k&7) | ((k>>4)&1)<<3
+// A [K,N] weight is kept in its natural layout and the MFMA B fragment (16
+// consecutive k of one column per lane) is read with two ds_read_b64_tr_b8:
+// in each 16-lane group, lane i receives byte (i&7) of the 8-byte rows
+// addressed by lanes 2b + (i>>3), b = 0..7 -- so lanes 2b / 2b+1 address row
+// k0+b at columns 0..7 / 8..15 of the tile and every lane gets its column's
+// 8 consecutive k bytes per read.
+// Workgroups are renumbered so each XCD (ids congruent mod 8) owns a compact
+// block of output tiles (8 tile-rows x 8 tile-cols share its L2).
+namespace big {
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int A_BYTES = BM * BK;
+constexpr int B_BYTES = BN * BK;
+constexpr int STAGE = A_BYTES + B_BYTES;
+
+__device__ __forceinline__ int rk_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
+__device__ __forceinline__ int kn_off(int k, int c16) {
+    const int h = (k & 7) | (((k >> 4) & 1) << 3);
+    return k * 256 + 16 * (c16 ^ h);
+}
+
+typedef int32_t v2i __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v2i lds_tr8(const int8_t* p) {
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(p));
+}
+
+// One output element from preloaded per-column / per-row operands; the same
+// float operations, in the same order, as qmm_store (bi = 0 / bf = +0 / pt = 1
+// when the op has no int32 bias / float bias / per-token scale).
+template <int OUT>
+__device__ __forceinline__ void store_elem(void* out, int64_t o, int32_t acc, float s, float bf, int32_t bi, float pt,
+                                           float off) {
+    acc = (int32_t)((uint32_t)acc + (uint32_t)bi);
+    if constexpr (OUT == QK_I32) {
+        ((int32_t*)out)[o] = acc;
+    } else if constexpr (OUT == QK_I8) {
+        float t = __builtin_rintf(__builtin_fmaf((float)acc, s, off));
+        t = fminf(fmaxf(t, -128.0f), 127.0f);
+        ((int8_t*)out)[o] = (int8_t)(int)t;
+    } else {
+        const float v = __builtin_fmaf((float)acc * pt, s, bf);
+        if constexpr (OUT == QK_BF16) ((uint16_t*)out)[o] = (uint16_t)f32_to_bf16_bits(v);
+        else if constexpr (OUT == QK_F16) ((uint16_t*)out)[o] = (uint16_t)f32_to_f16_bits(v);
+        else ((float*)out)[o] = v;
+    }
+}
+}  // namespace big
+
+template <bool B_KN, int OUT>
+__global__ __launch_bounds__(kThreads) void qmm_big(QmmArgs p, int tiles_m, int tiles_n) {
+    using namespace big;
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * STAGE];
+
+    // XCD-aware renumbering + grouped tile order
+    const int bid = xcd_swizzle(blockIdx.x, tiles_m * tiles_n);
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int grp = bid / per_group;
+    const int first_m = grp * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int tm = first_m + (bid % per_group) % gm;
+    const int tn = (bid % per_group) / gm;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int fr = lane & 15, g = lane >> 4;
+
+    // ---- global -> register prefetch (4 x 16 B of A and of B per thread)
+    i32x4 ra[4], rb[4];
+    auto gload = [&](int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 256 * i;
+            const int r = q >> 2, c = q & 3;
+            const int64_t m = m0 + r, k = k0 + 16 * c;
+            ra[i] = (m < p.M && k < p.K) ? *reinterpret_cast<const i32x4*>(p.a + m * p.lda + k) : (i32x4){0, 0, 0, 0};
+            if (!B_KN) {
+                const int64_t n = n0 + r;
+                rb[i] = (n < p.N && k < p.K) ? *reinterpret_cast<const i32x4*>(p.b + n * p.sbn + k)
+                                             : (i32x4){0, 0, 0, 0};
+            } else {
+                const int kr = q >> 4, c16 = q & 15;
+                const int64_t kk = k0 + kr, n = n0 + 16 * c16;
+                rb[i] = (kk < p.K && n < p.N) ? *reinterpret_cast<const i32x4*>(p.b + kk * p.sbk + n)
+                                              : (i32x4){0, 0, 0, 0};
+            }
+        }
+    };
+    auto lstore = [&](int st) {
+        int8_t* As = smem + st * STAGE;
+        int8_t* Bs = As + A_BYTES;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 256 * i;
+            *reinterpret_cast<i32x4*>(As + rk_off(q >> 2, q & 3)) = ra[i];
+            if (!B_KN) *reinterpret_cast<i32x4*>(Bs + rk_off(q >> 2, q & 3)) = rb[i];
+            else *reinterpret_cast<i32x4*>(Bs + kn_off(q >> 4, q & 15)) = rb[i];
+        }
+    };
+
+    i32x4 acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = (i32x4){0, 0, 0, 0};
+
+    // per-lane fragment addressing (constant over K)
+    const int tr_h = (fr >> 1) | ((g & 1) << 3);
+    const int tr_k = 16 * g + (fr >> 1);
+    const int tr_b = 8 * (fr & 1);
+
+    const int64_t nk = (p.K + big::BK - 1) / big::BK;
+    gload(0);
+    lstore(0);
+    if (nk > 1) gload(big::BK);
+    for (int64_t it = 0; it < nk; ++it) {
+        __syncthreads();
+        const int st = (int)(it & 1);
+        const int8_t* As = smem + st * STAGE;
+        const int8_t* Bs = As + A_BYTES;
+        i32x4 af[8], bfr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) af[i] = *reinterpret_cast<const i32x4*>(As + rk_off(wm * 128 + 16 * i + fr, g));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (!B_KN) {
+                bfr[j] = *reinterpret_cast<const i32x4*>(Bs + rk_off(wn * 128 + 16 * j + fr, g));
+            } else {
+                const int c16 = wn * 8 + j;
+                const v2i lo = lds_tr8(Bs + tr_k * 256 + 16 * (c16 ^ tr_h) + tr_b);
+                const v2i hi = lds_tr8(Bs + (tr_k + 8) * 256 + 16 * (c16 ^ tr_h) + tr_b);
+                bfr[j] = (i32x4){lo[0], lo[1], hi[0], hi[1]};
+            }
+        }
+        // stage it+1 (already in registers) goes to the other buffer, then fetch it+2
+        if (it + 1 < nk) {
+            lstore(st ^ 1);
+            if (it + 2 < nk) gload((it + 2) * big::BK);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+
+    // ---- epilogue: per-column and per-row operands loaded once per lane
+    const QmmEpilogue& e = p.epi;
+    float sc[8], bf[8], of[8];
+    int32_t bi[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t n = n0 + wn * 128 + 16 * j + fr;
+        const bool ok = n < p.N;
+        sc[j] = (ok && e.scale) ? e.scale[e.scale_per_ch ? n : 0] : 0.0f;
+        of[j] = (ok && e.offset) ? e.offset[e.offset_per_ch ? n : 0] : 0.0f;
+        bf[j] = 0.0f;
+        bi[j] = 0;
+        if (ok && e.bias_dtype == QK_I32) bi[j] = ((const int32_t*)e.bias)[n];
+        else if (ok && e.bias_dtype) bf[j] = load_scalar(e.bias, n, e.bias_dtype);
+    }
+    // Fully unrolled with compile-time register indices (a runtime-indexed
+    // accumulator would be demoted to scratch and spilled every K step).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = m0 + wm * 128 + 16 * i + 4 * g + r;
+            const bool row_ok = m < p.M;
+            // pertoken multiply by 1.0 is exact, so "no pertoken" needs no branch
+            const float pt = (e.pertoken && row_ok) ? e.pertoken[m] : 1.0f;
+            const int64_t ro = m * e.ldo + n0 + wn * 128 + fr;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool ok = row_ok && (n0 + wn * 128 + 16 * j + fr) < p.N;
+                if (ok) big::store_elem<OUT>(e.out, ro + 16 * j, acc[i][j][r], sc[j], bf[j], bi[j], pt, of[j]);
+            }
+        }
+    }
+}
+
 // Any shape / stride / alignment: one thread per output element.
 __global__ __launch_bounds__(kThreads) void qmm_generic(QmmArgs p) {
     const int64_t total = p.M * p.N;
@@ -209,6 +401,16 @@ hipError_t launch_by_m(const QmmArgs& p, hipStream_t stream) {
     return launch_tiled<128, 128, B_KN>(p, stream);
 }
 
+template <int OUT>
+hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, hipStream_t stream) {
+    const dim3 grid((uint32_t)(tiles_m * tiles_n));
+    if (b_kn)
+        qmm_big<true, OUT><<<grid, dim3(kThreads), 0, stream>>>(p, tiles_m, tiles_n);
+    else
+        qmm_big<false, OUT><<<grid, dim3(kThreads), 0, stream>>>(p, tiles_m, tiles_n);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t quant_matmul_workspace(int64_t, int64_t, int64_t) { return 0; }
@@ -218,6 +420,18 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void*, size_t, hipStream_t stre
     const bool a_ok = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.a % 16 == 0);
     const bool b_nk = (p.sbk == 1) && (p.sbn % 16 == 0) && ((uintptr_t)p.b % 16 == 0);
     const bool b_kn = (p.sbn == 1) && (p.sbk % 8 == 0) && (p.N % 8 == 0) && ((uintptr_t)p.b % 8 == 0);
+    const int64_t tiles_m = (p.M + big::BM - 1) / big::BM, tiles_n = (p.N + big::BN - 1) / big::BN;
+    const bool big_ok = p.K > 0 && a_ok && tiles_m * tiles_n >= 256 && tiles_m * tiles_n < (1 << 30) &&
+                        (b_nk || (b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0));
+    if (big_ok) {
+        switch (p.epi.out_dtype) {
+        case QK_BF16: return launch_big<QK_BF16>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
+        case QK_F16: return launch_big<QK_F16>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
+        case QK_F32: return launch_big<QK_F32>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
+        case QK_I8: return launch_big<QK_I8>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
+        default: return launch_big<QK_I32>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
+        }
+    }
     if (p.K > 0 && a_ok && b_kn) return launch_by_m<true>(p, stream);
     if (p.K > 0 && a_ok && b_nk) return launch_by_m<false>(p, stream);
     const int64_t total = p.M * p.N;
