@@ -16,20 +16,26 @@
 // where xs comes from one extra MFMA against a vector of ones.  Each piece
 // then adds  s*A + s*(offset - BASE)*xs  to the accumulator.
 //
-// Decode kernel (w4_skinny): HBM weight stream for M <= 64.  A workgroup owns
-// a strip of WCS packed word columns (8*WCS output columns) over all of K; its
-// waves take 128-row chunks of K round-robin, stream them with every load of
-// the next chunk in flight while the current one is unpacked and multiplied,
-// and are reduced through LDS in a fixed order (deterministic, no workspace).
-// MFMA column c of a wave maps to word column (c % WCS) and nibble
-// t*(16/WCS) + c/WCS of tile t, so every weight word is unpacked by exactly
-// the lanes that need it.
+// Decode kernel (w4_decode), an HBM weight stream for M <= 16 rows per
+// workgroup: a workgroup owns a strip of 32 packed words (256 output columns,
+// one 128-byte line per weight row) and a K range (a "split").  Its four waves
+// are 2 (word halves) x 2 (K halves); a wave streams 128-row chunks with the
+// next chunk's loads in flight.  MFMA lane (c, kg) holds word column c of the
+// wave's half for rows 8kg..8kg+7 of a 32-row block, and nibble j of those 8
+// words is the B operand of MFMA tile j, so each lane finally owns 8
+// consecutive output columns.  Splits write fp32 partials to the workspace
+// and w4_reduce sums them in split order (deterministic); with one split the
+// decode kernel writes the output itself.
+#include <cstdlib>
+
 #include "common.h"
 
 namespace qk {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int CHUNK = 128;  // K rows per streamed chunk (4 MFMA K-blocks)
+constexpr int STRIP = 32;   // packed words per workgroup
 
 template <int DT>
 struct Mfma;
@@ -58,170 +64,245 @@ struct Mfma<QK_F16> {
     }
 };
 
-// B operand of one MFMA tile: nibble `j` (byte bj = j/2, shift 4*(j&1)) of 8
-// offset-binary words, rows 0..7 -> bf16/fp16 lanes 0..7 (pairs per dword).
-template <uint32_t MAGIC>
-__device__ __forceinline__ u32x4 unpack_tile(const uint32_t w[8], uint32_t sel, uint32_t shift) {
+// B operand of MFMA tile j: nibble j of 8 offset-binary words (rows 0..7),
+// packed as 16-bit magic values, two rows per dword.
+template <uint32_t MAGIC, int J>
+__device__ __forceinline__ u32x4 unpack_tile(const uint32_t w[8]) {
+    constexpr uint32_t bj = (uint32_t)J >> 1;
+    constexpr uint32_t sel = bj | ((4u + bj) << 16) | 0x0c000c00u;  // byte bj of each word -> bits 0..7 / 16..23
     u32x4 b;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t pair = __builtin_amdgcn_perm(w[2 * q + 1], w[2 * q], sel) >> shift;
+        uint32_t pair = __builtin_amdgcn_perm(w[2 * q + 1], w[2 * q], sel);
+        if constexpr (J & 1) pair >>= 4;
         b[q] = (pair & 0x000f000fu) | MAGIC;
     }
     return b;
 }
 
-constexpr int CHUNK = 128;  // K rows a wave streams per step (4 MFMA K-blocks)
+__device__ __forceinline__ void halves8(u32x4 v, int dt, float f[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[2 * e] = load_half_bits(v[e] & 0xffffu, dt);
+        f[2 * e + 1] = load_half_bits(v[e] >> 16, dt);
+    }
+}
 
-template <int DT, int WCS, int MB, int NWAVE, bool HAS_OFF>
-__global__ __launch_bounds__(NWAVE * 64) void w4_skinny(WqbmmArgs p) {
+template <int OUTDT>
+__device__ __forceinline__ void store8(void* out, int64_t off, const float v[8]) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = OUTDT == QK_BF16 ? f32_to_bf16_bits(v[2 * e]) : f32_to_f16_bits(v[2 * e]);
+        const uint32_t hi = OUTDT == QK_BF16 ? f32_to_bf16_bits(v[2 * e + 1]) : f32_to_f16_bits(v[2 * e + 1]);
+        o[e] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + off) = o;
+}
+
+// PIECE_KB: 32-row K-blocks per scaling piece (min(group,128)/32).
+// FINAL: one split, write bf16/fp16 output (+bias) directly.
+// UPFRONT: each wave's K range is exactly 256 rows, loaded before any math.
+template <int DT, int PIECE_KB, bool HAS_OFF, bool FINAL, bool UPFRONT>
+__global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __restrict__ partial, int nsplit,
+                                                      int nstrip) {
     typedef Mfma<DT> MM;
-    constexpr int T = WCS / 2;        // MFMA tiles per wave (16 columns each)
-    constexpr int JSTEP = 16 / WCS;   // nibble stride between tiles
-    constexpr int NCOL = 8 * WCS;     // output columns of the strip
-    constexpr int ROWS = 16 * MB;
-    __shared__ float red[NWAVE][ROWS][NCOL + 1];
+    constexpr int NP = 4 / PIECE_KB;  // pieces per chunk
+    __shared__ float red[2][16][132];
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int c = lane & 15;
-    const int kg = lane >> 4;
-    const int64_t NW = p.N >> 3;
-    // 1-D grid: strips sharing 128-byte weight lines land on one XCD
-    const int nstrip = (int)((NW + WCS - 1) / WCS);
-    const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-    const int strip = bid % nstrip;
-    const int64_t wc = (int64_t)strip * WCS + (c % WCS);
-    const bool col_ok = wc < NW;
-    const int64_t m0 = (int64_t)(bid / nstrip) * ROWS;
-    const int64_t G = p.group;
-    const int64_t piece = G < CHUNK ? G : CHUNK;
-    const int64_t nchunk = p.K / CHUNK;
-    const uint32_t* W = static_cast<const uint32_t*>(p.w);
-    const uint16_t* X = static_cast<const uint16_t*>(p.x);
-    const uint16_t* S = static_cast<const uint16_t*>(p.scale);
-    const uint16_t* O = static_cast<const uint16_t*>(p.offset);
+    // wave index through readfirstlane so everything derived from it is scalar
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = wave & 1, kh = wave >> 1;
+    const int c = lane & 15, kg = lane >> 4;
+    const int blk = blockIdx.x;
+    const int strip = blk % nstrip;
+    const int split = (blk / nstrip) % nsplit;
+    const int rb = blk / (nstrip * nsplit);
+
+    const int NW = (int)(p.N >> 3);
+    const int wc_raw = strip * STRIP + 16 * h + c;
+    const bool col_ok = wc_raw < NW;
+    const int wc = col_ok ? wc_raw : NW - 1;  // clamped: loads stay in bounds, results discarded
+    const int M = (int)p.M, K = (int)p.K, N = (int)p.N, G = (int)p.group;
+    const int m_raw = rb * 16 + c;
+    const bool row_ok = m_raw < M;
+    const int m = row_ok ? m_raw : M - 1;
+
+    const int rows_split = K / nsplit;
+    const int k_begin = split * rows_split + kh * (rows_split >> 1);
+    const int nch = (rows_split >> 1) / CHUNK;
+
+    const uint32_t rowbytes = (uint32_t)NW * 4u;
+    const char* Wb = static_cast<const char*>(p.w);
+    const uint32_t w_lane = (uint32_t)(8 * kg) * rowbytes + (uint32_t)wc * 4u;
+    const char* Xb = static_cast<const char*>(p.x);
+    const uint32_t x_lane = ((uint32_t)m * (uint32_t)K + 8u * (uint32_t)kg) * 2u;
+    const char* Sb = static_cast<const char*>(p.scale);
+    const char* Ob = static_cast<const char*>(p.offset);
+    const uint32_t s_lane = (uint32_t)(8 * wc) * 2u;
     const u32x4 ones = {MM::ONES, MM::ONES, MM::ONES, MM::ONES};
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-    int jt[T];
-    uint32_t sel[T], shf[T];
+    f32x4 acc[8];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        jt[t] = t * JSTEP + c / WCS;
-        const uint32_t bj = (uint32_t)jt[t] >> 1;
-        sel[t] = bj | ((4u + bj) << 16) | 0x0c000c00u;
-        shf[t] = 4u * ((uint32_t)jt[t] & 1u);
-    }
-    bool row_ok[MB];
-    const uint16_t* xrow[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        const int64_t m = m0 + 16 * mb + c;
-        row_ok[mb] = m < p.M;
-        xrow[mb] = X + (row_ok[mb] ? m : 0) * p.K;
-    }
+    for (int t = 0; t < 8; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    f32x4 acc[MB][T];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int t = 0; t < T; ++t) acc[mb][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // The K range streams in 64-row halves (2 MFMA K-blocks) through two
+    // alternating register buffers: the next half's loads are in flight while
+    // the current half is unpacked and multiplied.  A chunk (128 rows) is an
+    // even half followed by an odd half, so piece ends (every 32/64/128 rows)
+    // fall at compile-time positions.
+    constexpr int HKB = 2;
+    constexpr int PPH = PIECE_KB <= HKB ? HKB / PIECE_KB : 1;  // scale points held per half
+    struct Half {
+        uint32_t w[HKB][8];
+        u32x4 x[HKB];
+        u32x4 s[PPH], o[PPH];
+    };
 
-    uint32_t wbuf[2][4][8];
-    u32x4 xbuf[2][4][MB];
-
-    auto load_chunk = [&](int64_t ch, uint32_t (&wv)[4][8], u32x4 (&xv)[4][MB]) {
+    auto load = [&](int hidx, Half& d, bool odd) {
+        const int k0 = k_begin + hidx * 64;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const int64_t k = ch * CHUNK + kb * 32 + 8 * kg;
+        for (int kb = 0; kb < HKB; ++kb) {
 #pragma unroll
-            for (int r = 0; r < 8; ++r) wv[kb][r] = col_ok ? W[(k + r) * NW + wc] : 0u;
+            for (int r = 0; r < 8; ++r) {
+                const char* rowp = Wb + (size_t)(uint32_t)(k0 + kb * 32 + r) * rowbytes;
+                d.w[kb][r] = *reinterpret_cast<const uint32_t*>(rowp + w_lane);
+            }
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(Xb + (size_t)(k0 + kb * 32) * 2u + x_lane);
+            d.x[kb] = row_ok ? xv : zero4;
+        }
+        if (PIECE_KB <= HKB || odd) {
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-                xv[kb][mb] = row_ok[mb] ? *reinterpret_cast<const u32x4*>(xrow[mb] + k) : (u32x4){0u, 0u, 0u, 0u};
+            for (int pp = 0; pp < PPH; ++pp) {
+                const uint32_t g = (uint32_t)(k0 + pp * PIECE_KB * 32) / (uint32_t)G;
+                d.s[pp] = *reinterpret_cast<const u32x4*>(Sb + (size_t)g * (uint32_t)N * 2u + s_lane);
+                if (HAS_OFF) d.o[pp] = *reinterpret_cast<const u32x4*>(Ob + (size_t)g * (uint32_t)N * 2u + s_lane);
+            }
         }
     };
 
-    auto compute_chunk = [&](int64_t ch, uint32_t (&wv)[4][8], u32x4 (&xv)[4][MB]) {
-        f32x4 ag[MB][T], xs[MB];
+    f32x4 ag[8], xs;
+    auto reset = [&]() {
+        xs = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            xs[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 8; ++t) ag[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    };
+    auto fold = [&](u32x4 sv, u32x4 ov) {  // acc += s*A + s*(offset - BASE)*xs, then start a new piece
+        float sf[8], of[8];
+        halves8(sv, p.s_dtype, sf);
+        if (HAS_OFF) halves8(ov, p.s_dtype, of);
 #pragma unroll
-            for (int t = 0; t < T; ++t) ag[mb][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 8; ++t) {
+            const float sb = sf[t] * ((HAS_OFF ? of[t] : 0.0f) - MM::BASE);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(sf[t], ag[t][r], __builtin_fmaf(sb, xs[r], acc[t][r]));
         }
+        reset();
+    };
+    auto compute = [&](const Half& d, bool odd) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+        for (int kb = 0; kb < HKB; ++kb) {
             uint32_t w8[8];
 #pragma unroll
-            for (int r = 0; r < 8; ++r) w8[r] = wv[kb][r] ^ 0x88888888u;
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const u32x4 b = unpack_tile<MM::MAGIC>(w8, sel[t], shf[t]);
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) ag[mb][t] = MM::mma(xv[kb][mb], b, ag[mb][t]);
-            }
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) xs[mb] = MM::mma(xv[kb][mb], ones, xs[mb]);
-            const int64_t kend = ch * CHUNK + (kb + 1) * 32;
-            if (kend % piece == 0) {   // end of a piece: fold it into the accumulators
-                const int64_t g = (kend - 1) / G;
-                if (col_ok) {
-#pragma unroll
-                    for (int t = 0; t < T; ++t) {
-                        const int64_t n = 8 * wc + jt[t];
-                        const float s = load_half_bits(S[g * p.N + n], p.s_dtype);
-                        const float off = HAS_OFF ? load_half_bits(O[g * p.N + n], p.s_dtype) : 0.0f;
-                        const float sb = s * (off - MM::BASE);
-#pragma unroll
-                        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                acc[mb][t][r] = __builtin_fmaf(s, ag[mb][t][r], __builtin_fmaf(sb, xs[mb][r], acc[mb][t][r]));
-                    }
-                }
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    xs[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int t = 0; t < T; ++t) ag[mb][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-                }
-            }
+            for (int r = 0; r < 8; ++r) w8[r] = d.w[kb][r] ^ 0x88888888u;
+            ag[0] = MM::mma(d.x[kb], unpack_tile<MM::MAGIC, 0>(w8), ag[0]);
+            ag[1] = MM::mma(d.x[kb], unpack_tile<MM::MAGIC, 1>(w8), ag[1]);
+            ag[2] = MM::mma(d.x[kb], unpack_tile<MM::MAGIC, 2>(w8), ag[2]);
+            ag[3] = MM::mma(d.x[kb], unpack_tile<MM::MAGIC, 3>(w8), ag[3]);
+            ag[4] = MM::mma(d.x[kb], unpack_tile<MM::MAGIC, 4>(w8), ag[4]);
+            ag[5] = MM::mma(d.x[kb], unpack_tile<MM::MAGIC, 5>(w8), ag[5]);
+            ag[6] = MM::mma(d.x[kb], unpack_tile<MM::MAGIC, 6>(w8), ag[6]);
+            ag[7] = MM::mma(d.x[kb], unpack_tile<MM::MAGIC, 7>(w8), ag[7]);
+            xs = MM::mma(d.x[kb], ones, xs);
+            if (PIECE_KB == 1) fold(d.s[kb], d.o[kb]);
         }
+        if (PIECE_KB == 2 || (PIECE_KB == 4 && odd)) fold(d.s[0], d.o[0]);
     };
 
-    int64_t ch = wave;
-    if (ch < nchunk) load_chunk(ch, wbuf[0], xbuf[0]);
-    while (ch < nchunk) {
-        const int64_t nx = ch + NWAVE;
-        if (nx < nchunk) load_chunk(nx, wbuf[1], xbuf[1]);
-        compute_chunk(ch, wbuf[0], xbuf[0]);
-        if (nx >= nchunk) break;
-        const int64_t nx2 = nx + NWAVE;
-        if (nx2 < nchunk) load_chunk(nx2, wbuf[0], xbuf[0]);
-        compute_chunk(nx, wbuf[1], xbuf[1]);
-        ch = nx2;
+    reset();
+    Half b0, b1;
+    const int nhalf = 2 * nch;
+    if constexpr (UPFRONT) {
+        // 256 rows per wave: every load of the wave is issued before the first
+        // MFMA, so the whole split is in flight at once
+        Half b2, b3;
+        load(0, b0, false);
+        load(1, b1, true);
+        load(2, b2, false);
+        load(3, b3, true);
+        compute(b0, false);
+        compute(b1, true);
+        compute(b2, false);
+        compute(b3, true);
+    } else {
+        if (nhalf > 0) load(0, b0, false);
+        for (int hidx = 0; hidx < nhalf; hidx += 2) {
+            load(hidx + 1, b1, true);
+            compute(b0, false);
+            if (hidx + 2 < nhalf) load(hidx + 2, b0, false);
+            compute(b1, true);
+        }
     }
 
-    // deterministic cross-wave reduction: LDS, summed in wave order
+    // K-half 1 hands its sums to K-half 0 (fixed order: half 0 + half 1)
+    if (kh == 1) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+        for (int t = 0; t < 8; ++t)
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) red[wave][16 * mb + 4 * kg + r][8 * (c % WCS) + jt[t]] = acc[mb][t][r];
+            for (int r = 0; r < 4; ++r) red[h][4 * kg + r][8 * c + t] = acc[t][r];
+    }
     __syncthreads();
-    uint16_t* out = static_cast<uint16_t*>(p.out);
-    const int64_t n0 = (int64_t)strip * NCOL;
-    for (int i = threadIdx.x; i < ROWS * NCOL; i += NWAVE * 64) {
-        const int row = i / NCOL, col = i % NCOL;
-        const int64_t m = m0 + row, n = n0 + col;
-        if (m >= p.M || n >= p.N) continue;
-        float v = red[0][row][col];
+    if (kh == 1) return;
+    const int64_t n0 = 8 * (int64_t)wc_raw;
 #pragma unroll
-        for (int w = 1; w < NWAVE; ++w) v += red[w][row][col];
-        if (p.bias_dtype) v += load_scalar(p.bias, n, p.bias_dtype);
-        out[m * p.N + n] = (uint16_t)(p.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+    for (int r = 0; r < 4; ++r) {
+        const int64_t mm = (int64_t)rb * 16 + 4 * kg + r;
+        float v[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = acc[t][r] + red[h][4 * kg + r][8 * c + t];
+        if (!col_ok || mm >= M) continue;
+        if (FINAL) {
+            if (p.bias_dtype) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[t] += load_scalar(p.bias, n0 + t, p.bias_dtype);
+            }
+            if (p.out_dtype == QK_BF16) store8<QK_BF16>(p.out, mm * N + n0, v);
+            else store8<QK_F16>(p.out, mm * N + n0, v);
+        } else {
+            f32x4* dst = reinterpret_cast<f32x4*>(partial + ((int64_t)split * M + mm) * N + n0);
+            dst[0] = (f32x4){v[0], v[1], v[2], v[3]};
+            dst[1] = (f32x4){v[4], v[5], v[6], v[7]};
+        }
+    }
+}
+
+// Sum split partials in split order, add bias, cast; 8 outputs per thread.
+template <int OUTDT>
+__global__ __launch_bounds__(kThreads) void w4_reduce(const float* __restrict__ partial, int nsplit, int64_t M,
+                                                      int64_t N, const void* bias, int bias_dtype, void* out) {
+    const int64_t n8 = N >> 3;
+    const int64_t total = M * n8;
+    for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * kThreads) {
+        const int64_t m = idx / n8, n0 = (idx % n8) * 8;
+        float v[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = 0.0f;
+        for (int s = 0; s < nsplit; ++s) {
+            const f32x4* src = reinterpret_cast<const f32x4*>(partial + ((int64_t)s * M + m) * N + n0);
+            const f32x4 a = src[0], b = src[1];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                v[t] += a[t];
+                v[4 + t] += b[t];
+            }
+        }
+        if (bias_dtype) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] += load_scalar(bias, n0 + t, bias_dtype);
+        }
+        store8<OUTDT>(out, m * N + n0, v);
     }
 }
 
@@ -263,26 +344,6 @@ __global__ __launch_bounds__(kThreads) void wq_generic(WqbmmArgs p) {
     }
 }
 
-template <int DT, int WCS, int MB, int NWAVE>
-hipError_t launch_skinny(const WqbmmArgs& p, hipStream_t stream) {
-    constexpr int ROWS = 16 * MB;
-    const int64_t NW = p.N / 8;
-    const int64_t nblk = ((NW + WCS - 1) / WCS) * ((p.M + ROWS - 1) / ROWS);
-    if (nblk >= (int64_t)1 << 31) return hipErrorInvalidValue;
-    dim3 grid((uint32_t)nblk);
-    if (p.offset)
-        w4_skinny<DT, WCS, MB, NWAVE, true><<<grid, dim3(NWAVE * 64), 0, stream>>>(p);
-    else
-        w4_skinny<DT, WCS, MB, NWAVE, false><<<grid, dim3(NWAVE * 64), 0, stream>>>(p);
-    return hipGetLastError();
-}
-
-template <int DT>
-hipError_t dispatch_skinny(const WqbmmArgs& p, hipStream_t stream) {
-    if (p.M <= 16) return launch_skinny<DT, 4, 1, 8>(p, stream);
-    return launch_skinny<DT, 4, 2, 8>(p, stream);
-}
-
 __global__ void int4_pack_kernel(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed) {
     const int64_t NW = N >> 3;
     const int64_t total = K * NW;
@@ -301,19 +362,127 @@ __global__ void int4_pack_kernel(const void* w, int w_dtype, int64_t K, int64_t 
     }
 }
 
+// ---------------------------------------------------------------- host-side planning
+
+struct DecodePlan {
+    bool ok;
+    bool upfront;
+    int nsplit, nstrip, nrb;
+    int piece_kb;
+};
+
+// The decode kernel's preconditions and its split count; used by both the
+// workspace query and the launch so the two always agree.
+DecodePlan decode_plan(const WqbmmArgs& p) {
+    DecodePlan d{false, false, 1, 0, 0, 4};
+    const int64_t G = p.group == 0 ? p.K : p.group;
+    if (p.w_dtype != QK_I32 || p.K <= 0 || p.N <= 0 || p.M <= 0) return d;
+    if (p.K % (2 * CHUNK) != 0 || G <= 0 || p.K % G != 0) return d;
+    if (!(G % CHUNK == 0 || G == 32 || G == 64)) return d;
+    // 32-bit offsets inside the kernel
+    if (p.K * (p.N / 2) >= ((int64_t)1 << 31) || p.M * p.K * 2 >= ((int64_t)1 << 31) ||
+        (p.K / G) * p.N * 2 >= ((int64_t)1 << 31))
+        return d;
+    if (((uintptr_t)p.x | (uintptr_t)p.scale | (uintptr_t)p.out) % 16 != 0 || (uintptr_t)p.w % 4 != 0 ||
+        (p.offset && (uintptr_t)p.offset % 16 != 0))
+        return d;
+    d.piece_kb = G >= CHUNK ? 4 : (int)(G / 32);
+    d.nstrip = (int)((p.N / 8 + STRIP - 1) / STRIP);
+    d.nrb = (int)((p.M + 15) / 16);
+    const int64_t tiles = (int64_t)d.nstrip * d.nrb;
+    int s = 1;
+    if (tiles < 256) {
+        // few output tiles (decode): split K so every wave owns 256 rows and
+        // issues all its loads at once; otherwise keep doubling splits while
+        // workgroups are short of ~2 per CU
+        if (p.K % 512 == 0 && (p.K / 512) * tiles <= 4096) {
+            s = (int)(p.K / 512);
+            d.upfront = true;
+        } else {
+            const int64_t want = 512 / tiles;
+            while (s * 2 <= want && p.K % ((int64_t)(s * 2) * 2 * CHUNK) == 0) s *= 2;
+        }
+    }
+    if (const char* e = std::getenv("QK_W4_SPLITS")) {  // tuning override (debug)
+        const int f = std::atoi(e);
+        if (f >= 1 && p.K % ((int64_t)f * 2 * CHUNK) == 0) {
+            s = f;
+            d.upfront = p.K / f == 512;
+        }
+    }
+    // partial sums stay a small fraction of the weight stream
+    if (s > 1 && (int64_t)s * p.M * p.N * 4 > ((int64_t)256 << 20)) {
+        s = 1;
+        d.upfront = false;
+    }
+    d.nsplit = s;
+    d.ok = tiles * d.nsplit < ((int64_t)1 << 31);
+    return d;
+}
+
+template <int DT, int PKB, bool HAS_OFF>
+hipError_t launch_decode_t(const WqbmmArgs& p, const DecodePlan& d, float* partial, hipStream_t stream) {
+    const dim3 grid((uint32_t)((int64_t)d.nstrip * d.nsplit * d.nrb));
+    if (d.nsplit == 1)
+        w4_decode<DT, PKB, HAS_OFF, true, false><<<grid, dim3(kThreads), 0, stream>>>(p, partial, 1, d.nstrip);
+    else if (d.upfront)
+        w4_decode<DT, PKB, HAS_OFF, false, true><<<grid, dim3(kThreads), 0, stream>>>(p, partial, d.nsplit, d.nstrip);
+    else
+        w4_decode<DT, PKB, HAS_OFF, false, false><<<grid, dim3(kThreads), 0, stream>>>(p, partial, d.nsplit, d.nstrip);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_decode_dt(const WqbmmArgs& p, const DecodePlan& d, float* partial, hipStream_t stream) {
+    const bool off = p.offset != nullptr;
+    switch (d.piece_kb) {
+    case 1: return off ? launch_decode_t<DT, 1, true>(p, d, partial, stream) : launch_decode_t<DT, 1, false>(p, d, partial, stream);
+    case 2: return off ? launch_decode_t<DT, 2, true>(p, d, partial, stream) : launch_decode_t<DT, 2, false>(p, d, partial, stream);
+    default: return off ? launch_decode_t<DT, 4, true>(p, d, partial, stream) : launch_decode_t<DT, 4, false>(p, d, partial, stream);
+    }
+}
+
 }  // namespace
 
-size_t weight_quant_bmm_workspace(int64_t, int64_t, int64_t, int, int64_t) { return 0; }
+size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group) {
+    WqbmmArgs p{};
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.w_dtype = w_dtype;
+    p.group = group;
+    // alignment does not change the split count; use aligned dummies
+    p.x = p.scale = p.out = (void*)(uintptr_t)256;
+    p.w = (void*)(uintptr_t)256;
+    const DecodePlan d = decode_plan(p);
+    if (!d.ok || d.nsplit == 1) return 0;
+    return (size_t)d.nsplit * (size_t)M * (size_t)N * sizeof(float);
+}
 
-hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void*, size_t, hipStream_t stream) {
+hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
     if (a.M == 0 || a.N == 0) return hipSuccess;
     WqbmmArgs p = a;
     if (p.group == 0) p.group = p.K;  // per channel == one group spanning K
-    // pieces of min(group, 128) rows must tile the 128-row chunks
-    const bool group_ok = p.group % 32 == 0 && (p.group % CHUNK == 0 || CHUNK % p.group == 0);
-    const bool fast = p.w_dtype == QK_I32 && p.K > 0 && p.K % CHUNK == 0 && p.K % p.group == 0 && group_ok &&
-                      ((uintptr_t)p.x % 16 == 0) && ((uintptr_t)p.w % 4 == 0);
-    if (fast) return p.x_dtype == QK_BF16 ? dispatch_skinny<QK_BF16>(p, stream) : dispatch_skinny<QK_F16>(p, stream);
+    const DecodePlan d = decode_plan(p);
+    if (d.ok) {
+        float* partial = static_cast<float*>(workspace);
+        if (d.nsplit > 1 && (!partial || ws_bytes < (size_t)d.nsplit * p.M * p.N * sizeof(float) ||
+                             (uintptr_t)partial % 16 != 0))
+            return hipErrorInvalidValue;
+        hipError_t e = p.x_dtype == QK_BF16 ? launch_decode_dt<QK_BF16>(p, d, partial, stream)
+                                            : launch_decode_dt<QK_F16>(p, d, partial, stream);
+        if (e != hipSuccess || d.nsplit == 1) return e;
+        const int64_t total = p.M * (p.N / 8);
+        int64_t blocks = (total + kThreads - 1) / kThreads;
+        if (blocks > 65536) blocks = 65536;
+        if (p.out_dtype == QK_BF16)
+            w4_reduce<QK_BF16><<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(partial, d.nsplit, p.M, p.N, p.bias,
+                                                                                     p.bias_dtype, p.out);
+        else
+            w4_reduce<QK_F16><<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(partial, d.nsplit, p.M, p.N, p.bias,
+                                                                                    p.bias_dtype, p.out);
+        return hipGetLastError();
+    }
     const int64_t total = p.M * p.N;
     int64_t blocks = (total + kThreads - 1) / kThreads;
     if (blocks > 65536) blocks = 65536;

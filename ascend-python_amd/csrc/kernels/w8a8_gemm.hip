@@ -201,16 +201,21 @@ __global__ __launch_bounds__(kThreads) void qmm_tiled(QmmArgs p) {
 // Workgroups are renumbered so each XCD (ids congruent mod 8) owns a compact
 // block of output tiles (8 tile-rows x 8 tile-cols share its L2).
 namespace big {
-constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int BM = 256, BN = 256, BK = 128;  // BK: K bytes per LDS stage (two MFMA k-steps)
 constexpr int A_BYTES = BM * BK;
-constexpr int B_BYTES = BN * BK;
-constexpr int STAGE = A_BYTES + B_BYTES;
+constexpr int CPR = BK / 16;                  // 16-byte chunks per [row][k] row
 
-__device__ __forceinline__ int rk_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
-__device__ __forceinline__ int kn_off(int k, int c16) {
-    const int h = (k & 7) | (((k >> 4) & 1) << 3);
-    return k * 256 + 16 * (c16 ^ h);
-}
+// [row][k] tiles (A, [N,K] weight): 128-byte rows, chunk c XOR-swizzled by
+// (r>>1)&7 so 16 consecutive rows at one chunk cover all banks.
+__device__ __forceinline__ int rk_off(int r, int c) { return r * BK + 16 * (c ^ ((r >> 1) & 7)); }
+// [k][n] tiles ([K,N] weight): 256-byte rows padded to 272 B plus 128 B per
+// 16-row block, so the 8 rows one 16-lane group of a transpose read touches
+// fall in distinct banks and the next group (16 rows on) in the other half;
+// the column offset stays a compile-time constant for the reads.
+__device__ __forceinline__ int kn_off(int k, int c16) { return k * 272 + 128 * (k >> 4) + 16 * c16; }
+constexpr int KN_BYTES = 127 * 272 + 128 * 7 + 256 + 144;  // kn_off(127, 16) rounded up to 256
+constexpr int B_BYTES = KN_BYTES > BN * BK ? KN_BYTES : BN * BK;
+constexpr int STAGE = A_BYTES + B_BYTES;
 
 typedef int32_t v2i __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ v2i lds_tr8(const int8_t* p) {
@@ -239,9 +244,18 @@ __device__ __forceinline__ void store_elem(void* out, int64_t o, int32_t acc, fl
 }
 }  // namespace big
 
-template <bool B_KN, int OUT>
-__global__ __launch_bounds__(kThreads) void qmm_big(QmmArgs p, int tiles_m, int tiles_n) {
+// NW = 4: 2x2 waves of 128x128 (one wave per SIMD); NW = 8: 4x2 waves of
+// 64x128 (two waves per SIMD, so one wave's MFMAs cover the other's waits).
+// FULL: every tile is inside M, N and K is a multiple of BK, so loads need no
+// predicates and use one 32-bit per-lane offset from a uniform base (no 64-bit
+// address registers live across the loop).
+template <bool B_KN, int OUT, int NW, bool FULL>
+__global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int tiles_n) {
     using namespace big;
+    constexpr int NT = 64 * NW;              // threads
+    constexpr int WMR = BM / (NW / 2);       // wave tile rows
+    constexpr int TM = WMR / 16;             // MFMA row tiles per wave
+    constexpr int NLD = BM * CPR / NT;       // 16-byte loads per thread per operand per stage
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * STAGE];
 
     // XCD-aware renumbering + grouped tile order
@@ -256,17 +270,32 @@ __global__ __launch_bounds__(kThreads) void qmm_big(QmmArgs p, int tiles_m, int 
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int fr = lane & 15, g = lane >> 4;
 
-    // ---- global -> register prefetch (4 x 16 B of A and of B per thread)
-    i32x4 ra[4], rb[4];
+    // ---- global -> register prefetch (NLD x 16 B of A and of B per thread)
+    i32x4 ra[NLD], rb[NLD];
+    // FULL path: lane offsets (rows advance NT/CPR per load; [K,N] rows NT/16)
+    const uint32_t a_lane = (uint32_t)(tid / CPR) * (uint32_t)p.lda + 16u * (uint32_t)(tid % CPR);
+    const uint32_t b_lane = B_KN ? (uint32_t)(tid >> 4) * (uint32_t)p.sbk + 16u * (uint32_t)(tid & 15)
+                                 : (uint32_t)(tid / CPR) * (uint32_t)p.sbn + 16u * (uint32_t)(tid % CPR);
     auto gload = [&](int64_t k0) {
+        if constexpr (FULL) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q = tid + 256 * i;
-            const int r = q >> 2, c = q & 3;
+            for (int i = 0; i < NLD; ++i) {
+                const int8_t* abase = p.a + (m0 + (int64_t)i * (NT / CPR)) * p.lda + k0;
+                ra[i] = *reinterpret_cast<const i32x4*>(abase + a_lane);
+                const int8_t* bbase = B_KN ? p.b + (k0 + (int64_t)i * (NT / 16)) * p.sbk + n0
+                                           : p.b + (n0 + (int64_t)i * (NT / CPR)) * p.sbn + k0;
+                rb[i] = *reinterpret_cast<const i32x4*>(bbase + b_lane);
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int q = tid + NT * i;
+            const int r = q / CPR, c = q % CPR;
             const int64_t m = m0 + r, k = k0 + 16 * c;
             ra[i] = (m < p.M && k < p.K) ? *reinterpret_cast<const i32x4*>(p.a + m * p.lda + k) : (i32x4){0, 0, 0, 0};
             if (!B_KN) {
@@ -285,24 +314,25 @@ __global__ __launch_bounds__(kThreads) void qmm_big(QmmArgs p, int tiles_m, int 
         int8_t* As = smem + st * STAGE;
         int8_t* Bs = As + A_BYTES;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q = tid + 256 * i;
-            *reinterpret_cast<i32x4*>(As + rk_off(q >> 2, q & 3)) = ra[i];
-            if (!B_KN) *reinterpret_cast<i32x4*>(Bs + rk_off(q >> 2, q & 3)) = rb[i];
+        for (int i = 0; i < NLD; ++i) {
+            const int q = tid + NT * i;
+            *reinterpret_cast<i32x4*>(As + rk_off(q / CPR, q % CPR)) = ra[i];
+            if (!B_KN) *reinterpret_cast<i32x4*>(Bs + rk_off(q / CPR, q % CPR)) = rb[i];
             else *reinterpret_cast<i32x4*>(Bs + kn_off(q >> 4, q & 15)) = rb[i];
         }
     };
 
-    i32x4 acc[8][8];
+    i32x4 acc[TM][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = (i32x4){0, 0, 0, 0};
 
     // per-lane fragment addressing (constant over K)
-    const int tr_h = (fr >> 1) | ((g & 1) << 3);
+    // transpose read: lanes 2b / 2b+1 of each 16-lane group address row
+    // k0 + b, columns 0..7 / 8..15 of the tile (the +8 rows half is kn_off + 8*272)
     const int tr_k = 16 * g + (fr >> 1);
-    const int tr_b = 8 * (fr & 1);
+    const int tr_base = kn_off(tr_k, 0) + 8 * (fr & 1);
 
     const int64_t nk = (p.K + big::BK - 1) / big::BK;
     gload(0);
@@ -313,29 +343,46 @@ __global__ __launch_bounds__(kThreads) void qmm_big(QmmArgs p, int tiles_m, int 
         const int st = (int)(it & 1);
         const int8_t* As = smem + st * STAGE;
         const int8_t* Bs = As + A_BYTES;
-        i32x4 af[8], bfr[8];
+        auto frags = [&](int kk, i32x4 (&af)[TM], i32x4 (&bfr)[8]) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) af[i] = *reinterpret_cast<const i32x4*>(As + rk_off(wm * 128 + 16 * i + fr, g));
+            for (int i = 0; i < TM; ++i)
+                af[i] = *reinterpret_cast<const i32x4*>(As + rk_off(wm * WMR + 16 * i + fr, 4 * kk + g));
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (!B_KN) {
-                bfr[j] = *reinterpret_cast<const i32x4*>(Bs + rk_off(wn * 128 + 16 * j + fr, g));
-            } else {
-                const int c16 = wn * 8 + j;
-                const v2i lo = lds_tr8(Bs + tr_k * 256 + 16 * (c16 ^ tr_h) + tr_b);
-                const v2i hi = lds_tr8(Bs + (tr_k + 8) * 256 + 16 * (c16 ^ tr_h) + tr_b);
-                bfr[j] = (i32x4){lo[0], lo[1], hi[0], hi[1]};
+            for (int j = 0; j < 8; ++j) {
+                if (!B_KN) {
+                    bfr[j] = *reinterpret_cast<const i32x4*>(Bs + rk_off(wn * 128 + 16 * j + fr, 4 * kk + g));
+                } else {
+                    // rows 64kk + tr_k (+8): kn_off is affine in k inside a 16-row block
+                    const int8_t* t = Bs + tr_base + kn_off(64 * kk, wn * 8 + j);
+                    const v2i lo = lds_tr8(t);
+                    const v2i hi = lds_tr8(t + 8 * 272);
+                    bfr[j] = (i32x4){lo[0], lo[1], hi[0], hi[1]};
+                }
             }
-        }
+        };
+        auto mma = [&](const i32x4 (&af)[TM], const i32x4 (&bfr)[8]) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        };
+        i32x4 af0[TM], bf0[8], af1[TM], bf1[8];
+        frags(0, af0, bf0);
         // stage it+1 (already in registers) goes to the other buffer, then fetch it+2
         if (it + 1 < nk) {
             lstore(st ^ 1);
             if (it + 2 < nk) gload((it + 2) * big::BK);
         }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        if constexpr (NW == 4) {  // one wave per SIMD: overlap its own LDS reads
+            frags(1, af1, bf1);
+            mma(af0, bf0);
+            mma(af1, bf1);
+        } else {                  // the SIMD's other wave covers the LDS latency
+            mma(af0, bf0);
+            frags(1, af1, bf1);
+            mma(af1, bf1);
+        }
     }
 
     // ---- epilogue: per-column and per-row operands loaded once per lane
@@ -356,10 +403,10 @@ __global__ __launch_bounds__(kThreads) void qmm_big(QmmArgs p, int tiles_m, int 
     // Fully unrolled with compile-time register indices (a runtime-indexed
     // accumulator would be demoted to scratch and spilled every K step).
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int64_t m = m0 + wm * 128 + 16 * i + 4 * g + r;
+            const int64_t m = m0 + wm * WMR + 16 * i + 4 * g + r;
             const bool row_ok = m < p.M;
             // pertoken multiply by 1.0 is exact, so "no pertoken" needs no branch
             const float pt = (e.pertoken && row_ok) ? e.pertoken[m] : 1.0f;
@@ -370,6 +417,151 @@ __global__ __launch_bounds__(kThreads) void qmm_big(QmmArgs p, int tiles_m, int 
                 if (ok) big::store_elem<OUT>(e.out, ro + 16 * j, acc[i][j][r], sc[j], bf[j], bi[j], pt, of[j]);
             }
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny kernel (decode, M <= 64): an HBM weight stream.  A workgroup owns
+// 16*MT rows x 256 columns and one K split; its 4 waves take 64 columns
+// each.  Stages of 128 k-rows go through LDS (the weight in its natural
+// layout, B fragments by ds_read_b64_tr_b8 for [K,N]) with the next stage's
+// global loads in flight.  With several splits each writes exact int32
+// partial sums and qmm_reduce adds them (order-free, exact) before the same
+// epilogue as every other path.
+namespace sk {
+constexpr int BN = 256, BK = 128;
+}
+
+template <bool B_KN, int MT, bool FINAL>
+__global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, int nsplit, int32_t* partial) {
+    using big::rk_off;
+    using big::kn_off;
+    constexpr int BM = 16 * MT;
+    constexpr int A_BYTES = BM * sk::BK, B_BYTES = big::B_BYTES, STAGE = A_BYTES + B_BYTES;
+    constexpr int A_CHUNKS = BM * 8;                 // 16-byte chunks per stage
+    constexpr int A_PER_T = (A_CHUNKS + kThreads - 1) / kThreads;
+    constexpr int B_PER_T = sk::BN * 8 / kThreads;   // 8
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * STAGE];
+
+    const int blk = blockIdx.x;
+    const int tn = blk % tiles_n;
+    const int split = (blk / tiles_n) % nsplit;
+    const int tm = blk / (tiles_n * nsplit);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * sk::BN;
+    const int64_t ks = p.K / nsplit, kbeg = (int64_t)split * ks;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int fr = lane & 15, g = lane >> 4;
+
+    i32x4 ra[A_PER_T], rb[B_PER_T];
+    auto gload = [&](int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < A_PER_T; ++i) {
+            const int q = tid + kThreads * i;
+            const int r = q >> 3, c = q & 7;
+            const int64_t m = m0 + r;
+            ra[i] = (q < A_CHUNKS && m < p.M) ? *reinterpret_cast<const i32x4*>(p.a + m * p.lda + k0 + 16 * c)
+                                              : (i32x4){0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < B_PER_T; ++i) {
+            const int q = tid + kThreads * i;
+            if (!B_KN) {
+                const int r = q >> 3, c = q & 7;
+                const int64_t n = n0 + r;
+                rb[i] = n < p.N ? *reinterpret_cast<const i32x4*>(p.b + n * p.sbn + k0 + 16 * c) : (i32x4){0, 0, 0, 0};
+            } else {
+                const int kr = q >> 4, c16 = q & 15;
+                const int64_t n = n0 + 16 * c16;
+                rb[i] = n < p.N ? *reinterpret_cast<const i32x4*>(p.b + (k0 + kr) * p.sbk + n) : (i32x4){0, 0, 0, 0};
+            }
+        }
+    };
+    auto lstore = [&](int st) {
+        int8_t* As = smem + st * STAGE;
+        int8_t* Bs = As + A_BYTES;
+#pragma unroll
+        for (int i = 0; i < A_PER_T; ++i) {
+            const int q = tid + kThreads * i;
+            if (q < A_CHUNKS) *reinterpret_cast<i32x4*>(As + rk_off(q >> 3, q & 7)) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_PER_T; ++i) {
+            const int q = tid + kThreads * i;
+            if (!B_KN) *reinterpret_cast<i32x4*>(Bs + rk_off(q >> 3, q & 7)) = rb[i];
+            else *reinterpret_cast<i32x4*>(Bs + kn_off(q >> 4, q & 15)) = rb[i];
+        }
+    };
+
+    i32x4 acc[MT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (i32x4){0, 0, 0, 0};
+    const int tr_base = kn_off(16 * g + (fr >> 1), 0) + 8 * (fr & 1);
+
+    const int64_t nk = ks / sk::BK;
+    gload(kbeg);
+    lstore(0);
+    if (nk > 1) gload(kbeg + sk::BK);
+    for (int64_t it = 0; it < nk; ++it) {
+        __syncthreads();
+        const int st = (int)(it & 1);
+        const int8_t* As = smem + st * STAGE;
+        const int8_t* Bs = As + A_BYTES;
+        i32x4 af[2][MT], bf[2][4];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i) af[kk][i] = *reinterpret_cast<const i32x4*>(As + rk_off(16 * i + fr, 4 * kk + g));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (!B_KN) {
+                    bf[kk][j] = *reinterpret_cast<const i32x4*>(Bs + rk_off(64 * wave + 16 * j + fr, 4 * kk + g));
+                } else {
+                    const int8_t* t = Bs + tr_base + kn_off(64 * kk, 4 * wave + j);
+                    const big::v2i lo = big::lds_tr8(t);
+                    const big::v2i hi = big::lds_tr8(t + 8 * 272);
+                    bf[kk][j] = (i32x4){lo[0], lo[1], hi[0], hi[1]};
+                }
+            }
+        }
+        if (it + 1 < nk) {
+            lstore(st ^ 1);
+            if (it + 2 < nk) gload(kbeg + (it + 2) * sk::BK);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
+    }
+
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + 16 * i + 4 * g + r;
+                const int64_t n = n0 + 64 * wave + 16 * j + fr;
+                if (m >= p.M || n >= p.N) continue;
+                if (FINAL) qmm_store(p.epi, m, n, acc[i][j][r]);
+                else partial[((int64_t)split * p.M + m) * p.N + n] = acc[i][j][r];
+            }
+}
+
+// Exact int32 sum of the split partials, then the common epilogue.
+__global__ __launch_bounds__(kThreads) void qmm_reduce(QmmArgs p, int nsplit, const int32_t* __restrict__ partial) {
+    const int64_t total = p.M * p.N;
+    for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * kThreads) {
+        uint32_t s = 0;
+        for (int k = 0; k < nsplit; ++k) s += (uint32_t)partial[(int64_t)k * total + idx];
+        qmm_store(p.epi, idx / p.N, idx % p.N, (int32_t)s);
     }
 }
 
@@ -404,22 +596,97 @@ hipError_t launch_by_m(const QmmArgs& p, hipStream_t stream) {
 template <int OUT>
 hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, hipStream_t stream) {
     const dim3 grid((uint32_t)(tiles_m * tiles_n));
-    if (b_kn)
-        qmm_big<true, OUT><<<grid, dim3(kThreads), 0, stream>>>(p, tiles_m, tiles_n);
-    else
-        qmm_big<false, OUT><<<grid, dim3(kThreads), 0, stream>>>(p, tiles_m, tiles_n);
+    static const int waves = [] {
+        const char* e = std::getenv("QK_QMM_WAVES");  // tuning override (debug)
+        return (e && std::atoi(e) == 4) ? 4 : 8;
+    }();
+    // full tiles and 32-bit per-lane offsets (the 64-bit bases stay uniform)
+    const bool full = p.M % big::BM == 0 && p.N % big::BN == 0 && p.K % big::BK == 0 &&
+                      p.lda < (1 << 24) && p.sbk < (1 << 24) && p.sbn < (1 << 24);
+    if (waves == 4) {
+        if (b_kn) qmm_big<true, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n);
+        else qmm_big<false, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n);
+    } else if (full) {
+        if (b_kn) qmm_big<true, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n);
+        else qmm_big<false, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n);
+    } else {
+        if (b_kn) qmm_big<true, OUT, 8, false><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n);
+        else qmm_big<false, OUT, 8, false><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n);
+    }
     return hipGetLastError();
 }
 
 }  // namespace
 
-size_t quant_matmul_workspace(int64_t, int64_t, int64_t) { return 0; }
+namespace {
 
-hipError_t launch_quant_matmul(const QmmArgs& p, void*, size_t, hipStream_t stream) {
+struct SkinnyPlan {
+    int mt = 0, nsplit = 1, tiles_n = 0, tiles_m = 0;
+};
+
+// Decode shapes (M <= 64, K a multiple of 128): row tiles, and K splits so
+// about 512 workgroups stream the weight while the int32 partials stay at
+// most 1/8 of the weight bytes.  Shared by the workspace query and the launch.
+SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
+    SkinnyPlan s;
+    if (M <= 0 || M > 64 || K <= 0 || K % sk::BK != 0 || N <= 0) return s;
+    s.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    s.tiles_m = (int)((M + 16 * s.mt - 1) / (16 * s.mt));
+    s.tiles_n = (int)((N + sk::BN - 1) / sk::BN);
+    const int64_t base = (int64_t)s.tiles_m * s.tiles_n;
+    while (base * s.nsplit * 2 <= 512 && K % ((int64_t)s.nsplit * 2 * sk::BK) == 0 &&
+           (int64_t)s.nsplit * 2 * M * 32 <= K)
+        s.nsplit *= 2;
+    if (base * s.nsplit >= ((int64_t)1 << 31)) s.mt = 0;
+    return s;
+}
+
+template <bool B_KN, int MT>
+hipError_t launch_skinny_t(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial, hipStream_t stream) {
+    const dim3 grid((uint32_t)((int64_t)s.tiles_m * s.tiles_n * s.nsplit));
+    if (s.nsplit == 1) {
+        qmm_skinny<B_KN, MT, true><<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, 1, nullptr);
+        return hipGetLastError();
+    }
+    qmm_skinny<B_KN, MT, false><<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, s.nsplit, partial);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    int64_t blocks = (p.M * p.N + kThreads - 1) / kThreads;
+    if (blocks > 65536) blocks = 65536;
+    qmm_reduce<<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(p, s.nsplit, partial);
+    return hipGetLastError();
+}
+
+template <bool B_KN>
+hipError_t launch_skinny(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial, hipStream_t stream) {
+    switch (s.mt) {
+    case 1: return launch_skinny_t<B_KN, 1>(p, s, partial, stream);
+    case 2: return launch_skinny_t<B_KN, 2>(p, s, partial, stream);
+    default: return launch_skinny_t<B_KN, 4>(p, s, partial, stream);
+    }
+}
+
+}  // namespace
+
+size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K) {
+    const SkinnyPlan s = skinny_plan(M, N, K);
+    if (s.mt == 0 || s.nsplit == 1) return 0;
+    return (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
+}
+
+hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_bytes, hipStream_t stream) {
     if (p.M == 0 || p.N == 0) return hipSuccess;
     const bool a_ok = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.a % 16 == 0);
     const bool b_nk = (p.sbk == 1) && (p.sbn % 16 == 0) && ((uintptr_t)p.b % 16 == 0);
     const bool b_kn = (p.sbn == 1) && (p.sbk % 8 == 0) && (p.N % 8 == 0) && ((uintptr_t)p.b % 8 == 0);
+    const bool b_kn16 = b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0;
+    const SkinnyPlan sp = skinny_plan(p.M, p.N, p.K);
+    if (sp.mt != 0 && a_ok && (b_nk || b_kn16)) {
+        const size_t need = sp.nsplit > 1 ? (size_t)sp.nsplit * p.M * p.N * sizeof(int32_t) : 0;
+        if (need && (!workspace || ws_bytes < need)) return hipErrorInvalidValue;
+        int32_t* partial = static_cast<int32_t*>(workspace);
+        return b_kn16 ? launch_skinny<true>(p, sp, partial, stream) : launch_skinny<false>(p, sp, partial, stream);
+    }
     const int64_t tiles_m = (p.M + big::BM - 1) / big::BM, tiles_n = (p.N + big::BN - 1) / big::BN;
     const bool big_ok = p.K > 0 && a_ok && tiles_m * tiles_n >= 256 && tiles_m * tiles_n < (1 << 30) &&
                         (b_nk || (b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0));
