@@ -64,18 +64,29 @@ struct Mfma<QK_F16> {
     }
 };
 
+// (a & m) | o in one v_and_or_b32.  Written out because the compiler splits
+// it into v_and + v_or when m and o are constants (a VOP3 op cannot take two
+// literals); keeping m and o in registers makes it one instruction.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+    return r;
+}
+
 // B operand of MFMA tile j: nibble j of 8 offset-binary words (rows 0..7),
 // packed as 16-bit magic values, two rows per dword.
 template <uint32_t MAGIC, int J>
 __device__ __forceinline__ u32x4 unpack_tile(const uint32_t w[8]) {
     constexpr uint32_t bj = (uint32_t)J >> 1;
     constexpr uint32_t sel = bj | ((4u + bj) << 16) | 0x0c000c00u;  // byte bj of each word -> bits 0..7 / 16..23
+    const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000f000fu);
+    const uint32_t magic = __builtin_amdgcn_readfirstlane(MAGIC);
     u32x4 b;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         uint32_t pair = __builtin_amdgcn_perm(w[2 * q + 1], w[2 * q], sel);
         if constexpr (J & 1) pair >>= 4;
-        b[q] = (pair & 0x000f000fu) | MAGIC;
+        b[q] = and_or(pair, mask, magic);
     }
     return b;
 }
@@ -108,7 +119,11 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
                                                       int nstrip) {
     typedef Mfma<DT> MM;
     constexpr int NP = 4 / PIECE_KB;  // pieces per chunk
-    __shared__ float red[2][16][132];
+    // LDS: the upfront path's per-wave transposed tiles, later reused by the
+    // cross-wave reduction (red)
+    constexpr int LDS_U32 = UPFRONT ? 4 * 16 * 260 : 2 * 16 * 132;
+    __shared__ __attribute__((aligned(16))) uint32_t lds_u32[LDS_U32];
+    float (*red)[16][132] = reinterpret_cast<float (*)[16][132]>(lds_u32);
 
     // wave index through readfirstlane so everything derived from it is scalar
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -224,17 +239,56 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
     Half b0, b1;
     const int nhalf = 2 * nch;
     if constexpr (UPFRONT) {
-        // 256 rows per wave: every load of the wave is issued before the first
-        // MFMA, so the whole split is in flight at once
-        Half b2, b3;
-        load(0, b0, false);
-        load(1, b1, true);
-        load(2, b2, false);
-        load(3, b3, true);
-        compute(b0, false);
-        compute(b1, true);
-        compute(b2, false);
-        compute(b3, true);
+        // 256 rows per wave, every load issued before the first MFMA.  The
+        // loads are 16 bytes per lane (4 lanes per 64-byte row piece, 16 rows
+        // per instruction); each wave transposes its own 16x256 word tile
+        // through LDS ([column][row], 260-dword columns: conflict-free 32-bit
+        // writes and 128-bit reads) into the MFMA lane layout.  LDS traffic
+        // of a wave stays inside that wave, so no barrier is needed.
+        uint32_t* wt = lds_u32 + wave * (16 * 260);
+        const int cw = lane & 3, rr = lane >> 2;
+        const int wcol_raw = strip * STRIP + 16 * h + 4 * cw;
+        const int wcol = wcol_raw < NW ? wcol_raw : NW - 4;  // NW % 4 == 0
+        const char* src = Wb + (size_t)(uint32_t)(k_begin + rr) * rowbytes + (uint32_t)wcol * 4u;
+        u32x4 raw[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) raw[i] = *reinterpret_cast<const u32x4*>(src + (size_t)(16 * i) * rowbytes);
+        u32x4 xa[8];
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(Xb + (size_t)(k_begin + kb * 32) * 2u + x_lane);
+            xa[kb] = row_ok ? xv : zero4;
+        }
+        constexpr int NPW = 8 / PIECE_KB;  // pieces per wave
+        u32x4 sv[NPW], ov[NPW];
+#pragma unroll
+        for (int pp = 0; pp < NPW; ++pp) {
+            const uint32_t gi = (uint32_t)(k_begin + pp * PIECE_KB * 32) / (uint32_t)G;
+            sv[pp] = *reinterpret_cast<const u32x4*>(Sb + (size_t)gi * (uint32_t)N * 2u + s_lane);
+            if (HAS_OFF) ov[pp] = *reinterpret_cast<const u32x4*>(Ob + (size_t)gi * (uint32_t)N * 2u + s_lane);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+#pragma unroll
+            for (int ii = 2 * kb; ii < 2 * kb + 2; ++ii)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) wt[(4 * cw + w) * 260 + 16 * ii + rr] = raw[ii][w];
+            const u32x4 lo = *reinterpret_cast<const u32x4*>(wt + c * 260 + 32 * kb + 8 * kg);
+            const u32x4 hi = *reinterpret_cast<const u32x4*>(wt + c * 260 + 32 * kb + 8 * kg + 4);
+            uint32_t w8[8] = {lo[0] ^ 0x88888888u, lo[1] ^ 0x88888888u, lo[2] ^ 0x88888888u, lo[3] ^ 0x88888888u,
+                              hi[0] ^ 0x88888888u, hi[1] ^ 0x88888888u, hi[2] ^ 0x88888888u, hi[3] ^ 0x88888888u};
+            ag[0] = MM::mma(xa[kb], unpack_tile<MM::MAGIC, 0>(w8), ag[0]);
+            ag[1] = MM::mma(xa[kb], unpack_tile<MM::MAGIC, 1>(w8), ag[1]);
+            ag[2] = MM::mma(xa[kb], unpack_tile<MM::MAGIC, 2>(w8), ag[2]);
+            ag[3] = MM::mma(xa[kb], unpack_tile<MM::MAGIC, 3>(w8), ag[3]);
+            ag[4] = MM::mma(xa[kb], unpack_tile<MM::MAGIC, 4>(w8), ag[4]);
+            ag[5] = MM::mma(xa[kb], unpack_tile<MM::MAGIC, 5>(w8), ag[5]);
+            ag[6] = MM::mma(xa[kb], unpack_tile<MM::MAGIC, 6>(w8), ag[6]);
+            ag[7] = MM::mma(xa[kb], unpack_tile<MM::MAGIC, 7>(w8), ag[7]);
+            xs = MM::mma(xa[kb], ones, xs);
+            if ((kb + 1) % PIECE_KB == 0) fold(sv[kb / PIECE_KB], ov[kb / PIECE_KB]);
+        }
+        __syncthreads();  // the reduction below reuses the LDS tile area
     } else {
         if (nhalf > 0) load(0, b0, false);
         for (int hidx = 0; hidx < nhalf; hidx += 2) {
@@ -277,32 +331,38 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
     }
 }
 
-// Sum split partials in split order, add bias, cast; 8 outputs per thread.
+// Sum split partials in split order, add bias, cast; 4 outputs per thread,
+// all split loads of a thread issued together (latency-bound at decode sizes).
 template <int OUTDT>
 __global__ __launch_bounds__(kThreads) void w4_reduce(const float* __restrict__ partial, int nsplit, int64_t M,
                                                       int64_t N, const void* bias, int bias_dtype, void* out) {
-    const int64_t n8 = N >> 3;
-    const int64_t total = M * n8;
-    for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total;
+    const int64_t total4 = (M * N) >> 2;
+    for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total4;
          idx += (int64_t)gridDim.x * kThreads) {
-        const int64_t m = idx / n8, n0 = (idx % n8) * 8;
-        float v[8];
+        const f32x4* src = reinterpret_cast<const f32x4*>(partial) + idx;
+        f32x4 part[16];
+        const int ns = nsplit < 16 ? nsplit : 16;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) v[t] = 0.0f;
-        for (int s = 0; s < nsplit; ++s) {
-            const f32x4* src = reinterpret_cast<const f32x4*>(partial + ((int64_t)s * M + m) * N + n0);
-            const f32x4 a = src[0], b = src[1];
+        for (int s = 0; s < 16; ++s)
+            if (s < ns) part[s] = src[(int64_t)s * total4];
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                v[t] += a[t];
-                v[4 + t] += b[t];
-            }
-        }
+        for (int s = 0; s < 16; ++s)
+            if (s < ns) v += part[s];
+        for (int s = 16; s < nsplit; ++s) v += src[(int64_t)s * total4];
+        const int64_t o = idx * 4, n0 = o % N;
         if (bias_dtype) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) v[t] += load_scalar(bias, n0 + t, bias_dtype);
+            for (int t = 0; t < 4; ++t) v[t] += load_scalar(bias, n0 + t, bias_dtype);
         }
-        store8<OUTDT>(out, m * N + n0, v);
+        u32x2 packed;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t lo = OUTDT == QK_BF16 ? f32_to_bf16_bits(v[2 * e]) : f32_to_f16_bits(v[2 * e]);
+            const uint32_t hi = OUTDT == QK_BF16 ? f32_to_bf16_bits(v[2 * e + 1]) : f32_to_f16_bits(v[2 * e + 1]);
+            packed[e] = lo | (hi << 16);
+        }
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + o) = packed;
     }
 }
 
@@ -395,7 +455,7 @@ DecodePlan decode_plan(const WqbmmArgs& p) {
         // few output tiles (decode): split K so every wave owns 256 rows and
         // issues all its loads at once; otherwise keep doubling splits while
         // workgroups are short of ~2 per CU
-        if (p.K % 512 == 0 && (p.K / 512) * tiles <= 4096) {
+        if (p.K % 512 == 0 && (p.K / 512) * tiles <= 4096 && (p.N / 8) % 4 == 0) {
             s = (int)(p.K / 512);
             d.upfront = true;
         } else {
@@ -407,7 +467,7 @@ DecodePlan decode_plan(const WqbmmArgs& p) {
         const int f = std::atoi(e);
         if (f >= 1 && p.K % ((int64_t)f * 2 * CHUNK) == 0) {
             s = f;
-            d.upfront = p.K / f == 512;
+            d.upfront = p.K / f == 512 && (p.N / 8) % 4 == 0;
         }
     }
     // partial sums stay a small fraction of the weight stream
@@ -472,7 +532,7 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
         hipError_t e = p.x_dtype == QK_BF16 ? launch_decode_dt<QK_BF16>(p, d, partial, stream)
                                             : launch_decode_dt<QK_F16>(p, d, partial, stream);
         if (e != hipSuccess || d.nsplit == 1) return e;
-        const int64_t total = p.M * (p.N / 8);
+        const int64_t total = p.M * p.N / 4;
         int64_t blocks = (total + kThreads - 1) / kThreads;
         if (blocks > 65536) blocks = 65536;
         if (p.out_dtype == QK_BF16)

@@ -370,16 +370,23 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
         i32x4 af0[TM], bf0[8], af1[TM], bf1[8];
         frags(0, af0, bf0);
         // stage it+1 (already in registers) goes to the other buffer, then fetch it+2
-        if (it + 1 < nk) {
-            lstore(st ^ 1);
-            if (it + 2 < nk) gload((it + 2) * big::BK);
-        }
         if constexpr (NW == 4) {  // one wave per SIMD: overlap its own LDS reads
+            if (it + 1 < nk) {
+                lstore(st ^ 1);
+                if (it + 2 < nk) gload((it + 2) * big::BK);
+            }
             frags(1, af1, bf1);
             mma(af0, bf0);
             mma(af1, bf1);
-        } else {                  // the SIMD's other wave covers the LDS latency
+        } else {
+            // the first half's MFMAs run before the wait on stage it+1's loads,
+            // which so get a step and a half to arrive; the SIMD's other wave
+            // covers the LDS latency of the second half
             mma(af0, bf0);
+            if (it + 1 < nk) {
+                lstore(st ^ 1);
+                if (it + 2 < nk) gload((it + 2) * big::BK);
+            }
             frags(1, af1, bf1);
             mma(af1, bf1);
         }
@@ -399,6 +406,39 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
         bi[j] = 0;
         if (ok && e.bias_dtype == QK_I32) bi[j] = ((const int32_t*)e.bias)[n];
         else if (ok && e.bias_dtype) bf[j] = load_scalar(e.bias, n, e.bias_dtype);
+    }
+    if constexpr (FULL && (OUT == QK_BF16 || OUT == QK_F16)) {
+        // 16-bit outputs of a full tile are staged through LDS (the operand
+        // stages are free now) so the global stores are whole 512-byte rows of
+        // 16 bytes per lane instead of 32-byte pieces of 4 rows.
+        constexpr int ROWB = 2 * BN + 16;  // padded LDS row (bytes)
+        static_assert(BM * ROWB <= 2 * STAGE, "output tile does not fit the LDS stages");
+        __syncthreads();
+        uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = wm * WMR + 16 * i + 4 * g + r;
+                const float pt = e.pertoken ? e.pertoken[m0 + row] : 1.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int32_t a = (int32_t)((uint32_t)acc[i][j][r] + (uint32_t)bi[j]);
+                    const float v = __builtin_fmaf((float)a * pt, sc[j], bf[j]);
+                    ot[row * (ROWB / 2) + wn * 128 + 16 * j + fr] =
+                        (uint16_t)(OUT == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+                }
+            }
+        }
+        __syncthreads();
+        constexpr int CPRO = 2 * BN / 16;  // 16-byte chunks per output row
+#pragma unroll
+        for (int q = tid; q < BM * CPRO; q += NT) {
+            const int row = q / CPRO, c = q % CPRO;
+            const i32x4 v = *reinterpret_cast<const i32x4*>(smem + row * ROWB + 16 * c);
+            *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo + n0 + 8 * c) = v;
+        }
+        return;
     }
     // Fully unrolled with compile-time register indices (a runtime-indexed
     // accumulator would be demoted to scratch and spilled every K step).
@@ -602,7 +642,8 @@ hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, hip
     }();
     // full tiles and 32-bit per-lane offsets (the 64-bit bases stay uniform)
     const bool full = p.M % big::BM == 0 && p.N % big::BN == 0 && p.K % big::BK == 0 &&
-                      p.lda < (1 << 24) && p.sbk < (1 << 24) && p.sbn < (1 << 24);
+                      p.lda < (1 << 24) && p.sbk < (1 << 24) && p.sbn < (1 << 24) &&
+                      (uintptr_t)p.epi.out % 16 == 0 && p.epi.ldo % 8 == 0;
     if (waves == 4) {
         if (b_kn) qmm_big<true, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n);
         else qmm_big<false, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n);
