@@ -18,6 +18,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 
@@ -38,8 +39,30 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 5 plain 256 MiB device copies (the reference kernel for scaling "
+                         "FETCH_SIZE / WRITE_SIZE counters in a rocprofv3 --pmc pass)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target length of the CPU baseline sample")
     return ap.parse_args()
+
+
+def hbm_traffic() -> dict:
+    """HBM bytes per launch per kernel, from the committed rocprofv3 --pmc summary.
+
+    The counters cannot be read from inside this process; profiles/hbm_traffic.md records
+    FETCH_SIZE and WRITE_SIZE per dispatch of this same workload, scaled by what the counters
+    read for a plain copy of known size, as lines `traffic_bytes <kernel> = <bytes>`.
+    """
+    out = {}
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.md")) as f:
+            for ln in f:
+                m = re.match(r"^traffic_bytes\s+(\w+)\s*=\s*([0-9]+)", ln.strip().strip("`"))
+                if m:
+                    out[m.group(1)] = int(m.group(2))
+    except OSError:
+        pass
+    return out
 
 
 def cpu_model() -> str:
@@ -140,6 +163,14 @@ def main():
             ev[3].record()
         return out, o3
 
+    if args.copy_calibration:
+        ca = torch.empty(256 * 1024 * 1024 // 4, device=dev)
+        cb = torch.empty_like(ca)
+        for _ in range(5):
+            cb.copy_(ca)
+        torch.cuda.synchronize()
+        del ca, cb
+
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -184,6 +215,9 @@ def main():
     qbytes = c4.M * c4.K * 3 + 4 * c4.M
     q_s = float(np.mean(t_quant))
 
+    traffic = hbm_traffic()
+    t_w4 = (traffic["w4_decode"] + traffic["w4_reduce"]) if "w4_decode" in traffic and "w4_reduce" in traffic else None
+
     line = {
         "metric": "W8A8 GEMM TOPS (M=4096) + W4A16 decode GB/s (M=16); % of MI355X roofline",
         "value": round(tops, 2),
@@ -201,13 +235,13 @@ def main():
                                "[4096,8192]x[8192,8192] bf16 out; cfg3 W4A16 decode M=16 K=4096 N=11008 G=128",
                    "w8a8_operand_sets": W8A8_SETS, "w4a16_operand_sets": W4_SETS},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": None,
+                     "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": traffic.get("qmm_big"),
                      "kernel": "qmm (W8A8 GEMM)", "avg_us": round(gemm_s * 1e6, 2),
                      "algorithmic": f"2*M*N*K = {ops4:.0f} int8 ops per launch"},
         "secondary": {
             "metric": "W4A16 decode GB/s (M=16)", "value": round(gbs3, 1), "unit": "GB/s",
             "roofline": {"bound": "hbm", "achieved": round(gbs3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(gbs3 / PEAK_HBM_GBS, 4), "traffic": None,
+                         "frac": round(gbs3 / PEAK_HBM_GBS, 4), "traffic": t_w4,
                          "avg_us": round(w4_s * 1e6, 3), "algorithmic_bytes": bytes3}},
         "dynamic_quant": {"avg_us": round(q_s * 1e6, 2), "GB/s": round(qbytes / q_s / 1e9, 1),
                           "hbm_frac": round(qbytes / q_s / 1e9 / PEAK_HBM_GBS, 4)},
