@@ -51,6 +51,15 @@ __device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dtype
     }
 }
 
+// ---------------------------------------------------------------- raw buffer loads
+// A raw buffer resource over [base, base + bytes).  Loads through it take a
+// 32-bit per-lane offset plus a wave-uniform offset that lives in an SGPR, so
+// a run of rows costs no 64-bit VALU address arithmetic; an offset past
+// `bytes` reads zero instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 // ---------------------------------------------------------------- XCD-aware ids
 // The dispatcher hands consecutive workgroup ids to the 8 XCDs round-robin,
 // and each XCD has its own L2.  Renumbering so that the ids one XCD receives

@@ -26,7 +26,10 @@
 // consecutive output columns.  Splits write fp32 partials to the workspace
 // and w4_reduce sums them in split order (deterministic); with one split the
 // decode kernel writes the output itself.
+#include <cstdio>
 #include <cstdlib>
+#include <cstring>
+#include <type_traits>
 
 #include "common.h"
 
@@ -64,15 +67,6 @@ struct Mfma<QK_F16> {
     }
 };
 
-// (a & m) | o in one v_and_or_b32.  Written out because the compiler splits
-// it into v_and + v_or when m and o are constants (a VOP3 op cannot take two
-// literals); keeping m and o in registers makes it one instruction.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
-    return r;
-}
-
 // B operand of MFMA tile j: nibble j of 8 offset-binary words (rows 0..7),
 // packed as 16-bit magic values, two rows per dword.
 template <uint32_t MAGIC, int J>
@@ -86,7 +80,30 @@ __device__ __forceinline__ u32x4 unpack_tile(const uint32_t w[8]) {
     for (int q = 0; q < 4; ++q) {
         uint32_t pair = __builtin_amdgcn_perm(w[2 * q + 1], w[2 * q], sel);
         if constexpr (J & 1) pair >>= 4;
-        b[q] = and_or(pair, mask, magic);
+        b[q] = (pair & mask) | magic;
+    }
+    return b;
+}
+
+// v_perm_b32 selector: byte b of the low source to bits 0..7, byte b of the
+// high source to bits 16..23, zeros elsewhere.
+__host__ __device__ constexpr uint32_t byte_sel(uint32_t b) { return b | ((4u + b) << 16) | 0x0c000c00u; }
+
+// Two's-complement nibble r straight to the magic operand: (r & 0xf) ^ 0x..08
+// leaves MAGIC's high bits and puts u = r ^ 8 = w + 8 in the low bits, so the
+// offset-binary flip costs nothing (gfx950 does and+xor in one v_bitop3_b32).
+// `sel` (per lane) picks byte b of rows 2q and 2q+1; odd nibbles are shifted
+// down first.
+template <uint32_t MAGIC, bool ODD>
+__device__ __forceinline__ u32x4 unpack_raw(const uint32_t w[8], uint32_t sel) {
+    const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000f000fu);
+    const uint32_t magic = __builtin_amdgcn_readfirstlane(MAGIC | 0x00080008u);
+    u32x4 b;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t pair = __builtin_amdgcn_perm(w[2 * q + 1], w[2 * q], sel);
+        if constexpr (ODD) pair >>= 4;
+        b[q] = (pair & mask) ^ magic;
     }
     return b;
 }
@@ -331,6 +348,189 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
     }
 }
 
+// Decode weight stream for up to 16 rows of x per workgroup.
+//
+// A workgroup owns a strip of 32 packed words (256 output columns: one full
+// 128-byte line of every weight row) and a K split.  Its waves are
+// HALVES = 32/WPL column sub-strips x KW = NWAVE/HALVES K ranges of NKB
+// 32-row K-blocks.  MFMA lane (c, kg) = (lane & 15, lane >> 4) reads, for each
+// of its K-blocks, rows 8kg..8kg+7 of one word column straight from HBM (one
+// dword per row; the 16 lanes of a k-group cover WPL consecutive words), so the
+// B operands are built in registers without any LDS transpose:
+//   WPL == 16: slot c owns word c and all 8 of its nibbles (8 MFMA tiles);
+//   WPL == 8:  slots c and c+8 share word c&7, slot c takes nibbles
+//              4(c>>3)..4(c>>3)+3 (4 tiles).
+// The sub-strip waves of one K range read the same rows, so every 128-byte
+// line is consumed whole inside one workgroup (lines split between
+// workgroups read at about 2/3 of the bandwidth).  Each wave issues its loads
+// block by block before its first MFMA.  The K ranges are added through LDS
+// in order (deterministic), each thread finishing 4 columns of one row.  With
+// one split the sums are the output (+bias, cast); otherwise fp32 partials
+// [split][M][N] for w4_reduce.
+template <int DT, int WPL, int NWAVE, int NKB, int PF, int PIECE_KB, bool HAS_OFF, bool FINAL>
+__global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __restrict__ partial, int nstrip,
+                                                        int nsplit) {
+    typedef Mfma<DT> MM;
+    constexpr int TPL = WPL == 16 ? 8 : 4;  // MFMA tiles per lane
+    constexpr int HALVES = 32 / WPL;        // column sub-strips per workgroup
+    constexpr int KW = NWAVE / HALVES;      // K ranges per workgroup
+    constexpr int NCOL = 8 * WPL;           // output columns per wave
+    constexpr int RSTR = NCOL + 4;          // LDS row pitch in floats
+    constexpr int NPIECE = NKB / PIECE_KB;
+    static_assert(NKB % PIECE_KB == 0, "pieces must tile the wave's K range");
+    static_assert(KW >= 1 && KW * HALVES == NWAVE, "waves must tile the strip");
+    __shared__ __attribute__((aligned(16))) float red[NWAVE][16][RSTR];
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, kg = lane >> 4;
+    const int h = wave % HALVES, kw = wave / HALVES;
+    // same-split strips share the x rows: keep neighbours on one XCD (one L2)
+    const int blk = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int strip = blk % nstrip;
+    const int split = (blk / nstrip) % nsplit;
+    const int rb = blk / (nstrip * nsplit);
+
+    const int M = (int)p.M, K = (int)p.K, N = (int)p.N, G = (int)p.group;
+    const int NW = N >> 3;
+    const int slot = WPL == 16 ? c : (c & 7);
+    const int nh = WPL == 16 ? 0 : (c >> 3);  // nibble half (WPL == 8)
+    const int wc_raw = strip * 32 + h * WPL + slot;
+    const int wc = wc_raw < NW ? wc_raw : NW - 1;  // clamped: loads stay in bounds, those columns are not stored
+    // rows past M read row M-1: every output row depends only on its own x row, and those rows are not stored
+    const int m = rb * 16 + c < M ? rb * 16 + c : M - 1;
+    const int k_wave = split * (KW * NKB * 32) + kw * (NKB * 32);
+
+    // buffer resources over this wave's rows: lane offsets in VGPRs, row
+    // offsets in SGPRs (no per-load address arithmetic)
+    const uint32_t rowbytes = (uint32_t)NW * 4u;
+    const __amdgpu_buffer_rsrc_t wr =
+        make_rsrc(static_cast<const char*>(p.w) + (size_t)(uint32_t)k_wave * rowbytes, NKB * 32 * rowbytes);
+    const uint32_t w_lane = (uint32_t)(8 * kg) * rowbytes + (uint32_t)wc * 4u;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
+    const uint32_t x_lane = ((uint32_t)m * (uint32_t)K + (uint32_t)k_wave + 8u * (uint32_t)kg) * 2u;
+    const uint32_t s_lane = (uint32_t)(8 * wc + 4 * nh) * 2u;
+
+    // Scale/offset of every piece first (small, needed from the first fold
+    // on), then the K-blocks as a software pipeline PF blocks deep: block
+    // kb+PF is issued right before block kb is consumed, into one of PF+1
+    // register slots.  Loads return in order, so consuming block kb waits only
+    // for it; keeping few blocks in flight per wave makes each block arrive
+    // early instead of every block finishing near the end of the stream.
+    typedef typename std::conditional<WPL == 16, u32x4, u32x2>::type SV;
+    SV sv[NPIECE], ov[NPIECE];
+#pragma unroll
+    for (int pc = 0; pc < NPIECE; ++pc) {
+        const uint32_t g = (uint32_t)(k_wave + pc * PIECE_KB * 32) / (uint32_t)G;
+        const size_t goff = (size_t)g * (uint32_t)N * 2u;
+        sv[pc] = *reinterpret_cast<const SV*>(static_cast<const char*>(p.scale) + goff + s_lane);
+        if (HAS_OFF) ov[pc] = *reinterpret_cast<const SV*>(static_cast<const char*>(p.offset) + goff + s_lane);
+    }
+    constexpr int SL = PF + 1;
+    uint32_t wv[SL][8];
+    u32x4 xa[SL];
+    auto issue = [&](int kb) {
+        // the scheduler must not interleave blocks: a later block's load moved
+        // ahead, or its use moved up, turns the in-order wait into a drain
+        __builtin_amdgcn_sched_barrier(0);
+        xa[kb % SL] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, x_lane, kb * 64, 0));
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            wv[kb % SL][r] = __builtin_amdgcn_raw_buffer_load_b32(wr, w_lane, (uint32_t)(kb * 32 + r) * rowbytes, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int kb = 0; kb < (PF < NKB ? PF : NKB); ++kb) issue(kb);
+
+    const u32x4 ones = {MM::ONES, MM::ONES, MM::ONES, MM::ONES};
+    // per-lane byte selectors: tiles 2i, 2i+1 read byte (2nh + i) of each word
+    const uint32_t sel0 = byte_sel(2u * nh), sel1 = byte_sel(2u * nh + 1u);
+
+    f32x4 acc[TPL], ag[TPL], xs;
+#pragma unroll
+    for (int t = 0; t < TPL; ++t) acc[t] = ag[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    xs = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        if (kb + PF < NKB) issue(kb + PF);
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 xk = xa[kb % SL];
+        const uint32_t* wk = wv[kb % SL];
+        if constexpr (WPL == 16) {
+            ag[0] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, byte_sel(0)), ag[0]);
+            ag[1] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wk, byte_sel(0)), ag[1]);
+            ag[2] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, byte_sel(1)), ag[2]);
+            ag[3] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wk, byte_sel(1)), ag[3]);
+            ag[4] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, byte_sel(2)), ag[4]);
+            ag[5] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wk, byte_sel(2)), ag[5]);
+            ag[6] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, byte_sel(3)), ag[6]);
+            ag[7] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wk, byte_sel(3)), ag[7]);
+        } else {
+            ag[0] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, sel0), ag[0]);
+            ag[1] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wk, sel0), ag[1]);
+            ag[2] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, sel1), ag[2]);
+            ag[3] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wk, sel1), ag[3]);
+        }
+        xs = MM::mma(xk, ones, xs);
+        if ((kb + 1) % PIECE_KB == 0) {
+            // acc += s*A + s*(offset - BASE)*xs, then a new piece starts
+            const int pc = kb / PIECE_KB;
+#pragma unroll
+            for (int t = 0; t < TPL; ++t) {
+                const uint32_t sb = sv[pc][t >> 1] >> (16 * (t & 1));
+                const float sf = load_half_bits(sb & 0xffffu, p.s_dtype);
+                float of = 0.0f;
+                if (HAS_OFF) of = load_half_bits((ov[pc][t >> 1] >> (16 * (t & 1))) & 0xffffu, p.s_dtype);
+                const float sx = sf * (of - MM::BASE);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[t][r] = __builtin_fmaf(sf, ag[t][r], __builtin_fmaf(sx, xs[r], acc[t][r]));
+                ag[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            }
+            xs = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    // lane (c, kg) holds rows 4kg..4kg+3 of columns  8*slot + 4*nh + t
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float* dst = &red[wave][4 * kg + r][8 * slot + 4 * nh];
+        *reinterpret_cast<f32x4*>(dst) = (f32x4){acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+        if constexpr (TPL == 8) *reinterpret_cast<f32x4*>(dst + 4) = (f32x4){acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+    }
+    __syncthreads();
+
+    // each thread finishes 4 consecutive columns of one row, summing the K ranges in order
+    constexpr int QUADS = 16 * 256 / 4;
+    const int n_strip0 = strip * 256;
+    for (int q = threadIdx.x; q < QUADS; q += 64 * NWAVE) {
+        const int row = q >> 6, col = 4 * (q & 63);
+        const int hh = col / NCOL, local = col % NCOL;
+        f32x4 v = *reinterpret_cast<const f32x4*>(&red[hh][row][local]);
+#pragma unroll
+        for (int w = 1; w < KW; ++w) v += *reinterpret_cast<const f32x4*>(&red[hh + HALVES * w][row][local]);
+        const int mm = rb * 16 + row, n = n_strip0 + col;
+        if (mm >= M || n >= N) continue;
+        if (FINAL) {
+            if (p.bias_dtype) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[t] += load_scalar(p.bias, n + t, p.bias_dtype);
+            }
+            u32x2 packed;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const bool bf = p.out_dtype == QK_BF16;
+                const uint32_t lo = bf ? f32_to_bf16_bits(v[2 * e]) : f32_to_f16_bits(v[2 * e]);
+                const uint32_t hi = bf ? f32_to_bf16_bits(v[2 * e + 1]) : f32_to_f16_bits(v[2 * e + 1]);
+                packed[e] = lo | (hi << 16);
+            }
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + (int64_t)mm * N + n) = packed;
+        } else {
+            *reinterpret_cast<f32x4*>(partial + ((int64_t)split * M + mm) * N + n) = v;
+        }
+    }
+}
+
 // Sum split partials in split order, add bias, cast; 4 outputs per thread,
 // all split loads of a thread issued together (latency-bound at decode sizes).
 template <int OUTDT>
@@ -502,6 +702,102 @@ hipError_t launch_decode_dt(const WqbmmArgs& p, const DecodePlan& d, float* part
     }
 }
 
+// Stream kernel plan (M <= 16): a strip of `wpl` words per workgroup of
+// `nwave` waves, 128 rows of K per wave, K split into nsplit workgroup ranges.
+struct StreamPlan {
+    bool ok;
+    int wpl, nwave, nkb, pf, nsplit, nstrip, piece_kb;
+};
+
+StreamPlan stream_plan(const WqbmmArgs& p) {
+    StreamPlan s{false, 16, 8, 4, 2, 1, 0, 4};
+    const int64_t G = p.group == 0 ? p.K : p.group;
+    if (p.w_dtype != QK_I32 || p.M <= 0 || p.M > 16 || p.N <= 0 || p.K <= 0) return s;
+    if (G <= 0 || p.K % G != 0 || !(G % 128 == 0 || G == 32 || G == 64)) return s;
+    if (p.K * (p.N / 2) >= ((int64_t)1 << 31) || p.M * p.K * 2 >= ((int64_t)1 << 31) ||
+        (p.K / G) * p.N * 2 >= ((int64_t)1 << 31))
+        return s;
+    if (((uintptr_t)p.x | (uintptr_t)p.scale) % 16 != 0 || (uintptr_t)p.out % 8 != 0 || (uintptr_t)p.w % 4 != 0 ||
+        (p.offset && (uintptr_t)p.offset % 16 != 0))
+        return s;
+    s.piece_kb = G >= 128 ? 4 : (int)(G / 32);
+    const int64_t nw = p.N / 8;
+    s.wpl = 16;
+    s.nwave = 16;
+    s.nkb = 4;
+    s.pf = 2;
+    if (const char* e = std::getenv("QK_W4_STREAM")) {  // tuning override: "nwave,nkb,pf" or "off"
+        if (std::strcmp(e, "off") == 0) return s;
+        int a = 0, b = 0, c = 0;
+        if (std::sscanf(e, "%d,%d,%d", &a, &b, &c) == 3 && (a == 8 || a == 16) &&
+            ((b == 4 && (c == 2 || c == 4)) || (b == 8 && (c == 2 || c == 3)))) {
+            s.nwave = a;
+            s.nkb = b;
+            s.pf = c;
+        }
+    }
+    if (s.piece_kb != 4) {  // short groups: one instantiated shape
+        s.nkb = 4;
+        s.pf = 2;
+    }
+    const int halves = 32 / s.wpl;
+    int kw = s.nwave / halves;
+    const int rows = s.nkb * 32;
+    while (kw > 1 && p.K % (kw * rows) != 0) kw >>= 1;  // fewer K ranges when K is short
+    if (p.K % (kw * rows) != 0) return s;
+    s.nwave = kw * halves;
+    if (s.nwave != 8 && s.nwave != 16) return s;  // the instantiated shapes
+    s.nsplit = (int)(p.K / (kw * rows));
+    s.nstrip = (int)((nw + 31) / 32);
+    if (s.nsplit > 1 && (int64_t)s.nsplit * p.M * p.N * 4 > ((int64_t)256 << 20)) return s;
+    s.ok = (int64_t)s.nstrip * s.nsplit < ((int64_t)1 << 31);
+    return s;
+}
+
+template <int DT, int NWAVE, int NKB, int PF, int PKB, bool HAS_OFF>
+hipError_t launch_stream_t(const WqbmmArgs& p, const StreamPlan& s, float* partial, hipStream_t stream) {
+    const dim3 grid((uint32_t)((int64_t)s.nstrip * s.nsplit));
+    if (s.nsplit == 1)
+        w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, true><<<grid, dim3(64 * NWAVE), 0, stream>>>(p, partial,
+                                                                                               s.nstrip, 1);
+    else
+        w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, false><<<grid, dim3(64 * NWAVE), 0, stream>>>(
+            p, partial, s.nstrip, s.nsplit);
+    return hipGetLastError();
+}
+
+template <int DT, int NWAVE, bool HAS_OFF>
+hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* partial, hipStream_t stream) {
+    switch (s.piece_kb) {
+    case 1: return launch_stream_t<DT, NWAVE, 4, 2, 1, HAS_OFF>(p, s, partial, stream);
+    case 2: return launch_stream_t<DT, NWAVE, 4, 2, 2, HAS_OFF>(p, s, partial, stream);
+    default: break;
+    }
+    if (s.nkb == 8)
+        return s.pf == 3 ? launch_stream_t<DT, NWAVE, 8, 3, 4, HAS_OFF>(p, s, partial, stream)
+                         : launch_stream_t<DT, NWAVE, 8, 2, 4, HAS_OFF>(p, s, partial, stream);
+    return s.pf == 4 ? launch_stream_t<DT, NWAVE, 4, 4, 4, HAS_OFF>(p, s, partial, stream)
+                     : launch_stream_t<DT, NWAVE, 4, 2, 4, HAS_OFF>(p, s, partial, stream);
+}
+
+template <int DT>
+hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* partial, hipStream_t stream) {
+    const bool off = p.offset != nullptr;
+    if (s.nwave == 8)
+        return off ? launch_stream_w<DT, 8, true>(p, s, partial, stream) : launch_stream_w<DT, 8, false>(p, s, partial, stream);
+    return off ? launch_stream_w<DT, 16, true>(p, s, partial, stream) : launch_stream_w<DT, 16, false>(p, s, partial, stream);
+}
+
+template <int OUTDT>
+hipError_t launch_reduce(const WqbmmArgs& p, int nsplit, const float* partial, hipStream_t stream) {
+    const int64_t total = p.M * p.N / 4;
+    int64_t blocks = (total + kThreads - 1) / kThreads;
+    if (blocks > 65536) blocks = 65536;
+    w4_reduce<OUTDT><<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(partial, nsplit, p.M, p.N, p.bias,
+                                                                           p.bias_dtype, p.out);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group) {
@@ -512,8 +808,11 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     p.w_dtype = w_dtype;
     p.group = group;
     // alignment does not change the split count; use aligned dummies
-    p.x = p.scale = p.out = (void*)(uintptr_t)256;
+    p.x = p.scale = p.offset = p.out = (void*)(uintptr_t)256;
     p.w = (void*)(uintptr_t)256;
+    if (p.group == 0) p.group = p.K;
+    const StreamPlan s = stream_plan(p);
+    if (s.ok) return s.nsplit == 1 ? 0 : (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
     const DecodePlan d = decode_plan(p);
     if (!d.ok || d.nsplit == 1) return 0;
     return (size_t)d.nsplit * (size_t)M * (size_t)N * sizeof(float);
@@ -523,6 +822,18 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
     if (a.M == 0 || a.N == 0) return hipSuccess;
     WqbmmArgs p = a;
     if (p.group == 0) p.group = p.K;  // per channel == one group spanning K
+    const StreamPlan sp = stream_plan(p);
+    if (sp.ok) {
+        float* partial = static_cast<float*>(workspace);
+        if (sp.nsplit > 1 && (!partial || ws_bytes < (size_t)sp.nsplit * p.M * p.N * sizeof(float) ||
+                              (uintptr_t)partial % 16 != 0))
+            return hipErrorInvalidValue;
+        hipError_t e = p.x_dtype == QK_BF16 ? launch_stream_dt<QK_BF16>(p, sp, partial, stream)
+                                            : launch_stream_dt<QK_F16>(p, sp, partial, stream);
+        if (e != hipSuccess || sp.nsplit == 1) return e;
+        return p.out_dtype == QK_BF16 ? launch_reduce<QK_BF16>(p, sp.nsplit, partial, stream)
+                                      : launch_reduce<QK_F16>(p, sp.nsplit, partial, stream);
+    }
     const DecodePlan d = decode_plan(p);
     if (d.ok) {
         float* partial = static_cast<float*>(workspace);

@@ -216,7 +216,7 @@ def main():
     q_s = float(np.mean(t_quant))
 
     traffic = hbm_traffic()
-    t_w4 = (traffic["w4_decode"] + traffic["w4_reduce"]) if "w4_decode" in traffic and "w4_reduce" in traffic else None
+    t_w4 = (traffic["w4_stream"] + traffic["w4_reduce"]) if "w4_stream" in traffic and "w4_reduce" in traffic else None
 
     line = {
         "metric": "W8A8 GEMM TOPS (M=4096) + W4A16 decode GB/s (M=16); % of MI355X roofline",

@@ -286,6 +286,13 @@ def test_w4a16_cfg3_prefill(ops, oracle):
     (40, 200, 256, 0, True, torch.bfloat16),
     (5, 24, 96, 0, False, torch.float16),
     (2, 16, 100, 0, True, torch.bfloat16),       # K % 32 != 0: generic kernel
+    # stream kernel (M <= 16, K a multiple of 512): ragged strips, clamped rows, every group size
+    (7, 1000, 1024, 32, True, torch.float16),
+    (16, 520, 2048, 64, True, torch.bfloat16),
+    (9, 4096, 4096, 0, True, torch.bfloat16),
+    (2, 8, 512, 128, False, torch.float16),
+    (1, 11008, 4096, 128, True, torch.bfloat16),
+    (13, 2056, 1536, 256, True, torch.float16),
 ])
 def test_w4a16_shapes(ops, oracle, M, N, K, group, offset, x_dtype):
     say(f"w4a16 M={M} N={N} K={K} group={group} offset={offset} {x_dtype}")
@@ -341,6 +348,20 @@ def test_abi_quant_matmul_matches_op(ops, oracle):
     rc = L.qk_quant_matmul(a.data_ptr(), K, w.data_ptr(), 2, 2, M, N, K, s.data_ptr(), N, None, 0, None, None, 0,
                            out.data_ptr(), BF16, None, 0, _stream())
     assert rc == -1 and "transposed view" in ops.last_error()
+
+
+@pytest.mark.parametrize("cfg", ["16,4,2", "16,4,4", "16,8,2", "16,8,3", "8,4,2", "8,8,3"])
+def test_w4a16_stream_configs(ops, oracle, monkeypatch, cfg):
+    """Every wave count / K-blocks per wave / prefetch depth of the decode stream kernel (forced through its
+    tuning variable)."""
+    monkeypatch.setenv("QK_W4_STREAM", cfg)
+    for (M, N, K, group) in [(5, 1096, 2048, 128), (16, 264, 4096, 32)]:
+        say(f"w4a16 stream cfg={cfg} M={M} N={N} K={K} group={group}")
+        case = W.W4A16Case(M=M, N=N, K=K, group=group, x_dtype=torch.bfloat16, offset=True)
+        d = W.w4a16_inputs(case, seed=7 * M + K)
+        b = torch.randn(N).to(torch.bfloat16)
+        out = _w4_run(ops, d, group, bias=b)
+        bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b))
 
 
 def test_abi_dynamic_quant_and_w4a16(ops, oracle):
