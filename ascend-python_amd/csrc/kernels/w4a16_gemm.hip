@@ -566,6 +566,233 @@ __global__ __launch_bounds__(kThreads) void w4_reduce(const float* __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill (large M): a bf16 / fp16 MFMA GEMM on the raw int4 values, with the
+// same group-wise algebra as the decode kernels, so the weights are never
+// rounded:  for each group g,  A_g = x . (128 + u)  (MFMA on exact magic
+// values),  xs_g = x . 1  (one MFMA per row tile against a vector of ones),
+// then  acc += s * A_g + s * (offset - BASE) * xs_g.
+//
+// Tile 256 x 128, 8 waves as 4 (M) x 2 (N), each 64 x 64 (16 MFMA tiles:
+// 64 accumulators + 64 group sums + 16 row sums per lane).  A stage holds
+// 64 k: x rows and weight columns are both 128-byte LDS rows ([m][k], [n][k])
+// with a 16-byte-chunk XOR swizzle; the weight columns also flip row parity in
+// odd groups of 8 so the unpacking threads' 8-byte writes are conflict-free.
+// A thread unpacks 4 rows x 1 packed word (8 columns): per column two
+// v_perm_b32 + two v_bitop3_b32 give 4 k of magic values.  Stage s+1 is
+// written to LDS between the two MFMA halves of stage s while stage s+2's
+// global loads are in flight.
+namespace pf {
+constexpr int BM = 256, BN = 128, BK = 64, ROWB = 128;
+__device__ __forceinline__ int off(int r, int c) { return r * ROWB + 16 * (c ^ ((r >> 1) & 7)); }
+__device__ __forceinline__ int boff(int n, int c) { return (n ^ ((n >> 3) & 1)) * ROWB + 16 * (c ^ ((n >> 1) & 7)); }
+}  // namespace pf
+
+template <int DT, bool HAS_OFF, bool FULL>
+__global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int tiles_n) {
+    typedef Mfma<DT> MM;
+    constexpr int NT = 512, BN = pf::BN;
+    constexpr int A_BYTES = pf::BM * pf::ROWB, B_BYTES = BN * pf::ROWB, STAGE = A_BYTES + B_BYTES;
+    constexpr int TM = 4, TN = 4;           // MFMA tiles per wave (wave tile 64 x 64)
+    constexpr int WQ = BN / 8;              // packed words per weight row of the tile (16)
+    constexpr int WT = WQ * 16;             // unpacking threads (4 rows each, 64 rows)
+    constexpr int OROWB = 2 * BN + 16;      // padded output staging row (bytes)
+    constexpr int SMEM = 2 * STAGE > pf::BM * OROWB ? 2 * STAGE : pf::BM * OROWB;
+    __shared__ __attribute__((aligned(16))) char smem[SMEM];
+
+    const int bid = xcd_swizzle(blockIdx.x, tiles_m * tiles_n);
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int grp = bid / per_group;
+    const int first_m = grp * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int tm = first_m + (bid % per_group) % gm;
+    const int tn = (bid % per_group) / gm;
+    const int M = (int)p.M, N = (int)p.N, K = (int)p.K, G = (int)p.group;
+    const int m0 = tm * pf::BM, n0 = tn * BN;
+    const int NWD = N >> 3;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int fr = lane & 15, g4 = lane >> 4;
+
+    // ---- A (x) loads: 4 x 16 bytes per thread per stage, rows tid/8 + 64i
+    const char* X = static_cast<const char*>(p.x);
+    uint32_t a_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int r = m0 + tid / 8 + 64 * i;
+        if (!FULL) r = r < M ? r : M - 1;  // rows past M are computed and not stored
+        a_off[i] = ((uint32_t)r * (uint32_t)K + 8u * (uint32_t)(tid % 8)) * 2u;
+    }
+    // ---- W loads: threads < WT take word column tid / 16, rows 4 (tid % 16) .. +3
+    const bool wthr = tid < WT;
+    const int wcol_l = (tid / 16) % WQ, rg = tid & 15;
+    int wcol = n0 / 8 + wcol_l;
+    if (!FULL) wcol = wcol < NWD ? wcol : NWD - 1;
+    const char* Wp = static_cast<const char*>(p.w);
+    const uint32_t w_off = (uint32_t)(4 * rg) * (uint32_t)NWD * 4u + (uint32_t)wcol * 4u;
+
+    u32x4 ra[4];
+    uint32_t rw[4];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const u32x4*>(X + (size_t)k0 * 2u + a_off[i]);
+        if (wthr) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                rw[i] = *reinterpret_cast<const uint32_t*>(Wp + (size_t)(uint32_t)(k0 + i) * (uint32_t)NWD * 4u + w_off);
+        }
+    };
+    auto lstore = [&](int st) {
+        char* As = smem + st * STAGE;
+        char* Bs = As + A_BYTES;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(As + pf::off(tid / 8 + 64 * i, tid % 8)) = ra[i];
+        if (wthr) {
+            const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000f000fu);
+            const uint32_t magic = __builtin_amdgcn_readfirstlane(MM::MAGIC | 0x00080008u);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                // rows (0,1) and (2,3): byte j/2 of each word, odd nibbles shifted down
+                uint32_t p01 = __builtin_amdgcn_perm(rw[1], rw[0], byte_sel(j >> 1));
+                uint32_t p23 = __builtin_amdgcn_perm(rw[3], rw[2], byte_sel(j >> 1));
+                if (j & 1) {
+                    p01 >>= 4;
+                    p23 >>= 4;
+                }
+                const u32x2 v = {(p01 & mask) ^ magic, (p23 & mask) ^ magic};
+                *reinterpret_cast<u32x2*>(Bs + pf::boff(8 * wcol_l + j, rg >> 1) + 8 * (rg & 1)) = v;
+            }
+        }
+    };
+
+    f32x4 acc[TM][TN], ag[TM][TN], xs[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        xs[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = ag[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    const u32x4 ones = {MM::ONES, MM::ONES, MM::ONES, MM::ONES};
+    // columns of this lane's MFMA tiles (clamped for loads; not stored past N)
+    int ncol[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn * 64 + 16 * j + fr;
+        ncol[j] = n < N ? n : N - 1;
+    }
+    // acc += s*A + s*(offset - BASE)*xs for the group containing row k_in, then restart the group sums
+    auto fold = [&](int k_in) {
+        const int gi = k_in / G;
+        float sf[TN], sx[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const size_t o = (size_t)gi * N + ncol[j];
+            sf[j] = load_half_bits(static_cast<const uint16_t*>(p.scale)[o], p.s_dtype);
+            const float of = HAS_OFF ? load_half_bits(static_cast<const uint16_t*>(p.offset)[o], p.s_dtype) : 0.0f;
+            sx[j] = sf[j] * (of - MM::BASE);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[i][j][r] = __builtin_fmaf(sf[j], ag[i][j][r], __builtin_fmaf(sx[j], xs[i][r], acc[i][j][r]));
+                ag[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            }
+            xs[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+    };
+
+    const int nk = K / pf::BK;
+    const int gsub = G / 32;  // 32-k MFMA steps per group
+    gload(0);
+    lstore(0);
+    if (nk > 1) gload(pf::BK);
+    for (int it = 0; it < nk; ++it) {
+        __syncthreads();
+        const int st = it & 1;
+        const char* As = smem + st * STAGE;
+        const char* Bs = As + A_BYTES;
+        auto frags = [&](int kk, u32x4 (&af)[TM], u32x4 (&bfr)[TN]) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                af[i] = *reinterpret_cast<const u32x4*>(As + pf::off(wm * 64 + 16 * i + fr, 4 * kk + g4));
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                bfr[j] = *reinterpret_cast<const u32x4*>(Bs + pf::boff(wn * 64 + 16 * j + fr, 4 * kk + g4));
+        };
+        auto mma = [&](const u32x4 (&af)[TM], const u32x4 (&bfr)[TN], int sub) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], bfr[j], ag[i][j]);
+                xs[i] = MM::mma(af[i], ones, xs[i]);
+            }
+            if ((sub + 1) % gsub == 0) fold(32 * sub);
+        };
+        u32x4 af[TM], bfr[TN];
+        frags(0, af, bfr);
+        mma(af, bfr, 2 * it);
+        if (it + 1 < nk) {
+            lstore(st ^ 1);
+            if (it + 2 < nk) gload((it + 2) * pf::BK);
+        }
+        frags(1, af, bfr);
+        mma(af, bfr, 2 * it + 1);
+    }
+
+    // ---- epilogue: + bias, cast
+    float bv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn * 64 + 16 * j + fr;
+        bv[j] = (p.bias_dtype && n < N) ? load_scalar(p.bias, n, p.bias_dtype) : 0.0f;
+    }
+    if constexpr (FULL) {
+        __syncthreads();
+        uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = wm * 64 + 16 * i + 4 * g4 + r;
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const float v = acc[i][j][r] + bv[j];
+                    ot[row * (OROWB / 2) + wn * 64 + 16 * j + fr] =
+                        (uint16_t)(p.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+                }
+            }
+        __syncthreads();
+        constexpr int CPRO = 2 * BN / 16;
+        for (int q = tid; q < pf::BM * CPRO; q += NT) {
+            const int row = q / CPRO, c = q % CPRO;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * OROWB + 16 * c);
+            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N + n0 + 8 * c) = v;
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * 64 + 16 * i + 4 * g4 + r;
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = n0 + wn * 64 + 16 * j + fr;
+                if (n >= N) continue;
+                const float v = acc[i][j][r] + bv[j];
+                static_cast<uint16_t*>(p.out)[(size_t)m * N + n] =
+                    (uint16_t)(p.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+            }
+        }
+}
+
 // Any shape: one thread per output, fp32 sums per group then the same
 // group-wise scale/offset algebra as the tiled kernels.
 __global__ __launch_bounds__(kThreads) void wq_generic(WqbmmArgs p) {
@@ -788,6 +1015,47 @@ hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* part
     return off ? launch_stream_w<DT, 16, true>(p, s, partial, stream) : launch_stream_w<DT, 16, false>(p, s, partial, stream);
 }
 
+// Prefill plan: large M, int4 weights, K a multiple of the 64-row stage and
+// G a multiple of the 32-row MFMA step.
+struct GemmPlan {
+    bool ok, full;
+    int tiles_m, tiles_n;
+};
+
+GemmPlan gemm_plan(const WqbmmArgs& p) {
+    GemmPlan g{false, false, 0, 0};
+    const int64_t G = p.group == 0 ? p.K : p.group;
+    if (p.w_dtype != QK_I32 || p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0) return g;
+    if (G <= 0 || p.K % G != 0 || G % 32 != 0) return g;
+    if (p.M * p.K * 2 >= ((int64_t)1 << 31) || p.K * (p.N / 2) >= ((int64_t)1 << 31) ||
+        (p.K / G) * p.N >= ((int64_t)1 << 31) || p.M * p.N >= ((int64_t)1 << 31))
+        return g;
+    if (((uintptr_t)p.x | (uintptr_t)p.out) % 16 != 0 || (uintptr_t)p.w % 4 != 0) return g;
+    g.tiles_m = (int)((p.M + 255) / 256);
+    g.tiles_n = (int)((p.N + 127) / 128);
+    const char* force = std::getenv("QK_W4_GEMM");  // tuning / test override: "force" or "off"
+    if (force && std::strcmp(force, "off") == 0) return g;
+    const bool forced = force && std::strcmp(force, "force") == 0;
+    // too few tiles: the decode kernels stream the weight better
+    if (!forced && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
+    g.full = p.M % 256 == 0 && p.N % 128 == 0;
+    g.ok = true;
+    return g;
+}
+
+template <int DT, bool OFF>
+hipError_t launch_gemm_t(const WqbmmArgs& p, const GemmPlan& g, hipStream_t stream) {
+    const dim3 grid((uint32_t)(g.tiles_m * g.tiles_n));
+    if (g.full) w4_gemm<DT, OFF, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    else w4_gemm<DT, OFF, false><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_gemm_dt(const WqbmmArgs& p, const GemmPlan& g, hipStream_t stream) {
+    return p.offset != nullptr ? launch_gemm_t<DT, true>(p, g, stream) : launch_gemm_t<DT, false>(p, g, stream);
+}
+
 template <int OUTDT>
 hipError_t launch_reduce(const WqbmmArgs& p, int nsplit, const float* partial, hipStream_t stream) {
     const int64_t total = p.M * p.N / 4;
@@ -813,6 +1081,7 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     if (p.group == 0) p.group = p.K;
     const StreamPlan s = stream_plan(p);
     if (s.ok) return s.nsplit == 1 ? 0 : (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
+    if (gemm_plan(p).ok) return 0;
     const DecodePlan d = decode_plan(p);
     if (!d.ok || d.nsplit == 1) return 0;
     return (size_t)d.nsplit * (size_t)M * (size_t)N * sizeof(float);
@@ -833,6 +1102,11 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
         if (e != hipSuccess || sp.nsplit == 1) return e;
         return p.out_dtype == QK_BF16 ? launch_reduce<QK_BF16>(p, sp.nsplit, partial, stream)
                                       : launch_reduce<QK_F16>(p, sp.nsplit, partial, stream);
+    }
+    if (!sp.ok) {
+        const GemmPlan gp = gemm_plan(p);
+        if (gp.ok)
+            return p.x_dtype == QK_BF16 ? launch_gemm_dt<QK_BF16>(p, gp, stream) : launch_gemm_dt<QK_F16>(p, gp, stream);
     }
     const DecodePlan d = decode_plan(p);
     if (d.ok) {

@@ -364,6 +364,26 @@ def test_w4a16_stream_configs(ops, oracle, monkeypatch, cfg):
         bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b))
 
 
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype", [
+    (300, 520, 512, 128, True, torch.bfloat16),     # ragged M and N
+    (256, 256, 256, 64, False, torch.float16),      # full tiles
+    (512, 1024, 1024, 32, True, torch.bfloat16),    # full tiles, 32-row groups
+    (70, 136, 64, 0, True, torch.bfloat16),         # one K stage, per-channel scale
+    (260, 264, 2048, 0, False, torch.float16),      # per-channel over a long K
+])
+def test_w4a16_prefill_kernel(ops, oracle, monkeypatch, M, N, K, group, offset, x_dtype):
+    """The large-M kernel (exact int4 MFMA operands + group fold), forced onto small shapes."""
+    monkeypatch.setenv("QK_W4_GEMM", "force")
+    say(f"w4a16 prefill kernel M={M} N={N} K={K} group={group} offset={offset} {x_dtype}")
+    case = W.W4A16Case(M=M, N=N, K=K, group=group, x_dtype=x_dtype, offset=offset)
+    d = W.w4a16_inputs(case, seed=M + 3 * N + K)
+    if group == 0:
+        d = dict(d, scale=d["scale"].reshape(-1), offset=None if d["offset"] is None else d["offset"].reshape(-1))
+    b = torch.randn(N).to(x_dtype)
+    out = _w4_run(ops, d, group, bias=b)
+    bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b, x_dtype=x_dtype), dtype=x_dtype)
+
+
 def test_abi_dynamic_quant_and_w4a16(ops, oracle):
     say("ABI qk_dynamic_quant / qk_weight_quant_bmm")
     L = ops.abi()
