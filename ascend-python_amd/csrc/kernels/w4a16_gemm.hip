@@ -588,7 +588,10 @@ __device__ __forceinline__ int off(int r, int c) { return r * ROWB + 16 * (c ^ (
 __device__ __forceinline__ int boff(int n, int c) { return (n ^ ((n >> 3) & 1)) * ROWB + 16 * (c ^ ((n >> 1) & 7)); }
 }  // namespace pf
 
-template <int DT, bool HAS_OFF, bool FULL>
+// G128: the group is exactly two stages, so the stage loop is unrolled by two
+// and the group's first MFMA step starts from C = 0 (no re-zeroing); other
+// group sizes count steps at run time and zero the group sums after a fold.
+template <int DT, bool HAS_OFF, bool FULL, bool G128>
 __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int tiles_n) {
     typedef Mfma<DT> MM;
     constexpr int NT = 512, BN = pf::BN;
@@ -599,6 +602,9 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
     constexpr int OROWB = 2 * BN + 16;      // padded output staging row (bytes)
     constexpr int SMEM = 2 * STAGE > pf::BM * OROWB ? 2 * STAGE : pf::BM * OROWB;
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
+    // group scale s and s*(offset - BASE) per column, a ring of 4 groups
+    // (written with the stage the group starts in, read by its fold)
+    __shared__ float sc_s[4][BN], sc_x[4][BN];
 
     const int bid = xcd_swizzle(blockIdx.x, tiles_m * tiles_n);
     constexpr int GM = 8;
@@ -617,8 +623,9 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
     const int wm = wave >> 1, wn = wave & 1;
     const int fr = lane & 15, g4 = lane >> 4;
 
-    // ---- A (x) loads: 4 x 16 bytes per thread per stage, rows tid/8 + 64i
-    const char* X = static_cast<const char*>(p.x);
+    // ---- A (x) loads: 4 x 16 bytes per thread per stage, rows tid/8 + 64i;
+    // buffer loads: per-lane offsets in VGPRs, the stage's k offset in an SGPR
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
     uint32_t a_off[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -631,25 +638,72 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
     const int wcol_l = (tid / 16) % WQ, rg = tid & 15;
     int wcol = n0 / 8 + wcol_l;
     if (!FULL) wcol = wcol < NWD ? wcol : NWD - 1;
-    const char* Wp = static_cast<const char*>(p.w);
-    const uint32_t w_off = (uint32_t)(4 * rg) * (uint32_t)NWD * 4u + (uint32_t)wcol * 4u;
+    const uint32_t rowb = (uint32_t)NWD * 4u;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (uint32_t)K * rowb);
+    const uint32_t w_off = (uint32_t)(4 * rg) * rowb + (uint32_t)wcol * 4u;
+    // LDS byte address of column 8*wcol_l + j, k chunk rg/2, half rg&1 of the
+    // weight tile is  wb_base + (KJ(j) ^ wb_x)  with  KJ(j) = 128 j | 16 (j/2)
+    // (the pf::boff layout written out so each column costs one v_xad_u32)
+    const uint32_t wb_base = 1024u * (uint32_t)wcol_l + 8u * (uint32_t)(rg & 1);
+    const uint32_t wb_x = (16u * ((uint32_t)(rg >> 1) ^ (4u * (uint32_t)(wcol_l & 1)))) | (128u * (uint32_t)(wcol_l & 1));
+    // scale / offset of the groups that start inside a stage: threads
+    // WT .. WT+BN-1 each fetch one column (G = 32 starts two groups per stage)
+    const bool sthr = tid >= WT && tid < WT + BN;
+    const int scol_l = tid - WT;
+    const int scol = n0 + scol_l < N ? n0 + scol_l : N - 1;
 
     u32x4 ra[4];
     uint32_t rw[4];
+    uint32_t rsc0 = 0, rof0 = 0, rsc1 = 0, rof1 = 0;
+    // next group start (k) and its index, advanced by gload (no division in the loop);
+    // a stage starts at most two groups (G = 32)
+    int ld_gk = 0, ld_g = 0;
+    int st_g0 = 0, st_n = 0;
     auto gload = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const u32x4*>(X + (size_t)k0 * 2u + a_off[i]);
+        for (int i = 0; i < 4; ++i)
+            ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, a_off[i], (uint32_t)k0 * 2u, 0));
         if (wthr) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                rw[i] = *reinterpret_cast<const uint32_t*>(Wp + (size_t)(uint32_t)(k0 + i) * (uint32_t)NWD * 4u + w_off);
+                rw[i] = __builtin_amdgcn_raw_buffer_load_b32(wr, w_off, (uint32_t)(k0 + i) * rowb, 0);
         }
+        const bool s0 = ld_gk < k0 + pf::BK;
+        const bool s1 = s0 && ld_gk + G < k0 + pf::BK;
+        if (sthr) {
+            const uint16_t* S = static_cast<const uint16_t*>(p.scale);
+            const uint16_t* O = static_cast<const uint16_t*>(p.offset);
+            if (s0) {
+                rsc0 = S[(size_t)ld_g * N + scol];
+                if (HAS_OFF) rof0 = O[(size_t)ld_g * N + scol];
+            }
+            if (s1) {
+                rsc1 = S[(size_t)(ld_g + 1) * N + scol];
+                if (HAS_OFF) rof1 = O[(size_t)(ld_g + 1) * N + scol];
+            }
+        }
+        st_g0 = ld_g;
+        st_n = (int)s0 + (int)s1;
+        ld_g += st_n;
+        ld_gk += st_n * G;
     };
     auto lstore = [&](int st) {
         char* As = smem + st * STAGE;
         char* Bs = As + A_BYTES;
 #pragma unroll
         for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(As + pf::off(tid / 8 + 64 * i, tid % 8)) = ra[i];
+        if (sthr && st_n > 0) {
+            const float sf = load_half_bits(rsc0, p.s_dtype);
+            const float of = HAS_OFF ? load_half_bits(rof0, p.s_dtype) : 0.0f;
+            sc_s[st_g0 & 3][scol_l] = sf;
+            sc_x[st_g0 & 3][scol_l] = sf * (of - MM::BASE);
+            if (st_n > 1) {
+                const float sf1 = load_half_bits(rsc1, p.s_dtype);
+                const float of1 = HAS_OFF ? load_half_bits(rof1, p.s_dtype) : 0.0f;
+                sc_s[(st_g0 + 1) & 3][scol_l] = sf1;
+                sc_x[(st_g0 + 1) & 3][scol_l] = sf1 * (of1 - MM::BASE);
+            }
+        }
         if (wthr) {
             const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000f000fu);
             const uint32_t magic = __builtin_amdgcn_readfirstlane(MM::MAGIC | 0x00080008u);
@@ -663,7 +717,8 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
                     p23 >>= 4;
                 }
                 const u32x2 v = {(p01 & mask) ^ magic, (p23 & mask) ^ magic};
-                *reinterpret_cast<u32x2*>(Bs + pf::boff(8 * wcol_l + j, rg >> 1) + 8 * (rg & 1)) = v;
+                constexpr uint32_t kj[8] = {0u, 128u, 256u | 16u, 384u | 16u, 512u | 32u, 640u | 32u, 768u | 48u, 896u | 48u};
+                *reinterpret_cast<u32x2*>(Bs + wb_base + (kj[j] ^ wb_x)) = v;
             }
         }
     };
@@ -676,73 +731,96 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
         for (int j = 0; j < TN; ++j) acc[i][j] = ag[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
     const u32x4 ones = {MM::ONES, MM::ONES, MM::ONES, MM::ONES};
-    // columns of this lane's MFMA tiles (clamped for loads; not stored past N)
-    int ncol[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn * 64 + 16 * j + fr;
-        ncol[j] = n < N ? n : N - 1;
-    }
-    // acc += s*A + s*(offset - BASE)*xs for the group containing row k_in, then restart the group sums
-    auto fold = [&](int k_in) {
-        const int gi = k_in / G;
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const int nk = K / pf::BK;
+    // acc += s*A + s*(offset - BASE)*xs for group slot `slot`
+    auto fold = [&](int slot) {
         float sf[TN], sx[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const size_t o = (size_t)gi * N + ncol[j];
-            sf[j] = load_half_bits(static_cast<const uint16_t*>(p.scale)[o], p.s_dtype);
-            const float of = HAS_OFF ? load_half_bits(static_cast<const uint16_t*>(p.offset)[o], p.s_dtype) : 0.0f;
-            sx[j] = sf[j] * (of - MM::BASE);
+            sf[j] = sc_s[slot][wn * 64 + 16 * j + fr];
+            sx[j] = sc_x[slot][wn * 64 + 16 * j + fr];
         }
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     acc[i][j][r] = __builtin_fmaf(sf[j], ag[i][j][r], __builtin_fmaf(sx[j], xs[i][r], acc[i][j][r]));
-                ag[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            }
-            xs[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    };
+    auto frags = [&](const char* As, const char* Bs, int kk, u32x4 (&af)[TM], u32x4 (&bfr)[TN]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            af[i] = *reinterpret_cast<const u32x4*>(As + pf::off(wm * 64 + 16 * i + fr, 4 * kk + g4));
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            bfr[j] = *reinterpret_cast<const u32x4*>(Bs + pf::boff(wn * 64 + 16 * j + fr, 4 * kk + g4));
+    };
+    auto mma = [&](const u32x4 (&af)[TM], const u32x4 (&bfr)[TN], bool first) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], bfr[j], first ? zero4 : ag[i][j]);
+            xs[i] = MM::mma(af[i], ones, first ? zero4 : xs[i]);
         }
     };
-
-    const int nk = K / pf::BK;
-    const int gsub = G / 32;  // 32-k MFMA steps per group
-    gload(0);
-    lstore(0);
-    if (nk > 1) gload(pf::BK);
-    for (int it = 0; it < nk; ++it) {
+    // one 64-k stage: two MFMA steps around the write of stage it+1 and the fetch of stage it+2
+    auto stage = [&](int it, bool first0, bool fold1, int slot) {
         __syncthreads();
         const int st = it & 1;
         const char* As = smem + st * STAGE;
         const char* Bs = As + A_BYTES;
-        auto frags = [&](int kk, u32x4 (&af)[TM], u32x4 (&bfr)[TN]) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                af[i] = *reinterpret_cast<const u32x4*>(As + pf::off(wm * 64 + 16 * i + fr, 4 * kk + g4));
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bfr[j] = *reinterpret_cast<const u32x4*>(Bs + pf::boff(wn * 64 + 16 * j + fr, 4 * kk + g4));
-        };
-        auto mma = [&](const u32x4 (&af)[TM], const u32x4 (&bfr)[TN], int sub) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-#pragma unroll
-                for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], bfr[j], ag[i][j]);
-                xs[i] = MM::mma(af[i], ones, xs[i]);
-            }
-            if ((sub + 1) % gsub == 0) fold(32 * sub);
-        };
         u32x4 af[TM], bfr[TN];
-        frags(0, af, bfr);
-        mma(af, bfr, 2 * it);
+        frags(As, Bs, 0, af, bfr);
+        mma(af, bfr, first0);
         if (it + 1 < nk) {
             lstore(st ^ 1);
             if (it + 2 < nk) gload((it + 2) * pf::BK);
         }
-        frags(1, af, bfr);
-        mma(af, bfr, 2 * it + 1);
+        frags(As, Bs, 1, af, bfr);
+        mma(af, bfr, false);
+        if (fold1) fold(slot);
+    };
+
+    gload(0);
+    lstore(0);
+    if (nk > 1) gload(pf::BK);
+    if constexpr (G128) {
+        for (int it = 0; it < nk; it += 2) {
+            stage(it, true, false, 0);
+            stage(it + 1, false, true, (it >> 1) & 3);
+        }
+    } else {
+        const int gsub = G / 32;  // 32-k MFMA steps per group
+        int sub_left = gsub, fold_g = 0;
+        for (int it = 0; it < nk; ++it) {
+            __syncthreads();
+            const int st = it & 1;
+            const char* As = smem + st * STAGE;
+            const char* Bs = As + A_BYTES;
+            u32x4 af[TM], bfr[TN];
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                frags(As, Bs, kk, af, bfr);
+                mma(af, bfr, false);
+                if (kk == 0 && it + 1 < nk) {
+                    lstore(st ^ 1);
+                    if (it + 2 < nk) gload((it + 2) * pf::BK);
+                }
+                if (--sub_left == 0) {
+                    fold(fold_g & 3);
+                    ++fold_g;
+                    sub_left = gsub;
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        xs[i] = zero4;
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) ag[i][j] = zero4;
+                    }
+                }
+            }
+        }
     }
 
     // ---- epilogue: + bias, cast
@@ -1018,12 +1096,12 @@ hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* part
 // Prefill plan: large M, int4 weights, K a multiple of the 64-row stage and
 // G a multiple of the 32-row MFMA step.
 struct GemmPlan {
-    bool ok, full;
+    bool ok, full, g128;
     int tiles_m, tiles_n;
 };
 
 GemmPlan gemm_plan(const WqbmmArgs& p) {
-    GemmPlan g{false, false, 0, 0};
+    GemmPlan g{false, false, false, 0, 0};
     const int64_t G = p.group == 0 ? p.K : p.group;
     if (p.w_dtype != QK_I32 || p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0) return g;
     if (G <= 0 || p.K % G != 0 || G % 32 != 0) return g;
@@ -1039,6 +1117,7 @@ GemmPlan gemm_plan(const WqbmmArgs& p) {
     // too few tiles: the decode kernels stream the weight better
     if (!forced && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
     g.full = p.M % 256 == 0 && p.N % 128 == 0;
+    g.g128 = false;  // the unrolled G = 128 variant spills at 8 waves; kept for the 4-wave layout
     g.ok = true;
     return g;
 }
@@ -1046,8 +1125,10 @@ GemmPlan gemm_plan(const WqbmmArgs& p) {
 template <int DT, bool OFF>
 hipError_t launch_gemm_t(const WqbmmArgs& p, const GemmPlan& g, hipStream_t stream) {
     const dim3 grid((uint32_t)(g.tiles_m * g.tiles_n));
-    if (g.full) w4_gemm<DT, OFF, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
-    else w4_gemm<DT, OFF, false><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    if (g.full && g.g128) w4_gemm<DT, OFF, true, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    else if (g.full) w4_gemm<DT, OFF, true, false><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    else if (g.g128) w4_gemm<DT, OFF, false, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    else w4_gemm<DT, OFF, false, false><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
     return hipGetLastError();
 }
 
