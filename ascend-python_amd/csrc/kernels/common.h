@@ -60,6 +60,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// ---------------------------------------------------------------- per-row quantization
+// Row reductions for 256-thread workgroups (4 wave64): xor-shuffles inside a
+// wave, LDS across the four waves.  Every thread gets the result.
+__device__ __forceinline__ float block_absmax(float amax) {
+    __shared__ float red_absmax[4];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red_absmax[wave] = amax;
+    __syncthreads();
+    float r = red_absmax[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) r = fmaxf(r, red_absmax[w]);
+    return r;
+}
+
+// Symmetric int8 of one value under the row scale s = absmax / 127 (the
+// npu_dynamic_quant contract): clamp(rint(v / s)) with an IEEE division and
+// ties to even; a zero row (s == 0) quantizes to 0.
+__device__ __forceinline__ int32_t quant1(float v, float s) {
+    if (s == 0.0f) return 0;
+    float t = __builtin_rintf(v / s);
+    t = fminf(fmaxf(t, -128.0f), 127.0f);
+    return (int32_t)t;
+}
+
 // ---------------------------------------------------------------- XCD-aware ids
 // The dispatcher hands consecutive workgroup ids to the 8 XCDs round-robin,
 // and each XCD has its own L2.  Renumbering so that the ids one XCD receives
@@ -147,5 +173,11 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
 
 hipError_t launch_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed,
                             hipStream_t stream);
+
+// Quantized MLP block neighbours (x, gamma, h, y in the 16-bit dtype `dt`).
+hipError_t launch_rms_norm(const void* x, int dt, const void* gamma, int64_t rows, int64_t D, float eps, void* y,
+                           int8_t* q, float* scale, float* rstd, hipStream_t stream);
+hipError_t launch_swiglu(const void* h, int dt, int64_t rows, int64_t I, void* y, int8_t* q, float* scale,
+                         hipStream_t stream);
 
 }  // namespace qk

@@ -14,26 +14,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float block_absmax(float amax) {
-    __shared__ float red[kThreads / 64];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[wave] = amax;
-    __syncthreads();
-    float r = red[0];
-#pragma unroll
-    for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, red[w]);
-    return r;
-}
-
-__device__ __forceinline__ int32_t quant1(float v, float s) {
-    if (s == 0.0f) return 0;
-    float t = __builtin_rintf(v / s);
-    t = fminf(fmaxf(t, -128.0f), 127.0f);
-    return (int32_t)t;
-}
-
 // Vector path: K % 8 == 0, 16-byte aligned rows, K <= 8 * 256 * VPT.
 template <int DT, int VPT, bool SMOOTH>
 __global__ __launch_bounds__(kThreads) void dyn_quant_vec(const uint16_t* __restrict__ x, int64_t K,

@@ -1,0 +1,292 @@
+// RMSNorm and SwiGLU for the quantized MLP block, each alone or fused with
+// npu_dynamic_quant, on gfx950.
+//
+// One 256-thread workgroup (4 wave64) per row.  The row is read once with
+// 128-bit loads and kept in registers; row reductions (sum of squares,
+// absmax) go through xor-shuffles inside a wave and LDS across the four
+// waves.  All arithmetic is fp32 and the 16-bit results are rounded to
+// nearest even:
+//   rms_norm:  rstd = 1 / sqrt(sum(x^2) / D + eps)  (IEEE division and square
+//              root),  y = (x * rstd) * gamma                 (op contract:
+//              op_plugin/ops/base_ops/opapi/RmsNormKernelOpApi.cpp:24-35,
+//              golden test/test_custom_ops/test_npu_rms_norm.py:10-17)
+//   swiglu:    y = a / (1 + exp(-a)) * b  with  a, b = h.chunk(2, -1), the
+//              first half the gate (the halving of npu_geglu,
+//              op_plugin/ops/v1r11/opapi/GeGluKernelNpuOpApi.cpp:29-38)
+// The fused variants quantize the 16-bit y exactly as npu_dynamic_quant would
+// quantize it after a round trip through HBM (s = absmax / 127, clamp(rint(y
+// / s))), so fused and unfused paths give identical int8 rows; the fusion
+// saves writing and re-reading y.  HBM-bound: RMSNorm+quant reads 2 B and
+// writes 1 B per element, SwiGLU+quant reads 4 B and writes 1 B per output.
+#include "common.h"
+
+namespace qk {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float block_sum(float v) {
+    __shared__ float red_sum[4];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red_sum[wave] = v;
+    __syncthreads();
+    return (red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3]);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t to16(float f) {
+    return DT == QK_BF16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f);
+}
+
+__device__ __forceinline__ void unpack8(u32x4 d, int dt, float v[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        v[2 * e] = load_half_bits(d[e] & 0xffffu, dt);
+        v[2 * e + 1] = load_half_bits(d[e] >> 16, dt);
+    }
+}
+
+// y (8 values, already rounded to 16 bits and widened back) -> 16-bit store, or
+// (second pass) int8 under the row scale
+template <int DT>
+__device__ __forceinline__ u32x4 pack16(const uint32_t yb[8]) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = yb[2 * e] | (yb[2 * e + 1] << 16);
+    return o;
+}
+
+__device__ __forceinline__ u32x2 packq(const float yf[8], float s) {
+    u32x2 o = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        o[0] |= ((uint32_t)quant1(yf[e], s) & 0xffu) << (8 * e);
+        o[1] |= ((uint32_t)quant1(yf[4 + e], s) & 0xffu) << (8 * e);
+    }
+    return o;
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// Vector path: D % 8 == 0, 16-byte aligned rows, D <= 8 * 256 * VPT.
+template <int DT, int VPT, bool QUANT>
+__global__ __launch_bounds__(kThreads) void rms_norm_vec(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ gamma, int64_t D, float eps,
+                                                         uint16_t* __restrict__ y, int8_t* __restrict__ q,
+                                                         float* __restrict__ scale, float* __restrict__ rstd) {
+    const int64_t row = blockIdx.x;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * D);
+    const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
+    const int nv = (int)(D >> 3);
+    float v[VPT][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        if (idx < nv) {
+            unpack8(xr[idx], DT, v[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[i][e], v[i][e], ss);
+        }
+    }
+    ss = block_sum(ss);
+    const float rs = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+    if (threadIdx.x == 0 && rstd) rstd[row] = rs;
+    float amax = 0.0f;
+    uint32_t yb[VPT][8];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        if (idx < nv) {
+            float g[8];
+            unpack8(gr[idx], DT, g);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                yb[i][e] = to16<DT>((v[i][e] * rs) * g[e]);
+                v[i][e] = load_half_bits(yb[i][e], DT);  // y as a later read of it would see it
+                amax = fmaxf(amax, fabsf(v[i][e]));
+            }
+            if (!QUANT) reinterpret_cast<u32x4*>(y + row * D)[idx] = pack16<DT>(yb[i]);
+        }
+    }
+    if (!QUANT) return;
+    amax = block_absmax(amax);
+    const float s = amax / 127.0f;
+    if (threadIdx.x == 0) scale[row] = s;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        if (idx < nv) reinterpret_cast<u32x2*>(q + row * D)[idx] = packq(v[i], s);
+    }
+}
+
+// Any D and alignment: the row is read again for the output pass.
+template <int DT, bool QUANT>
+__global__ __launch_bounds__(kThreads) void rms_norm_generic(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ gamma, int64_t D, float eps,
+                                                             uint16_t* __restrict__ y, int8_t* __restrict__ q,
+                                                             float* __restrict__ scale, float* __restrict__ rstd) {
+    const int64_t row = blockIdx.x;
+    const uint16_t* xr = x + row * D;
+    float ss = 0.0f;
+    for (int64_t d = threadIdx.x; d < D; d += kThreads) {
+        const float v = load_half_bits(xr[d], DT);
+        ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = block_sum(ss);
+    const float rs = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+    if (threadIdx.x == 0 && rstd) rstd[row] = rs;
+    auto yat = [&](int64_t d) {
+        return to16<DT>((load_half_bits(xr[d], DT) * rs) * load_half_bits(gamma[d], DT));
+    };
+    if (!QUANT) {
+        for (int64_t d = threadIdx.x; d < D; d += kThreads) y[row * D + d] = (uint16_t)yat(d);
+        return;
+    }
+    float amax = 0.0f;
+    for (int64_t d = threadIdx.x; d < D; d += kThreads) amax = fmaxf(amax, fabsf(load_half_bits(yat(d), DT)));
+    amax = block_absmax(amax);
+    const float s = amax / 127.0f;
+    if (threadIdx.x == 0) scale[row] = s;
+    for (int64_t d = threadIdx.x; d < D; d += kThreads)
+        q[row * D + d] = (int8_t)quant1(load_half_bits(yat(d), DT), s);
+}
+
+// ---------------------------------------------------------------- SwiGLU
+__device__ __forceinline__ float silu_mul(float a, float b) { return a / (1.0f + expf(-a)) * b; }
+
+template <int DT, int VPT, bool QUANT>
+__global__ __launch_bounds__(kThreads) void swiglu_vec(const uint16_t* __restrict__ h, int64_t I,
+                                                       uint16_t* __restrict__ y, int8_t* __restrict__ q,
+                                                       float* __restrict__ scale) {
+    const int64_t row = blockIdx.x;
+    const u32x4* ar = reinterpret_cast<const u32x4*>(h + row * 2 * I);
+    const u32x4* br = reinterpret_cast<const u32x4*>(h + row * 2 * I + I);
+    const int nv = (int)(I >> 3);
+    float v[VPT][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        if (idx < nv) {
+            float a[8], b[8];
+            unpack8(ar[idx], DT, a);
+            unpack8(br[idx], DT, b);
+            uint32_t yb[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                yb[e] = to16<DT>(silu_mul(a[e], b[e]));
+                v[i][e] = load_half_bits(yb[e], DT);
+                amax = fmaxf(amax, fabsf(v[i][e]));
+            }
+            if (!QUANT) reinterpret_cast<u32x4*>(y + row * I)[idx] = pack16<DT>(yb);
+        }
+    }
+    if (!QUANT) return;
+    amax = block_absmax(amax);
+    const float s = amax / 127.0f;
+    if (threadIdx.x == 0) scale[row] = s;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        if (idx < nv) reinterpret_cast<u32x2*>(q + row * I)[idx] = packq(v[i], s);
+    }
+}
+
+template <int DT, bool QUANT>
+__global__ __launch_bounds__(kThreads) void swiglu_generic(const uint16_t* __restrict__ h, int64_t I,
+                                                           uint16_t* __restrict__ y, int8_t* __restrict__ q,
+                                                           float* __restrict__ scale) {
+    const int64_t row = blockIdx.x;
+    const uint16_t* hr = h + row * 2 * I;
+    auto yat = [&](int64_t i) {
+        return to16<DT>(silu_mul(load_half_bits(hr[i], DT), load_half_bits(hr[I + i], DT)));
+    };
+    if (!QUANT) {
+        for (int64_t i = threadIdx.x; i < I; i += kThreads) y[row * I + i] = (uint16_t)yat(i);
+        return;
+    }
+    float amax = 0.0f;
+    for (int64_t i = threadIdx.x; i < I; i += kThreads) amax = fmaxf(amax, fabsf(load_half_bits(yat(i), DT)));
+    amax = block_absmax(amax);
+    const float s = amax / 127.0f;
+    if (threadIdx.x == 0) scale[row] = s;
+    for (int64_t i = threadIdx.x; i < I; i += kThreads) q[row * I + i] = (int8_t)quant1(load_half_bits(yat(i), DT), s);
+}
+
+// ---------------------------------------------------------------- dispatch
+template <int DT, int VPT>
+hipError_t rms_vec(const uint16_t* x, const uint16_t* g, int64_t rows, int64_t D, float eps, uint16_t* y, int8_t* q,
+                   float* scale, float* rstd, hipStream_t stream) {
+    const dim3 grid((uint32_t)rows), block(kThreads);
+    if (q) rms_norm_vec<DT, VPT, true><<<grid, block, 0, stream>>>(x, g, D, eps, y, q, scale, rstd);
+    else rms_norm_vec<DT, VPT, false><<<grid, block, 0, stream>>>(x, g, D, eps, y, q, scale, rstd);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t rms_dispatch(const uint16_t* x, const uint16_t* g, int64_t rows, int64_t D, float eps, uint16_t* y,
+                        int8_t* q, float* scale, float* rstd, hipStream_t stream) {
+    const bool aligned = D % 8 == 0 && ((uintptr_t)x | (uintptr_t)g) % 16 == 0 &&
+                         (q ? (uintptr_t)q % 8 == 0 : (uintptr_t)y % 16 == 0);
+    const int64_t per_thread = (D / 8 + kThreads - 1) / kThreads;
+    if (aligned && D > 0 && per_thread <= 16) {
+        if (per_thread <= 2) return rms_vec<DT, 2>(x, g, rows, D, eps, y, q, scale, rstd, stream);
+        if (per_thread <= 4) return rms_vec<DT, 4>(x, g, rows, D, eps, y, q, scale, rstd, stream);
+        if (per_thread <= 8) return rms_vec<DT, 8>(x, g, rows, D, eps, y, q, scale, rstd, stream);
+        return rms_vec<DT, 16>(x, g, rows, D, eps, y, q, scale, rstd, stream);
+    }
+    const dim3 grid((uint32_t)rows), block(kThreads);
+    if (q) rms_norm_generic<DT, true><<<grid, block, 0, stream>>>(x, g, D, eps, y, q, scale, rstd);
+    else rms_norm_generic<DT, false><<<grid, block, 0, stream>>>(x, g, D, eps, y, q, scale, rstd);
+    return hipGetLastError();
+}
+
+template <int DT, int VPT>
+hipError_t swi_vec(const uint16_t* h, int64_t rows, int64_t I, uint16_t* y, int8_t* q, float* scale,
+                   hipStream_t stream) {
+    const dim3 grid((uint32_t)rows), block(kThreads);
+    if (q) swiglu_vec<DT, VPT, true><<<grid, block, 0, stream>>>(h, I, y, q, scale);
+    else swiglu_vec<DT, VPT, false><<<grid, block, 0, stream>>>(h, I, y, q, scale);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t swi_dispatch(const uint16_t* h, int64_t rows, int64_t I, uint16_t* y, int8_t* q, float* scale,
+                        hipStream_t stream) {
+    const bool aligned = I % 8 == 0 && (uintptr_t)h % 16 == 0 && (q ? (uintptr_t)q % 8 == 0 : (uintptr_t)y % 16 == 0);
+    const int64_t per_thread = (I / 8 + kThreads - 1) / kThreads;
+    if (aligned && I > 0 && per_thread <= 8) {
+        if (per_thread <= 2) return swi_vec<DT, 2>(h, rows, I, y, q, scale, stream);
+        if (per_thread <= 4) return swi_vec<DT, 4>(h, rows, I, y, q, scale, stream);
+        return swi_vec<DT, 8>(h, rows, I, y, q, scale, stream);
+    }
+    const dim3 grid((uint32_t)rows), block(kThreads);
+    if (q) swiglu_generic<DT, true><<<grid, block, 0, stream>>>(h, I, y, q, scale);
+    else swiglu_generic<DT, false><<<grid, block, 0, stream>>>(h, I, y, q, scale);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_rms_norm(const void* x, int dt, const void* gamma, int64_t rows, int64_t D, float eps, void* y,
+                           int8_t* q, float* scale, float* rstd, hipStream_t stream) {
+    if (rows == 0) return hipSuccess;
+    const uint16_t* xh = static_cast<const uint16_t*>(x);
+    const uint16_t* gh = static_cast<const uint16_t*>(gamma);
+    uint16_t* yh = static_cast<uint16_t*>(y);
+    if (dt == QK_BF16) return rms_dispatch<QK_BF16>(xh, gh, rows, D, eps, yh, q, scale, rstd, stream);
+    return rms_dispatch<QK_F16>(xh, gh, rows, D, eps, yh, q, scale, rstd, stream);
+}
+
+hipError_t launch_swiglu(const void* h, int dt, int64_t rows, int64_t I, void* y, int8_t* q, float* scale,
+                         hipStream_t stream) {
+    if (rows == 0 || I == 0) return hipSuccess;
+    const uint16_t* hh = static_cast<const uint16_t*>(h);
+    uint16_t* yh = static_cast<uint16_t*>(y);
+    if (dt == QK_BF16) return swi_dispatch<QK_BF16>(hh, rows, I, yh, q, scale, stream);
+    return swi_dispatch<QK_F16>(hh, rows, I, yh, q, scale, stream);
+}
+
+}  // namespace qk

@@ -21,6 +21,7 @@
 
 #include <optional>
 #include <tuple>
+#include <vector>
 
 #include "../../../include/qk_abi.h"
 
@@ -308,6 +309,132 @@ at::Tensor npu_convert_weight_to_int4pack_meta(const at::Tensor& weight, int64_t
     return at::empty(int4pack_shape(weight), weight.options().dtype(at::kInt));
 }
 
+// ---------------------------------------------------------------- npu_rms_norm (+ dynamic quant)
+
+// Normalized size D = gamma.numel() over the trailing gamma.dim() dims of self;
+// rstd keeps the batch dims and has size 1 in the normalized ones
+// (op_plugin/utils/KernelNpuOutputSize.cpp:1514-1530).
+int64_t rms_norm_check(const char* op, const at::Tensor& self, const at::Tensor& gamma, bool quant) {
+    TORCH_CHECK(self.scalar_type() == at::kHalf || self.scalar_type() == at::kBFloat16, op,
+                ": self must be float16 or bfloat16, got ", self.scalar_type());
+    TORCH_CHECK(gamma.scalar_type() == self.scalar_type(), op, ": gamma must have the dtype of self (",
+                self.scalar_type(), "), got ", gamma.scalar_type());
+    TORCH_CHECK(gamma.dim() >= 1 && gamma.dim() <= self.dim(), op, ": gamma must have 1..", self.dim(),
+                " dims, got ", gamma.dim());
+    TORCH_CHECK(!quant || gamma.dim() == 1, op, ": the fused quantization needs a 1-D gamma");
+    for (int64_t i = 0; i < gamma.dim(); ++i)
+        TORCH_CHECK(self.size(self.dim() - gamma.dim() + i) == gamma.size(i), op, ": gamma shape ", gamma.sizes(),
+                    " does not match the trailing dims of self ", self.sizes());
+    TORCH_CHECK(gamma.numel() > 0, op, ": the normalized dims must not be empty");
+    return gamma.numel();
+}
+
+std::vector<int64_t> rstd_shape(const at::Tensor& self, const at::Tensor& gamma) {
+    std::vector<int64_t> sh(self.sizes().begin(), self.sizes().end() - gamma.dim());
+    for (int64_t i = 0; i < gamma.dim(); ++i) sh.push_back(1);
+    return sh;
+}
+
+std::tuple<at::Tensor, at::Tensor> npu_rms_norm(const at::Tensor& self, const at::Tensor& gamma, double epsilon) {
+    const int64_t D = rms_norm_check("npu_rms_norm", self, gamma, false);
+    const c10::DeviceGuard guard(self.device());
+    auto x = self.contiguous();
+    auto g = gamma.contiguous();
+    auto y = at::empty(x.sizes(), x.options());
+    auto rstd = at::empty(rstd_shape(self, gamma), x.options().dtype(at::kFloat));
+    const int rc = qk_rms_norm(x.data_ptr(), qk_dtype_of(x.scalar_type()), g.data_ptr(), x.numel() / D, D,
+                               (float)epsilon, y.data_ptr(), rstd.data_ptr<float>(), current_stream(x));
+    check_rc(rc, "npu_rms_norm");
+    return {y, rstd};
+}
+
+std::tuple<at::Tensor, at::Tensor> npu_rms_norm_meta(const at::Tensor& self, const at::Tensor& gamma, double) {
+    rms_norm_check("npu_rms_norm", self, gamma, false);
+    return {at::empty(self.sizes(), self.options()), at::empty(rstd_shape(self, gamma), self.options().dtype(at::kFloat))};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> rms_norm_quant_outputs(const at::Tensor& self, const at::Tensor& gamma) {
+    auto q = at::empty(self.sizes(), self.options().dtype(at::kChar));
+    auto s = at::empty(self.sizes().slice(0, self.dim() - 1), self.options().dtype(at::kFloat));
+    auto rstd = at::empty(rstd_shape(self, gamma), self.options().dtype(at::kFloat));
+    return {q, s, rstd};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> npu_rms_norm_dynamic_quant(const at::Tensor& self,
+                                                                          const at::Tensor& gamma, double epsilon) {
+    const char* op = "npu_rms_norm_dynamic_quant";
+    const int64_t D = rms_norm_check(op, self, gamma, true);
+    const c10::DeviceGuard guard(self.device());
+    auto x = self.contiguous();
+    auto g = gamma.contiguous();
+    auto [q, s, rstd] = rms_norm_quant_outputs(x, gamma);
+    const int rc = qk_rms_norm_quant(x.data_ptr(), qk_dtype_of(x.scalar_type()), g.data_ptr(), x.numel() / D, D,
+                                     (float)epsilon, q.data_ptr<int8_t>(), s.data_ptr<float>(), rstd.data_ptr<float>(),
+                                     current_stream(x));
+    check_rc(rc, op);
+    return {q, s, rstd};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> npu_rms_norm_dynamic_quant_meta(const at::Tensor& self,
+                                                                               const at::Tensor& gamma, double) {
+    rms_norm_check("npu_rms_norm_dynamic_quant", self, gamma, true);
+    return rms_norm_quant_outputs(self, gamma);
+}
+
+// ---------------------------------------------------------------- npu_swiglu (+ dynamic quant)
+
+int64_t swiglu_check(const char* op, const at::Tensor& self, int64_t dim) {
+    TORCH_CHECK(self.scalar_type() == at::kHalf || self.scalar_type() == at::kBFloat16, op,
+                ": self must be float16 or bfloat16, got ", self.scalar_type());
+    TORCH_CHECK(self.dim() >= 1, op, ": self must have at least one dimension");
+    TORCH_CHECK(dim == -1 || dim == self.dim() - 1, op, ": only the last dimension can be split (dim=", dim, ")");
+    TORCH_CHECK(self.size(-1) % 2 == 0, op, ": the split dimension must be even, got ", self.size(-1));
+    return self.size(-1) / 2;
+}
+
+std::vector<int64_t> half_last(const at::Tensor& self) {
+    std::vector<int64_t> sh(self.sizes().begin(), self.sizes().end());
+    sh.back() /= 2;
+    return sh;
+}
+
+at::Tensor npu_swiglu(const at::Tensor& self, int64_t dim) {
+    const int64_t I = swiglu_check("npu_swiglu", self, dim);
+    const c10::DeviceGuard guard(self.device());
+    auto h = self.contiguous();
+    auto y = at::empty(half_last(h), h.options());
+    const int64_t rows = I == 0 ? 0 : h.numel() / (2 * I);
+    const int rc = qk_swiglu(h.data_ptr(), qk_dtype_of(h.scalar_type()), rows, I, y.data_ptr(), current_stream(h));
+    check_rc(rc, "npu_swiglu");
+    return y;
+}
+
+at::Tensor npu_swiglu_meta(const at::Tensor& self, int64_t dim) {
+    swiglu_check("npu_swiglu", self, dim);
+    return at::empty(half_last(self), self.options());
+}
+
+std::tuple<at::Tensor, at::Tensor> npu_swiglu_dynamic_quant(const at::Tensor& self, int64_t dim) {
+    const char* op = "npu_swiglu_dynamic_quant";
+    const int64_t I = swiglu_check(op, self, dim);
+    TORCH_CHECK(I > 0, op, ": the split dimension must not be empty");
+    const c10::DeviceGuard guard(self.device());
+    auto h = self.contiguous();
+    auto q = at::empty(half_last(h), h.options().dtype(at::kChar));
+    auto s = at::empty(h.sizes().slice(0, h.dim() - 1), h.options().dtype(at::kFloat));
+    const int rc = qk_swiglu_quant(h.data_ptr(), qk_dtype_of(h.scalar_type()), h.numel() / (2 * I), I,
+                                   q.data_ptr<int8_t>(), s.data_ptr<float>(), current_stream(h));
+    check_rc(rc, op);
+    return {q, s};
+}
+
+std::tuple<at::Tensor, at::Tensor> npu_swiglu_dynamic_quant_meta(const at::Tensor& self, int64_t dim) {
+    const int64_t I = swiglu_check("npu_swiglu_dynamic_quant", self, dim);
+    TORCH_CHECK(I > 0, "npu_swiglu_dynamic_quant: the split dimension must not be empty");
+    return {at::empty(half_last(self), self.options().dtype(at::kChar)),
+            at::empty(self.sizes().slice(0, self.dim() - 1), self.options().dtype(at::kFloat))};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(npu, m) {
@@ -319,6 +446,12 @@ TORCH_LIBRARY(npu, m) {
         "npu_weight_quant_batchmatmul(Tensor x, Tensor weight, Tensor antiquant_scale, Tensor? antiquant_offset=None, "
         "Tensor? quant_scale=None, Tensor? quant_offset=None, Tensor? bias=None, int antiquant_group_size=0) -> Tensor");
     m.def("npu_convert_weight_to_int4pack(Tensor weight, int inner_k_tiles=0) -> Tensor");
+    // schema as op_plugin/config/v2r2/op_plugin_functions.yaml:2047
+    m.def("npu_rms_norm(Tensor self, Tensor gamma, float epsilon=1e-06) -> (Tensor, Tensor)");
+    m.def("npu_swiglu(Tensor self, int dim=-1) -> Tensor");
+    // fusions of this build for the quantized MLP block (no reference op): (q, scale, rstd) and (q, scale)
+    m.def("npu_rms_norm_dynamic_quant(Tensor self, Tensor gamma, float epsilon=1e-06) -> (Tensor, Tensor, Tensor)");
+    m.def("npu_swiglu_dynamic_quant(Tensor self, int dim=-1) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(npu, CUDA, m) {
@@ -326,6 +459,10 @@ TORCH_LIBRARY_IMPL(npu, CUDA, m) {
     m.impl("npu_quant_matmul", &npu_quant_matmul);
     m.impl("npu_weight_quant_batchmatmul", &npu_weight_quant_batchmatmul);
     m.impl("npu_convert_weight_to_int4pack", &npu_convert_weight_to_int4pack);
+    m.impl("npu_rms_norm", &npu_rms_norm);
+    m.impl("npu_swiglu", &npu_swiglu);
+    m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant);
+    m.impl("npu_swiglu_dynamic_quant", &npu_swiglu_dynamic_quant);
 }
 
 TORCH_LIBRARY_IMPL(npu, Meta, m) {
@@ -333,4 +470,8 @@ TORCH_LIBRARY_IMPL(npu, Meta, m) {
     m.impl("npu_quant_matmul", &npu_quant_matmul_meta);
     m.impl("npu_weight_quant_batchmatmul", &npu_weight_quant_batchmatmul_meta);
     m.impl("npu_convert_weight_to_int4pack", &npu_convert_weight_to_int4pack_meta);
+    m.impl("npu_rms_norm", &npu_rms_norm_meta);
+    m.impl("npu_swiglu", &npu_swiglu_meta);
+    m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant_meta);
+    m.impl("npu_swiglu_dynamic_quant", &npu_swiglu_dynamic_quant_meta);
 }

@@ -184,4 +184,59 @@ int qk_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* pack
     return launched(qk::launch_int4_pack(w, w_dtype, K, N, packed, (hipStream_t)stream), op);
 }
 
+static int rms_common(const char* op, const void* x, int x_dtype, const void* gamma, int64_t rows, int64_t D,
+                      float eps, const void* out) {
+    if (!is_half(x_dtype)) return fail(QK_ERR_ARG, "%s: x must be float16 or bfloat16 (got dtype %d)", op, x_dtype);
+    if (rows < 0 || D <= 0) return fail(QK_ERR_ARG, "%s: need rows >= 0 and D > 0 (rows=%lld D=%lld)", op, (long long)rows, (long long)D);
+    if (!(eps >= 0.0f)) return fail(QK_ERR_ARG, "%s: epsilon must be >= 0", op);
+    if (rows > 0 && (!x || !gamma || !out)) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    if (rows >= kMaxGrid) return fail(QK_ERR_UNSUPPORTED, "%s: %lld rows exceed the launch limit", op, (long long)rows);
+    return QK_OK;
+}
+
+int qk_rms_norm(const void* x, int x_dtype, const void* gamma, int64_t rows, int64_t D, float eps, void* y,
+                float* rstd, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_rms_norm";
+    if (int rc = rms_common(op, x, x_dtype, gamma, rows, D, eps, y)) return rc;
+    if (rows == 0) return QK_OK;
+    return launched(qk::launch_rms_norm(x, x_dtype, gamma, rows, D, eps, y, nullptr, nullptr, rstd, (hipStream_t)stream), op);
+}
+
+int qk_rms_norm_quant(const void* x, int x_dtype, const void* gamma, int64_t rows, int64_t D, float eps, int8_t* q,
+                      float* scale, float* rstd, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_rms_norm_dynamic_quant";
+    if (int rc = rms_common(op, x, x_dtype, gamma, rows, D, eps, q)) return rc;
+    if (rows == 0) return QK_OK;
+    if (!scale) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    return launched(qk::launch_rms_norm(x, x_dtype, gamma, rows, D, eps, nullptr, q, scale, rstd, (hipStream_t)stream), op);
+}
+
+static int swiglu_common(const char* op, const void* h, int dtype, int64_t rows, int64_t I, const void* out) {
+    if (!is_half(dtype)) return fail(QK_ERR_ARG, "%s: input must be float16 or bfloat16 (got dtype %d)", op, dtype);
+    if (rows < 0 || I < 0) return fail(QK_ERR_ARG, "%s: negative size rows=%lld I=%lld", op, (long long)rows, (long long)I);
+    if (rows > 0 && I > 0 && (!h || !out)) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    if (rows >= kMaxGrid) return fail(QK_ERR_UNSUPPORTED, "%s: %lld rows exceed the launch limit", op, (long long)rows);
+    return QK_OK;
+}
+
+int qk_swiglu(const void* h, int dtype, int64_t rows, int64_t I, void* y, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_swiglu";
+    if (int rc = swiglu_common(op, h, dtype, rows, I, y)) return rc;
+    if (rows == 0 || I == 0) return QK_OK;
+    return launched(qk::launch_swiglu(h, dtype, rows, I, y, nullptr, nullptr, (hipStream_t)stream), op);
+}
+
+int qk_swiglu_quant(const void* h, int dtype, int64_t rows, int64_t I, int8_t* q, float* scale, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_swiglu_dynamic_quant";
+    if (int rc = swiglu_common(op, h, dtype, rows, I, q)) return rc;
+    if (rows == 0) return QK_OK;
+    if (!scale) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    if (I == 0) return fail(QK_ERR_ARG, "%s: empty rows have no scale", op);
+    return launched(qk::launch_swiglu(h, dtype, rows, I, nullptr, q, scale, (hipStream_t)stream), op);
+}
+
 }  // extern "C"

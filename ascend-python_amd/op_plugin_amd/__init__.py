@@ -9,6 +9,11 @@ Importing this package loads ``_npu_ops.so``, which registers
   antiquant_offset=None, quant_scale=None, quant_offset=None, bias=None,
   antiquant_group_size=0) -> Tensor``  (W4A16 / W8A16)
 * ``torch.ops.npu.npu_convert_weight_to_int4pack(weight, inner_k_tiles=0) -> Tensor``
+* ``torch.ops.npu.npu_rms_norm(self, gamma, epsilon=1e-6) -> (y, fp32 rstd)``
+* ``torch.ops.npu.npu_swiglu(self, dim=-1) -> Tensor``
+* ``torch.ops.npu.npu_rms_norm_dynamic_quant(self, gamma, epsilon=1e-6) -> (int8 q, fp32 scale, fp32 rstd)``
+  and ``torch.ops.npu.npu_swiglu_dynamic_quant(self, dim=-1) -> (int8 q, fp32 scale)``: RMSNorm / SwiGLU
+  fused with npu_dynamic_quant of their 16-bit output (bit-identical to the unfused chain)
 
 and exposes the same callables here, so code written as
 ``torch_npu.npu_quant_matmul(...)`` runs as ``op_plugin_amd.npu_quant_matmul(...)``
@@ -41,6 +46,10 @@ npu_dynamic_quant = torch.ops.npu.npu_dynamic_quant
 npu_quant_matmul = torch.ops.npu.npu_quant_matmul
 npu_weight_quant_batchmatmul = torch.ops.npu.npu_weight_quant_batchmatmul
 npu_convert_weight_to_int4pack = torch.ops.npu.npu_convert_weight_to_int4pack
+npu_rms_norm = torch.ops.npu.npu_rms_norm
+npu_swiglu = torch.ops.npu.npu_swiglu
+npu_rms_norm_dynamic_quant = torch.ops.npu.npu_rms_norm_dynamic_quant
+npu_swiglu_dynamic_quant = torch.ops.npu.npu_swiglu_dynamic_quant
 
 # qk_abi.h constants
 QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32 = 1, 2, 3, 4, 5
@@ -49,6 +58,7 @@ QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, 
 ABI_SYMBOLS = (
     "qk_last_error", "qk_abi_version", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",
     "qk_quant_matmul", "qk_weight_quant_bmm_workspace_size", "qk_weight_quant_bmm", "qk_int4_pack",
+    "qk_rms_norm", "qk_rms_norm_quant", "qk_swiglu", "qk_swiglu_quant",
 )
 
 _abi = None
@@ -69,6 +79,11 @@ def abi() -> ctypes.CDLL:
         L.qk_weight_quant_bmm_workspace_size.argtypes = [I64, I64, I64, I, I64, ctypes.POINTER(SZ)]
         L.qk_weight_quant_bmm.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P, SZ, P]
         L.qk_int4_pack.argtypes = [P, I, I64, I64, P, P]
+        F = ctypes.c_float
+        L.qk_rms_norm.argtypes = [P, I, P, I64, I64, F, P, P, P]
+        L.qk_rms_norm_quant.argtypes = [P, I, P, I64, I64, F, P, P, P, P]
+        L.qk_swiglu.argtypes = [P, I, I64, I64, P, P]
+        L.qk_swiglu_quant.argtypes = [P, I, I64, I64, P, P, P]
         for name in ABI_SYMBOLS:
             getattr(L, name).restype = I if name != "qk_last_error" else ctypes.c_char_p
         _abi = L
@@ -81,5 +96,6 @@ def last_error() -> str:
 
 __all__ = [
     "npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
-    "npu_convert_weight_to_int4pack", "abi", "last_error", "LIB_PATH", "OPS_PATH",
+    "npu_convert_weight_to_int4pack", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
+    "npu_swiglu_dynamic_quant", "abi", "last_error", "LIB_PATH", "OPS_PATH",
 ]

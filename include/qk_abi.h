@@ -143,6 +143,43 @@ int qk_weight_quant_bmm(const void* x, int x_dtype,
 int qk_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed,
                  qk_stream_t stream);
 
+/*
+ * npu_rms_norm -- replaces aclnnRmsNorm behind EXEC_NPU_CMD
+ * (op_plugin/ops/base_ops/opapi/RmsNormKernelOpApi.cpp:24-35: y has the dtype
+ * of x, :31; rstd is fp32, :32; schema op_plugin/config/v2r2/op_plugin_functions.yaml:2047).
+ * x: [rows, D] fp16/bf16.  gamma: [D], same dtype.  y: [rows, D], x's dtype.
+ * rstd: [rows] fp32 or NULL.  rstd = 1/sqrt(mean(x^2) + eps); y = x * rstd * gamma
+ * (golden test/test_custom_ops/test_npu_rms_norm.py:10-17), fp32 arithmetic.
+ */
+int qk_rms_norm(const void* x, int x_dtype, const void* gamma, int64_t rows, int64_t D, float eps,
+                void* y, float* rstd, qk_stream_t stream);
+
+/*
+ * RMSNorm followed by npu_dynamic_quant of its 16-bit output, in one pass
+ * (the first two steps of the quantized MLP block).  No single reference op:
+ * the unfused chain is qk_rms_norm then qk_dynamic_quant, and q / scale are
+ * bit-identical to it.  q: [rows, D] int8.  scale: [rows] fp32.  rstd as above.
+ */
+int qk_rms_norm_quant(const void* x, int x_dtype, const void* gamma, int64_t rows, int64_t D, float eps,
+                      int8_t* q, float* scale, float* rstd, qk_stream_t stream);
+
+/*
+ * npu_swiglu (dim = -1) -- silu(a) * b with a, b = h.chunk(2, -1), the first
+ * half the gate; the gated halving follows npu_geglu
+ * (op_plugin/ops/v1r11/opapi/GeGluKernelNpuOpApi.cpp:23-40), silu follows
+ * op_plugin/ops/base_ops/opapi/SiluKernelNpuOpApi.cpp:22-43.
+ * h: [rows, 2*I] fp16/bf16.  y: [rows, I], same dtype.  fp32 arithmetic.
+ */
+int qk_swiglu(const void* h, int dtype, int64_t rows, int64_t I, void* y, qk_stream_t stream);
+
+/*
+ * SwiGLU followed by npu_dynamic_quant of its 16-bit output, in one pass (the
+ * activation step of the quantized MLP block); bit-identical to qk_swiglu then
+ * qk_dynamic_quant.  q: [rows, I] int8.  scale: [rows] fp32.
+ */
+int qk_swiglu_quant(const void* h, int dtype, int64_t rows, int64_t I, int8_t* q, float* scale,
+                    qk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

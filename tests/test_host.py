@@ -59,6 +59,16 @@ def test_abi_refuses_bad_arguments_without_launch():
     ws = ctypes.c_size_t(123)
     assert L.qk_weight_quant_bmm_workspace_size(16, 11008, 4096, I32, 128, ctypes.byref(ws)) == 0
     assert L.qk_int4_pack(fake, I8, 4, 12, fake, None) == q.QK_ERR_ARG
+    assert L.qk_rms_norm(fake, 9, fake, 4, 64, 1e-6, fake, None, None) == q.QK_ERR_ARG
+    assert "float16 or bfloat16" in q.last_error()
+    assert L.qk_rms_norm(fake, BF16, fake, 4, 0, 1e-6, fake, None, None) == q.QK_ERR_ARG and "D > 0" in q.last_error()
+    assert L.qk_rms_norm(fake, BF16, fake, 4, 64, -1.0, fake, None, None) == q.QK_ERR_ARG
+    assert L.qk_rms_norm(None, BF16, fake, 4, 64, 1e-6, fake, None, None) == q.QK_ERR_ARG
+    assert L.qk_rms_norm(None, BF16, None, 0, 64, 1e-6, None, None, None) == q.QK_OK
+    assert L.qk_rms_norm_quant(fake, BF16, fake, 4, 64, 1e-6, fake, None, None, None) == q.QK_ERR_ARG
+    assert L.qk_swiglu(fake, F16, -1, 8, fake, None) == q.QK_ERR_ARG
+    assert L.qk_swiglu(None, F16, 3, 8, None, None) == q.QK_ERR_ARG and "null pointer" in q.last_error()
+    assert L.qk_swiglu_quant(fake, BF16, 3, 0, fake, fake, None) == q.QK_ERR_ARG and "empty" in q.last_error()
 
 
 def _m(shape, dtype):
@@ -67,7 +77,8 @@ def _m(shape, dtype):
 
 def test_schemas_registered():
     for name in ("npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
-                 "npu_convert_weight_to_int4pack"):
+                 "npu_convert_weight_to_int4pack", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
+                 "npu_swiglu_dynamic_quant"):
         assert hasattr(torch.ops.npu, name)
     s = str(torch.ops.npu.npu_quant_matmul.default._schema)
     assert "pertoken_scale" in s and "ScalarType? output_dtype" in s
@@ -87,6 +98,16 @@ def test_meta_shapes():
                                          antiquant_group_size=128)
     assert out.shape == (16, 11008) and out.dtype == torch.bfloat16
     assert q.npu_convert_weight_to_int4pack(_m((64, 96), torch.int32)).shape == (64, 12)
+    y, rstd = q.npu_rms_norm(_m((2, 7, 4096), torch.bfloat16), _m((4096,), torch.bfloat16))
+    assert y.shape == (2, 7, 4096) and y.dtype == torch.bfloat16 and rstd.shape == (2, 7, 1) \
+        and rstd.dtype == torch.float32
+    y, rstd = q.npu_rms_norm(_m((3, 4, 8), torch.float16), _m((4, 8), torch.float16))   # 2-D gamma
+    assert y.shape == (3, 4, 8) and rstd.shape == (3, 1, 1)
+    qq, sc, rstd = q.npu_rms_norm_dynamic_quant(_m((512, 4096), torch.bfloat16), _m((4096,), torch.bfloat16))
+    assert qq.dtype == torch.int8 and qq.shape == (512, 4096) and sc.shape == (512,) and rstd.shape == (512, 1)
+    assert q.npu_swiglu(_m((512, 28672), torch.bfloat16)).shape == (512, 14336)
+    qq, sc = q.npu_swiglu_dynamic_quant(_m((2, 5, 64), torch.float16), dim=2)
+    assert qq.shape == (2, 5, 32) and qq.dtype == torch.int8 and sc.shape == (2, 5)
 
 
 @pytest.mark.parametrize("call,msg", [
@@ -108,6 +129,12 @@ def test_meta_shapes():
                                             _m((1, 16), torch.float16), quant_scale=_m((16,), torch.float32),
                                             antiquant_group_size=128), "not supported"),
     (lambda: q.npu_convert_weight_to_int4pack(_m((4, 12), torch.int32)), "multiple of 8"),
+    (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((64,), torch.float16)), "dtype of self"),
+    (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((32,), torch.bfloat16)), "trailing dims"),
+    (lambda: q.npu_rms_norm_dynamic_quant(_m((4, 8, 8), torch.bfloat16), _m((8, 8), torch.bfloat16)), "1-D gamma"),
+    (lambda: q.npu_swiglu(_m((4, 63), torch.bfloat16)), "even"),
+    (lambda: q.npu_swiglu(_m((4, 64), torch.bfloat16), dim=0), "last dimension"),
+    (lambda: q.npu_swiglu(_m((4, 64), torch.float32)), "float16 or bfloat16"),
 ])
 def test_meta_errors(call, msg):
     with pytest.raises(RuntimeError, match=msg):
