@@ -249,8 +249,12 @@ __device__ __forceinline__ void store_elem(void* out, int64_t o, int32_t acc, fl
 // FULL: every tile is inside M, N and K is a multiple of BK, so loads need no
 // predicates and use one 32-bit per-lane offset from a uniform base (no 64-bit
 // address registers live across the loop).
+// nsplit > 1 (FULL only): workgroup bid/tiles takes the K range
+// [split * K/nsplit, (split+1) * K/nsplit) and writes its exact int32 sums to
+// partial[split][M][N]; qmm_reduce adds the splits and applies the epilogue.
 template <bool B_KN, int OUT, int NW, bool FULL>
-__global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int tiles_n) {
+__global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int tiles_n, int nsplit,
+                                                   int32_t* __restrict__ partial) {
     using namespace big;
     constexpr int NT = 64 * NW;              // threads
     constexpr int WMR = BM / (NW / 2);       // wave tile rows
@@ -258,8 +262,13 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
     constexpr int NLD = BM * CPR / NT;       // 16-byte loads per thread per operand per stage
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * STAGE];
 
-    // XCD-aware renumbering + grouped tile order
-    const int bid = xcd_swizzle(blockIdx.x, tiles_m * tiles_n);
+    // XCD-aware renumbering + grouped tile order (splits outermost)
+    const int tiles = tiles_m * tiles_n;
+    const int bid_all = xcd_swizzle(blockIdx.x, tiles * nsplit);
+    const int split = bid_all / tiles;
+    const int bid = bid_all - split * tiles;
+    const int64_t k_len = p.K / nsplit;
+    const int64_t k_base = (int64_t)split * k_len;
     constexpr int GM = 8;
     const int per_group = GM * tiles_n;
     const int grp = bid / per_group;
@@ -281,6 +290,7 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
     const uint32_t b_lane = B_KN ? (uint32_t)(tid >> 4) * (uint32_t)p.sbk + 16u * (uint32_t)(tid & 15)
                                  : (uint32_t)(tid / CPR) * (uint32_t)p.sbn + 16u * (uint32_t)(tid % CPR);
     auto gload = [&](int64_t k0) {
+        k0 += k_base;
         if constexpr (FULL) {
 #pragma unroll
             for (int i = 0; i < NLD; ++i) {
@@ -334,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
     const int tr_k = 16 * g + (fr >> 1);
     const int tr_base = kn_off(tr_k, 0) + 8 * (fr & 1);
 
-    const int64_t nk = (p.K + big::BK - 1) / big::BK;
+    const int64_t nk = (k_len + big::BK - 1) / big::BK;
     gload(0);
     lstore(0);
     if (nk > 1) gload(big::BK);
@@ -390,6 +400,19 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
             frags(1, af1, bf1);
             mma(af1, bf1);
         }
+    }
+
+    if (FULL && nsplit > 1) {  // exact int32 partial sums of this K range
+        int32_t* dst = partial + (int64_t)split * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t ro = (m0 + wm * WMR + 16 * i + 4 * g + r) * p.N + n0 + wn * 128 + fr;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[ro + 16 * j] = acc[i][j][r];
+            }
+        return;
     }
 
     // ---- epilogue: per-column and per-row operands loaded once per lane
@@ -597,6 +620,33 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
 // Exact int32 sum of the split partials, then the common epilogue.
 __global__ __launch_bounds__(kThreads) void qmm_reduce(QmmArgs p, int nsplit, const int32_t* __restrict__ partial) {
     const int64_t total = p.M * p.N;
+    if (p.N % 4 == 0) {  // 4 outputs of one row per thread, every split's 16-byte load in flight together
+        const int64_t total4 = total >> 2;
+        const i32x4* src = reinterpret_cast<const i32x4*>(partial);
+        for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total4;
+             idx += (int64_t)gridDim.x * kThreads) {
+            i32x4 part[16];
+            const int ns = nsplit < 16 ? nsplit : 16;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (k < ns) part[k] = src[(int64_t)k * total4 + idx];
+            uint32_t s[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (k < ns)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) s[t] += (uint32_t)part[k][t];
+            for (int k = 16; k < nsplit; ++k) {
+                const i32x4 v = src[(int64_t)k * total4 + idx];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) s[t] += (uint32_t)v[t];
+            }
+            const int64_t o = idx * 4, m = o / p.N, n = o % p.N;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qmm_store(p.epi, m, n + t, (int32_t)s[t]);
+        }
+        return;
+    }
     for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * kThreads) {
         uint32_t s = 0;
@@ -634,27 +684,58 @@ hipError_t launch_by_m(const QmmArgs& p, hipStream_t stream) {
 }
 
 template <int OUT>
-hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, hipStream_t stream) {
-    const dim3 grid((uint32_t)(tiles_m * tiles_n));
+hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, int nsplit, int32_t* partial,
+                      hipStream_t stream) {
+    const dim3 grid((uint32_t)(tiles_m * tiles_n * nsplit));
     static const int waves = [] {
         const char* e = std::getenv("QK_QMM_WAVES");  // tuning override (debug)
         return (e && std::atoi(e) == 4) ? 4 : 8;
     }();
     // full tiles and 32-bit per-lane offsets (the 64-bit bases stay uniform)
-    const bool full = p.M % big::BM == 0 && p.N % big::BN == 0 && p.K % big::BK == 0 &&
+    const bool full = p.M % big::BM == 0 && p.N % big::BN == 0 && p.K % (big::BK * nsplit) == 0 &&
                       p.lda < (1 << 24) && p.sbk < (1 << 24) && p.sbn < (1 << 24) &&
                       (uintptr_t)p.epi.out % 16 == 0 && p.epi.ldo % 8 == 0;
-    if (waves == 4) {
-        if (b_kn) qmm_big<true, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n);
-        else qmm_big<false, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n);
+    if (nsplit > 1 && !full) return hipErrorInvalidValue;  // the plan only splits whole tiles
+    if (waves == 4 && nsplit == 1) {
+        if (b_kn) qmm_big<true, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n, 1, partial);
+        else qmm_big<false, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n, 1, partial);
     } else if (full) {
-        if (b_kn) qmm_big<true, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n);
-        else qmm_big<false, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n);
+        if (b_kn) qmm_big<true, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
+        else qmm_big<false, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
     } else {
-        if (b_kn) qmm_big<true, OUT, 8, false><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n);
-        else qmm_big<false, OUT, 8, false><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n);
+        if (b_kn) qmm_big<true, OUT, 8, false><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, 1, partial);
+        else qmm_big<false, OUT, 8, false><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, 1, partial);
     }
     return hipGetLastError();
+}
+
+// 256x256 tiles: enough of them (192 fill three quarters of the CUs) run as
+// they are; fewer whole tiles get a power-of-two K split (K/nsplit a multiple
+// of 128 and at least 512) until about 192 workgroups run, when the int32
+// partials stay within 512 MB.  From sizes only, so the workspace query and
+// the launch agree.
+struct BigPlan {
+    bool ok = false;
+    int tiles_m = 0, tiles_n = 0, nsplit = 1;
+};
+
+BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
+    BigPlan b;
+    const int64_t tm = (M + big::BM - 1) / big::BM, tn = (N + big::BN - 1) / big::BN;
+    if (K <= 0 || tm * tn >= (1 << 30)) return b;
+    b.tiles_m = (int)tm;
+    b.tiles_n = (int)tn;
+    if (tm * tn >= 192) {
+        b.ok = true;
+        return b;
+    }
+    if (M % big::BM != 0 || N % big::BN != 0 || K % big::BK != 0) return b;
+    int ns = 1;
+    while (tm * tn * ns < 192 && ns < 16 && K % ((int64_t)ns * 2 * big::BK) == 0 && K / (ns * 2) >= 512) ns *= 2;
+    if (ns == 1 || tm * tn * ns < 64 || (int64_t)ns * M * N * 4 > ((int64_t)512 << 20)) return b;
+    b.nsplit = ns;
+    b.ok = true;
+    return b;
 }
 
 }  // namespace
@@ -711,8 +792,10 @@ hipError_t launch_skinny(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial
 
 size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K) {
     const SkinnyPlan s = skinny_plan(M, N, K);
-    if (s.mt == 0 || s.nsplit == 1) return 0;
-    return (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
+    if (s.mt != 0) return s.nsplit == 1 ? 0 : (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
+    const BigPlan b = big_plan(M, N, K);
+    if (b.ok && b.nsplit > 1) return (size_t)b.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
+    return 0;
 }
 
 hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_bytes, hipStream_t stream) {
@@ -728,16 +811,31 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
         int32_t* partial = static_cast<int32_t*>(workspace);
         return b_kn16 ? launch_skinny<true>(p, sp, partial, stream) : launch_skinny<false>(p, sp, partial, stream);
     }
-    const int64_t tiles_m = (p.M + big::BM - 1) / big::BM, tiles_n = (p.N + big::BN - 1) / big::BN;
-    const bool big_ok = p.K > 0 && a_ok && tiles_m * tiles_n >= 256 && tiles_m * tiles_n < (1 << 30) &&
-                        (b_nk || (b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0));
-    if (big_ok) {
+    const BigPlan bp = big_plan(p.M, p.N, p.K);
+    bool big_ok = bp.ok && a_ok && (b_nk || (b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0));
+    int32_t* partial = static_cast<int32_t*>(workspace);
+    if (big_ok && bp.nsplit > 1) {
+        // splits need whole aligned tiles and the workspace; otherwise the tiled kernels take the shape
+        const size_t need = (size_t)bp.nsplit * p.M * p.N * sizeof(int32_t);
+        big_ok = p.lda < (1 << 24) && p.sbk < (1 << 24) && p.sbn < (1 << 24) && partial && ws_bytes >= need &&
+                 (uintptr_t)partial % 16 == 0;
+        if (big_ok) {
+            const hipError_t e = b_kn ? launch_big<QK_I32>(p, true, bp.tiles_m, bp.tiles_n, bp.nsplit, partial, stream)
+                                      : launch_big<QK_I32>(p, false, bp.tiles_m, bp.tiles_n, bp.nsplit, partial, stream);
+            if (e != hipSuccess) return e;
+            int64_t blocks = (p.M * p.N / 4 + kThreads - 1) / kThreads;
+            if (blocks > 65536) blocks = 65536;
+            qmm_reduce<<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(p, bp.nsplit, partial);
+            return hipGetLastError();
+        }
+    } else if (big_ok) {
+        const int tm = bp.tiles_m, tn = bp.tiles_n;
         switch (p.epi.out_dtype) {
-        case QK_BF16: return launch_big<QK_BF16>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
-        case QK_F16: return launch_big<QK_F16>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
-        case QK_F32: return launch_big<QK_F32>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
-        case QK_I8: return launch_big<QK_I8>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
-        default: return launch_big<QK_I32>(p, b_kn, (int)tiles_m, (int)tiles_n, stream);
+        case QK_BF16: return launch_big<QK_BF16>(p, b_kn, tm, tn, 1, nullptr, stream);
+        case QK_F16: return launch_big<QK_F16>(p, b_kn, tm, tn, 1, nullptr, stream);
+        case QK_F32: return launch_big<QK_F32>(p, b_kn, tm, tn, 1, nullptr, stream);
+        case QK_I8: return launch_big<QK_I8>(p, b_kn, tm, tn, 1, nullptr, stream);
+        default: return launch_big<QK_I32>(p, b_kn, tm, tn, 1, nullptr, stream);
         }
     }
     if (p.K > 0 && a_ok && b_kn) return launch_by_m<true>(p, stream);

@@ -177,6 +177,36 @@ def test_quant_matmul_cfg4_prefill(ops, oracle):
     assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
 
 
+@pytest.mark.parametrize("M,N,K,kn", [
+    (512, 28672, 4096, True),    # cfg5 gate_up: 224 tiles of 256x256, no split
+    (512, 4096, 14336, True),    # cfg5 down: 32 tiles, K split 8 ways (int32 partials + in-order reduce)
+    (512, 4096, 14336, False),   # the same through an [N, K] weight view
+    (512, 1024, 8192, True),     # 8 tiles, K split 16 ways
+])
+def test_quant_matmul_big_tiles_and_split_k(ops, oracle, M, N, K, kn):
+    """Every int32 accumulator through exact row and column checksums; a row subset of the bf16
+    output (per-token and per-channel scales, bf16 bias) bit-exact against the oracle."""
+    say(f"quant_matmul M={M} N={N} K={K} {'[K,N]' if kn else '[N,K] view'}")
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    wd = w.to(DEV) if kn else w.t().contiguous().to(DEV).t()
+    ad = a.to(DEV)
+    acc = ops.npu_quant_matmul(ad, wd, torch.ones(1, device=DEV), output_dtype=torch.int32)
+    a64, w64, acc64 = a.to(torch.int64), w.to(torch.int64), acc.cpu().to(torch.int64)
+    assert torch.equal(acc64.sum(0), a64.sum(0) @ w64)
+    assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
+    s = 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    pt = 1e-2 * torch.rand(M, generator=g)
+    b = torch.randn(N, generator=g).to(torch.bfloat16)
+    out = ops.npu_quant_matmul(ad, wd, s.to(DEV), pertoken_scale=pt.to(DEV), bias=b.to(DEV),
+                               output_dtype=torch.bfloat16)
+    rows = np.r_[0:8, M - 8:M]
+    ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(), pertoken=pt[rows].numpy(), bias=W.bits(b),
+                              bias_dtype=BF16, out_dtype=BF16)
+    assert np.array_equal(to_bits(out)[rows], ref)
+
+
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32, torch.int32])
 @pytest.mark.parametrize("per_tensor", [False, True])
