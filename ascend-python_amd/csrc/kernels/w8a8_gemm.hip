@@ -484,7 +484,7 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
 }
 
 // ---------------------------------------------------------------------------
-// Skinny kernel (decode, M <= 64): an HBM weight stream.  A workgroup owns
+// Skinny kernel (decode and small M <= 128): an HBM weight stream.  A workgroup owns
 // 16*MT rows x 256 columns and one K split; its 4 waves take 64 columns
 // each.  Stages of 128 k-rows go through LDS (the weight in its natural
 // layout, B fragments by ds_read_b64_tr_b8 for [K,N]) with the next stage's
@@ -746,20 +746,23 @@ struct SkinnyPlan {
     int mt = 0, nsplit = 1, tiles_n = 0, tiles_m = 0;
 };
 
-// Decode shapes (M <= 64, K a multiple of 128): row tiles, and K splits so
-// about 512 workgroups stream the weight while the int32 partials stay at
-// most 1/8 of the weight bytes.  Shared by the workspace query and the launch.
+// Decode and small-M shapes (M <= 128, K a multiple of 128): row tiles of
+// 16/32/64/128, and K splits so about 512 workgroups stream the weight.
+// Shared by the workspace query and the launch.
 SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
     SkinnyPlan s;
-    if (M <= 0 || M > 64 || K <= 0 || K % sk::BK != 0 || N <= 0) return s;
-    s.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    if (M <= 0 || M > 128 || K <= 0 || K % sk::BK != 0 || N <= 0) return s;
+    s.mt = M <= 16 ? 1 : (M <= 32 ? 2 : (M <= 64 ? 4 : 8));
     s.tiles_m = (int)((M + 16 * s.mt - 1) / (16 * s.mt));
     s.tiles_n = (int)((N + sk::BN - 1) / sk::BN);
     const int64_t base = (int64_t)s.tiles_m * s.tiles_n;
+    // split while short of ~512 workgroups, keeping the int32 partials (nsplit*M*N*4 bytes)
+    // within the weight's K*N bytes and every split at least 256 rows of K
     while (base * s.nsplit * 2 <= 512 && K % ((int64_t)s.nsplit * 2 * sk::BK) == 0 &&
-           (int64_t)s.nsplit * 2 * M * 32 <= K)
+           (int64_t)s.nsplit * 2 * M * 4 <= K && K / (s.nsplit * 2) >= 256)
         s.nsplit *= 2;
     if (base * s.nsplit >= ((int64_t)1 << 31)) s.mt = 0;
+    if (s.mt == 8 && s.nsplit == 1) s.mt = 0;  // 128-row tiles only as a split stream (their in-place epilogue is not unrolled)
     return s;
 }
 
@@ -784,7 +787,8 @@ hipError_t launch_skinny(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial
     switch (s.mt) {
     case 1: return launch_skinny_t<B_KN, 1>(p, s, partial, stream);
     case 2: return launch_skinny_t<B_KN, 2>(p, s, partial, stream);
-    default: return launch_skinny_t<B_KN, 4>(p, s, partial, stream);
+    case 4: return launch_skinny_t<B_KN, 4>(p, s, partial, stream);
+    default: return launch_skinny_t<B_KN, 8>(p, s, partial, stream);
     }
 }
 

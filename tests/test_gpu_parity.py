@@ -182,6 +182,8 @@ def test_quant_matmul_cfg4_prefill(ops, oracle):
     (512, 4096, 14336, True),    # cfg5 down: 32 tiles, K split 8 ways (int32 partials + in-order reduce)
     (512, 4096, 14336, False),   # the same through an [N, K] weight view
     (512, 1024, 8192, True),     # 8 tiles, K split 16 ways
+    (100, 2048, 4096, True),     # small M: 128-row stream tiles, K split
+    (128, 4096, 4096, False),    # cfg1 shape through an [N, K] weight view
 ])
 def test_quant_matmul_big_tiles_and_split_k(ops, oracle, M, N, K, kn):
     """Every int32 accumulator through exact row and column checksums; a row subset of the bf16
