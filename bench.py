@@ -11,6 +11,8 @@ the kernels run on, around each launch inside the timed region.
 
 Prints one JSON line.  `value` is the W8A8 GEMM throughput (TOPS, M=4096);
 the W4A16 decode GB/s (M=16) is the `secondary` entry; both carry a roofline.
+`other_configs` times the remaining BASELINE configs on their own (cfg1, cfg2 at
+M=1/4/16, cfg3 at M=2048, the cfg5 MLP block); they are reported, not the value.
 """
 from __future__ import annotations
 
@@ -43,6 +45,10 @@ def parse():
                     help="first run 5 plain 256 MiB device copies (the reference kernel for scaling "
                          "FETCH_SIZE / WRITE_SIZE counters in a rocprofv3 --pmc pass)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target length of the CPU baseline sample")
+    ap.add_argument("--no-configs", action="store_true", help="skip timing the other BASELINE configs")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="time only the other BASELINE configs (for a kernel trace of them alone)")
+    ap.add_argument("--config-reps", type=int, default=20, help="timed launches per other config")
     return ap.parse_args()
 
 
@@ -105,6 +111,88 @@ def cpu_baseline(target_s: float) -> dict:
             "cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
 
 
+def _timed(fn, reps: int, warm: int = 3) -> float:
+    """Mean seconds per call of fn(i), from events recorded on the current stream around each call."""
+    import torch
+    for i in range(warm):
+        fn(i)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    for i in range(reps):
+        ev[i][0].record()
+        fn(i)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) / reps * 1e-3
+
+
+def other_configs(q, W, dev, reps: int) -> dict:
+    """The remaining BASELINE configs, each timed on its own (kernel time per launch).
+
+    Weights rotate over enough operand sets to exceed the 256 MB Infinity Cache where the
+    shape is bandwidth-bound; operands come from seeded device generators."""
+    import torch
+    from op_plugin_amd.mlp import quant_mlp
+
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(7)
+
+    def i8(shape):
+        return torch.randint(-127, 128, shape, generator=g, device=dev, dtype=torch.int8)
+
+    def u(shape, lo, hi):
+        return lo + (hi - lo) * torch.rand(shape, generator=g, device=dev)
+
+    # cfg1: W8A8 M=128, K=N=4096 (dynamic quant + GEMM, bf16 out, bias)
+    c = W.CFG1
+    ws = [i8((c.K, c.N)) for _ in range(32)]
+    x = torch.randn((c.M, c.K), generator=g, device=dev).half()
+    xq, xs = q.npu_dynamic_quant(x)
+    sc, b = u((c.N,), 1e-3, 1e-2), (0.1 * torch.randn(c.N, generator=g, device=dev)).bfloat16()
+    t = _timed(lambda i: q.npu_quant_matmul(xq, ws[i % 32], sc, pertoken_scale=xs, bias=b,
+                                            output_dtype=torch.bfloat16), reps)
+    res["cfg1_w8a8_m128_k4096_n4096"] = {"avg_us": round(t * 1e6, 2), "TOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1),
+                                         "mfma_frac": round(2 * c.M * c.N * c.K / t / 1e12 / PEAK_I8_TOPS, 4)}
+    del ws
+
+    # cfg2: decode-shaped W8A8, K=8192, N=28672, M in {1,4,16}; W 235 MB per set, 3 sets
+    c0 = W.CFG2[0]
+    ws = [i8((c0.K, c0.N)) for _ in range(3)]
+    sc = u((c0.N,), 1e-3, 1e-2)
+    for c in W.CFG2:
+        x = torch.randn((c.M, c.K), generator=g, device=dev).half()
+        xq, xs = q.npu_dynamic_quant(x)
+        t = _timed(lambda i: q.npu_quant_matmul(xq, ws[i % 3], sc, pertoken_scale=xs, output_dtype=torch.bfloat16),
+                   reps)
+        nb = c.K * c.N + c.M * c.K + 4 * c.M + 4 * c.N + 2 * c.M * c.N
+        res[f"cfg2_w8a8_m{c.M}_k8192_n28672"] = {"avg_us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
+                                                 "hbm_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4)}
+    del ws
+
+    # cfg3 M=2048: W4A16 prefill, K=4096, N=11008, group 128, fp16 scale + offset
+    c = W.CFG3[1]
+    wp = torch.randint(-2**31, 2**31 - 1, (c.K, c.N // 8), generator=g, device=dev, dtype=torch.int32)
+    s = u((c.K // c.group, c.N), 5e-3, 2e-2).half()
+    o = u((c.K // c.group, c.N), -1.0, 1.0).half()
+    x = torch.randn((c.M, c.K), generator=g, device=dev).bfloat16()
+    t = _timed(lambda i: q.npu_weight_quant_batchmatmul(x, wp, s, o, antiquant_group_size=c.group), reps)
+    res["cfg3_w4a16_m2048_k4096_n11008"] = {"avg_us": round(t * 1e6, 2),
+                                            "TFLOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1),
+                                            "mfma_frac_bf16": round(2 * c.M * c.N * c.K / t / 1e12 / 2500.0, 4)}
+
+    # cfg5: quantized MLP block, 512 tokens, hidden 4096, intermediate 14336 (whole block)
+    T, H, I = W.CFG5["tokens"], W.CFG5["hidden"], W.CFG5["intermediate"]
+    x = torch.randn((T, H), generator=g, device=dev).bfloat16()
+    gamma = (1 + 0.02 * torch.randn(H, generator=g, device=dev)).bfloat16()
+    wgu, sgu = i8((H, 2 * I)), u((2 * I,), 1e-3, 1e-2)
+    wd, sd = i8((I, H)), u((H,), 1e-3, 1e-2)
+    t = _timed(lambda i: quant_mlp(x, gamma, wgu, sgu, wd, sd, eps=W.CFG5["eps"]), reps)
+    ops = 2 * T * H * 2 * I + 2 * T * I * H
+    res["cfg5_quant_mlp_t512_h4096_i14336"] = {"avg_us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 1),
+                                               "mfma_frac": round(ops / t / 1e12 / PEAK_I8_TOPS, 4)}
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -120,6 +208,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.configs_only:
+        print(json.dumps({"other_configs": other_configs(q, W, dev, args.config_reps)}), flush=True)
+        return
 
     # ---------------- cfg4 operands (set 0 = the seeded config inputs)
     c4 = W.CFG4
@@ -247,6 +338,8 @@ def main():
                           "hbm_frac": round(qbytes / q_s / 1e9 / PEAK_HBM_GBS, 4)},
         "parity": parity,
     }
+    if not args.no_configs:
+        line["other_configs"] = other_configs(q, W, dev, args.config_reps)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
