@@ -33,7 +33,12 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 }
 
 // fp32 -> fp16 with round-to-nearest-even (hardware conversion, default mode).
+// The empty asm pins f as a rounded fp32 value: without it the compiler folds
+// fmaf(a, b, c) followed by this cast into one v_fma_mixlo_f16, which rounds
+// once from the exact product-sum instead of first to fp32, and so differs by
+// an ulp from the fp32-then-fp16 rounding the ops specify.
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    asm volatile("" : "+v"(f));
     _Float16 h = (_Float16)f;
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }

@@ -244,6 +244,98 @@ __device__ __forceinline__ void store_elem(void* out, int64_t o, int32_t acc, fl
 }
 }  // namespace big
 
+// The end of a 256x256 tile: exact int32 partials of a K split (FULL only), or
+// the fused epilogue; FULL 16-bit tiles are staged through LDS (smem must
+// hold BM x (2*BN + 16) bytes) so the global stores are 16-byte and
+// row-contiguous.  acc[i][j] holds rows wm*WMR + 16i + 4(lane>>4) + r, column
+// wn*128 + 16j + (lane&15) of the tile (the MFMA 16x16 output layout).
+template <int OUT, int TM, int NT, bool FULL>
+__device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc)[TM][8], int8_t* smem, int64_t m0,
+                                             int64_t n0, int wm, int wn, int lane, int tid, int split, int nsplit,
+                                             int32_t* __restrict__ partial) {
+    using namespace big;
+    constexpr int WMR = 16 * TM;
+    const int fr = lane & 15, g = lane >> 4;
+    if (FULL && nsplit > 1) {  // exact int32 partial sums of this K range
+        int32_t* dst = partial + (int64_t)split * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t ro = (m0 + wm * WMR + 16 * i + 4 * g + r) * p.N + n0 + wn * 128 + fr;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[ro + 16 * j] = acc[i][j][r];
+            }
+        return;
+    }
+
+    // ---- epilogue: per-column and per-row operands loaded once per lane
+    const QmmEpilogue& e = p.epi;
+    float sc[8], bf[8], of[8];
+    int32_t bi[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t n = n0 + wn * 128 + 16 * j + fr;
+        const bool ok = n < p.N;
+        sc[j] = (ok && e.scale) ? e.scale[e.scale_per_ch ? n : 0] : 0.0f;
+        of[j] = (ok && e.offset) ? e.offset[e.offset_per_ch ? n : 0] : 0.0f;
+        bf[j] = 0.0f;
+        bi[j] = 0;
+        if (ok && e.bias_dtype == QK_I32) bi[j] = ((const int32_t*)e.bias)[n];
+        else if (ok && e.bias_dtype) bf[j] = load_scalar(e.bias, n, e.bias_dtype);
+    }
+    if constexpr (FULL && (OUT == QK_BF16 || OUT == QK_F16)) {
+        // 16-bit outputs of a full tile are staged through LDS (the operand
+        // stages are free now) so the global stores are whole 512-byte rows of
+        // 16 bytes per lane instead of 32-byte pieces of 4 rows.
+        constexpr int ROWB = 2 * BN + 16;  // padded LDS row (bytes)
+        __syncthreads();
+        uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = wm * WMR + 16 * i + 4 * g + r;
+                const float pt = e.pertoken ? e.pertoken[m0 + row] : 1.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int32_t a = (int32_t)((uint32_t)acc[i][j][r] + (uint32_t)bi[j]);
+                    const float v = __builtin_fmaf((float)a * pt, sc[j], bf[j]);
+                    ot[row * (ROWB / 2) + wn * 128 + 16 * j + fr] =
+                        (uint16_t)(OUT == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+                }
+            }
+        }
+        __syncthreads();
+        constexpr int CPRO = 2 * BN / 16;  // 16-byte chunks per output row
+#pragma unroll
+        for (int q = tid; q < BM * CPRO; q += NT) {
+            const int row = q / CPRO, c = q % CPRO;
+            const i32x4 v = *reinterpret_cast<const i32x4*>(smem + row * ROWB + 16 * c);
+            *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo + n0 + 8 * c) = v;
+        }
+        return;
+    }
+    // Fully unrolled with compile-time register indices (a runtime-indexed
+    // accumulator would be demoted to scratch and spilled every K step).
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = m0 + wm * WMR + 16 * i + 4 * g + r;
+            const bool row_ok = m < p.M;
+            // pertoken multiply by 1.0 is exact, so "no pertoken" needs no branch
+            const float pt = (e.pertoken && row_ok) ? e.pertoken[m] : 1.0f;
+            const int64_t ro = m * e.ldo + n0 + wn * 128 + fr;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool ok = row_ok && (n0 + wn * 128 + 16 * j + fr) < p.N;
+                if (ok) big::store_elem<OUT>(e.out, ro + 16 * j, acc[i][j][r], sc[j], bf[j], bi[j], pt, of[j]);
+            }
+        }
+    }
+}
+
 // NW = 4: 2x2 waves of 128x128 (one wave per SIMD); NW = 8: 4x2 waves of
 // 64x128 (two waves per SIMD, so one wave's MFMAs cover the other's waits).
 // FULL: every tile is inside M, N and K is a multiple of BK, so loads need no
@@ -261,6 +353,7 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
     constexpr int TM = WMR / 16;             // MFMA row tiles per wave
     constexpr int NLD = BM * CPR / NT;       // 16-byte loads per thread per operand per stage
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * STAGE];
+    static_assert(BM * (2 * BN + 16) <= 2 * STAGE, "output tile does not fit the LDS stages");
 
     // XCD-aware renumbering + grouped tile order (splits outermost)
     const int tiles = tiles_m * tiles_n;
@@ -402,85 +495,178 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
         }
     }
 
-    if (FULL && nsplit > 1) {  // exact int32 partial sums of this K range
-        int32_t* dst = partial + (int64_t)split * p.M * p.N;
+    big_epilogue<OUT, TM, NT, FULL>(p, acc, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill kernel with direct global->LDS loads (the aligned shapes whose K
+// range is a multiple of 256): the same 256x256 tile and 4x2 waves of 64x128
+// as qmm_big, but the operands never pass through registers.  Each
+// buffer_load_dwordx4 ... lds writes one wave's 64 x 16 bytes to 1 KB of LDS
+// at m0, so the swizzle is applied on the global side: lane l of an
+// instruction fetches the chunk that belongs at LDS byte 16*l.  Four LDS
+// stages of 64 K-bytes (32 KB each) form a ring: while stage kt is
+// multiplied, stages kt+1..kt+3 are in flight, and the fragments of stage
+// kt+1 are read into the second register set.  One barrier per stage, after
+// this wave's part of stage kt+1 has landed (vmcnt counts the wave's DMA
+// instructions in order).
+//   [row][64 B] tiles (A, [N,K] weight): chunk c of row r at r*64 + 16*(c ^ ((r>>1)&3))
+//   [k][256 B]  tiles ([K,N] weight):    chunk c of row k at k*256 + 16*(c ^ h(k)),
+//                                         h(k) = (k&7) | ((k>>4)&1)<<3
+// Both are free of LDS bank conflicts for the fragment reads (b128 row
+// reads; transpose reads for [K,N]), measured with SQ_LDS_BANK_CONFLICT.
+namespace dm {
+constexpr int BM = 256, BN = 256, BK = 64, NST = 4, NW = 8, NT = 64 * NW;
+constexpr int TM = 4;                   // 64-row wave tiles: 4 x 8 MFMA tiles
+constexpr int A_ST = BM * BK, B_ST = BN * BK;
+constexpr int A_BASE = NST * B_ST;      // A stages follow the B stages, so every fragment read offset fits the
+                                        // 16-bit immediate of ds_read
+constexpr int OUT_BYTES = BM * (2 * BN + 16);
+constexpr int SMEM = NST * (A_ST + B_ST) > OUT_BYTES ? NST * (A_ST + B_ST) : OUT_BYTES;
+constexpr int NDMA = 16 / NW;           // DMA instructions per wave per operand per stage
+constexpr int VPS = 2 * NDMA;           // of which vmcnt counts per stage
+
+// s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt[3:0], [15:14]; others at their maximum)
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
+
+// 16 bytes per lane from a buffer into LDS bytes [lds + 16*lane, +16).  Written
+// as asm so the compiler's wait-count pass, which cannot tell which LDS bytes
+// a DMA writes, does not put a vmcnt(0) before every LDS read; the kernel
+// waits on vmcnt itself.  m0 (the LDS base) is an operand, so the compiler
+// sets it and knows it is in use.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds));
+}
+}  // namespace dm
+
+template <bool B_KN, int OUT>
+__global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int tiles_n, int nsplit,
+                                                  int32_t* __restrict__ partial) {
+    using namespace dm;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[SMEM];
+
+    const int tiles = tiles_m * tiles_n;
+    const int bid_all = xcd_swizzle(blockIdx.x, tiles * nsplit);
+    const int split = bid_all / tiles;
+    const int bid = bid_all - split * tiles;
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int grp = bid / per_group;
+    const int first_m = grp * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int tm = first_m + (bid % per_group) % gm;
+    const int tn = (bid % per_group) / gm;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t k_len = p.K / nsplit;
+    const uint32_t k_base = (uint32_t)(split * k_len);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int fr = lane & 15, g = lane >> 4;
+
+    // buffer views of this tile's operand rows (sizes checked on the host to fit 32 bits)
+    const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem;
+    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.a + m0 * p.lda, (uint32_t)(BM * p.lda));
+    const __amdgpu_buffer_rsrc_t rsB = B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
+                                            : make_rsrc(p.b + n0 * p.sbn, (uint32_t)(BN * p.sbn));
+    const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)(B_KN ? p.sbk : p.sbn);
+    // [row][64 B]: one instruction = 16 rows; lane l -> row l>>2, LDS chunk l&3
+    const uint32_t vrk_a = (uint32_t)(lane >> 2) * lda + 16u * (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
+    const uint32_t vrk_b = (uint32_t)(lane >> 2) * ldb + 16u * (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
+    // [k][256 B]: one instruction = 4 rows 4b..4b+3 (b = NDMA*wave + i); lane l -> row l>>4, LDS chunk
+    // l&15, and h = 4*(b&1) + (l>>4) + 8*((b>>2)&1)
+    const int hb = 8 * (((NDMA * wave) >> 2) & 1);
+    const uint32_t vkn0 = (uint32_t)(lane >> 4) * ldb + 16u * (uint32_t)((lane & 15) ^ ((lane >> 4) + hb));
+    const uint32_t vkn1 = (uint32_t)(lane >> 4) * ldb + 16u * (uint32_t)((lane & 15) ^ (4 + (lane >> 4) + hb));
+
+    auto issue = [&](int kt, int st) {
+        const uint32_t k0 = k_base + (uint32_t)kt * dm::BK;
+#pragma unroll
+        for (int i = 0; i < NDMA; ++i) {
+            const int b = NDMA * wave + i;
+            dma16(rsA, sbase + A_BASE + st * A_ST + b * 1024, vrk_a, (uint32_t)(16 * b) * lda + k0);
+            if constexpr (B_KN)
+                dma16(rsB, sbase + st * B_ST + b * 1024, (i & 1) ? vkn1 : vkn0, (k0 + 4u * b) * ldb);
+            else
+                dma16(rsB, sbase + st * B_ST + b * 1024, vrk_b, (uint32_t)(16 * b) * ldb + k0);
+        }
+    };
+
+    // fragment read offsets for stage 0 (stage st adds st * 16 KB)
+    const int a_rd = A_BASE + (wm * 64 + fr) * 64 + 16 * (g ^ ((fr >> 1) & 3));
+    const int b_rd = (wn * 128 + fr) * 64 + 16 * (g ^ ((fr >> 1) & 3));
+    // transpose reads: lanes 2b / 2b+1 of each 16-lane group address k row 16g + b (and +8), columns
+    // 0..7 / 8..15 of the 16-column tile, whose chunk index is XOR-ed by h(k)
+    const int t_rd = (16 * g + (fr >> 1)) * 256 + 128 * (wn ^ (g & 1)) + 8 * (fr & 1);
+    const int xr = fr >> 1;
+
+    auto frags = [&](int st, i32x4 (&af)[TM], i32x4 (&bfr)[8]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i32x4*>(smem + a_rd + st * A_ST + i * 1024);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if constexpr (!B_KN) {
+                bfr[j] = *reinterpret_cast<const i32x4*>(smem + b_rd + st * B_ST + j * 1024);
+            } else {
+                const int8_t* t = smem + t_rd + st * B_ST + 16 * (j ^ xr);
+                const big::v2i lo = big::lds_tr8(t);
+                const big::v2i hi = big::lds_tr8(t + 8 * 256);
+                bfr[j] = (i32x4){lo[0], lo[1], hi[0], hi[1]};
+            }
+        }
+    };
+
+    i32x4 acc[TM][8];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = (i32x4){0, 0, 0, 0};
+    auto mma = [&](const i32x4 (&af)[TM], const i32x4 (&bfr)[8]) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t ro = (m0 + wm * WMR + 16 * i + 4 * g + r) * p.N + n0 + wn * 128 + fr;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) dst[ro + 16 * j] = acc[i][j][r];
-            }
-        return;
-    }
+            for (int j = 0; j < 8; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    };
 
-    // ---- epilogue: per-column and per-row operands loaded once per lane
-    const QmmEpilogue& e = p.epi;
-    float sc[8], bf[8], of[8];
-    int32_t bi[8];
+    const int nk = (int)(k_len / dm::BK);  // a multiple of NST (checked on the host)
+    issue(0, 0);
+    issue(1, 1);
+    issue(2, 2);
+    issue(3, 3);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * VPS));
+    __syncthreads();
+    i32x4 fa[2][TM], fb[2][8];
+    frags(0, fa[0], fb[0]);
+
+    // stages 0 .. nk-NST-1: stage kt+1 must have landed, kt+2 and kt+3 stay in flight; buffer kt&3 is free
+    // once every wave is past the barrier (its fragments are in registers), so stage kt+4 goes there
+    for (int kt0 = 0; kt0 < nk - NST; kt0 += NST) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int64_t n = n0 + wn * 128 + 16 * j + fr;
-        const bool ok = n < p.N;
-        sc[j] = (ok && e.scale) ? e.scale[e.scale_per_ch ? n : 0] : 0.0f;
-        of[j] = (ok && e.offset) ? e.offset[e.offset_per_ch ? n : 0] : 0.0f;
-        bf[j] = 0.0f;
-        bi[j] = 0;
-        if (ok && e.bias_dtype == QK_I32) bi[j] = ((const int32_t*)e.bias)[n];
-        else if (ok && e.bias_dtype) bf[j] = load_scalar(e.bias, n, e.bias_dtype);
-    }
-    if constexpr (FULL && (OUT == QK_BF16 || OUT == QK_F16)) {
-        // 16-bit outputs of a full tile are staged through LDS (the operand
-        // stages are free now) so the global stores are whole 512-byte rows of
-        // 16 bytes per lane instead of 32-byte pieces of 4 rows.
-        constexpr int ROWB = 2 * BN + 16;  // padded LDS row (bytes)
-        static_assert(BM * ROWB <= 2 * STAGE, "output tile does not fit the LDS stages");
-        __syncthreads();
-        uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = wm * WMR + 16 * i + 4 * g + r;
-                const float pt = e.pertoken ? e.pertoken[m0 + row] : 1.0f;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int32_t a = (int32_t)((uint32_t)acc[i][j][r] + (uint32_t)bi[j]);
-                    const float v = __builtin_fmaf((float)a * pt, sc[j], bf[j]);
-                    ot[row * (ROWB / 2) + wn * 128 + 16 * j + fr] =
-                        (uint16_t)(OUT == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
-                }
-            }
-        }
-        __syncthreads();
-        constexpr int CPRO = 2 * BN / 16;  // 16-byte chunks per output row
-#pragma unroll
-        for (int q = tid; q < BM * CPRO; q += NT) {
-            const int row = q / CPRO, c = q % CPRO;
-            const i32x4 v = *reinterpret_cast<const i32x4*>(smem + row * ROWB + 16 * c);
-            *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo + n0 + 8 * c) = v;
-        }
-        return;
-    }
-    // Fully unrolled with compile-time register indices (a runtime-indexed
-    // accumulator would be demoted to scratch and spilled every K step).
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t m = m0 + wm * WMR + 16 * i + 4 * g + r;
-            const bool row_ok = m < p.M;
-            // pertoken multiply by 1.0 is exact, so "no pertoken" needs no branch
-            const float pt = (e.pertoken && row_ok) ? e.pertoken[m] : 1.0f;
-            const int64_t ro = m * e.ldo + n0 + wn * 128 + fr;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const bool ok = row_ok && (n0 + wn * 128 + 16 * j + fr) < p.N;
-                if (ok) big::store_elem<OUT>(e.out, ro + 16 * j, acc[i][j][r], sc[j], bf[j], bi[j], pt, of[j]);
-            }
+        for (int u = 0; u < NST; ++u) {
+            const int cur = u & 1;
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * VPS));
+            __syncthreads();
+            issue(kt0 + u + NST, u);
+            frags((u + 1) & 3, fa[cur ^ 1], fb[cur ^ 1]);
+            mma(fa[cur], fb[cur]);
         }
     }
+    // the last NST stages (buffers 0..3): nothing more to issue
+#pragma unroll
+    for (int u = 0; u < NST; ++u) {
+        const int cur = u & 1;
+        if (u < NST - 1) {
+            if (u == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * VPS));
+            else if (u == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(VPS));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();
+            frags((u + 1) & 3, fa[cur ^ 1], fb[cur ^ 1]);
+        }
+        mma(fa[cur], fb[cur]);
+    }
+    big_epilogue<OUT, TM, NT, true>(p, acc, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -687,18 +873,24 @@ template <int OUT>
 hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, int nsplit, int32_t* partial,
                       hipStream_t stream) {
     const dim3 grid((uint32_t)(tiles_m * tiles_n * nsplit));
-    static const int waves = [] {
-        const char* e = std::getenv("QK_QMM_WAVES");  // tuning override (debug)
-        return (e && std::atoi(e) == 4) ? 4 : 8;
-    }();
     // full tiles and 32-bit per-lane offsets (the 64-bit bases stay uniform)
     const bool full = p.M % big::BM == 0 && p.N % big::BN == 0 && p.K % (big::BK * nsplit) == 0 &&
                       p.lda < (1 << 24) && p.sbk < (1 << 24) && p.sbn < (1 << 24) &&
                       (uintptr_t)p.epi.out % 16 == 0 && p.epi.ldo % 8 == 0;
     if (nsplit > 1 && !full) return hipErrorInvalidValue;  // the plan only splits whole tiles
-    if (waves == 4 && nsplit == 1) {
-        if (b_kn) qmm_big<true, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n, 1, partial);
-        else qmm_big<false, OUT, 4, false><<<grid, dim3(256), 0, stream>>>(p, tiles_m, tiles_n, 1, partial);
+    // direct-to-LDS kernel: K ranges of whole 4-stage rings, 16-byte aligned rows, and every operand
+    // range of a tile addressable by a 32-bit buffer offset
+    static const bool dma_on = [] {
+        const char* e = std::getenv("QK_QMM_DMA");  // tuning override: 0 keeps the register-staged kernel
+        return !(e && std::atoi(e) == 0);
+    }();
+    const bool dma = dma_on && full && (p.K / nsplit) % (dm::BK * dm::NST) == 0 && p.lda % 16 == 0 &&
+                     (uintptr_t)p.a % 16 == 0 && (uintptr_t)p.b % 16 == 0 &&
+                     (b_kn ? (p.sbk % 16 == 0 && (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32))
+                           : (p.sbn % 16 == 0));
+    if (dma) {
+        if (b_kn) qmm_dma<true, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
+        else qmm_dma<false, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
     } else if (full) {
         if (b_kn) qmm_big<true, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
         else qmm_big<false, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);

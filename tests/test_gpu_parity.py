@@ -209,6 +209,57 @@ def test_quant_matmul_big_tiles_and_split_k(ops, oracle, M, N, K, kn):
     assert np.array_equal(to_bits(out)[rows], ref)
 
 
+@pytest.mark.parametrize("K,out_dtype,bias_dtype,kn", [
+    (256, torch.bfloat16, torch.bfloat16, True),   # 192 whole 256x256 tiles, direct-to-LDS kernel (one ring)
+    (256, torch.float16, torch.float32, False),
+    (256, torch.float32, torch.int32, True),
+    (512, torch.int32, None, False),
+    (512, torch.int8, torch.int32, True),
+    (384, torch.bfloat16, torch.bfloat16, True),   # K not a multiple of 256: register-staged kernel
+    (384, torch.float16, None, False),
+])
+def test_quant_matmul_prefill_kernel_epilogues(ops, oracle, K, out_dtype, bias_dtype, kn):
+    """Full-tile shapes with enough tiles to run unsplit: int32 checksums of every accumulator, and
+    rows of each output dtype / bias dtype bit-exact against the oracle (both weight layouts)."""
+    M, N = 512, 24576
+    say(f"quant_matmul prefill tiles M={M} N={N} K={K} out={out_dtype} bias={bias_dtype} kn={kn}")
+    g = torch.Generator().manual_seed(K + (7 if kn else 0))
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    ad = a.to(DEV)
+    wd = w.to(DEV) if kn else w.t().contiguous().to(DEV).t()
+    acc = ops.npu_quant_matmul(ad, wd, torch.ones(1, device=DEV), output_dtype=torch.int32)
+    a64, w64, acc64 = a.to(torch.int64), w.to(torch.int64), acc.cpu().to(torch.int64)
+    assert torch.equal(acc64.sum(0), a64.sum(0) @ w64)
+    assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
+    s = (1e-4 + 1e-3 * torch.rand(N, generator=g)) if out_dtype is torch.int8 else 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    pt = 1e-2 * torch.rand(M, generator=g)
+    off = torch.randn(N, generator=g) if out_dtype is torch.int8 else None
+    b = None
+    if bias_dtype is torch.int32:
+        b = torch.randint(-1000, 1000, (N,), generator=g, dtype=torch.int32)
+    elif bias_dtype is not None:
+        b = torch.randn(N, generator=g).to(bias_dtype)
+    kw = dict(bias=None if b is None else b.to(DEV), output_dtype=out_dtype)
+    integer_out = out_dtype in (torch.int8, torch.int32)   # no per-token scale on integer outputs
+    if out_dtype is torch.int8:
+        kw["offset"] = off.to(DEV)
+    elif not integer_out:
+        kw["pertoken_scale"] = pt.to(DEV)
+    out = ops.npu_quant_matmul(ad, wd, s.to(DEV), **kw).cpu()
+    rows = np.r_[0:4, 250:262, M - 4:M]
+    bias_np = None if b is None else (b.numpy() if b.dtype in (torch.int32, torch.float32) else W.bits(b))
+    ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(),
+                              pertoken=None if integer_out else pt[rows].numpy(),
+                              offset=None if off is None else off.numpy(), bias=bias_np,
+                              bias_dtype=CODE[b.dtype] if b is not None else BF16, out_dtype=CODE[out_dtype])
+    got = out[rows]
+    got_np = got.numpy() if out_dtype in (torch.float32, torch.int32, torch.int8) else W.bits(got)
+    bad = np.argwhere(got_np != ref)
+    assert bad.size == 0, (f"{len(bad)} mismatches, first at (row {rows[bad[0][0]]}, col {bad[0][1]}): "
+                           f"{got_np[tuple(bad[0])]} vs {ref[tuple(bad[0])]}")
+
+
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32, torch.int32])
 @pytest.mark.parametrize("per_tensor", [False, True])
