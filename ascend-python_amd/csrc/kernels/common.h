@@ -91,6 +91,37 @@ __device__ __forceinline__ int32_t quant1(float v, float s) {
     return (int32_t)t;
 }
 
+// The same result as quant1 for every v of a row with |v| <= absmax, without
+// a division for almost all elements.  With r = RN(1/s) and t = RN(v * r),
+// t lies within 2^-16 of the exact v/s (two roundings, |v/s| <= 127.x < 128)
+// and the IEEE quotient RN(v/s) within 2^-17 of it.  When t is more than
+// 2^-14 from floor(t) + 0.5 (the half-integer nearest t), no rounding
+// boundary lies between t and RN(v/s), so rint(t) = rint(RN(v/s)).  The other
+// elements (a fraction of about 2^-13) and rows whose 1/s is not a safely
+// normal number take the division.
+struct RowQuant {
+    float s, r;
+    bool fast;
+};
+__device__ __forceinline__ RowQuant row_quant(float s) {
+    RowQuant q;
+    q.s = s;
+    q.r = 1.0f / s;  // correctly rounded (the kernels are built with correctly rounded division)
+    q.fast = s >= 0x1p-96f && s <= 0x1p96f;
+    return q;
+}
+__device__ __forceinline__ int32_t quant_row(float v, const RowQuant& q) {
+    if (q.fast) {
+        const float t = v * q.r;
+        const float h = __builtin_floorf(t) + 0.5f;
+        if (fabsf(t - h) > 0x1p-14f) {
+            const float n = fminf(fmaxf(__builtin_rintf(t), -128.0f), 127.0f);
+            return (int32_t)n;
+        }
+    }
+    return quant1(v, q.s);
+}
+
 // ---------------------------------------------------------------- XCD-aware ids
 // The dispatcher hands consecutive workgroup ids to the 8 XCDs round-robin,
 // and each XCD has its own L2.  Renumbering so that the ids one XCD receives

@@ -7,6 +7,8 @@
 // arithmetic is exactly the op contract: s = amax / 127 (IEEE division),
 // y = clamp(rint(x / s)) with ties to even, a zero row giving s = 0, y = 0.
 // HBM-bound: 2 B read + 1 B written per element, 4 B per row for the scale.
+#include <cstdlib>
+
 #include "common.h"
 
 namespace qk {
@@ -14,57 +16,91 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Vector path: K % 8 == 0, 16-byte aligned rows, K <= 8 * 256 * VPT.
-template <int DT, int VPT, bool SMOOTH>
-__global__ __launch_bounds__(kThreads) void dyn_quant_vec(const uint16_t* __restrict__ x, int64_t K,
+// Vector path: K % 8 == 0, 16-byte aligned rows, K <= 8 * 256 * VPT.  A
+// workgroup quantizes RPW consecutive rows at once: every load of its rows is
+// issued before the first reduction, so each thread has VPT * RPW 16-byte
+// loads in flight.  Smooth scales (the same for every row) are loaded once.
+template <int DT, int VPT, int RPW, bool SMOOTH>
+__global__ __launch_bounds__(kThreads) void dyn_quant_vec(const uint16_t* __restrict__ x, int64_t rows, int64_t K,
                                                           const float* __restrict__ smooth,
                                                           int8_t* __restrict__ y, float* __restrict__ scale) {
-    const int64_t row = blockIdx.x;
-    const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * K);
+    __shared__ float red[RPW][4];
     const int nv = (int)(K >> 3);
-    float v[VPT][8];
-    float amax = 0.0f;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row0 = (int64_t)blockIdx.x * RPW;
+    u32x4 raw[RPW][VPT];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int idx = threadIdx.x + i * kThreads;
-        if (idx < nv) {
-            u32x4 d = xr[idx];
+    for (int r = 0; r < RPW; ++r) {
+        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;  // a ragged last group re-reads a valid row
+        const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * K);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[i][2 * e] = load_half_bits(d[e] & 0xffffu, DT);
-                v[i][2 * e + 1] = load_half_bits(d[e] >> 16, DT);
-            }
-            if (SMOOTH) {
-                const f32x4* sm = reinterpret_cast<const f32x4*>(smooth + (int64_t)idx * 8);
-                f32x4 s0 = sm[0], s1 = sm[1];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[i][e] = v[i][e] * s0[e];
-                    v[i][4 + e] = v[i][4 + e] * s1[e];
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = threadIdx.x + i * kThreads;
+            if (idx < nv) raw[r][i] = xr[idx];
         }
     }
-    amax = block_absmax(amax);
-    const float s = amax / 127.0f;
-    if (threadIdx.x == 0) scale[row] = s;
-    u32x2* yr = reinterpret_cast<u32x2*>(y + row * K);
+    float sm[SMOOTH ? VPT : 1][8];
+    if constexpr (SMOOTH) {
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int idx = threadIdx.x + i * kThreads;
-        if (idx < nv) {
-            uint32_t lo = 0, hi = 0;
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = threadIdx.x + i * kThreads;
+            if (idx < nv) {
+                const f32x4* sp = reinterpret_cast<const f32x4*>(smooth + (int64_t)idx * 8);
+                const f32x4 s0 = sp[0], s1 = sp[1];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                lo |= ((uint32_t)quant1(v[i][e], s) & 0xffu) << (8 * e);
-                hi |= ((uint32_t)quant1(v[i][4 + e], s) & 0xffu) << (8 * e);
+                for (int e = 0; e < 4; ++e) {
+                    sm[i][e] = s0[e];
+                    sm[i][4 + e] = s1[e];
+                }
             }
-            u32x2 o;
-            o[0] = lo;
-            o[1] = hi;
-            yr[idx] = o;
+        }
+    }
+    auto value = [&](int r, int i, int e) {
+        const uint32_t d = raw[r][i][e >> 1];
+        float v = load_half_bits((e & 1) ? (d >> 16) : (d & 0xffffu), DT);
+        if constexpr (SMOOTH) v = v * sm[i][e];
+        return v;
+    };
+    float amax[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        amax[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = threadIdx.x + i * kThreads;
+            if (idx < nv) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) amax[r] = fmaxf(amax[r], fabsf(value(r, i, e)));
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) amax[r] = fmaxf(amax[r], __shfl_xor(amax[r], off));
+        if (lane == 0) red[r][wave] = amax[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int64_t row = row0 + r;
+        if (row >= rows) break;
+        const float s = fmaxf(fmaxf(red[r][0], red[r][1]), fmaxf(red[r][2], red[r][3])) / 127.0f;
+        if (threadIdx.x == 0) scale[row] = s;
+        const RowQuant rq = row_quant(s);
+        u32x2* yr = reinterpret_cast<u32x2*>(y + row * K);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = threadIdx.x + i * kThreads;
+            if (idx < nv) {
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    lo |= ((uint32_t)quant_row(value(r, i, e), rq) & 0xffu) << (8 * e);
+                    hi |= ((uint32_t)quant_row(value(r, i, 4 + e), rq) & 0xffu) << (8 * e);
+                }
+                u32x2 o;
+                o[0] = lo;
+                o[1] = hi;
+                yr[idx] = o;
+            }
         }
     }
 }
@@ -85,21 +121,37 @@ __global__ __launch_bounds__(kThreads) void dyn_quant_generic(const uint16_t* __
     amax = block_absmax(amax);
     const float s = amax / 127.0f;
     if (threadIdx.x == 0) scale[row] = s;
+    const RowQuant rq = row_quant(s);
     for (int64_t k = threadIdx.x; k < K; k += kThreads) {
         float v = load_half_bits(xr[k], DT);
         if (smooth) v = v * smooth[k];
-        y[row * K + k] = (int8_t)quant1(v, s);
+        y[row * K + k] = (int8_t)quant_row(v, rq);
     }
 }
 
+template <int DT, int VPT, int RPW>
+hipError_t launch_rows(const uint16_t* x, int64_t rows, int64_t K, const float* smooth, int8_t* y, float* scale,
+                       hipStream_t stream) {
+    const dim3 grid((uint32_t)((rows + RPW - 1) / RPW));
+    if (smooth)
+        dyn_quant_vec<DT, VPT, RPW, true><<<grid, dim3(kThreads), 0, stream>>>(x, rows, K, smooth, y, scale);
+    else
+        dyn_quant_vec<DT, VPT, RPW, false><<<grid, dim3(kThreads), 0, stream>>>(x, rows, K, smooth, y, scale);
+    return hipGetLastError();
+}
+
+// Two rows per workgroup where the registers allow (VPT <= 4), so each thread has 8 loads in flight.
 template <int DT, int VPT>
 hipError_t launch_vec(const uint16_t* x, int64_t rows, int64_t K, const float* smooth, int8_t* y, float* scale,
                       hipStream_t stream) {
-    if (smooth)
-        dyn_quant_vec<DT, VPT, true><<<dim3((uint32_t)rows), dim3(kThreads), 0, stream>>>(x, K, smooth, y, scale);
-    else
-        dyn_quant_vec<DT, VPT, false><<<dim3((uint32_t)rows), dim3(kThreads), 0, stream>>>(x, K, smooth, y, scale);
-    return hipGetLastError();
+    static const int rpw = [] {
+        const char* e = std::getenv("QK_DQ_RPW");  // tuning override: rows per workgroup (1, 2)
+        return (e && std::atoi(e) == 1) ? 1 : 2;
+    }();
+    if constexpr (VPT <= 4) {
+        if (rpw == 2 && rows >= 512) return launch_rows<DT, VPT, 2>(x, rows, K, smooth, y, scale, stream);
+    }
+    return launch_rows<DT, VPT, 1>(x, rows, K, smooth, y, scale, stream);
 }
 
 template <int DT>

@@ -58,12 +58,12 @@ __device__ __forceinline__ u32x4 pack16(const uint32_t yb[8]) {
     return o;
 }
 
-__device__ __forceinline__ u32x2 packq(const float yf[8], float s) {
+__device__ __forceinline__ u32x2 packq(const float yf[8], const RowQuant& rq) {
     u32x2 o = {0u, 0u};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        o[0] |= ((uint32_t)quant1(yf[e], s) & 0xffu) << (8 * e);
-        o[1] |= ((uint32_t)quant1(yf[4 + e], s) & 0xffu) << (8 * e);
+        o[0] |= ((uint32_t)quant_row(yf[e], rq) & 0xffu) << (8 * e);
+        o[1] |= ((uint32_t)quant_row(yf[4 + e], rq) & 0xffu) << (8 * e);
     }
     return o;
 }
@@ -114,10 +114,11 @@ __global__ __launch_bounds__(kThreads) void rms_norm_vec(const uint16_t* __restr
     amax = block_absmax(amax);
     const float s = amax / 127.0f;
     if (threadIdx.x == 0) scale[row] = s;
+    const RowQuant rq = row_quant(s);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = threadIdx.x + i * kThreads;
-        if (idx < nv) reinterpret_cast<u32x2*>(q + row * D)[idx] = packq(v[i], s);
+        if (idx < nv) reinterpret_cast<u32x2*>(q + row * D)[idx] = packq(v[i], rq);
     }
 }
 
@@ -149,8 +150,9 @@ __global__ __launch_bounds__(kThreads) void rms_norm_generic(const uint16_t* __r
     amax = block_absmax(amax);
     const float s = amax / 127.0f;
     if (threadIdx.x == 0) scale[row] = s;
+    const RowQuant rq = row_quant(s);
     for (int64_t d = threadIdx.x; d < D; d += kThreads)
-        q[row * D + d] = (int8_t)quant1(load_half_bits(yat(d), DT), s);
+        q[row * D + d] = (int8_t)quant_row(load_half_bits(yat(d), DT), rq);
 }
 
 // ---------------------------------------------------------------- SwiGLU
@@ -187,10 +189,11 @@ __global__ __launch_bounds__(kThreads) void swiglu_vec(const uint16_t* __restric
     amax = block_absmax(amax);
     const float s = amax / 127.0f;
     if (threadIdx.x == 0) scale[row] = s;
+    const RowQuant rq = row_quant(s);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = threadIdx.x + i * kThreads;
-        if (idx < nv) reinterpret_cast<u32x2*>(q + row * I)[idx] = packq(v[i], s);
+        if (idx < nv) reinterpret_cast<u32x2*>(q + row * I)[idx] = packq(v[i], rq);
     }
 }
 
@@ -212,7 +215,8 @@ __global__ __launch_bounds__(kThreads) void swiglu_generic(const uint16_t* __res
     amax = block_absmax(amax);
     const float s = amax / 127.0f;
     if (threadIdx.x == 0) scale[row] = s;
-    for (int64_t i = threadIdx.x; i < I; i += kThreads) q[row * I + i] = (int8_t)quant1(load_half_bits(yat(i), DT), s);
+    const RowQuant rq = row_quant(s);
+    for (int64_t i = threadIdx.x; i < I; i += kThreads) q[row * I + i] = (int8_t)quant_row(load_half_bits(yat(i), DT), rq);
 }
 
 // ---------------------------------------------------------------- dispatch
