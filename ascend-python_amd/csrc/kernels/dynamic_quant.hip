@@ -18,8 +18,10 @@ constexpr int kThreads = 256;
 
 // Vector path: K % 8 == 0, 16-byte aligned rows, K <= 8 * 256 * VPT.  A
 // workgroup quantizes RPW consecutive rows at once: every load of its rows is
-// issued before the first reduction, so each thread has VPT * RPW 16-byte
-// loads in flight.  Smooth scales (the same for every row) are loaded once.
+// issued before the first reduction.  The rows stay packed in registers and
+// each value is widened where it is used (in the absmax and again in the
+// quantizer), which keeps the register count, and so the number of rows in
+// flight per CU, high.
 template <int DT, int VPT, int RPW, bool SMOOTH>
 __global__ __launch_bounds__(kThreads) void dyn_quant_vec(const uint16_t* __restrict__ x, int64_t rows, int64_t K,
                                                           const float* __restrict__ smooth,
@@ -140,17 +142,12 @@ hipError_t launch_rows(const uint16_t* x, int64_t rows, int64_t K, const float* 
     return hipGetLastError();
 }
 
-// Two rows per workgroup where the registers allow (VPT <= 4), so each thread has 8 loads in flight.
+// One row per workgroup: with the row kept packed (VPT * 4 VGPRs) the kernel
+// needs about 30 VGPRs at VPT = 4, so 16 workgroups share a CU and their loads
+// overlap the other rows' reductions.  (Two rows per workgroup measured slower.)
 template <int DT, int VPT>
 hipError_t launch_vec(const uint16_t* x, int64_t rows, int64_t K, const float* smooth, int8_t* y, float* scale,
                       hipStream_t stream) {
-    static const int rpw = [] {
-        const char* e = std::getenv("QK_DQ_RPW");  // tuning override: rows per workgroup (1, 2)
-        return (e && std::atoi(e) == 1) ? 1 : 2;
-    }();
-    if constexpr (VPT <= 4) {
-        if (rpw == 2 && rows >= 512) return launch_rows<DT, VPT, 2>(x, rows, K, smooth, y, scale, stream);
-    }
     return launch_rows<DT, VPT, 1>(x, rows, K, smooth, y, scale, stream);
 }
 
