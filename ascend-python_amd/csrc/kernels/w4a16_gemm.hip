@@ -108,6 +108,23 @@ __device__ __forceinline__ u32x4 unpack_raw(const uint32_t w[8], uint32_t sel) {
     return b;
 }
 
+// int8 weights: byte t of rows 2q and 2q+1 as exact 16-bit values (every
+// int8 is both a bf16 and an fp16 number), two rows per dword.
+template <int DT>
+__device__ __forceinline__ u32x4 unpack_i8(const uint32_t w[8], int t) {
+    u32x4 b;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float lo = (float)(int8_t)(w[2 * q] >> (8 * t));
+        const float hi = (float)(int8_t)(w[2 * q + 1] >> (8 * t));
+        if constexpr (DT == QK_BF16)  // exact values: the upper halves are the bf16 numbers
+            b[q] = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+        else  // exact values: round-toward-zero packing is exact
+            b[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+    }
+    return b;
+}
+
 __device__ __forceinline__ void halves8(u32x4 v, int dt, float f[8]) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -367,14 +384,22 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
 // in order (deterministic), each thread finishing 4 columns of one row.  With
 // one split the sums are the output (+bias, cast); otherwise fp32 partials
 // [split][M][N] for w4_reduce.
-template <int DT, int WPL, int NWAVE, int NKB, int PF, int PIECE_KB, bool HAS_OFF, bool FINAL>
+// W8 (int8 weights [K, N], W8A16): a strip is 64 dwords (256 columns, two
+// lines per row), slot c owns dword c of its sub-strip and its 4 bytes (4
+// MFMA tiles, columns 4c + t), and the operands are the exact 16-bit values
+// of the bytes (no magic offset: BASE = 0).
+template <int DT, int WPL, int NWAVE, int NKB, int PF, int PIECE_KB, bool HAS_OFF, bool FINAL, bool W8>
 __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __restrict__ partial, int nstrip,
                                                         int nsplit) {
     typedef Mfma<DT> MM;
-    constexpr int TPL = WPL == 16 ? 8 : 4;  // MFMA tiles per lane
-    constexpr int HALVES = 32 / WPL;        // column sub-strips per workgroup
+    static_assert(!W8 || WPL == 16, "int8 weights use 16-dword sub-strips");
+    constexpr int CPW = W8 ? 4 : 8;         // output columns per weight dword
+    constexpr int SW = 256 / CPW;           // dwords per strip row (256 columns)
+    constexpr int TPL = W8 ? 4 : (WPL == 16 ? 8 : 4);  // MFMA tiles per lane
+    constexpr int HALVES = SW / WPL;        // column sub-strips per workgroup
     constexpr int KW = NWAVE / HALVES;      // K ranges per workgroup
-    constexpr int NCOL = 8 * WPL;           // output columns per wave
+    constexpr int NCOL = CPW * WPL;         // output columns per wave
+    constexpr float BASE = W8 ? 0.0f : MM::BASE;
     constexpr int RSTR = NCOL + 4;          // LDS row pitch in floats
     constexpr int NPIECE = NKB / PIECE_KB;
     static_assert(NKB % PIECE_KB == 0, "pieces must tile the wave's K range");
@@ -391,10 +416,10 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
     const int rb = blk / (nstrip * nsplit);
 
     const int M = (int)p.M, K = (int)p.K, N = (int)p.N, G = (int)p.group;
-    const int NW = N >> 3;
+    const int NW = W8 ? (N >> 2) : (N >> 3);  // weight dwords per row
     const int slot = WPL == 16 ? c : (c & 7);
     const int nh = WPL == 16 ? 0 : (c >> 3);  // nibble half (WPL == 8)
-    const int wc_raw = strip * 32 + h * WPL + slot;
+    const int wc_raw = strip * SW + h * WPL + slot;
     const int wc = wc_raw < NW ? wc_raw : NW - 1;  // clamped: loads stay in bounds, those columns are not stored
     // rows past M read row M-1: every output row depends only on its own x row, and those rows are not stored
     const int m = rb * 16 + c < M ? rb * 16 + c : M - 1;
@@ -408,7 +433,7 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
     const uint32_t w_lane = (uint32_t)(8 * kg) * rowbytes + (uint32_t)wc * 4u;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
     const uint32_t x_lane = ((uint32_t)m * (uint32_t)K + (uint32_t)k_wave + 8u * (uint32_t)kg) * 2u;
-    const uint32_t s_lane = (uint32_t)(8 * wc + 4 * nh) * 2u;
+    const uint32_t s_lane = (uint32_t)(CPW * wc + 4 * nh) * 2u;
 
     // Scale/offset of every piece first (small, needed from the first fold
     // on), then the K-blocks as a software pipeline PF blocks deep: block
@@ -416,7 +441,7 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
     // register slots.  Loads return in order, so consuming block kb waits only
     // for it; keeping few blocks in flight per wave makes each block arrive
     // early instead of every block finishing near the end of the stream.
-    typedef typename std::conditional<WPL == 16, u32x4, u32x2>::type SV;
+    typedef typename std::conditional<TPL == 8, u32x4, u32x2>::type SV;
     SV sv[NPIECE], ov[NPIECE];
 #pragma unroll
     for (int pc = 0; pc < NPIECE; ++pc) {
@@ -456,7 +481,12 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 xk = xa[kb % SL];
         const uint32_t* wk = wv[kb % SL];
-        if constexpr (WPL == 16) {
+        if constexpr (W8) {
+            ag[0] = MM::mma(xk, unpack_i8<DT>(wk, 0), ag[0]);
+            ag[1] = MM::mma(xk, unpack_i8<DT>(wk, 1), ag[1]);
+            ag[2] = MM::mma(xk, unpack_i8<DT>(wk, 2), ag[2]);
+            ag[3] = MM::mma(xk, unpack_i8<DT>(wk, 3), ag[3]);
+        } else if constexpr (WPL == 16) {
             ag[0] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, byte_sel(0)), ag[0]);
             ag[1] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wk, byte_sel(0)), ag[1]);
             ag[2] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, byte_sel(1)), ag[2]);
@@ -481,7 +511,7 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
                 const float sf = load_half_bits(sb & 0xffffu, p.s_dtype);
                 float of = 0.0f;
                 if (HAS_OFF) of = load_half_bits((ov[pc][t >> 1] >> (16 * (t & 1))) & 0xffffu, p.s_dtype);
-                const float sx = sf * (of - MM::BASE);
+                const float sx = sf * (of - BASE);
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     acc[t][r] = __builtin_fmaf(sf, ag[t][r], __builtin_fmaf(sx, xs[r], acc[t][r]));
@@ -491,10 +521,10 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
         }
     }
 
-    // lane (c, kg) holds rows 4kg..4kg+3 of columns  8*slot + 4*nh + t
+    // lane (c, kg) holds rows 4kg..4kg+3 of columns  CPW*slot + 4*nh + t
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        float* dst = &red[wave][4 * kg + r][8 * slot + 4 * nh];
+        float* dst = &red[wave][4 * kg + r][CPW * slot + 4 * nh];
         *reinterpret_cast<f32x4*>(dst) = (f32x4){acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
         if constexpr (TPL == 8) *reinterpret_cast<f32x4*>(dst + 4) = (f32x4){acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
     }
@@ -588,10 +618,12 @@ __device__ __forceinline__ int off(int r, int c) { return r * ROWB + 16 * (c ^ (
 __device__ __forceinline__ int boff(int n, int c) { return (n ^ ((n >> 3) & 1)) * ROWB + 16 * (c ^ ((n >> 1) & 7)); }
 }  // namespace pf
 
-// G128: the group is exactly two stages, so the stage loop is unrolled by two
-// and the group's first MFMA step starts from C = 0 (no re-zeroing); other
-// group sizes count steps at run time and zero the group sums after a fold.
-template <int DT, bool HAS_OFF, bool FULL, bool G128>
+// The group sums are folded into the accumulators after G/32 MFMA steps
+// (counted at run time) and zeroed for the next group.
+// W8: int8 weights [K, N] (W8A16).  Every thread loads one dword (4
+// columns) of 4 rows per stage and writes their exact 16-bit values (no
+// magic offset, BASE = 0) to the same LDS layout.
+template <int DT, bool HAS_OFF, bool FULL, bool W8>
 __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int tiles_n) {
     typedef Mfma<DT> MM;
     constexpr int NT = 512, BN = pf::BN;
@@ -599,6 +631,7 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
     constexpr int TM = 4, TN = 4;           // MFMA tiles per wave (wave tile 64 x 64)
     constexpr int WQ = BN / 8;              // packed words per weight row of the tile (16)
     constexpr int WT = WQ * 16;             // unpacking threads (4 rows each, 64 rows)
+    constexpr float BASE = W8 ? 0.0f : MM::BASE;
     constexpr int OROWB = 2 * BN + 16;      // padded output staging row (bytes)
     constexpr int SMEM = 2 * STAGE > pf::BM * OROWB ? 2 * STAGE : pf::BM * OROWB;
     __shared__ __attribute__((aligned(16))) char smem[SMEM];
@@ -616,7 +649,7 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
     const int tn = (bid % per_group) / gm;
     const int M = (int)p.M, N = (int)p.N, K = (int)p.K, G = (int)p.group;
     const int m0 = tm * pf::BM, n0 = tn * BN;
-    const int NWD = N >> 3;
+    const int NWD = W8 ? (N >> 2) : (N >> 3);  // weight dwords per row
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -634,9 +667,9 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
         a_off[i] = ((uint32_t)r * (uint32_t)K + 8u * (uint32_t)(tid % 8)) * 2u;
     }
     // ---- W loads: threads < WT take word column tid / 16, rows 4 (tid % 16) .. +3
-    const bool wthr = tid < WT;
-    const int wcol_l = (tid / 16) % WQ, rg = tid & 15;
-    int wcol = n0 / 8 + wcol_l;
+    const bool wthr = W8 || tid < WT;
+    const int wcol_l = W8 ? tid / 16 : (tid / 16) % WQ, rg = tid & 15;
+    int wcol = n0 / (W8 ? 4 : 8) + wcol_l;
     if (!FULL) wcol = wcol < NWD ? wcol : NWD - 1;
     const uint32_t rowb = (uint32_t)NWD * 4u;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (uint32_t)K * rowb);
@@ -696,15 +729,32 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
             const float sf = load_half_bits(rsc0, p.s_dtype);
             const float of = HAS_OFF ? load_half_bits(rof0, p.s_dtype) : 0.0f;
             sc_s[st_g0 & 3][scol_l] = sf;
-            sc_x[st_g0 & 3][scol_l] = sf * (of - MM::BASE);
+            sc_x[st_g0 & 3][scol_l] = sf * (of - BASE);
             if (st_n > 1) {
                 const float sf1 = load_half_bits(rsc1, p.s_dtype);
                 const float of1 = HAS_OFF ? load_half_bits(rof1, p.s_dtype) : 0.0f;
                 sc_s[(st_g0 + 1) & 3][scol_l] = sf1;
-                sc_x[(st_g0 + 1) & 3][scol_l] = sf1 * (of1 - MM::BASE);
+                sc_x[(st_g0 + 1) & 3][scol_l] = sf1 * (of1 - BASE);
             }
         }
-        if (wthr) {
+        if constexpr (W8) {
+            // columns 4*wcol_l + j, rows 4rg..4rg+3: half (rg & 1) of k chunk rg / 2
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t q[4] = {rw[0], rw[1], rw[2], rw[3]};
+                u32x2 v;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float lo = (float)(int8_t)(q[2 * e] >> (8 * j));
+                    const float hi = (float)(int8_t)(q[2 * e + 1] >> (8 * j));
+                    if constexpr (DT == QK_BF16)
+                        v[e] = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+                    else
+                        v[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+                }
+                *reinterpret_cast<u32x2*>(Bs + pf::boff(4 * wcol_l + j, rg >> 1) + 8 * (rg & 1)) = v;
+            }
+        } else if (wthr) {
             const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000f000fu);
             const uint32_t magic = __builtin_amdgcn_readfirstlane(MM::MAGIC | 0x00080008u);
 #pragma unroll
@@ -757,41 +807,18 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
         for (int j = 0; j < TN; ++j)
             bfr[j] = *reinterpret_cast<const u32x4*>(Bs + pf::boff(wn * 64 + 16 * j + fr, 4 * kk + g4));
     };
-    auto mma = [&](const u32x4 (&af)[TM], const u32x4 (&bfr)[TN], bool first) {
+    auto mma = [&](const u32x4 (&af)[TM], const u32x4 (&bfr)[TN]) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
-            for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], bfr[j], first ? zero4 : ag[i][j]);
-            xs[i] = MM::mma(af[i], ones, first ? zero4 : xs[i]);
+            for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], bfr[j], ag[i][j]);
+            xs[i] = MM::mma(af[i], ones, xs[i]);
         }
     };
-    // one 64-k stage: two MFMA steps around the write of stage it+1 and the fetch of stage it+2
-    auto stage = [&](int it, bool first0, bool fold1, int slot) {
-        __syncthreads();
-        const int st = it & 1;
-        const char* As = smem + st * STAGE;
-        const char* Bs = As + A_BYTES;
-        u32x4 af[TM], bfr[TN];
-        frags(As, Bs, 0, af, bfr);
-        mma(af, bfr, first0);
-        if (it + 1 < nk) {
-            lstore(st ^ 1);
-            if (it + 2 < nk) gload((it + 2) * pf::BK);
-        }
-        frags(As, Bs, 1, af, bfr);
-        mma(af, bfr, false);
-        if (fold1) fold(slot);
-    };
-
     gload(0);
     lstore(0);
     if (nk > 1) gload(pf::BK);
-    if constexpr (G128) {
-        for (int it = 0; it < nk; it += 2) {
-            stage(it, true, false, 0);
-            stage(it + 1, false, true, (it >> 1) & 3);
-        }
-    } else {
+    {
         const int gsub = G / 32;  // 32-k MFMA steps per group
         int sub_left = gsub, fold_g = 0;
         for (int it = 0; it < nk; ++it) {
@@ -803,7 +830,7 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
                 frags(As, Bs, kk, af, bfr);
-                mma(af, bfr, false);
+                mma(af, bfr);
                 if (kk == 0 && it + 1 < nk) {
                     lstore(st ^ 1);
                     if (it + 2 < nk) gload((it + 2) * pf::BK);
@@ -1017,16 +1044,16 @@ struct StreamPlan {
 StreamPlan stream_plan(const WqbmmArgs& p) {
     StreamPlan s{false, 16, 8, 4, 2, 1, 0, 4};
     const int64_t G = p.group == 0 ? p.K : p.group;
-    if (p.w_dtype != QK_I32 || p.M <= 0 || p.M > 16 || p.N <= 0 || p.K <= 0) return s;
+    const bool w8 = p.w_dtype == QK_I8;
+    if (!(p.w_dtype == QK_I32 || (w8 && p.N % 4 == 0)) || p.M <= 0 || p.M > 16 || p.N <= 0 || p.K <= 0) return s;
     if (G <= 0 || p.K % G != 0 || !(G % 128 == 0 || G == 32 || G == 64)) return s;
-    if (p.K * (p.N / 2) >= ((int64_t)1 << 31) || p.M * p.K * 2 >= ((int64_t)1 << 31) ||
+    if (p.K * (w8 ? p.N : p.N / 2) >= ((int64_t)1 << 31) || p.M * p.K * 2 >= ((int64_t)1 << 31) ||
         (p.K / G) * p.N * 2 >= ((int64_t)1 << 31))
         return s;
     if (((uintptr_t)p.x | (uintptr_t)p.scale) % 16 != 0 || (uintptr_t)p.out % 8 != 0 || (uintptr_t)p.w % 4 != 0 ||
         (p.offset && (uintptr_t)p.offset % 16 != 0))
         return s;
     s.piece_kb = G >= 128 ? 4 : (int)(G / 32);
-    const int64_t nw = p.N / 8;
     s.wpl = 16;
     s.nwave = 16;
     s.nkb = 4;
@@ -1041,48 +1068,65 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
             s.pf = c;
         }
     }
-    if (s.piece_kb != 4) {  // short groups: one instantiated shape
+    if (s.piece_kb != 4) {  // short groups: one instantiated shape, 8 waves (16 would spill their scales)
+        s.nwave = 8;
         s.nkb = 4;
         s.pf = 2;
     }
-    const int halves = 32 / s.wpl;
+    if (w8) {  // int8 weights: one instantiated shape
+        s.nwave = 16;
+        s.nkb = 4;
+        s.pf = 2;
+    }
+    const int halves = (w8 ? 64 : 32) / s.wpl;
     int kw = s.nwave / halves;
     const int rows = s.nkb * 32;
     while (kw > 1 && p.K % (kw * rows) != 0) kw >>= 1;  // fewer K ranges when K is short
     if (p.K % (kw * rows) != 0) return s;
     s.nwave = kw * halves;
     if (s.nwave != 8 && s.nwave != 16) return s;  // the instantiated shapes
+    if (w8 && s.nwave != 16) return s;
     s.nsplit = (int)(p.K / (kw * rows));
-    s.nstrip = (int)((nw + 31) / 32);
+    s.nstrip = (int)((p.N + 255) / 256);
     if (s.nsplit > 1 && (int64_t)s.nsplit * p.M * p.N * 4 > ((int64_t)256 << 20)) return s;
     s.ok = (int64_t)s.nstrip * s.nsplit < ((int64_t)1 << 31);
     return s;
 }
 
-template <int DT, int NWAVE, int NKB, int PF, int PKB, bool HAS_OFF>
+template <int DT, int NWAVE, int NKB, int PF, int PKB, bool HAS_OFF, bool W8>
 hipError_t launch_stream_t(const WqbmmArgs& p, const StreamPlan& s, float* partial, hipStream_t stream) {
     const dim3 grid((uint32_t)((int64_t)s.nstrip * s.nsplit));
     if (s.nsplit == 1)
-        w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, true><<<grid, dim3(64 * NWAVE), 0, stream>>>(p, partial,
-                                                                                               s.nstrip, 1);
+        w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, true, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
+            p, partial, s.nstrip, 1);
     else
-        w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, false><<<grid, dim3(64 * NWAVE), 0, stream>>>(
+        w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, false, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
             p, partial, s.nstrip, s.nsplit);
     return hipGetLastError();
 }
 
 template <int DT, int NWAVE, bool HAS_OFF>
 hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* partial, hipStream_t stream) {
+    if (p.w_dtype == QK_I8) {  // int8 weights: the default shape only
+        if constexpr (NWAVE == 16) {
+            switch (s.piece_kb) {
+            case 1: return launch_stream_t<DT, 16, 4, 2, 1, HAS_OFF, true>(p, s, partial, stream);
+            case 2: return launch_stream_t<DT, 16, 4, 2, 2, HAS_OFF, true>(p, s, partial, stream);
+            default: return launch_stream_t<DT, 16, 4, 2, 4, HAS_OFF, true>(p, s, partial, stream);
+            }
+        }
+        return hipErrorInvalidValue;
+    }
     switch (s.piece_kb) {
-    case 1: return launch_stream_t<DT, NWAVE, 4, 2, 1, HAS_OFF>(p, s, partial, stream);
-    case 2: return launch_stream_t<DT, NWAVE, 4, 2, 2, HAS_OFF>(p, s, partial, stream);
+    case 1: return launch_stream_t<DT, NWAVE, 4, 2, 1, HAS_OFF, false>(p, s, partial, stream);
+    case 2: return launch_stream_t<DT, NWAVE, 4, 2, 2, HAS_OFF, false>(p, s, partial, stream);
     default: break;
     }
     if (s.nkb == 8)
-        return s.pf == 3 ? launch_stream_t<DT, NWAVE, 8, 3, 4, HAS_OFF>(p, s, partial, stream)
-                         : launch_stream_t<DT, NWAVE, 8, 2, 4, HAS_OFF>(p, s, partial, stream);
-    return s.pf == 4 ? launch_stream_t<DT, NWAVE, 4, 4, 4, HAS_OFF>(p, s, partial, stream)
-                     : launch_stream_t<DT, NWAVE, 4, 2, 4, HAS_OFF>(p, s, partial, stream);
+        return s.pf == 3 ? launch_stream_t<DT, NWAVE, 8, 3, 4, HAS_OFF, false>(p, s, partial, stream)
+                         : launch_stream_t<DT, NWAVE, 8, 2, 4, HAS_OFF, false>(p, s, partial, stream);
+    return s.pf == 4 ? launch_stream_t<DT, NWAVE, 4, 4, 4, HAS_OFF, false>(p, s, partial, stream)
+                     : launch_stream_t<DT, NWAVE, 4, 2, 4, HAS_OFF, false>(p, s, partial, stream);
 }
 
 template <int DT>
@@ -1096,16 +1140,18 @@ hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* part
 // Prefill plan: large M, int4 weights, K a multiple of the 64-row stage and
 // G a multiple of the 32-row MFMA step.
 struct GemmPlan {
-    bool ok, full, g128;
+    bool ok, full;
     int tiles_m, tiles_n;
 };
 
 GemmPlan gemm_plan(const WqbmmArgs& p) {
-    GemmPlan g{false, false, false, 0, 0};
+    GemmPlan g{false, false, 0, 0};
     const int64_t G = p.group == 0 ? p.K : p.group;
-    if (p.w_dtype != QK_I32 || p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0) return g;
+    const bool w8 = p.w_dtype == QK_I8;
+    if (!(p.w_dtype == QK_I32 || (w8 && p.N % 4 == 0)) || p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0)
+        return g;
     if (G <= 0 || p.K % G != 0 || G % 32 != 0) return g;
-    if (p.M * p.K * 2 >= ((int64_t)1 << 31) || p.K * (p.N / 2) >= ((int64_t)1 << 31) ||
+    if (p.M * p.K * 2 >= ((int64_t)1 << 31) || p.K * (w8 ? p.N : p.N / 2) >= ((int64_t)1 << 31) ||
         (p.K / G) * p.N >= ((int64_t)1 << 31) || p.M * p.N >= ((int64_t)1 << 31))
         return g;
     if (((uintptr_t)p.x | (uintptr_t)p.out) % 16 != 0 || (uintptr_t)p.w % 4 != 0) return g;
@@ -1117,7 +1163,6 @@ GemmPlan gemm_plan(const WqbmmArgs& p) {
     // too few tiles: the decode kernels stream the weight better
     if (!forced && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
     g.full = p.M % 256 == 0 && p.N % 128 == 0;
-    g.g128 = false;  // the unrolled G = 128 variant spills at 8 waves; kept for the 4-wave layout
     g.ok = true;
     return g;
 }
@@ -1125,10 +1170,14 @@ GemmPlan gemm_plan(const WqbmmArgs& p) {
 template <int DT, bool OFF>
 hipError_t launch_gemm_t(const WqbmmArgs& p, const GemmPlan& g, hipStream_t stream) {
     const dim3 grid((uint32_t)(g.tiles_m * g.tiles_n));
-    if (g.full && g.g128) w4_gemm<DT, OFF, true, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
-    else if (g.full) w4_gemm<DT, OFF, true, false><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
-    else if (g.g128) w4_gemm<DT, OFF, false, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
-    else w4_gemm<DT, OFF, false, false><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    if (p.w_dtype == QK_I8) {
+        if (g.full) w4_gemm<DT, OFF, true, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+        else w4_gemm<DT, OFF, false, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    } else if (g.full) {
+        w4_gemm<DT, OFF, true, false><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    } else {
+        w4_gemm<DT, OFF, false, false><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
+    }
     return hipGetLastError();
 }
 

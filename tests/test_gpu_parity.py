@@ -467,6 +467,49 @@ def test_w4a16_prefill_kernel(ops, oracle, monkeypatch, M, N, K, group, offset, 
     bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b, x_dtype=x_dtype), dtype=x_dtype)
 
 
+# ----------------------------------------------------------------------------- W8A16 (int8 weights)
+
+def _w8_inputs(M, N, K, group, offset, x_dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((M, K), generator=g).to(x_dtype)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    ng = K // group if group > 0 else 1
+    scale = (5e-4 + 2.5e-3 * torch.rand((ng, N), generator=g)).to(torch.float16)
+    off = (8 * torch.rand((ng, N), generator=g) - 4).to(torch.float16) if offset else None
+    if group == 0:
+        scale = scale.reshape(-1)
+        off = None if off is None else off.reshape(-1)
+    return dict(x=x, w=w, scale=scale, offset=off)
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,force", [
+    (16, 11008, 4096, 128, True, torch.bfloat16, None),   # decode weight stream, the cfg3 shape with int8 weights
+    (1, 4096, 4096, 128, True, torch.float16, None),
+    (7, 2048, 1024, 64, False, torch.bfloat16, None),
+    (16, 1024, 2048, 32, True, torch.float16, None),
+    (16, 768, 512, 0, True, torch.bfloat16, None),        # per-channel scales
+    (300, 512, 512, 128, True, torch.bfloat16, "force"),   # prefill kernel, ragged M
+    (256, 384, 256, 64, False, torch.float16, "force"),
+    (2048, 11008, 4096, 128, True, torch.bfloat16, None),  # prefill at the cfg3 shape (row subset)
+    (5, 24, 96, 0, True, torch.bfloat16, None),            # generic kernel
+])
+def test_w8a16(ops, oracle, monkeypatch, M, N, K, group, offset, x_dtype, force):
+    """npu_weight_quant_batchmatmul with int8 weights [K, N] (W8A16) against the float64 oracle."""
+    if force:
+        monkeypatch.setenv("QK_W4_GEMM", force)
+    say(f"w8a16 M={M} N={N} K={K} group={group} offset={offset} {x_dtype} {force or ''}")
+    d = _w8_inputs(M, N, K, group, offset, x_dtype, seed=M + 5 * N + K)
+    b = torch.randn(N).to(x_dtype)
+    out = ops.npu_weight_quant_batchmatmul(d["x"].to(DEV), d["w"].to(DEV), d["scale"].to(DEV),
+                                           None if d["offset"] is None else d["offset"].to(DEV), bias=b.to(DEV),
+                                           antiquant_group_size=group)
+    rows = np.arange(M) if M <= 300 else np.r_[0:16, 1000:1016, M - 16:M]
+    ref = oracle.weight_quant_bmm(W.bits(d["x"][rows]), CODE[x_dtype], d["w"].numpy(), W.bits(d["scale"]),
+                                  None if d["offset"] is None else W.bits(d["offset"]), F16, group,
+                                  bias=W.bits(b), bias_dtype=CODE[x_dtype], out_dtype=CODE[x_dtype])
+    bf16_close(to_bits(out)[rows], ref, dtype=x_dtype)
+
+
 def test_abi_dynamic_quant_and_w4a16(ops, oracle):
     say("ABI qk_dynamic_quant / qk_weight_quant_bmm")
     L = ops.abi()
