@@ -65,6 +65,47 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// ---------------------------------------------------------------- split-K completion
+// Each of the nsplit workgroups that own one output tile stores its partial
+// sums device-coherently (store_dev, or buffer stores with kCoherent: written
+// through the XCD's L2) and
+// then calls splitk_last, which returns true in exactly one of them -- the
+// last to arrive.  That workgroup reads every split's partials device-coherently
+// (load_dev / kCoherent: not served from a possibly stale L2 line) and finishes the
+// tile.  A split's stores have completed (s_waitcnt vmcnt(0)) before its
+// arrival is counted, so the last arrival sees them all; no cache-wide
+// writeback or invalidate is needed.  The counter must be zero before the
+// tile's first split arrives; the last arrival sets it back to zero (every
+// other arrival has happened by then).  Call from every thread of the
+// workgroup (it contains barriers).
+// Cache-policy operand of the raw buffer loads/stores for device-coherent
+// access (the sc1 bit on gfx950).
+constexpr int kCoherent = 16;
+__device__ __forceinline__ void store_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(int32_t* p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t load_dev(const int32_t* p) {
+    return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool splitk_last(uint32_t* ctr, uint32_t nsplit) {
+    __shared__ uint32_t splitk_ticket;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t == nsplit - 1) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        splitk_ticket = t;
+    }
+    __syncthreads();
+    return splitk_ticket == nsplit - 1;
+}
+
 // ---------------------------------------------------------------- per-row quantization
 // Row reductions for 256-thread workgroups (4 wave64): xor-shuffles inside a
 // wave, LDS across the four waves.  Every thread gets the result.

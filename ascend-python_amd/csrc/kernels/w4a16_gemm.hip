@@ -390,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
 // of the bytes (no magic offset: BASE = 0).
 template <int DT, int WPL, int NWAVE, int NKB, int PF, int PIECE_KB, bool HAS_OFF, bool FINAL, bool W8>
 __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __restrict__ partial, int nstrip,
-                                                        int nsplit) {
+                                                        int nsplit, uint32_t* __restrict__ ctr) {
     typedef Mfma<DT> MM;
     static_assert(!W8 || WPL == 16, "int8 weights use 16-dword sub-strips");
     constexpr int CPW = W8 ? 4 : 8;         // output columns per weight dword
@@ -532,6 +532,7 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
 
     // each thread finishes 4 consecutive columns of one row, summing the K ranges in order
     constexpr int QUADS = 16 * 256 / 4;
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(partial, (uint32_t)((int64_t)nsplit * M * N * 4));
     const int n_strip0 = strip * 256;
     for (int q = threadIdx.x; q < QUADS; q += 64 * NWAVE) {
         const int row = q >> 6, col = 4 * (q & 63);
@@ -555,8 +556,64 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
                 packed[e] = lo | (hi << 16);
             }
             *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + (int64_t)mm * N + n) = packed;
+        } else if (ctr) {  // finished in this kernel by the strip's last split: device-coherent stores
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
+                                                   (uint32_t)(((int64_t)split * M + mm) * N + n) * 4u, 0, kCoherent);
         } else {
             *reinterpret_cast<f32x4*>(partial + ((int64_t)split * M + mm) * N + n) = v;
+        }
+    }
+    // split-K: the last split of this strip to finish adds all splits in split order (deterministic)
+    if constexpr (!FINAL) {
+        if (ctr == nullptr || !splitk_last(ctr + (int64_t)rb * nstrip + strip, (uint32_t)nsplit)) return;
+        constexpr int QPT = QUADS / (64 * NWAVE);  // quads per thread
+        uint32_t qoff[QPT];
+        bool qok[QPT];
+#pragma unroll
+        for (int i = 0; i < QPT; ++i) {
+            const int q = threadIdx.x + i * 64 * NWAVE;
+            const int mm = rb * 16 + (q >> 6), n = n_strip0 + 4 * (q & 63);
+            qok[i] = mm < M && n < N;
+            qoff[i] = (uint32_t)(qok[i] ? (int64_t)mm * N + n : 0) * 4u;
+        }
+        // four splits' loads in flight at a time, added in split order
+        const uint32_t sstride = (uint32_t)((int64_t)M * N * 4);
+        f32x4 v[QPT];
+        for (int s0 = 0; s0 < nsplit; s0 += 4) {
+            f32x4 part[4][QPT];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < QPT; ++i)
+                    if (s0 + j < nsplit)
+                        part[j][i] = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, qoff[i], (uint32_t)(s0 + j) * sstride,
+                                                                         kCoherent));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < QPT; ++i)
+                    if (s0 + j < nsplit) v[i] = (s0 + j == 0) ? part[j][i] : v[i] + part[j][i];
+        }
+#pragma unroll
+        for (int i = 0; i < QPT; ++i) {
+            if (!qok[i]) continue;
+            const int q = threadIdx.x + i * 64 * NWAVE;
+            const int mm = rb * 16 + (q >> 6), n = n_strip0 + 4 * (q & 63);
+            f32x4 w = v[i];
+            if (p.bias_dtype) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) w[t] += load_scalar(p.bias, n + t, p.bias_dtype);
+            }
+            u32x2 packed;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const bool bf = p.out_dtype == QK_BF16;
+                const uint32_t lo = bf ? f32_to_bf16_bits(w[2 * e]) : f32_to_f16_bits(w[2 * e]);
+                const uint32_t hi = bf ? f32_to_bf16_bits(w[2 * e + 1]) : f32_to_f16_bits(w[2 * e + 1]);
+                packed[e] = lo | (hi << 16);
+            }
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + (int64_t)mm * N + n) = packed;
         }
     }
 }
@@ -1094,47 +1151,52 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
 }
 
 template <int DT, int NWAVE, int NKB, int PF, int PKB, bool HAS_OFF, bool W8>
-hipError_t launch_stream_t(const WqbmmArgs& p, const StreamPlan& s, float* partial, hipStream_t stream) {
+hipError_t launch_stream_t(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint32_t* ctr,
+                           hipStream_t stream) {
     const dim3 grid((uint32_t)((int64_t)s.nstrip * s.nsplit));
     if (s.nsplit == 1)
         w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, true, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
-            p, partial, s.nstrip, 1);
+            p, partial, s.nstrip, 1, nullptr);
     else
         w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, false, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
-            p, partial, s.nstrip, s.nsplit);
+            p, partial, s.nstrip, s.nsplit, ctr);
     return hipGetLastError();
 }
 
 template <int DT, int NWAVE, bool HAS_OFF>
-hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* partial, hipStream_t stream) {
+hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint32_t* ctr,
+                           hipStream_t stream) {
     if (p.w_dtype == QK_I8) {  // int8 weights: the default shape only
         if constexpr (NWAVE == 16) {
             switch (s.piece_kb) {
-            case 1: return launch_stream_t<DT, 16, 4, 2, 1, HAS_OFF, true>(p, s, partial, stream);
-            case 2: return launch_stream_t<DT, 16, 4, 2, 2, HAS_OFF, true>(p, s, partial, stream);
-            default: return launch_stream_t<DT, 16, 4, 2, 4, HAS_OFF, true>(p, s, partial, stream);
+            case 1: return launch_stream_t<DT, 16, 4, 2, 1, HAS_OFF, true>(p, s, partial, ctr, stream);
+            case 2: return launch_stream_t<DT, 16, 4, 2, 2, HAS_OFF, true>(p, s, partial, ctr, stream);
+            default: return launch_stream_t<DT, 16, 4, 2, 4, HAS_OFF, true>(p, s, partial, ctr, stream);
             }
         }
         return hipErrorInvalidValue;
     }
     switch (s.piece_kb) {
-    case 1: return launch_stream_t<DT, NWAVE, 4, 2, 1, HAS_OFF, false>(p, s, partial, stream);
-    case 2: return launch_stream_t<DT, NWAVE, 4, 2, 2, HAS_OFF, false>(p, s, partial, stream);
+    case 1: return launch_stream_t<DT, NWAVE, 4, 2, 1, HAS_OFF, false>(p, s, partial, ctr, stream);
+    case 2: return launch_stream_t<DT, NWAVE, 4, 2, 2, HAS_OFF, false>(p, s, partial, ctr, stream);
     default: break;
     }
     if (s.nkb == 8)
-        return s.pf == 3 ? launch_stream_t<DT, NWAVE, 8, 3, 4, HAS_OFF, false>(p, s, partial, stream)
-                         : launch_stream_t<DT, NWAVE, 8, 2, 4, HAS_OFF, false>(p, s, partial, stream);
-    return s.pf == 4 ? launch_stream_t<DT, NWAVE, 4, 4, 4, HAS_OFF, false>(p, s, partial, stream)
-                     : launch_stream_t<DT, NWAVE, 4, 2, 4, HAS_OFF, false>(p, s, partial, stream);
+        return s.pf == 3 ? launch_stream_t<DT, NWAVE, 8, 3, 4, HAS_OFF, false>(p, s, partial, ctr, stream)
+                         : launch_stream_t<DT, NWAVE, 8, 2, 4, HAS_OFF, false>(p, s, partial, ctr, stream);
+    return s.pf == 4 ? launch_stream_t<DT, NWAVE, 4, 4, 4, HAS_OFF, false>(p, s, partial, ctr, stream)
+                     : launch_stream_t<DT, NWAVE, 4, 2, 4, HAS_OFF, false>(p, s, partial, ctr, stream);
 }
 
 template <int DT>
-hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* partial, hipStream_t stream) {
+hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint32_t* ctr,
+                            hipStream_t stream) {
     const bool off = p.offset != nullptr;
     if (s.nwave == 8)
-        return off ? launch_stream_w<DT, 8, true>(p, s, partial, stream) : launch_stream_w<DT, 8, false>(p, s, partial, stream);
-    return off ? launch_stream_w<DT, 16, true>(p, s, partial, stream) : launch_stream_w<DT, 16, false>(p, s, partial, stream);
+        return off ? launch_stream_w<DT, 8, true>(p, s, partial, ctr, stream)
+                   : launch_stream_w<DT, 8, false>(p, s, partial, ctr, stream);
+    return off ? launch_stream_w<DT, 16, true>(p, s, partial, ctr, stream)
+               : launch_stream_w<DT, 16, false>(p, s, partial, ctr, stream);
 }
 
 // Prefill plan: large M, int4 weights, K a multiple of the 64-row stage and
@@ -1209,27 +1271,33 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     p.x = p.scale = p.offset = p.out = (void*)(uintptr_t)256;
     p.w = (void*)(uintptr_t)256;
     if (p.group == 0) p.group = p.K;
+    // [split-K counters][fp32 partials [nsplit][M][N]]
     const StreamPlan s = stream_plan(p);
-    if (s.ok) return s.nsplit == 1 ? 0 : (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
+    if (s.ok) return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
     if (gemm_plan(p).ok) return 0;
     const DecodePlan d = decode_plan(p);
     if (!d.ok || d.nsplit == 1) return 0;
-    return (size_t)d.nsplit * (size_t)M * (size_t)N * sizeof(float);
+    return QK_SPLIT_COUNTER_BYTES + (size_t)d.nsplit * (size_t)M * (size_t)N * sizeof(float);
 }
 
 hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t ws_bytes, hipStream_t stream) {
     if (a.M == 0 || a.N == 0) return hipSuccess;
     WqbmmArgs p = a;
     if (p.group == 0) p.group = p.K;  // per channel == one group spanning K
+    // a split workspace is [counters][partials]: the stream kernel finishes each strip in its last
+    // split's workgroup (one counter per strip); the decode kernel uses the reduce kernel
+    char* ws = static_cast<char*>(workspace);
+    float* partial = ws ? reinterpret_cast<float*>(ws + QK_SPLIT_COUNTER_BYTES) : nullptr;
     const StreamPlan sp = stream_plan(p);
     if (sp.ok) {
-        float* partial = static_cast<float*>(workspace);
-        if (sp.nsplit > 1 && (!partial || ws_bytes < (size_t)sp.nsplit * p.M * p.N * sizeof(float) ||
-                              (uintptr_t)partial % 16 != 0))
+        if (sp.nsplit > 1 && (!ws || ws_bytes < QK_SPLIT_COUNTER_BYTES + (size_t)sp.nsplit * p.M * p.N * sizeof(float) ||
+                              (uintptr_t)ws % 256 != 0))
             return hipErrorInvalidValue;
-        hipError_t e = p.x_dtype == QK_BF16 ? launch_stream_dt<QK_BF16>(p, sp, partial, stream)
-                                            : launch_stream_dt<QK_F16>(p, sp, partial, stream);
-        if (e != hipSuccess || sp.nsplit == 1) return e;
+        uint32_t* ctr = (sp.nsplit > 1 && (size_t)sp.nstrip * 4 <= QK_SPLIT_COUNTER_BYTES)
+                            ? reinterpret_cast<uint32_t*>(ws) : nullptr;
+        hipError_t e = p.x_dtype == QK_BF16 ? launch_stream_dt<QK_BF16>(p, sp, partial, ctr, stream)
+                                            : launch_stream_dt<QK_F16>(p, sp, partial, ctr, stream);
+        if (e != hipSuccess || sp.nsplit == 1 || ctr) return e;
         return p.out_dtype == QK_BF16 ? launch_reduce<QK_BF16>(p, sp.nsplit, partial, stream)
                                       : launch_reduce<QK_F16>(p, sp.nsplit, partial, stream);
     }
@@ -1240,9 +1308,8 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
     }
     const DecodePlan d = decode_plan(p);
     if (d.ok) {
-        float* partial = static_cast<float*>(workspace);
-        if (d.nsplit > 1 && (!partial || ws_bytes < (size_t)d.nsplit * p.M * p.N * sizeof(float) ||
-                             (uintptr_t)partial % 16 != 0))
+        if (d.nsplit > 1 && (!ws || ws_bytes < QK_SPLIT_COUNTER_BYTES + (size_t)d.nsplit * p.M * p.N * sizeof(float) ||
+                             (uintptr_t)ws % 256 != 0))
             return hipErrorInvalidValue;
         hipError_t e = p.x_dtype == QK_BF16 ? launch_decode_dt<QK_BF16>(p, d, partial, stream)
                                             : launch_decode_dt<QK_F16>(p, d, partial, stream);

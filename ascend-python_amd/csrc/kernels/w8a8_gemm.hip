@@ -986,11 +986,13 @@ hipError_t launch_skinny(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial
 
 }  // namespace
 
+// A split workspace is [split-K counters][int32 partials [nsplit][M][N]].
 size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K) {
     const SkinnyPlan s = skinny_plan(M, N, K);
-    if (s.mt != 0) return s.nsplit == 1 ? 0 : (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
+    if (s.mt != 0)
+        return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
     const BigPlan b = big_plan(M, N, K);
-    if (b.ok && b.nsplit > 1) return (size_t)b.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
+    if (b.ok && b.nsplit > 1) return QK_SPLIT_COUNTER_BYTES + (size_t)b.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
     return 0;
 }
 
@@ -1000,19 +1002,19 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
     const bool b_nk = (p.sbk == 1) && (p.sbn % 16 == 0) && ((uintptr_t)p.b % 16 == 0);
     const bool b_kn = (p.sbn == 1) && (p.sbk % 8 == 0) && (p.N % 8 == 0) && ((uintptr_t)p.b % 8 == 0);
     const bool b_kn16 = b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0;
+    char* ws = static_cast<char*>(workspace);
+    int32_t* partial = ws ? reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES) : nullptr;
     const SkinnyPlan sp = skinny_plan(p.M, p.N, p.K);
     if (sp.mt != 0 && a_ok && (b_nk || b_kn16)) {
-        const size_t need = sp.nsplit > 1 ? (size_t)sp.nsplit * p.M * p.N * sizeof(int32_t) : 0;
+        const size_t need = sp.nsplit > 1 ? QK_SPLIT_COUNTER_BYTES + (size_t)sp.nsplit * p.M * p.N * sizeof(int32_t) : 0;
         if (need && (!workspace || ws_bytes < need)) return hipErrorInvalidValue;
-        int32_t* partial = static_cast<int32_t*>(workspace);
         return b_kn16 ? launch_skinny<true>(p, sp, partial, stream) : launch_skinny<false>(p, sp, partial, stream);
     }
     const BigPlan bp = big_plan(p.M, p.N, p.K);
     bool big_ok = bp.ok && a_ok && (b_nk || (b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0));
-    int32_t* partial = static_cast<int32_t*>(workspace);
     if (big_ok && bp.nsplit > 1) {
         // splits need whole aligned tiles and the workspace; otherwise the tiled kernels take the shape
-        const size_t need = (size_t)bp.nsplit * p.M * p.N * sizeof(int32_t);
+        const size_t need = QK_SPLIT_COUNTER_BYTES + (size_t)bp.nsplit * p.M * p.N * sizeof(int32_t);
         big_ok = p.lda < (1 << 24) && p.sbk < (1 << 24) && p.sbn < (1 << 24) && partial && ws_bytes >= need &&
                  (uintptr_t)partial % 16 == 0;
         if (big_ok) {

@@ -5,8 +5,9 @@
 // impl_ns op_api), a host function that checks shapes and dtypes with
 // TORCH_CHECK, allocates every output on the input's device
 // (apply_tensor_without_format, op_plugin/ops/base_ops/opapi/MmKernelNpuOpApi.cpp:27-30),
-// asks for the workspace size, allocates the workspace from the caching
-// allocator (op_plugin/utils/op_api_common.h:547-551), and launches through
+// asks for the workspace size, takes the workspace from the caching
+// allocator (op_plugin/utils/op_api_common.h:547-551; kept per stream here,
+// because its split-K counters persist between calls), and launches through
 // the C ABI on the current stream (op_plugin/utils/op_api_common.h:530).
 // A non-zero ABI return becomes a TORCH_CHECK failure carrying
 // qk_last_error(), as EXEC_NPU_CMD does with aclGetRecentErrMsg()
@@ -19,6 +20,8 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <map>
+#include <mutex>
 #include <optional>
 #include <tuple>
 #include <vector>
@@ -46,8 +49,21 @@ void check_rc(int rc, const char* op) {
     TORCH_CHECK(rc == QK_OK, "call ", op, " failed, detail:", qk_last_error());
 }
 
+// A split workspace starts with counters that must be zero the first time it
+// is used and that every call leaves at zero (include/qk_abi.h), so each
+// (device, stream) keeps one zero-initialised workspace, replaced by a larger
+// one when a call needs more.  Calls on one stream run in order, so they can
+// share it; the zero fill of a new workspace is enqueued on that stream before
+// the call.  The map is never destroyed (its tensors must not outlive the
+// HIP runtime at exit).
 at::Tensor workspace_for(const at::Tensor& like, size_t bytes) {
-    return at::empty({(int64_t)bytes}, like.options().dtype(at::kByte));
+    static std::mutex mu;
+    static auto* cache = new std::map<std::pair<int, qk_stream_t>, at::Tensor>();
+    const auto key = std::make_pair((int)like.device().index(), current_stream(like));
+    std::lock_guard<std::mutex> lock(mu);
+    at::Tensor& ws = (*cache)[key];
+    if (!ws.defined() || (size_t)ws.numel() < bytes) ws = at::zeros({(int64_t)bytes}, like.options().dtype(at::kByte));
+    return ws;
 }
 
 // ---------------------------------------------------------------- npu_dynamic_quant

@@ -42,7 +42,7 @@ extern "C" {
 
 const char* qk_last_error(void) { return g_last_error.c_str(); }
 
-int qk_abi_version(void) { return 1; }
+int qk_abi_version(void) { return 2; }
 
 int qk_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t K, const float* smooth_scales, int8_t* y,
                      float* scale, qk_stream_t stream) {
@@ -102,6 +102,8 @@ int qk_quant_matmul(const int8_t* x1, int64_t ldx1, const int8_t* x2, int64_t x2
     const size_t need = qk::quant_matmul_workspace(M, N, K);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(QK_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, workspace_bytes);
+    if (need > 0 && (uintptr_t)workspace % 256 != 0)
+        return fail(QK_ERR_WORKSPACE, "%s: the workspace must be 256-byte aligned", op);
 
     qk::QmmArgs p;
     p.a = x1;
@@ -155,6 +157,8 @@ int qk_weight_quant_bmm(const void* x, int x_dtype, const void* weight, int weig
     const size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(QK_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, workspace_bytes);
+    if (need > 0 && (uintptr_t)workspace % 256 != 0)
+        return fail(QK_ERR_WORKSPACE, "%s: the workspace must be 256-byte aligned", op);
     qk::WqbmmArgs p;
     p.x = x;
     p.x_dtype = x_dtype;

@@ -22,6 +22,15 @@
  *     message (the reference's aclGetRecentErrMsg(),
  *     op_plugin/utils/op_api_common.h:546, 555).
  * All functions are thread-safe; calls on one stream execute in order.
+ *
+ * Workspaces (this build's one departure from the reference's per-call
+ * scratch): a non-empty workspace begins with QK_SPLIT_COUNTER_BYTES of
+ * split-K arrival counters, followed by the partial sums.  The counters must
+ * be zero the first time a workspace is used -- allocate it once, zero it
+ * (hipMemset), and keep reusing it; every call leaves them zero again.  The
+ * workgroup that completes a tile's splits adds them up itself, so no second
+ * kernel runs.  Calls that may be in flight at the same time need distinct
+ * workspaces.
  */
 #ifndef QK_ABI_H
 #define QK_ABI_H
@@ -57,8 +66,12 @@ enum {
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char* qk_last_error(void);
 
-/* ABI revision; bumped on any incompatible signature change. */
+/* ABI revision; bumped on any incompatible signature or contract change
+ * (2: the split-K counters at the head of a workspace). */
 int qk_abi_version(void);
+
+/* Bytes of split-K counters at the start of every non-empty workspace. */
+#define QK_SPLIT_COUNTER_BYTES 4096
 
 /*
  * npu_dynamic_quant -- replaces aclnnDynamicQuant behind EXEC_NPU_CMD

@@ -420,7 +420,7 @@ def test_abi_quant_matmul_matches_op(ops, oracle):
     import ctypes
     ws = ctypes.c_size_t(0)
     assert L.qk_quant_matmul_workspace_size(M, N, K, BF16, ctypes.byref(ws)) == 0
-    wsbuf = torch.empty(max(1, ws.value), dtype=torch.uint8, device=DEV)
+    wsbuf = torch.zeros(max(1, ws.value), dtype=torch.uint8, device=DEV)   # split-K counters start at zero
     rc = L.qk_quant_matmul(a.data_ptr(), K, w.data_ptr(), N, 1, M, N, K, s.data_ptr(), N, None, 0, pt.data_ptr(),
                            b.data_ptr(), BF16, out.data_ptr(), BF16, wsbuf.data_ptr(), ws.value, _stream())
     assert rc == 0, ops.last_error()
@@ -531,3 +531,31 @@ def test_abi_dynamic_quant_and_w4a16(ops, oracle):
     assert rc == 0, ops.last_error()
     torch.cuda.synchronize()
     bf16_close(to_bits(out), _w4_ref(oracle, d, 128))
+
+
+def test_abi_split_workspace_reuse(ops, oracle):
+    """A split-K call through the ABI: one zeroed workspace reused by several calls of different shapes
+    (each call must leave the counters at zero for the next), every result against the oracle."""
+    say("ABI qk_weight_quant_bmm split workspace reuse")
+    import ctypes
+    L = ops.abi()
+    cases = [W.W4A16Case(M=16, N=11008, K=4096), W.W4A16Case(M=5, N=2048, K=2048), W.W4A16Case(M=16, N=11008, K=4096)]
+    need = []
+    for c in cases:
+        n = ctypes.c_size_t(0)
+        assert L.qk_weight_quant_bmm_workspace_size(c.M, c.N, c.K, I32, 128, ctypes.byref(n)) == 0
+        need.append(n.value)
+    assert min(need) > 0, "the shapes must split K"
+    wsbuf = torch.zeros(max(need), dtype=torch.uint8, device=DEV)
+    for i, c in enumerate(cases):
+        d = W.w4a16_inputs(c, seed=20 + i)
+        xd, wd, sd, od = (d[k].to(DEV) for k in ("x", "w_packed", "scale", "offset"))
+        out = torch.empty((c.M, c.N), dtype=torch.bfloat16, device=DEV)
+        rc = L.qk_weight_quant_bmm(xd.data_ptr(), BF16, wd.data_ptr(), I32, sd.data_ptr(), od.data_ptr(), F16, c.M,
+                                   c.N, c.K, 128, None, 0, out.data_ptr(), BF16, wsbuf.data_ptr(), wsbuf.numel(),
+                                   _stream())
+        assert rc == 0, ops.last_error()
+        torch.cuda.synchronize()
+        bf16_close(to_bits(out), _w4_ref(oracle, d, 128))
+    head = wsbuf[:4096].cpu()
+    assert int(head.count_nonzero()) == 0, "split-K counters must be left at zero"

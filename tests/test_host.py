@@ -28,7 +28,7 @@ def test_abi_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), f"{n} declared in qk_abi.h but not exported"
     assert set(names) == set(q.ABI_SYMBOLS)
-    assert q.abi().qk_abi_version() == 1
+    assert q.abi().qk_abi_version() == 2
 
 
 def test_abi_refuses_bad_arguments_without_launch():
