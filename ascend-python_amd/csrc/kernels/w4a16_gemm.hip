@@ -383,7 +383,9 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
 // block by block before its first MFMA.  The K ranges are added through LDS
 // in order (deterministic), each thread finishing 4 columns of one row.  With
 // one split the sums are the output (+bias, cast); otherwise fp32 partials
-// [split][M][N] for w4_reduce.
+// [split][M][N]: with a counter array (ctr) they are stored device-coherent
+// and the strip's last split to arrive adds them in split order, adds bias
+// and casts (one kernel); without one, w4_reduce finishes.
 // W8 (int8 weights [K, N], W8A16): a strip is 64 dwords (256 columns, two
 // lines per row), slot c owns dword c of its sub-strip and its 4 bytes (4
 // MFMA tiles, columns 4c + t), and the operands are the exact 16-bit values

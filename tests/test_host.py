@@ -145,3 +145,28 @@ def test_product_path_has_no_cpu_kernel():
     """The ops have no CPU implementation: a CPU tensor is refused, never computed on the host."""
     with pytest.raises(NotImplementedError):
         q.npu_dynamic_quant(torch.zeros((2, 8), dtype=torch.float16))
+
+
+def test_fast_quantizer_rule():
+    """The kernels' quantizer (csrc/kernels/common.h, row_quant / quant_row) replaces rint(RN(v / s)) by
+    rint(RN(v * RN(1/s))) wherever that product lies farther than 2^-14 from a half-integer, and divides
+    otherwise.  Checked here in float32 against the IEEE division on rows of widely varying magnitude, a third
+    of them holding exact ties (k + 0.5) * s, where a reciprocal-multiply alone goes wrong."""
+    import numpy as np
+
+    rng = np.random.default_rng(1)
+    f32 = np.float32
+    slow = 0
+    for trial in range(24):
+        v = (rng.standard_normal(16384) * 2.0 ** int(rng.integers(-60, 60))).astype(f32)
+        s = f32(f32(np.max(np.abs(v))) / f32(127))
+        if trial % 3 == 0:
+            v[:1000] = ((rng.integers(-126, 126, 1000).astype(f32) + f32(0.5)) * s).astype(f32)
+            s = f32(f32(np.max(np.abs(v))) / f32(127))
+        ref = np.clip(np.rint((v / s).astype(f32)), -128, 127)
+        t = (v * f32(f32(1) / s)).astype(f32)
+        fast = np.abs((t - (np.floor(t) + f32(0.5)).astype(f32)).astype(f32)) > f32(2.0 ** -14)
+        got = np.where(fast, np.clip(np.rint(t), -128, 127), ref)
+        assert np.array_equal(got, ref), trial
+        slow += int(np.sum(~fast))
+    assert slow >= 8 * 1000  # the tie rows took the division path
