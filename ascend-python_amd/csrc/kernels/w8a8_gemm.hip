@@ -504,25 +504,32 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
 // as qmm_big, but the operands never pass through registers.  Each
 // buffer_load_dwordx4 ... lds writes one wave's 64 x 16 bytes to 1 KB of LDS
 // at m0, so the swizzle is applied on the global side: lane l of an
-// instruction fetches the chunk that belongs at LDS byte 16*l.  Four LDS
-// stages of 64 K-bytes (32 KB each) form a ring: while stage kt is
-// multiplied, stages kt+1..kt+3 are in flight, and the fragments of stage
-// kt+1 are read into the second register set.  One barrier per stage, after
-// this wave's part of stage kt+1 has landed (vmcnt counts the wave's DMA
-// instructions in order).
-//   [row][64 B] tiles (A, [N,K] weight): chunk c of row r at r*64 + 16*(c ^ ((r>>1)&3))
-//   [k][256 B]  tiles ([K,N] weight):    chunk c of row k at k*256 + 16*(c ^ h(k)),
+// instruction fetches the chunk that belongs at LDS byte 16*l.  The MFMAs step
+// through K 64 bytes at a time.  The weight sits in a ring of four 64-K stages
+// (16 KB each); A sits in a ring of three 128-K slots (32 KB each), so every
+// A DMA fetches whole 128-byte lines (a 64-K stage of A would fetch each line
+// in two halves, at two different times).  Iteration kt issues the weight
+// stage kt+4 and one half (128 rows) of A slot ((kt-1)>>1)+3, reads the
+// fragments of stage kt+1 into the second register set and multiplies stage
+// kt; stages kt+2..kt+4 stay in flight.  One barrier per stage, after this
+// wave's part of stage kt+1 has landed (vmcnt counts the wave's DMA
+// instructions in order, four per iteration).
+//   [row][128 B] A slots:                chunk c of row r at r*128 + 16*(c ^ ((r>>1)&7))
+//   [row][64 B] weight stages ([N,K]):   chunk c of row r at r*64 + 16*(c ^ ((r>>1)&3))
+//   [k][256 B]  weight stages ([K,N]):   chunk c of row k at k*256 + 16*(c ^ h(k)),
 //                                         h(k) = (k&7) | ((k>>4)&1)<<3
-// Both are free of LDS bank conflicts for the fragment reads (b128 row
+// All three are free of LDS bank conflicts for the fragment reads (b128 row
 // reads; transpose reads for [K,N]), measured with SQ_LDS_BANK_CONFLICT.
 namespace dm {
 constexpr int BM = 256, BN = 256, BK = 64, NST = 4, NW = 8, NT = 64 * NW;
 constexpr int TM = 4;                   // 64-row wave tiles: 4 x 8 MFMA tiles
-constexpr int A_ST = BM * BK, B_ST = BN * BK;
-constexpr int A_BASE = NST * B_ST;      // A stages follow the B stages, so every fragment read offset fits the
-                                        // 16-bit immediate of ds_read
+constexpr int B_ST = BN * BK;           // one weight stage (16 KB)
+constexpr int A_KB = 128, NSA = 3;      // A slots: 128 K-bytes each, three of them
+constexpr int A_SL = BM * A_KB;         // one A slot (32 KB)
+constexpr int A_BASE = NST * B_ST;      // A slots follow the weight stages
 constexpr int OUT_BYTES = BM * (2 * BN + 16);
-constexpr int SMEM = NST * (A_ST + B_ST) > OUT_BYTES ? NST * (A_ST + B_ST) : OUT_BYTES;
+constexpr int RING = NST * B_ST + NSA * A_SL;  // 160 KB: all of the CU's LDS
+constexpr int SMEM = RING > OUT_BYTES ? RING : OUT_BYTES;
 constexpr int NDMA = 16 / NW;           // DMA instructions per wave per operand per stage
 constexpr int VPS = 2 * NDMA;           // of which vmcnt counts per stage
 
@@ -571,8 +578,11 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     const __amdgpu_buffer_rsrc_t rsB = B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
                                             : make_rsrc(p.b + n0 * p.sbn, (uint32_t)(BN * p.sbn));
     const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)(B_KN ? p.sbk : p.sbn);
-    // [row][64 B]: one instruction = 16 rows; lane l -> row l>>2, LDS chunk l&3
-    const uint32_t vrk_a = (uint32_t)(lane >> 2) * lda + 16u * (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
+    // A [row][128 B]: one instruction = 8 rows 8b..8b+7; lane l -> row l>>3, LDS chunk l&7, and
+    // (r>>1)&7 = 4*(b&1) + (l>>4)
+    const uint32_t va0 = (uint32_t)(lane >> 3) * lda + 16u * (uint32_t)((lane & 7) ^ (lane >> 4));
+    const uint32_t va1 = (uint32_t)(lane >> 3) * lda + 16u * (uint32_t)((lane & 7) ^ (4 + (lane >> 4)));
+    // [N,K] weight [row][64 B]: one instruction = 16 rows; lane l -> row l>>2, LDS chunk l&3
     const uint32_t vrk_b = (uint32_t)(lane >> 2) * ldb + 16u * (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
     // [k][256 B]: one instruction = 4 rows 4b..4b+3 (b = NDMA*wave + i); lane l -> row l>>4, LDS chunk
     // l&15, and h = 4*(b&1) + (l>>4) + 8*((b>>2)&1)
@@ -580,30 +590,54 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     const uint32_t vkn0 = (uint32_t)(lane >> 4) * ldb + 16u * (uint32_t)((lane & 15) ^ ((lane >> 4) + hb));
     const uint32_t vkn1 = (uint32_t)(lane >> 4) * ldb + 16u * (uint32_t)((lane & 15) ^ (4 + (lane >> 4) + hb));
 
-    auto issue = [&](int kt, int st) {
+    const int nk = (int)(k_len / dm::BK);  // a multiple of NST (checked on the host)
+    const int nr = nk / 2;                 // A slots' worth of K
+    auto issue_b = [&](int kt, int st) {
         const uint32_t k0 = k_base + (uint32_t)kt * dm::BK;
 #pragma unroll
         for (int i = 0; i < NDMA; ++i) {
             const int b = NDMA * wave + i;
-            dma16(rsA, sbase + A_BASE + st * A_ST + b * 1024, vrk_a, (uint32_t)(16 * b) * lda + k0);
             if constexpr (B_KN)
                 dma16(rsB, sbase + st * B_ST + b * 1024, (i & 1) ? vkn1 : vkn0, (k0 + 4u * b) * ldb);
             else
                 dma16(rsB, sbase + st * B_ST + b * 1024, vrk_b, (uint32_t)(16 * b) * ldb + k0);
         }
     };
+    // rows 128h..128h+127 of A range r (K bytes 128r..128r+127 of this split) into slot r % 3.  Past the
+    // last range the final range is fetched again into the slot nobody reads any more, so every iteration
+    // issues the same number of DMAs and the vmcnt arithmetic stays uniform.
+    auto issue_a = [&](int r, int h) {
+        const int rs = r < nr ? r : nr - 1;
+        const uint32_t lds = sbase + A_BASE + (uint32_t)(r % NSA) * A_SL;
+        const uint32_t k0 = k_base + (uint32_t)rs * A_KB;
+#pragma unroll
+        for (int i = 0; i < NDMA; ++i) {
+            const int b = 16 * h + NDMA * wave + i;
+            dma16(rsA, lds + b * 1024, i ? va1 : va0, (uint32_t)(8 * b) * lda + k0);
+        }
+    };
+    // iteration kt's DMAs: weight stage kt+4 and half (kt+1)&1 of A range ((kt-1)>>1)+3.  That range's
+    // slot held range ((kt-1)>>1), whose last fragments (those of stage kt or kt-1) were read before
+    // this iteration's barrier.
+    auto issue = [&](int kt, int st) {
+        issue_a(((kt - 1) >> 1) + 3, (kt + 1) & 1);
+        issue_b(kt + NST, st);
+    };
 
-    // fragment read offsets for stage 0 (stage st adds st * 16 KB)
-    const int a_rd = A_BASE + (wm * 64 + fr) * 64 + 16 * (g ^ ((fr >> 1) & 3));
+    // fragment read offsets: A for the low / high 64 K-bytes of a slot (slot s adds s * 32 KB); the
+    // weight for stage 0 (stage st adds st * 16 KB)
+    const int a_rd0 = A_BASE + (wm * 64 + fr) * A_KB + 16 * (g ^ ((fr >> 1) & 7));
+    const int a_rd1 = A_BASE + (wm * 64 + fr) * A_KB + 16 * ((4 + g) ^ ((fr >> 1) & 7));
     const int b_rd = (wn * 128 + fr) * 64 + 16 * (g ^ ((fr >> 1) & 3));
     // transpose reads: lanes 2b / 2b+1 of each 16-lane group address k row 16g + b (and +8), columns
     // 0..7 / 8..15 of the 16-column tile, whose chunk index is XOR-ed by h(k)
     const int t_rd = (16 * g + (fr >> 1)) * 256 + 128 * (wn ^ (g & 1)) + 8 * (fr & 1);
     const int xr = fr >> 1;
 
-    auto frags = [&](int st, i32x4 (&af)[TM], i32x4 (&bfr)[8]) {
+    auto frags = [&](int kt, int st, i32x4 (&af)[TM], i32x4 (&bfr)[8]) {
+        const int ard = ((kt & 1) ? a_rd1 : a_rd0) + ((kt >> 1) % NSA) * A_SL;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i32x4*>(smem + a_rd + st * A_ST + i * 1024);
+        for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i32x4*>(smem + ard + i * 16 * A_KB);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if constexpr (!B_KN) {
@@ -630,15 +664,18 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bfr[j], acc[i][j], 0, 0, 0);
     };
 
-    const int nk = (int)(k_len / dm::BK);  // a multiple of NST (checked on the host)
-    issue(0, 0);
-    issue(1, 1);
-    issue(2, 2);
-    issue(3, 3);
+    // prologue: the groups of iterations -4..-1 (weight stages 0..3, A ranges 0 and 1 and the first half
+    // of range 2), preceded by the first half of range 0
+    issue_a(0, 0);
+#pragma unroll
+    for (int kt = -NST; kt < 0; ++kt) {
+        issue_a(((kt - 1) >> 1) + 3, (kt + 1) & 1);
+        issue_b(kt + NST, kt + NST);
+    }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * VPS));
     __syncthreads();
     i32x4 fa[2][TM], fb[2][8];
-    frags(0, fa[0], fb[0]);
+    frags(0, 0, fa[0], fb[0]);
 
     // stages 0 .. nk-NST-1: stage kt+1 must have landed, kt+2 and kt+3 stay in flight; buffer kt&3 is free
     // once every wave is past the barrier (its fragments are in registers), so stage kt+4 goes there
@@ -648,8 +685,8 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
             const int cur = u & 1;
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * VPS));
             __syncthreads();
-            issue(kt0 + u + NST, u);
-            frags((u + 1) & 3, fa[cur ^ 1], fb[cur ^ 1]);
+            issue(kt0 + u, u);
+            frags(kt0 + u + 1, (u + 1) & 3, fa[cur ^ 1], fb[cur ^ 1]);
             mma(fa[cur], fb[cur]);
         }
     }
@@ -662,7 +699,7 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
             else if (u == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(VPS));
             else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
-            frags((u + 1) & 3, fa[cur ^ 1], fb[cur ^ 1]);
+            frags(nk - NST + u + 1, (u + 1) & 3, fa[cur ^ 1], fb[cur ^ 1]);
         }
         mma(fa[cur], fb[cur]);
     }
