@@ -534,14 +534,20 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
 
     // each thread finishes 4 consecutive columns of one row, summing the K ranges in order
     constexpr int QUADS = 16 * 256 / 4;
+    constexpr int QPT = QUADS / (64 * NWAVE);  // quads per thread
+    static_assert(QPT * 64 * NWAVE == QUADS, "every thread finishes the same number of quads");
     const __amdgpu_buffer_rsrc_t prs = make_rsrc(partial, (uint32_t)((int64_t)nsplit * M * N * 4));
     const int n_strip0 = strip * 256;
-    for (int q = threadIdx.x; q < QUADS; q += 64 * NWAVE) {
+    f32x4 own[QPT];  // this split's sums, reused if this workgroup finishes the strip
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+        const int q = threadIdx.x + i * 64 * NWAVE;
         const int row = q >> 6, col = 4 * (q & 63);
         const int hh = col / NCOL, local = col % NCOL;
         f32x4 v = *reinterpret_cast<const f32x4*>(&red[hh][row][local]);
 #pragma unroll
         for (int w = 1; w < KW; ++w) v += *reinterpret_cast<const f32x4*>(&red[hh + HALVES * w][row][local]);
+        own[i] = v;
         const int mm = rb * 16 + row, n = n_strip0 + col;
         if (mm >= M || n >= N) continue;
         if (FINAL) {
@@ -568,7 +574,6 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
     // split-K: the last split of this strip to finish adds all splits in split order (deterministic)
     if constexpr (!FINAL) {
         if (ctr == nullptr || !splitk_last(ctr + (int64_t)rb * nstrip + strip, (uint32_t)nsplit)) return;
-        constexpr int QPT = QUADS / (64 * NWAVE);  // quads per thread
         uint32_t qoff[QPT];
         bool qok[QPT];
 #pragma unroll
@@ -578,7 +583,8 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
             qok[i] = mm < M && n < N;
             qoff[i] = (uint32_t)(qok[i] ? (int64_t)mm * N + n : 0) * 4u;
         }
-        // four splits' loads in flight at a time, added in split order
+        // four splits' loads in flight at a time (this split's own sums come from registers), added in
+        // split order
         const uint32_t sstride = (uint32_t)((int64_t)M * N * 4);
         f32x4 v[QPT];
         for (int s0 = 0; s0 < nsplit; s0 += 4) {
@@ -586,11 +592,14 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int i = 0; i < QPT; ++i)
-                    if (s0 + j < nsplit)
+                for (int i = 0; i < QPT; ++i) {
+                    if (s0 + j == split)
+                        part[j][i] = own[i];
+                    else if (s0 + j < nsplit)
                         part[j][i] = __builtin_bit_cast(
                             f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, qoff[i], (uint32_t)(s0 + j) * sstride,
                                                                          kCoherent));
+                }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -1046,7 +1055,7 @@ DecodePlan decode_plan(const WqbmmArgs& p) {
         // few output tiles (decode): split K so every wave owns 256 rows and
         // issues all its loads at once; otherwise keep doubling splits while
         // workgroups are short of ~2 per CU
-        if (p.K % 512 == 0 && (p.K / 512) * tiles <= 4096 && (p.N / 8) % 4 == 0) {
+        if (p.K % 512 == 0 && (p.K / 512) * tiles <= 4096 && (p.N / 8) % 4 == 0 && d.piece_kb != 1) {
             s = (int)(p.K / 512);
             d.upfront = true;
         } else {
@@ -1076,8 +1085,9 @@ hipError_t launch_decode_t(const WqbmmArgs& p, const DecodePlan& d, float* parti
     const dim3 grid((uint32_t)((int64_t)d.nstrip * d.nsplit * d.nrb));
     if (d.nsplit == 1)
         w4_decode<DT, PKB, HAS_OFF, true, false><<<grid, dim3(kThreads), 0, stream>>>(p, partial, 1, d.nstrip);
-    else if (d.upfront)
-        w4_decode<DT, PKB, HAS_OFF, false, true><<<grid, dim3(kThreads), 0, stream>>>(p, partial, d.nsplit, d.nstrip);
+    else if (PKB != 1 && d.upfront)  // 32-row groups hold 8 scale pieces per wave up front: too many registers
+        w4_decode<DT, PKB != 1 ? PKB : 2, HAS_OFF, false, true><<<grid, dim3(kThreads), 0, stream>>>(p, partial, d.nsplit,
+                                                                                                      d.nstrip);
     else
         w4_decode<DT, PKB, HAS_OFF, false, false><<<grid, dim3(kThreads), 0, stream>>>(p, partial, d.nsplit, d.nstrip);
     return hipGetLastError();
@@ -1121,7 +1131,7 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
         if (std::strcmp(e, "off") == 0) return s;
         int a = 0, b = 0, c = 0;
         if (std::sscanf(e, "%d,%d,%d", &a, &b, &c) == 3 && (a == 8 || a == 16) &&
-            ((b == 4 && (c == 2 || c == 4)) || (b == 8 && (c == 2 || c == 3)))) {
+            ((b == 4 && (c == 2 || c == 4)) || (a == 8 && b == 8 && (c == 2 || c == 3)))) {
             s.nwave = a;
             s.nkb = b;
             s.pf = c;
@@ -1178,14 +1188,18 @@ hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* parti
         }
         return hipErrorInvalidValue;
     }
-    switch (s.piece_kb) {
-    case 1: return launch_stream_t<DT, NWAVE, 4, 2, 1, HAS_OFF, false>(p, s, partial, ctr, stream);
-    case 2: return launch_stream_t<DT, NWAVE, 4, 2, 2, HAS_OFF, false>(p, s, partial, ctr, stream);
-    default: break;
+    if constexpr (NWAVE == 8) {  // short groups and 8-row-block waves run 8-wave strips only (16 would spill)
+        switch (s.piece_kb) {
+        case 1: return launch_stream_t<DT, 8, 4, 2, 1, HAS_OFF, false>(p, s, partial, ctr, stream);
+        case 2: return launch_stream_t<DT, 8, 4, 2, 2, HAS_OFF, false>(p, s, partial, ctr, stream);
+        default: break;
+        }
+        if (s.nkb == 8)
+            return s.pf == 3 ? launch_stream_t<DT, 8, 8, 3, 4, HAS_OFF, false>(p, s, partial, ctr, stream)
+                             : launch_stream_t<DT, 8, 8, 2, 4, HAS_OFF, false>(p, s, partial, ctr, stream);
+    } else if (s.piece_kb != 4 || s.nkb != 4) {
+        return hipErrorInvalidValue;  // not planned (stream_plan gives these shapes 8 waves)
     }
-    if (s.nkb == 8)
-        return s.pf == 3 ? launch_stream_t<DT, NWAVE, 8, 3, 4, HAS_OFF, false>(p, s, partial, ctr, stream)
-                         : launch_stream_t<DT, NWAVE, 8, 2, 4, HAS_OFF, false>(p, s, partial, ctr, stream);
     return s.pf == 4 ? launch_stream_t<DT, NWAVE, 4, 4, 4, HAS_OFF, false>(p, s, partial, ctr, stream)
                      : launch_stream_t<DT, NWAVE, 4, 2, 4, HAS_OFF, false>(p, s, partial, ctr, stream);
 }

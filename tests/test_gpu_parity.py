@@ -433,7 +433,7 @@ def test_abi_quant_matmul_matches_op(ops, oracle):
     assert rc == -1 and "transposed view" in ops.last_error()
 
 
-@pytest.mark.parametrize("cfg", ["16,4,2", "16,4,4", "16,8,2", "16,8,3", "8,4,2", "8,8,3"])
+@pytest.mark.parametrize("cfg", ["16,4,2", "16,4,4", "8,4,2", "8,4,4", "8,8,2", "8,8,3"])
 def test_w4a16_stream_configs(ops, oracle, monkeypatch, cfg):
     """Every wave count / K-blocks per wave / prefetch depth of the decode stream kernel (forced through its
     tuning variable)."""
