@@ -308,8 +308,10 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
         }
         __syncthreads();
         constexpr int CPRO = 2 * BN / 16;  // 16-byte chunks per output row
+        static_assert(BM * CPRO % NT == 0, "whole chunks per thread");
 #pragma unroll
-        for (int q = tid; q < BM * CPRO; q += NT) {
+        for (int it = 0; it < BM * CPRO / NT; ++it) {
+            const int q = tid + it * NT;
             const int row = q / CPRO, c = q % CPRO;
             const i32x4 v = *reinterpret_cast<const i32x4*>(smem + row * ROWB + 16 * c);
             *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo + n0 + 8 * c) = v;
@@ -508,12 +510,11 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
 // through K 64 bytes at a time.  The weight sits in a ring of four 64-K stages
 // (16 KB each); A sits in a ring of three 128-K slots (32 KB each), so every
 // A DMA fetches whole 128-byte lines (a 64-K stage of A would fetch each line
-// in two halves, at two different times).  Iteration kt issues the weight
-// stage kt+4 and one half (128 rows) of A slot ((kt-1)>>1)+3, reads the
-// fragments of stage kt+1 into the second register set and multiplies stage
-// kt; stages kt+2..kt+4 stay in flight.  One barrier per stage, after this
-// wave's part of stage kt+1 has landed (vmcnt counts the wave's DMA
-// instructions in order, four per iteration).
+// in two halves, at two different times).  The eight waves form two groups
+// (rows 0-127 and 128-255 of the tile, one wave of each per SIMD) that run
+// half a stage apart: while one group issues its MFMAs the other reads its
+// next fragments and issues DMAs (group 0 A, group 1 the weight), with two
+// barriers per stage.  vmcnt counts a wave's DMA instructions in order.
 //   [row][128 B] A slots:                chunk c of row r at r*128 + 16*(c ^ ((r>>1)&7))
 //   [row][64 B] weight stages ([N,K]):   chunk c of row r at r*64 + 16*(c ^ ((r>>1)&3))
 //   [k][256 B]  weight stages ([K,N]):   chunk c of row k at k*256 + 16*(c ^ h(k)),
@@ -530,8 +531,6 @@ constexpr int A_BASE = NST * B_ST;      // A slots follow the weight stages
 constexpr int OUT_BYTES = BM * (2 * BN + 16);
 constexpr int RING = NST * B_ST + NSA * A_SL;  // 160 KB: all of the CU's LDS
 constexpr int SMEM = RING > OUT_BYTES ? RING : OUT_BYTES;
-constexpr int NDMA = 16 / NW;           // DMA instructions per wave per operand per stage
-constexpr int VPS = 2 * NDMA;           // of which vmcnt counts per stage
 
 // s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt[3:0], [15:14]; others at their maximum)
 constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
@@ -570,6 +569,8 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
+    const int pg = wave >> 2;  // ping-pong group: waves 0-3 own rows 0-127, waves 4-7 rows 128-255
+    const int gw = wave & 3;   // wave within its group
     const int fr = lane & 15, g = lane >> 4;
 
     // buffer views of this tile's operand rows (sizes checked on the host to fit 32 bits)
@@ -584,44 +585,38 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     const uint32_t va1 = (uint32_t)(lane >> 3) * lda + 16u * (uint32_t)((lane & 7) ^ (4 + (lane >> 4)));
     // [N,K] weight [row][64 B]: one instruction = 16 rows; lane l -> row l>>2, LDS chunk l&3
     const uint32_t vrk_b = (uint32_t)(lane >> 2) * ldb + 16u * (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
-    // [k][256 B]: one instruction = 4 rows 4b..4b+3 (b = NDMA*wave + i); lane l -> row l>>4, LDS chunk
-    // l&15, and h = 4*(b&1) + (l>>4) + 8*((b>>2)&1)
-    const int hb = 8 * (((NDMA * wave) >> 2) & 1);
+    // [k][256 B]: one instruction = 4 rows 4b..4b+3 (b = 4*gw + i); lane l -> row l>>4, LDS chunk l&15, and
+    // h = 4*(b&1) + (l>>4) + 8*((b>>2)&1), (b>>2)&1 = gw&1
+    const int hb = 8 * (gw & 1);
     const uint32_t vkn0 = (uint32_t)(lane >> 4) * ldb + 16u * (uint32_t)((lane & 15) ^ ((lane >> 4) + hb));
     const uint32_t vkn1 = (uint32_t)(lane >> 4) * ldb + 16u * (uint32_t)((lane & 15) ^ (4 + (lane >> 4) + hb));
 
     const int nk = (int)(k_len / dm::BK);  // a multiple of NST (checked on the host)
     const int nr = nk / 2;                 // A slots' worth of K
+    // group 1 issues the weight: stage kt into buffer st, four instructions per wave (a stage past the end
+    // fetches the last one again into its free buffer, so every stage issues the same number of DMAs)
     auto issue_b = [&](int kt, int st) {
-        const uint32_t k0 = k_base + (uint32_t)kt * dm::BK;
+        const uint32_t k0 = k_base + (uint32_t)(kt < nk ? kt : nk - 1) * dm::BK;
 #pragma unroll
-        for (int i = 0; i < NDMA; ++i) {
-            const int b = NDMA * wave + i;
+        for (int i = 0; i < 4; ++i) {
+            const int b = 4 * gw + i;
             if constexpr (B_KN)
                 dma16(rsB, sbase + st * B_ST + b * 1024, (i & 1) ? vkn1 : vkn0, (k0 + 4u * b) * ldb);
             else
                 dma16(rsB, sbase + st * B_ST + b * 1024, vrk_b, (uint32_t)(16 * b) * ldb + k0);
         }
     };
-    // rows 128h..128h+127 of A range r (K bytes 128r..128r+127 of this split) into slot r % 3.  Past the
-    // last range the final range is fetched again into the slot nobody reads any more, so every iteration
-    // issues the same number of DMAs and the vmcnt arithmetic stays uniform.
+    // group 0 issues A: rows 128h..128h+127 of range r (K bytes 128r..128r+127 of this split) into slot
+    // r % 3 (past the last range, the last range again)
     auto issue_a = [&](int r, int h) {
         const int rs = r < nr ? r : nr - 1;
         const uint32_t lds = sbase + A_BASE + (uint32_t)(r % NSA) * A_SL;
         const uint32_t k0 = k_base + (uint32_t)rs * A_KB;
 #pragma unroll
-        for (int i = 0; i < NDMA; ++i) {
-            const int b = 16 * h + NDMA * wave + i;
-            dma16(rsA, lds + b * 1024, i ? va1 : va0, (uint32_t)(8 * b) * lda + k0);
+        for (int i = 0; i < 4; ++i) {
+            const int b = 16 * h + 4 * gw + i;
+            dma16(rsA, lds + b * 1024, (i & 1) ? va1 : va0, (uint32_t)(8 * b) * lda + k0);
         }
-    };
-    // iteration kt's DMAs: weight stage kt+4 and half (kt+1)&1 of A range ((kt-1)>>1)+3.  That range's
-    // slot held range ((kt-1)>>1), whose last fragments (those of stage kt or kt-1) were read before
-    // this iteration's barrier.
-    auto issue = [&](int kt, int st) {
-        issue_a(((kt - 1) >> 1) + 3, (kt + 1) & 1);
-        issue_b(kt + NST, st);
     };
 
     // fragment read offsets: A for the low / high 64 K-bytes of a slot (slot s adds s * 32 KB); the
@@ -634,7 +629,8 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     const int t_rd = (16 * g + (fr >> 1)) * 256 + 128 * (wn ^ (g & 1)) + 8 * (fr & 1);
     const int xr = fr >> 1;
 
-    auto frags = [&](int kt, int st, i32x4 (&af)[TM], i32x4 (&bfr)[8]) {
+    i32x4 af[TM], bfr[8];
+    auto frags = [&](int kt, int st) {
         const int ard = ((kt & 1) ? a_rd1 : a_rd0) + ((kt >> 1) % NSA) * A_SL;
 #pragma unroll
         for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i32x4*>(smem + ard + i * 16 * A_KB);
@@ -656,53 +652,82 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = (i32x4){0, 0, 0, 0};
-    auto mma = [&](const i32x4 (&af)[TM], const i32x4 (&bfr)[8]) {
+    auto mma = [&]() {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < 8; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bfr[j], acc[i][j], 0, 0, 0);
     };
+    // a barrier nothing is scheduled across (the compiler would otherwise hoist MFMAs above it)
+    auto bar = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    constexpr int LGKM0 = 0xc07f;  // s_waitcnt lgkmcnt(0) alone
 
-    // prologue: the groups of iterations -4..-1 (weight stages 0..3, A ranges 0 and 1 and the first half
-    // of range 2), preceded by the first half of range 0
-    issue_a(0, 0);
-#pragma unroll
-    for (int kt = -NST; kt < 0; ++kt) {
-        issue_a(((kt - 1) >> 1) + 3, (kt + 1) & 1);
-        issue_b(kt + NST, kt + NST);
+    // Ping-pong: the two groups run half a stage apart, so while one issues its 32 MFMAs the other reads
+    // fragments and issues DMAs, and every SIMD (one wave of each group) always has MFMAs to run.
+    //   half-step 2t:   group 0 multiplies stage t;  group 1 reads stage t, issues weight stage t+3
+    //   half-step 2t+1: group 0 reads stage t+1, issues half (t+1)&1 of A range (t+5)>>1;  group 1 multiplies t
+    // A range R goes out at t = 2R-5 and 2R-4: after its slot's last reader (range R-3, group 1 at half-step
+    // 4R-10) and four half-steps before its first reader (group 0 at half-step 4R-1).  Weight stage s goes out
+    // at half-step 2s-6, after its buffer's last reader (stage s-4, group 1 at 2s-8).  Each wave issues four
+    // DMAs per stage; waiting for all but the last two stages' (vmcnt(8)) before the barrier that ends
+    // half-step 2t lands everything stage t+1 needs (its A range went out at loop index t-3 at the latest,
+    // its weight at t-2).
+    // Both groups pass the same barriers in the same order.
+    if (pg == 0) {  // loop indices -5..-1: A ranges 0, 1 and the first half of range 2
+        issue_a(0, 0);
+        issue_a(0, 1);
+        issue_a(1, 0);
+        issue_a(1, 1);
+        issue_a(2, 0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(12));  // range 0 (stages 0 and 1)
+    } else {        // loop indices -3..-1: weight stages 0..2
+        issue_b(0, 0);
+        issue_b(1, 1);
+        issue_b(2, 2);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));   // stage 0
     }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * VPS));
-    __syncthreads();
-    i32x4 fa[2][TM], fb[2][8];
-    frags(0, 0, fa[0], fb[0]);
-
-    // stages 0 .. nk-NST-1: stage kt+1 must have landed, kt+2 and kt+3 stay in flight; buffer kt&3 is free
-    // once every wave is past the barrier (its fragments are in registers), so stage kt+4 goes there
-    for (int kt0 = 0; kt0 < nk - NST; kt0 += NST) {
+    bar();
+    if (pg == 0) {
+        frags(0, 0);
+        __builtin_amdgcn_s_waitcnt(LGKM0);
+    }
+    bar();
+    if (pg == 0) {
+        for (int t0 = 0; t0 < nk; t0 += NST) {
 #pragma unroll
-        for (int u = 0; u < NST; ++u) {
-            const int cur = u & 1;
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * VPS));
-            __syncthreads();
-            issue(kt0 + u, u);
-            frags(kt0 + u + 1, (u + 1) & 3, fa[cur ^ 1], fb[cur ^ 1]);
-            mma(fa[cur], fb[cur]);
+            for (int u = 0; u < NST; ++u) {
+                const int t = t0 + u;
+                mma();
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+                bar();
+                if (t + 1 < nk) frags(t + 1, (u + 1) & 3);
+                issue_a((t + 5) >> 1, (t + 1) & 1);
+                __builtin_amdgcn_s_waitcnt(LGKM0);
+                bar();
+            }
+        }
+    } else {
+        for (int t0 = 0; t0 < nk; t0 += NST) {
+#pragma unroll
+            for (int u = 0; u < NST; ++u) {
+                const int t = t0 + u;
+                frags(t, u);
+                issue_b(t + 3, (u + 3) & 3);
+                __builtin_amdgcn_s_waitcnt(LGKM0);
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+                bar();
+                mma();
+                bar();
+            }
         }
     }
-    // the last NST stages (buffers 0..3): nothing more to issue
-#pragma unroll
-    for (int u = 0; u < NST; ++u) {
-        const int cur = u & 1;
-        if (u < NST - 1) {
-            if (u == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * VPS));
-            else if (u == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(VPS));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            __syncthreads();
-            frags(nk - NST + u + 1, (u + 1) & 3, fa[cur ^ 1], fb[cur ^ 1]);
-        }
-        mma(fa[cur], fb[cur]);
-    }
+    // the trailing DMAs (past the last stage) land before the LDS is reused or released
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     big_epilogue<OUT, TM, NT, true>(p, acc, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
 }
 
