@@ -24,12 +24,17 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)v;
 }
 
-// fp32 -> bf16 with round-to-nearest-even; NaN stays a quiet NaN.
+// fp32 -> bf16 with round-to-nearest-even; a NaN keeps its upper bits and is
+// quieted ((u >> 16) | 0x40).  This is the hardware conversion
+// (v_cvt_pk_bf16_f32), which gives exactly that result for all 2^32 fp32
+// patterns with fp32 denormals enabled, as this library is built (checked
+// exhaustively on gfx950).  The empty asm pins f as a rounded fp32 value, so
+// the compiler cannot fold an fmaf feeding it into a mixed-precision fma that
+// rounds only once.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    asm volatile("" : "+v"(f));
+    const __bf16 h = (__bf16)f;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
 // fp32 -> fp16 with round-to-nearest-even (hardware conversion, default mode).
