@@ -559,3 +559,61 @@ def test_abi_split_workspace_reuse(ops, oracle):
         bf16_close(to_bits(out), _w4_ref(oracle, d, 128))
     head = wsbuf[:4096].cpu()
     assert int(head.count_nonzero()) == 0, "split-K counters must be left at zero"
+
+
+def test_abi_w8a8_split_workspace_reuse(ops, oracle):
+    """W8A8 split-K calls through the ABI (skinny stream and 256x256 tiles with int32 partials and the
+    split reduce): one zeroed workspace reused by calls of different shapes and output types, each result
+    against the oracle (int32 fully through checksums, 16-bit and int8 on a row subset), and the split-K
+    counter area left at zero."""
+    say("ABI qk_quant_matmul split workspace reuse")
+    import ctypes
+    L = ops.abi()
+    cases = [(16, 4096, 8192, BF16), (512, 4096, 14336, BF16), (100, 2048, 4096, I8), (512, 1024, 8192, I32),
+             (16, 4096, 8192, F16)]
+    need = []
+    for (M, N, K, od) in cases:
+        n = ctypes.c_size_t(0)
+        assert L.qk_quant_matmul_workspace_size(M, N, K, od, ctypes.byref(n)) == 0
+        need.append(n.value)
+    assert min(need) > 0, "every shape must split K"
+    wsbuf = torch.zeros(max(need), dtype=torch.uint8, device=DEV)
+    tdt = {BF16: torch.bfloat16, F16: torch.float16, I8: torch.int8, I32: torch.int32}
+    for ci, (M, N, K, od) in enumerate(cases):
+        say(f"  M={M} N={N} K={K} out={od}")
+        g = torch.Generator().manual_seed(40 + ci)
+        a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+        s = 1e-4 + 1e-3 * torch.rand(N, generator=g) if od == I8 else 1e-3 + 9e-3 * torch.rand(N, generator=g)
+        off = torch.randn(N, generator=g) if od == I8 else None
+        pt = 1e-2 * torch.rand(M, generator=g) if od in (BF16, F16) else None
+        b = torch.randint(-500, 500, (N,), generator=g, dtype=torch.int32) if od in (I8, I32) else \
+            torch.randn(N, generator=g).to(torch.bfloat16)
+        bdt = I32 if od in (I8, I32) else BF16
+        if od == I32:
+            s = torch.ones(1)
+        ad, wd, sd, bd = a.to(DEV), w.to(DEV), s.to(DEV), b.to(DEV)
+        offd = off.to(DEV) if off is not None else None
+        ptd = pt.to(DEV) if pt is not None else None
+        out = torch.empty((M, N), dtype=tdt[od], device=DEV)
+        rc = L.qk_quant_matmul(ad.data_ptr(), K, wd.data_ptr(), N, 1, M, N, K, sd.data_ptr(), sd.numel(),
+                               offd.data_ptr() if offd is not None else None, N if offd is not None else 0,
+                               ptd.data_ptr() if ptd is not None else None, bd.data_ptr(), bdt, out.data_ptr(), od,
+                               wsbuf.data_ptr(), wsbuf.numel(), _stream())
+        assert rc == 0, ops.last_error()
+        torch.cuda.synchronize()
+        if od == I32:
+            a64, w64 = a.to(torch.int64), w.to(torch.int64)
+            acc64 = out.cpu().to(torch.int64) - b.to(torch.int64)
+            assert torch.equal(acc64.sum(0), a64.sum(0) @ w64)
+            assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
+            continue
+        rows = np.r_[0:8, M - 8:M]
+        ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(),
+                                  offset=off.numpy() if off is not None else None,
+                                  pertoken=pt[rows].numpy() if pt is not None else None,
+                                  bias=b.numpy() if bdt == I32 else W.bits(b), bias_dtype=bdt, out_dtype=od)
+        got = out.cpu().numpy()[rows] if od == I8 else to_bits(out)[rows]
+        assert np.array_equal(got, ref)
+    head = wsbuf[:4096].cpu()
+    assert int(head.count_nonzero()) == 0, "split-K counters must be left at zero"
