@@ -72,12 +72,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 // ---------------------------------------------------------------- split-K completion
 // Each of the nsplit workgroups that own one output tile stores its partial
-// sums device-coherently (store_dev, or buffer stores with kCoherent: written
-// through the XCD's L2) and
-// then calls splitk_last, which returns true in exactly one of them -- the
-// last to arrive.  That workgroup reads every split's partials device-coherently
-// (load_dev / kCoherent: not served from a possibly stale L2 line) and finishes the
-// tile.  A split's stores have completed (s_waitcnt vmcnt(0)) before its
+// sums device-coherently (buffer stores with kCoherent: written through the
+// XCD's L2) and then calls splitk_last, which returns true in exactly one of
+// them -- the last to arrive.  That workgroup reads the other splits' partials
+// device-coherently (buffer loads with kCoherent: not served from a possibly
+// stale L2 line) and finishes the tile.  Whole 16-byte pieces of output rows
+// per lane keep these write-through stores and loads as full lines; scattered
+// 4-byte pieces make them an order of magnitude slower.  A split's stores have completed (s_waitcnt vmcnt(0)) before its
 // arrival is counted, so the last arrival sees them all; no cache-wide
 // writeback or invalidate is needed.  The counter must be zero before the
 // tile's first split arrives; the last arrival sets it back to zero (every
@@ -86,18 +87,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // Cache-policy operand of the raw buffer loads/stores for device-coherent
 // access (the sc1 bit on gfx950).
 constexpr int kCoherent = 16;
-__device__ __forceinline__ void store_dev(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_dev(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_dev(int32_t* p, int32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int32_t load_dev(const int32_t* p) {
-    return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ bool splitk_last(uint32_t* ctr, uint32_t nsplit) {
     __shared__ uint32_t splitk_ticket;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
