@@ -1010,11 +1010,17 @@ SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
     s.tiles_m = (int)((M + 16 * s.mt - 1) / (16 * s.mt));
     s.tiles_n = (int)((N + sk::BN - 1) / sk::BN);
     const int64_t base = (int64_t)s.tiles_m * s.tiles_n;
-    // split while short of ~512 workgroups, keeping the int32 partials (nsplit*M*N*4 bytes)
-    // within the weight's K*N bytes and every split at least 256 rows of K
-    while (base * s.nsplit * 2 <= 512 && K % ((int64_t)s.nsplit * 2 * sk::BK) == 0 &&
+    // split while short of ~512 workgroups (~256, one per CU, for 16-row tiles: the decode stream
+    // measured fastest there), keeping the int32 partials (nsplit*M*N*4 bytes) within the weight's K*N
+    // bytes and every split at least 256 rows of K
+    const int64_t target = s.mt == 1 ? 256 : 512;
+    while (base * s.nsplit * 2 <= target && K % ((int64_t)s.nsplit * 2 * sk::BK) == 0 &&
            (int64_t)s.nsplit * 2 * M * 4 <= K && K / (s.nsplit * 2) >= 256)
         s.nsplit *= 2;
+    if (const char* e = std::getenv("QK_SKINNY_SPLITS")) {  // tuning override: a power of two dividing K in stages
+        const int v = std::atoi(e);
+        if (v >= 1 && v <= 64 && (v & (v - 1)) == 0 && K % ((int64_t)v * sk::BK) == 0) s.nsplit = v;
+    }
     if (base * s.nsplit >= ((int64_t)1 << 31)) s.mt = 0;
     if (s.mt == 8 && s.nsplit == 1) s.mt = 0;  // 128-row tiles only as a split stream (their in-place epilogue is not unrolled)
     return s;
