@@ -70,6 +70,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt[3:0], [15:14]; others at their maximum)
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
+
+// 16 bytes per lane from a buffer into LDS bytes [lds + 16*lane, +16).  Written
+// as asm so the compiler's wait-count pass, which cannot tell which LDS bytes
+// a DMA writes, does not put a vmcnt(0) before every LDS read; the kernel
+// waits on vmcnt itself.  m0 (the LDS base) is an operand, so the compiler
+// sets it and knows it is in use.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds));
+}
+
 // ---------------------------------------------------------------- split-K completion
 // Each of the nsplit workgroups that own one output tile stores its partial
 // sums device-coherently (buffer stores with kCoherent: written through the

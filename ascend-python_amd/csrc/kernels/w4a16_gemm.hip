@@ -966,6 +966,337 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
         }
 }
 
+// Group sums of the activations for the prefill kernel: xsum[g][m] =
+// sum of x[m][k] over group g, in fp32, k ascending (one thread per (m, g),
+// consecutive threads on consecutive rows so the stores are contiguous).
+__global__ __launch_bounds__(kThreads) void w4_xsum(WqbmmArgs p, float* __restrict__ xsum) {
+    const int64_t M = p.M, G = p.group, ng = p.K / G;
+    const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (t >= M * ng) return;
+    const int64_t g = t / M, m = t - g * M;
+    const uint16_t* row = static_cast<const uint16_t*>(p.x) + m * p.K + g * G;
+    float s = 0.0f;
+    for (int64_t k = 0; k < G; k += 8) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(row + k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            s += load_half_bits(v[e] & 0xffffu, p.x_dtype);
+            s += load_half_bits(v[e] >> 16, p.x_dtype);
+        }
+    }
+    xsum[t] = s;
+}
+
+// Prefill on whole tiles (M % 256 == 0, N % 128 == 0, G % 64 == 0): the tile
+// and MFMA layout of w4_gemm and its group algebra, with a deeper pipeline
+// and the group sums of x taken from w4_xsum instead of a ones-vector MFMA
+// (a fifth of w4_gemm's MFMAs).  The activation stages go from HBM straight
+// into a ring of three LDS slots by DMA, two stages ahead, with each stage's
+// scale / offset rows and group sums; the packed weight words go into
+// registers three stages ahead and are unpacked into the LDS weight tile one
+// stage ahead.  Waves 4-7 issue the DMAs and count them with their own vmcnt
+// waits (asm DMAs are invisible to the compiler's wait counts); waves 0-3
+// issue only the register loads, so the compiler's waits before the unpack
+// stay exact.
+namespace pd {
+constexpr int BM = 256, BN = 128, BK = 64, NT = 512, NSX = 3;
+constexpr int X_SL = BM * 128;               // x stage [row][128 B] in the pf::off layout (32 KB)
+constexpr int B_SL = BN * 128;               // unpacked weight stage in the pf::boff layout (16 KB)
+constexpr int SC_SL = 3072;                  // scale row, offset row, group sums of the 256 rows (1 KB DMA each)
+constexpr int B_BASE = NSX * X_SL;
+constexpr int SC_BASE = B_BASE + 2 * B_SL;
+constexpr int RING = SC_BASE + NSX * SC_SL;  // 137 KB
+constexpr int OROWB = 2 * BN + 16;           // padded output staging row (bytes)
+constexpr int OUT_BYTES = BM * OROWB;
+constexpr int SMEM = RING > OUT_BYTES ? RING : OUT_BYTES;
+constexpr int LGKM0 = 0xc07f;                // s_waitcnt lgkmcnt(0) alone
+}  // namespace pd
+
+template <int DT, bool HAS_OFF, bool W8>
+__global__ __launch_bounds__(pd::NT) void w4_dma(WqbmmArgs p, int tiles_m, int tiles_n, const float* __restrict__ xsum) {
+    typedef Mfma<DT> MM;
+    using namespace pd;
+    constexpr int TM = 4, TN = 4;           // MFMA tiles per wave (wave tile 64 x 64)
+    constexpr float BASE = W8 ? 0.0f : MM::BASE;
+    constexpr int NSC = HAS_OFF ? 3 : 2;    // scale (+ offset) + group-sum DMAs per stage, issued by wave 4
+    constexpr int NWL = W8 ? 8 : 4;         // weight loads per thread per stage (waves 0-3)
+    __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+
+    const int bid = xcd_swizzle(blockIdx.x, tiles_m * tiles_n);
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int grp = bid / per_group;
+    const int first_m = grp * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int tm = first_m + (bid % per_group) % gm;
+    const int tn = (bid % per_group) / gm;
+    const int N = (int)p.N, K = (int)p.K, G = (int)p.group;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int NWD = W8 ? (N >> 2) : (N >> 3);  // weight dwords per row
+    const int nk = K / BK, gst = G / BK;       // stages, stages per group
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int fr = lane & 15, g4 = lane >> 4;
+    const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+
+    // ---- waves 4-7: x rows m0..m0+255, one DMA = rows 8b..8b+7 x 128 B (64 k); lane l -> row 8b + (l>>3),
+    // LDS chunk l&7, which holds k chunk (l&7) ^ ((row>>1)&7), and (row>>1)&7 = 4*(b&1) + (l>>4)
+    const uint32_t ldx = (uint32_t)K * 2u;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(p.x) + (size_t)m0 * ldx, (uint32_t)BM * ldx);
+    const uint32_t vx0 = (uint32_t)(lane >> 3) * ldx + 16u * (uint32_t)((lane & 7) ^ (lane >> 4));
+    const uint32_t vx1 = (uint32_t)(lane >> 3) * ldx + 16u * (uint32_t)((lane & 7) ^ (4 + (lane >> 4)));
+    const int xw = wave - 4;  // DMA wave xw issues blocks 8xw .. 8xw+7
+    // scale / offset row of a stage's group: lanes 16..63 repeat lanes 0..15 (the first 256 B are used)
+    const uint32_t nsb = (uint32_t)(K / G) * (uint32_t)N * 2u;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scale, nsb);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(HAS_OFF ? p.offset : p.scale, nsb);
+    const uint32_t vsc = (uint32_t)n0 * 2u + 16u * (uint32_t)(lane & 15);
+    // group sums xsum[g][m0 .. m0+255]: 1 KB, one DMA
+    const __amdgpu_buffer_rsrc_t rxs = make_rsrc(xsum, (uint32_t)(K / G) * (uint32_t)p.M * 4u);
+    const uint32_t vxs = ((uint32_t)m0 + 4u * (uint32_t)lane) * 4u;
+    int sc_g = 0, sc_left = gst;  // group of the next stage whose scale rows go out
+    // stage s into slot s % 3 (past the end: the last stage again, into a slot no wave reads)
+    auto issue_x = [&](int s) {
+        const int sl = s < nk ? s : nk - 1;
+        const uint32_t k2 = (uint32_t)sl * (uint32_t)(BK * 2);
+        const uint32_t dst = sbase + (uint32_t)(s % NSX) * X_SL;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int b = 8 * xw + j;
+            dma16(rx, dst + (uint32_t)b * 1024u, (j & 1) ? vx1 : vx0, (uint32_t)(8 * b) * ldx + k2);
+        }
+        if (wave == 4) {
+            const uint32_t sdst = sbase + SC_BASE + (uint32_t)(s % NSX) * SC_SL;
+            const uint32_t goff = (uint32_t)sc_g * (uint32_t)N * 2u;
+            dma16(rs, sdst, vsc, goff);
+            if (HAS_OFF) dma16(ro, sdst + 1024u, vsc, goff);
+            dma16(rxs, sdst + 2048u, vxs, (uint32_t)sc_g * (uint32_t)p.M * 4u);
+            if (s < nk - 1 && --sc_left == 0) {
+                ++sc_g;
+                sc_left = gst;
+            }
+        }
+    };
+
+    // ---- waves 0-3: packed words; thread t takes word column (t>>4)&15 (and +16 for int8 weights), rows
+    // 4(t&15) .. +3 of the stage
+    const int wcol_l = (tid >> 4) & 15, rg = tid & 15;
+    const uint32_t rowb = (uint32_t)NWD * 4u;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (uint32_t)K * rowb);
+    const uint32_t w_off = (uint32_t)(4 * rg) * rowb + (uint32_t)(n0 / (W8 ? 4 : 8) + wcol_l) * 4u;
+    uint32_t rw[3][NWL];
+    auto issue_w = [&](int s, uint32_t(&r)[NWL]) {
+        const uint32_t k0 = (uint32_t)(s < nk ? s : nk - 1) * (uint32_t)BK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_raw_buffer_load_b32(wr, w_off, (k0 + i) * rowb, 0);
+        if constexpr (W8) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                r[4 + i] = __builtin_amdgcn_raw_buffer_load_b32(wr, w_off + 64u, (k0 + i) * rowb, 0);
+        }
+    };
+    // LDS byte address of column 8*wcol_l + j, k chunk rg/2, half rg&1 of the weight tile (int4) is
+    // wb_base + (KJ(j) ^ wb_x) with KJ(j) = 128 j | 16 (j/2): the pf::boff layout written out
+    const uint32_t wb_base = 1024u * (uint32_t)wcol_l + 8u * (uint32_t)(rg & 1);
+    const uint32_t wb_x = (16u * ((uint32_t)(rg >> 1) ^ (4u * (uint32_t)(wcol_l & 1)))) | (128u * (uint32_t)(wcol_l & 1));
+    auto unpack = [&](const uint32_t(&r)[NWL], char* Bs) {
+        if constexpr (W8) {
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int wc = wcol_l + 16 * hf;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    u32x2 v;
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const float lo = (float)(int8_t)(r[4 * hf + 2 * e] >> (8 * j));
+                        const float hi = (float)(int8_t)(r[4 * hf + 2 * e + 1] >> (8 * j));
+                        if constexpr (DT == QK_BF16)
+                            v[e] = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+                        else
+                            v[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+                    }
+                    *reinterpret_cast<u32x2*>(Bs + pf::boff(4 * wc + j, rg >> 1) + 8 * (rg & 1)) = v;
+                }
+            }
+        } else {
+            const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000f000fu);
+            const uint32_t magic = __builtin_amdgcn_readfirstlane(MM::MAGIC | 0x00080008u);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                // rows (0,1) and (2,3): byte j/2 of each word, odd nibbles shifted down
+                uint32_t p01 = __builtin_amdgcn_perm(r[1], r[0], byte_sel(j >> 1));
+                uint32_t p23 = __builtin_amdgcn_perm(r[3], r[2], byte_sel(j >> 1));
+                if (j & 1) {
+                    p01 >>= 4;
+                    p23 >>= 4;
+                }
+                const u32x2 v = {(p01 & mask) ^ magic, (p23 & mask) ^ magic};
+                constexpr uint32_t kj[8] = {0u, 128u, 256u | 16u, 384u | 16u, 512u | 32u, 640u | 32u, 768u | 48u, 896u | 48u};
+                *reinterpret_cast<u32x2*>(Bs + wb_base + (kj[j] ^ wb_x)) = v;
+            }
+        }
+    };
+
+    f32x4 acc[TM][TN], ag[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = ag[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    // acc += s*A + s*(offset - BASE)*xsum with the group's rows from scale slot `slot`
+    auto fold = [&](int slot) {
+        const char* sc = smem + SC_BASE + slot * SC_SL;
+        f32x4 xs[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xs[i] = *reinterpret_cast<const f32x4*>(sc + 2048 + 4 * (wm * 64 + 16 * i + 4 * g4));
+        float sf[TN], sx[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = wn * 64 + 16 * j + fr;
+            sf[j] = load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 2 * col), p.s_dtype);
+            const float of = HAS_OFF ? load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 1024 + 2 * col), p.s_dtype)
+                                     : 0.0f;
+            sx[j] = sf[j] * (of - BASE);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[i][j][r] = __builtin_fmaf(sf[j], ag[i][j][r], __builtin_fmaf(sx[j], xs[i][r], acc[i][j][r]));
+    };
+    auto mma_step = [&](const char* As, const char* Bs, int kk) {
+        u32x4 af[TM], bfr[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            af[i] = *reinterpret_cast<const u32x4*>(As + pf::off(wm * 64 + 16 * i + fr, 4 * kk + g4));
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            bfr[j] = *reinterpret_cast<const u32x4*>(Bs + pf::boff(wn * 64 + 16 * j + fr, 4 * kk + g4));
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], bfr[j], ag[i][j]);
+    };
+
+    // Stage i reads x slot i % 3, scale slot i % 3 and weight buffer i & 1.  Iteration i issues x stage i+2
+    // (into the slot stage i-1 read) and weight words of stage i+3 (into the registers stage i's words
+    // left), and unpacks stage i+1 (into the buffer stage i-1 read); one barrier per stage.  A DMA wave
+    // waits, before that barrier, for all but the DMAs it issued in iteration i-1, which lands stage i.
+    // The two kinds of wave run loops of their own (same barriers, same order): a branch inside one loop
+    // would merge a path without the weight loads into the compiler's wait counts, and it would then wait
+    // for every load before each unpack.
+    int left = gst;
+    auto stage_mma = [&](int i, int u) {
+        const char* As = smem + u * X_SL;
+        const char* Bs = smem + B_BASE + (i & 1) * B_SL;
+        mma_step(As, Bs, 0);
+        return Bs;
+    };
+    auto stage_end = [&](int i, int u) {
+        const char* As = smem + u * X_SL;
+        const char* Bs = smem + B_BASE + (i & 1) * B_SL;
+        mma_step(As, Bs, 1);
+        if (--left == 0) {
+            fold(u);
+            left = gst;
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < TN; ++b) ag[a][b] = zero4;
+        }
+    };
+    auto bar = [&]() {
+        __builtin_amdgcn_s_waitcnt(LGKM0);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // whole triples of stages in the loop, the last one or two after it: an exit from inside the loop body
+    // becomes (after the compiler restructures it) a path back to the loop head that skips loads, and the
+    // compiler's waits then count too few loads in flight
+    const int nk3 = nk - nk % 3;
+    if (wave < 4) {
+        auto w_stage = [&](int i, int u) {
+            bar();
+            issue_w(i + 3, rw[u]);
+            __builtin_amdgcn_sched_barrier(0);
+            stage_mma(i, u);
+            // unconditional (past the last stage it fills a buffer no stage reads)
+            unpack(rw[(u + 1) % 3], smem + B_BASE + ((i + 1) & 1) * B_SL);
+            stage_end(i, u);
+        };
+        // in stage order (interleaved stages would make the loop's first waits count too few loads)
+        issue_w(0, rw[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_w(1, rw[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_w(2, rw[2]);
+        __builtin_amdgcn_sched_barrier(0);
+        unpack(rw[0], smem + B_BASE);
+        for (int i0 = 0; i0 < nk3; i0 += 3) {
+#pragma unroll
+            for (int u = 0; u < 3; ++u) w_stage(i0 + u, u);
+        }
+        if (nk3 < nk) w_stage(nk3, 0);
+        if (nk3 + 1 < nk) w_stage(nk3 + 1, 1);
+    } else {
+        auto x_stage = [&](int i, int u) {
+            if (wave == 4)
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 + NSC));
+            else
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+            bar();
+            issue_x(i + 2);
+            stage_mma(i, u);
+            stage_end(i, u);
+        };
+        issue_x(0);
+        issue_x(1);
+        for (int i0 = 0; i0 < nk3; i0 += 3) {
+#pragma unroll
+            for (int u = 0; u < 3; ++u) x_stage(i0 + u, u);
+        }
+        if (nk3 < nk) x_stage(nk3, 0);
+        if (nk3 + 1 < nk) x_stage(nk3 + 1, 1);
+    }
+    // the trailing loads (past the last stage) land before the LDS is reused
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+
+    // ---- epilogue: + bias, cast, staged through LDS for 16-byte row stores
+    float bv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn * 64 + 16 * j + fr;
+        bv[j] = p.bias_dtype ? load_scalar(p.bias, n, p.bias_dtype) : 0.0f;
+    }
+    uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = wm * 64 + 16 * i + 4 * g4 + r;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const float v = acc[i][j][r] + bv[j];
+                ot[row * (OROWB / 2) + wn * 64 + 16 * j + fr] =
+                    (uint16_t)(p.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+            }
+        }
+    __syncthreads();
+    constexpr int CPRO = 2 * BN / 16;
+    for (int q = tid; q < BM * CPRO; q += NT) {
+        const int row = q / CPRO, c = q % CPRO;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * OROWB + 16 * c);
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N + n0 + 8 * c) = v;
+    }
+}
+
 // Any shape: one thread per output, fp32 sums per group then the same
 // group-wise scale/offset algebra as the tiled kernels.
 __global__ __launch_bounds__(kThreads) void wq_generic(WqbmmArgs p) {
@@ -1218,12 +1549,12 @@ hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* part
 // Prefill plan: large M, int4 weights, K a multiple of the 64-row stage and
 // G a multiple of the 32-row MFMA step.
 struct GemmPlan {
-    bool ok, full;
+    bool ok, full, dma;
     int tiles_m, tiles_n;
 };
 
 GemmPlan gemm_plan(const WqbmmArgs& p) {
-    GemmPlan g{false, false, 0, 0};
+    GemmPlan g{false, false, false, 0, 0};
     const int64_t G = p.group == 0 ? p.K : p.group;
     const bool w8 = p.w_dtype == QK_I8;
     if (!(p.w_dtype == QK_I32 || (w8 && p.N % 4 == 0)) || p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0)
@@ -1235,20 +1566,29 @@ GemmPlan gemm_plan(const WqbmmArgs& p) {
     if (((uintptr_t)p.x | (uintptr_t)p.out) % 16 != 0 || (uintptr_t)p.w % 4 != 0) return g;
     g.tiles_m = (int)((p.M + 255) / 256);
     g.tiles_n = (int)((p.N + 127) / 128);
-    const char* force = std::getenv("QK_W4_GEMM");  // tuning / test override: "force" or "off"
+    // tuning / test override: "force" (even with few tiles), "nodma" (register-staged kernel only) or "off"
+    const char* force = std::getenv("QK_W4_GEMM");
     if (force && std::strcmp(force, "off") == 0) return g;
     const bool forced = force && std::strcmp(force, "force") == 0;
     // too few tiles: the decode kernels stream the weight better
     if (!forced && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
     g.full = p.M % 256 == 0 && p.N % 128 == 0;
+    // the DMA pipeline: whole tiles, whole 64-row stages per group, 16-byte aligned scale / offset rows
+    g.dma = g.full && G % 64 == 0 && ((uintptr_t)p.scale | (uintptr_t)(p.offset ? p.offset : p.scale)) % 16 == 0 &&
+            !(force && std::strcmp(force, "nodma") == 0);
     g.ok = true;
     return g;
 }
 
 template <int DT, bool OFF>
-hipError_t launch_gemm_t(const WqbmmArgs& p, const GemmPlan& g, hipStream_t stream) {
+hipError_t launch_gemm_t(const WqbmmArgs& p, const GemmPlan& g, float* xsum, hipStream_t stream) {
     const dim3 grid((uint32_t)(g.tiles_m * g.tiles_n));
-    if (p.w_dtype == QK_I8) {
+    if (g.dma) {
+        const int64_t sums = p.M * (p.K / p.group);
+        w4_xsum<<<dim3((uint32_t)((sums + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream>>>(p, xsum);
+        if (p.w_dtype == QK_I8) w4_dma<DT, OFF, true><<<grid, dim3(pd::NT), 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+        else w4_dma<DT, OFF, false><<<grid, dim3(pd::NT), 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+    } else if (p.w_dtype == QK_I8) {
         if (g.full) w4_gemm<DT, OFF, true, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
         else w4_gemm<DT, OFF, false, true><<<grid, dim3(512), 0, stream>>>(p, g.tiles_m, g.tiles_n);
     } else if (g.full) {
@@ -1260,8 +1600,13 @@ hipError_t launch_gemm_t(const WqbmmArgs& p, const GemmPlan& g, hipStream_t stre
 }
 
 template <int DT>
-hipError_t launch_gemm_dt(const WqbmmArgs& p, const GemmPlan& g, hipStream_t stream) {
-    return p.offset != nullptr ? launch_gemm_t<DT, true>(p, g, stream) : launch_gemm_t<DT, false>(p, g, stream);
+hipError_t launch_gemm_dt(const WqbmmArgs& p, const GemmPlan& g, float* xsum, hipStream_t stream) {
+    return p.offset != nullptr ? launch_gemm_t<DT, true>(p, g, xsum, stream) : launch_gemm_t<DT, false>(p, g, xsum, stream);
+}
+
+// workspace of the DMA prefill kernel: [split counters, unused][group sums fp32 [K/G][M]]
+size_t gemm_dma_workspace(const WqbmmArgs& p) {
+    return QK_SPLIT_COUNTER_BYTES + (size_t)(p.K / p.group) * (size_t)p.M * sizeof(float);
 }
 
 template <int OUTDT>
@@ -1290,7 +1635,8 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     // [split-K counters][fp32 partials [nsplit][M][N]]
     const StreamPlan s = stream_plan(p);
     if (s.ok) return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
-    if (gemm_plan(p).ok) return 0;
+    const GemmPlan gp = gemm_plan(p);
+    if (gp.ok) return gp.dma ? gemm_dma_workspace(p) : 0;
     const DecodePlan d = decode_plan(p);
     if (!d.ok || d.nsplit == 1) return 0;
     return QK_SPLIT_COUNTER_BYTES + (size_t)d.nsplit * (size_t)M * (size_t)N * sizeof(float);
@@ -1318,9 +1664,17 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
                                       : launch_reduce<QK_F16>(p, sp.nsplit, partial, stream);
     }
     if (!sp.ok) {
-        const GemmPlan gp = gemm_plan(p);
-        if (gp.ok)
-            return p.x_dtype == QK_BF16 ? launch_gemm_dt<QK_BF16>(p, gp, stream) : launch_gemm_dt<QK_F16>(p, gp, stream);
+        GemmPlan gp = gemm_plan(p);
+        if (gp.ok) {
+            // without the workspace the size query asked for, the register-staged kernel runs
+            float* xsum = nullptr;
+            if (gp.dma && ws && ws_bytes >= gemm_dma_workspace(p) && (uintptr_t)ws % 256 == 0)
+                xsum = reinterpret_cast<float*>(ws + QK_SPLIT_COUNTER_BYTES);
+            else
+                gp.dma = false;
+            return p.x_dtype == QK_BF16 ? launch_gemm_dt<QK_BF16>(p, gp, xsum, stream)
+                                        : launch_gemm_dt<QK_F16>(p, gp, xsum, stream);
+        }
     }
     const DecodePlan d = decode_plan(p);
     if (d.ok) {

@@ -453,9 +453,14 @@ def test_w4a16_stream_configs(ops, oracle, monkeypatch, cfg):
     (512, 1024, 1024, 32, True, torch.bfloat16),    # full tiles, 32-row groups
     (70, 136, 64, 0, True, torch.bfloat16),         # one K stage, per-channel scale
     (260, 264, 2048, 0, False, torch.float16),      # per-channel over a long K
+    # whole tiles and groups of whole 64-row stages: the DMA pipeline
+    (256, 128, 64, 64, True, torch.bfloat16),       # a single stage (no full triple of stages)
+    (512, 256, 320, 64, True, torch.float16),       # five stages (two after the last triple)
+    (256, 384, 1024, 0, True, torch.bfloat16),      # per-channel scale, 16 stages per group
+    (768, 640, 512, 256, False, torch.bfloat16),    # 256-row groups, several tile rows
 ])
 def test_w4a16_prefill_kernel(ops, oracle, monkeypatch, M, N, K, group, offset, x_dtype):
-    """The large-M kernel (exact int4 MFMA operands + group fold), forced onto small shapes."""
+    """The large-M kernels (exact int4 MFMA operands + group fold), forced onto small shapes."""
     monkeypatch.setenv("QK_W4_GEMM", "force")
     say(f"w4a16 prefill kernel M={M} N={N} K={K} group={group} offset={offset} {x_dtype}")
     case = W.W4A16Case(M=M, N=N, K=K, group=group, x_dtype=x_dtype, offset=offset)
@@ -465,6 +470,23 @@ def test_w4a16_prefill_kernel(ops, oracle, monkeypatch, M, N, K, group, offset, 
     b = torch.randn(N).to(x_dtype)
     out = _w4_run(ops, d, group, bias=b)
     bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b, x_dtype=x_dtype), dtype=x_dtype)
+
+
+@pytest.mark.parametrize("mode", ["dma", "nodma"])
+def test_w4a16_prefill_pipelines(ops, oracle, monkeypatch, mode):
+    """Both prefill pipelines on one whole-tile shape with 128 tiles: the DMA kernel (default, group sums
+    from the pre-pass) and the register-staged kernel (QK_W4_GEMM=nodma), each against the oracle."""
+    if mode == "nodma":
+        monkeypatch.setenv("QK_W4_GEMM", "nodma")
+    M, N, K, group = 2048, 2048, 384, 128
+    say(f"w4a16 prefill {mode} M={M} N={N} K={K} group={group}")
+    case = W.W4A16Case(M=M, N=N, K=K, group=group, x_dtype=torch.bfloat16, offset=True)
+    d = W.w4a16_inputs(case, seed=31)
+    b = torch.randn(N).to(torch.bfloat16)
+    out = _w4_run(ops, d, group, bias=b)
+    rows = np.r_[0:8, 700:708, 2040:2048]
+    sub = dict(d, x=d["x"][rows])
+    bf16_close(to_bits(out)[rows], _w4_ref(oracle, sub, group, bias=b))
 
 
 # ----------------------------------------------------------------------------- W8A16 (int8 weights)
