@@ -968,7 +968,8 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
 
 // Group sums of the activations for the prefill kernel: xsum[g][m] =
 // sum of x[m][k] over group g, in fp32, k ascending (one thread per (m, g),
-// consecutive threads on consecutive rows so the stores are contiguous).
+// consecutive threads on consecutive rows so the stores are contiguous; the
+// group is read 64 elements at a time, eight 16-byte loads in flight).
 __global__ __launch_bounds__(kThreads) void w4_xsum(WqbmmArgs p, float* __restrict__ xsum) {
     const int64_t M = p.M, G = p.group, ng = p.K / G;
     const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
@@ -976,13 +977,17 @@ __global__ __launch_bounds__(kThreads) void w4_xsum(WqbmmArgs p, float* __restri
     const int64_t g = t / M, m = t - g * M;
     const uint16_t* row = static_cast<const uint16_t*>(p.x) + m * p.K + g * G;
     float s = 0.0f;
-    for (int64_t k = 0; k < G; k += 8) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(row + k);
+    for (int64_t k0 = 0; k0 < G; k0 += 64) {  // G is a multiple of 64 on this path
+        u32x4 v[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            s += load_half_bits(v[e] & 0xffffu, p.x_dtype);
-            s += load_half_bits(v[e] >> 16, p.x_dtype);
-        }
+        for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const u32x4*>(row + k0 + 8 * j);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s += load_half_bits(v[j][e] & 0xffffu, p.x_dtype);
+                s += load_half_bits(v[j][e] >> 16, p.x_dtype);
+            }
     }
     xsum[t] = s;
 }

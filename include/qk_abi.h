@@ -25,12 +25,13 @@
  *
  * Workspaces (this build's one departure from the reference's per-call
  * scratch): a non-empty workspace begins with QK_SPLIT_COUNTER_BYTES of
- * split-K arrival counters, followed by the partial sums.  The counters must
- * be zero the first time a workspace is used -- allocate it once, zero it
- * (hipMemset), and keep reusing it; every call leaves them zero again.  The
- * workgroup that completes a tile's splits adds them up itself, so no second
- * kernel runs.  Calls that may be in flight at the same time need distinct
- * workspaces.
+ * split-K arrival counters, followed by the partial sums (split-K shapes) or
+ * by the activations' per-group sums (weight-quant matmul at large M).  The
+ * counters must be zero the first time a workspace is used -- allocate it
+ * once, zero it (hipMemset), and keep reusing it; every call leaves them zero
+ * again.  The workgroup that completes a tile's splits adds them up itself,
+ * so no second kernel runs.  Calls that may be in flight at the same time
+ * need distinct workspaces.
  */
 #ifndef QK_ABI_H
 #define QK_ABI_H
