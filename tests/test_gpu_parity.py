@@ -472,6 +472,43 @@ def test_w4a16_prefill_kernel(ops, oracle, monkeypatch, M, N, K, group, offset, 
     bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b, x_dtype=x_dtype), dtype=x_dtype)
 
 
+def test_w4a16_prefill_dma_sweep(ops, oracle, monkeypatch):
+    """Seeded random whole-tile shapes through the DMA prefill kernel (int4 and int8 weights, fp16 and bf16,
+    group sizes 64..K, with and without offset and bias), each against the oracle on a row sample."""
+    monkeypatch.setenv("QK_W4_GEMM", "force")
+    rng = np.random.default_rng(2024)
+    for t in range(10):
+        M = 256 * int(rng.integers(1, 4))
+        N = 128 * int(rng.integers(1, 9))
+        K = 64 * int(rng.integers(1, 33))
+        gs = [g for g in (64, 128, 192, 256, 512) if K % g == 0] + [0]
+        group = int(rng.choice(gs))
+        x_dtype = torch.bfloat16 if t % 2 == 0 else torch.float16
+        offset = bool(t % 3)
+        w8 = t % 4 == 3
+        say(f"w4a16 dma sweep {t}: M={M} N={N} K={K} group={group} offset={offset} {x_dtype} int8={w8}")
+        b = torch.randn(N).to(x_dtype) if t % 2 else None
+        rows = np.r_[0:8, M - 8:M]
+        if w8:
+            d = _w8_inputs(M, N, K, group, offset, x_dtype, seed=100 + t)
+            out = ops.npu_weight_quant_batchmatmul(d["x"].to(DEV), d["w"].to(DEV), d["scale"].to(DEV),
+                                                   None if d["offset"] is None else d["offset"].to(DEV),
+                                                   bias=None if b is None else b.to(DEV), antiquant_group_size=group)
+            ref = oracle.weight_quant_bmm(W.bits(d["x"][rows]), CODE[x_dtype], d["w"].numpy(), W.bits(d["scale"]),
+                                          None if d["offset"] is None else W.bits(d["offset"]), F16, group,
+                                          bias=None if b is None else W.bits(b), bias_dtype=CODE[x_dtype],
+                                          out_dtype=CODE[x_dtype])
+        else:
+            case = W.W4A16Case(M=M, N=N, K=K, group=group, x_dtype=x_dtype, offset=offset)
+            d = W.w4a16_inputs(case, seed=100 + t)
+            if group == 0:
+                d = dict(d, scale=d["scale"].reshape(-1),
+                         offset=None if d["offset"] is None else d["offset"].reshape(-1))
+            out = _w4_run(ops, d, group, bias=b)
+            ref = _w4_ref(oracle, dict(d, x=d["x"][rows]), group, bias=b, x_dtype=x_dtype)
+        bf16_close(to_bits(out)[rows], ref, dtype=x_dtype)
+
+
 @pytest.mark.parametrize("mode", ["dma", "nodma"])
 def test_w4a16_prefill_pipelines(ops, oracle, monkeypatch, mode):
     """Both prefill pipelines on one whole-tile shape with 128 tiles: the DMA kernel (default, group sums
