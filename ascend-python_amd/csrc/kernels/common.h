@@ -92,25 +92,43 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, u
 // per lane keep these write-through stores and loads as full lines; scattered
 // 4-byte pieces make them an order of magnitude slower.  A split's stores have completed (s_waitcnt vmcnt(0)) before its
 // arrival is counted, so the last arrival sees them all; no cache-wide
-// writeback or invalidate is needed.  The counter must be zero before the
-// tile's first split arrives; the last arrival sets it back to zero (every
-// other arrival has happened by then).  Call from every thread of the
-// workgroup (it contains barriers).
+// writeback or invalidate is needed.  Call from every thread of the workgroup
+// (it contains barriers).
+//
+// A counter is one 64-bit word: bits 63..16 hold the tag of the call that
+// counted into it, bits 15..0 that call's arrivals.  Every call draws its own
+// tag (48 bits, never 0 and never all ones), and an arrival that finds a
+// different tag starts the count at one.  So the word needs no
+// initialisation: leftovers of any earlier call, a zero fill, a 0xFF fill or
+// other data all count as "no arrivals yet" unless their upper 48 bits equal
+// this call's tag.  The last arrival sets the word to zero (every other
+// arrival has happened by then), so a captured graph that replays one tag
+// also finds an empty counter each time.
 // Cache-policy operand of the raw buffer loads/stores for device-coherent
 // access (the sc1 bit on gfx950).
 constexpr int kCoherent = 16;
-__device__ __forceinline__ bool splitk_last(uint32_t* ctr, uint32_t nsplit) {
-    __shared__ uint32_t splitk_ticket;
+constexpr int kSplitCountBits = 16;
+__device__ __forceinline__ bool splitk_last(uint64_t* ctr, uint32_t nsplit, uint64_t tag) {
+    __shared__ uint32_t splitk_count;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (t == nsplit - 1) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        splitk_ticket = t;
+        uint64_t old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint64_t nw;
+        do {
+            nw = (old >> kSplitCountBits) == tag ? old + 1 : (tag << kSplitCountBits) | 1u;
+        } while (!__hip_atomic_compare_exchange_weak(ctr, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+        const uint32_t n = (uint32_t)(nw & ((1u << kSplitCountBits) - 1));
+        if (n == nsplit) __hip_atomic_store(ctr, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        splitk_count = n;
     }
     __syncthreads();
-    return splitk_ticket == nsplit - 1;
+    return splitk_count == nsplit;
 }
+
+// Host side: a fresh 48-bit tag per call for splitk_last (never 0, never all ones).
+uint64_t next_split_tag();
 
 // ---------------------------------------------------------------- per-row quantization
 // Row reductions for 256-thread workgroups (4 wave64): xor-shuffles inside a
@@ -220,6 +238,29 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
     else if (e.out_dtype == QK_F16) ((uint16_t*)e.out)[o] = (uint16_t)f32_to_f16_bits(v);
     else ((float*)e.out)[o] = v;
 }
+
+// ---------------------------------------------------------------- planner override
+// One debug override of the kernel planners, for tests and tuning only: parsed
+// once from the QK_DEBUG_PLAN environment variable, or replaced through
+// qk_debug_set_plan().  Planners read one snapshot per call (an atomic
+// pointer, no environment lookups), so the workspace query and the launch of
+// a call agree unless the override changes between them.  Spec: a
+// comma-separated list of
+//   w4_stream=off | w4_stream=<nwave>:<nkb>:<pf>   decode stream shape (16:4:2 16:4:4 8:4:2 8:4:4 8:8:2 8:8:3)
+//   w4_gemm=force | nodma | off                     prefill kernels on few tiles / register-staged only / never
+//   w4_splits=<n>                                   K splits of the 32-row-block decode kernel
+//   qmm_dma=0                                       W8A8 prefill: register-staged kernel instead of the DMA one
+//   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
+struct PlanOverride {
+    int w4_stream_nwave = 0, w4_stream_nkb = 0, w4_stream_pf = 0;  // 0: the planner's choice
+    bool w4_stream_off = false;
+    int w4_gemm = 0;  // 0 planner, 1 force, 2 nodma, 3 off
+    int w4_splits = 0;
+    bool qmm_dma = true;
+    int skinny_splits = 0;
+};
+const PlanOverride& plan_override();
+bool set_plan_override(const char* spec);  // false: spec not understood (override unchanged)
 
 // ---------------------------------------------------------------- launchers
 // Host-side entry points of each kernel file (validated arguments only).

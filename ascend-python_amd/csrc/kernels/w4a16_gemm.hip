@@ -392,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
 // of the bytes (no magic offset: BASE = 0).
 template <int DT, int WPL, int NWAVE, int NKB, int PF, int PIECE_KB, bool HAS_OFF, bool FINAL, bool W8>
 __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __restrict__ partial, int nstrip,
-                                                        int nsplit, uint32_t* __restrict__ ctr) {
+                                                        int nsplit, uint64_t* __restrict__ ctr, uint64_t tag) {
     typedef Mfma<DT> MM;
     static_assert(!W8 || WPL == 16, "int8 weights use 16-dword sub-strips");
     constexpr int CPW = W8 ? 4 : 8;         // output columns per weight dword
@@ -573,7 +573,7 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
     }
     // split-K: the last split of this strip to finish adds all splits in split order (deterministic)
     if constexpr (!FINAL) {
-        if (ctr == nullptr || !splitk_last(ctr + (int64_t)rb * nstrip + strip, (uint32_t)nsplit)) return;
+        if (ctr == nullptr || !splitk_last(ctr + (int64_t)rb * nstrip + strip, (uint32_t)nsplit, tag)) return;
         uint32_t qoff[QPT];
         bool qok[QPT];
 #pragma unroll
@@ -1399,9 +1399,8 @@ DecodePlan decode_plan(const WqbmmArgs& p) {
             while (s * 2 <= want && p.K % ((int64_t)(s * 2) * 2 * CHUNK) == 0) s *= 2;
         }
     }
-    if (const char* e = std::getenv("QK_W4_SPLITS")) {  // tuning override (debug)
-        const int f = std::atoi(e);
-        if (f >= 1 && p.K % ((int64_t)f * 2 * CHUNK) == 0) {
+    if (const int f = plan_override().w4_splits) {  // debug override
+        if (p.K % ((int64_t)f * 2 * CHUNK) == 0) {
             s = f;
             d.upfront = p.K / f == 512 && (p.N / 8) % 4 == 0;
         }
@@ -1463,15 +1462,12 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
     s.nwave = 16;
     s.nkb = 4;
     s.pf = 2;
-    if (const char* e = std::getenv("QK_W4_STREAM")) {  // tuning override: "nwave,nkb,pf" or "off"
-        if (std::strcmp(e, "off") == 0) return s;
-        int a = 0, b = 0, c = 0;
-        if (std::sscanf(e, "%d,%d,%d", &a, &b, &c) == 3 && (a == 8 || a == 16) &&
-            ((b == 4 && (c == 2 || c == 4)) || (a == 8 && b == 8 && (c == 2 || c == 3)))) {
-            s.nwave = a;
-            s.nkb = b;
-            s.pf = c;
-        }
+    const PlanOverride& ov = plan_override();  // debug override: a stream shape, or no stream kernel
+    if (ov.w4_stream_off) return s;
+    if (ov.w4_stream_nwave) {
+        s.nwave = ov.w4_stream_nwave;
+        s.nkb = ov.w4_stream_nkb;
+        s.pf = ov.w4_stream_pf;
     }
     if (s.piece_kb != 4) {  // short groups: one instantiated shape, 8 waves (16 would spill their scales)
         s.nwave = 8;
@@ -1499,20 +1495,20 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
 }
 
 template <int DT, int NWAVE, int NKB, int PF, int PKB, bool HAS_OFF, bool W8>
-hipError_t launch_stream_t(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint32_t* ctr,
+hipError_t launch_stream_t(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint64_t* ctr,
                            hipStream_t stream) {
     const dim3 grid((uint32_t)((int64_t)s.nstrip * s.nsplit));
     if (s.nsplit == 1)
         w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, true, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
-            p, partial, s.nstrip, 1, nullptr);
+            p, partial, s.nstrip, 1, nullptr, 0);
     else
         w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, false, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
-            p, partial, s.nstrip, s.nsplit, ctr);
+            p, partial, s.nstrip, s.nsplit, ctr, ctr ? next_split_tag() : 0);
     return hipGetLastError();
 }
 
 template <int DT, int NWAVE, bool HAS_OFF>
-hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint32_t* ctr,
+hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint64_t* ctr,
                            hipStream_t stream) {
     if (p.w_dtype == QK_I8) {  // int8 weights: the default shape only
         if constexpr (NWAVE == 16) {
@@ -1541,7 +1537,7 @@ hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* parti
 }
 
 template <int DT>
-hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint32_t* ctr,
+hipError_t launch_stream_dt(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint64_t* ctr,
                             hipStream_t stream) {
     const bool off = p.offset != nullptr;
     if (s.nwave == 8)
@@ -1571,16 +1567,16 @@ GemmPlan gemm_plan(const WqbmmArgs& p) {
     if (((uintptr_t)p.x | (uintptr_t)p.out) % 16 != 0 || (uintptr_t)p.w % 4 != 0) return g;
     g.tiles_m = (int)((p.M + 255) / 256);
     g.tiles_n = (int)((p.N + 127) / 128);
-    // tuning / test override: "force" (even with few tiles), "nodma" (register-staged kernel only) or "off"
-    const char* force = std::getenv("QK_W4_GEMM");
-    if (force && std::strcmp(force, "off") == 0) return g;
-    const bool forced = force && std::strcmp(force, "force") == 0;
+    // debug override: "force" (even with few tiles), "nodma" (register-staged kernel only) or "off"
+    const int force = plan_override().w4_gemm;
+    if (force == 3) return g;
+    const bool forced = force == 1;
     // too few tiles: the decode kernels stream the weight better
     if (!forced && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
     g.full = p.M % 256 == 0 && p.N % 128 == 0;
     // the DMA pipeline: whole tiles, whole 64-row stages per group, 16-byte aligned scale / offset rows
     g.dma = g.full && G % 64 == 0 && ((uintptr_t)p.scale | (uintptr_t)(p.offset ? p.offset : p.scale)) % 16 == 0 &&
-            !(force && std::strcmp(force, "nodma") == 0);
+            force != 2;
     g.ok = true;
     return g;
 }
@@ -1660,8 +1656,11 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
         if (sp.nsplit > 1 && (!ws || ws_bytes < QK_SPLIT_COUNTER_BYTES + (size_t)sp.nsplit * p.M * p.N * sizeof(float) ||
                               (uintptr_t)ws % 256 != 0))
             return hipErrorInvalidValue;
-        uint32_t* ctr = (sp.nsplit > 1 && (size_t)sp.nstrip * 4 <= QK_SPLIT_COUNTER_BYTES)
-                            ? reinterpret_cast<uint32_t*>(ws) : nullptr;
+        // one 64-bit tagged counter per strip (no initialisation needed); more strips than the
+        // counter area holds, or more splits than the count field holds, take the reduce kernel
+        uint64_t* ctr = (sp.nsplit > 1 && (size_t)sp.nstrip * 8 <= QK_SPLIT_COUNTER_BYTES &&
+                         sp.nsplit < (1 << kSplitCountBits))
+                            ? reinterpret_cast<uint64_t*>(ws) : nullptr;
         hipError_t e = p.x_dtype == QK_BF16 ? launch_stream_dt<QK_BF16>(p, sp, partial, ctr, stream)
                                             : launch_stream_dt<QK_F16>(p, sp, partial, ctr, stream);
         if (e != hipSuccess || sp.nsplit == 1 || ctr) return e;

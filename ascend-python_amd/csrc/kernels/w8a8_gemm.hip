@@ -931,10 +931,7 @@ hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, int
     if (nsplit > 1 && !full) return hipErrorInvalidValue;  // the plan only splits whole tiles
     // direct-to-LDS kernel: K ranges of whole 4-stage rings, 16-byte aligned rows, and every operand
     // range of a tile addressable by a 32-bit buffer offset
-    static const bool dma_on = [] {
-        const char* e = std::getenv("QK_QMM_DMA");  // tuning override: 0 keeps the register-staged kernel
-        return !(e && std::atoi(e) == 0);
-    }();
+    const bool dma_on = plan_override().qmm_dma;  // debug override: off keeps the register-staged kernel
     const bool dma = dma_on && full && (p.K / nsplit) % (dm::BK * dm::NST) == 0 && p.lda % 16 == 0 &&
                      (uintptr_t)p.a % 16 == 0 && (uintptr_t)p.b % 16 == 0 &&
                      (b_kn ? (p.sbk % 16 == 0 && (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32))
@@ -1003,12 +1000,13 @@ SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
     // measured fastest there), keeping the int32 partials (nsplit*M*N*4 bytes) within the weight's K*N
     // bytes and every split at least 256 rows of K
     const int64_t target = s.mt == 1 ? 256 : 512;
-    while (base * s.nsplit * 2 <= target && K % ((int64_t)s.nsplit * 2 * sk::BK) == 0 &&
-           (int64_t)s.nsplit * 2 * M * 4 <= K && K / (s.nsplit * 2) >= 256)
-        s.nsplit *= 2;
-    if (const char* e = std::getenv("QK_SKINNY_SPLITS")) {  // tuning override: a power of two dividing K in stages
-        const int v = std::atoi(e);
-        if (v >= 1 && v <= 64 && (v & (v - 1)) == 0 && K % ((int64_t)v * sk::BK) == 0) s.nsplit = v;
+    auto fits = [&](int64_t ns) {
+        return K % (ns * sk::BK) == 0 && ns * M * 4 <= K && K / ns >= 256;
+    };
+    while (base * s.nsplit * 2 <= target && fits((int64_t)s.nsplit * 2)) s.nsplit *= 2;
+    // debug override: a power of two within the same bounds as the planned count
+    if (const int v = plan_override().skinny_splits) {
+        if (v == 1 || fits(v)) s.nsplit = v;
     }
     if (base * s.nsplit >= ((int64_t)1 << 31)) s.mt = 0;
     if (s.mt == 8 && s.nsplit == 1) s.mt = 0;  // 128-row tiles only as a split stream (their in-place epilogue is not unrolled)
@@ -1019,8 +1017,12 @@ template <bool B_KN, int MT>
 hipError_t launch_skinny_t(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial, hipStream_t stream) {
     const dim3 grid((uint32_t)((int64_t)s.tiles_m * s.tiles_n * s.nsplit));
     if (s.nsplit == 1) {
-        qmm_skinny<B_KN, MT, true><<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, 1, nullptr);
-        return hipGetLastError();
+        // 128-row tiles run only as a split stream (skinny_plan), so that instance is not built
+        if constexpr (MT == 8) return hipErrorInvalidValue;
+        else {
+            qmm_skinny<B_KN, MT, true><<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, 1, nullptr);
+            return hipGetLastError();
+        }
     }
     qmm_skinny<B_KN, MT, false><<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, s.nsplit, partial);
     hipError_t e = hipGetLastError();

@@ -6,8 +6,7 @@
 // TORCH_CHECK, allocates every output on the input's device
 // (apply_tensor_without_format, op_plugin/ops/base_ops/opapi/MmKernelNpuOpApi.cpp:27-30),
 // asks for the workspace size, takes the workspace from the caching
-// allocator (op_plugin/utils/op_api_common.h:547-551; kept per stream here,
-// because its split-K counters persist between calls), and launches through
+// allocator uninitialised (op_plugin/utils/op_api_common.h:547-551), and launches through
 // the C ABI on the current stream (op_plugin/utils/op_api_common.h:530).
 // A non-zero ABI return becomes a TORCH_CHECK failure carrying
 // qk_last_error(), as EXEC_NPU_CMD does with aclGetRecentErrMsg()
@@ -49,21 +48,20 @@ void check_rc(int rc, const char* op) {
     TORCH_CHECK(rc == QK_OK, "call ", op, " failed, detail:", qk_last_error());
 }
 
-// A split workspace starts with counters that must be zero the first time it
-// is used and that every call leaves at zero (include/qk_abi.h), so each
-// (device, stream) keeps one zero-initialised workspace, replaced by a larger
-// one when a call needs more.  Calls on one stream run in order, so they can
-// share it; the zero fill of a new workspace is enqueued on that stream before
-// the call.  The map is never destroyed (its tensors must not outlive the
-// HIP runtime at exit).
+// Phase-2 scratch for one call, taken from the caching allocator on the
+// call's stream and left uninitialised, as EXEC_NPU_CMD does
+// (op_plugin/utils/op_api_common.h:547-551): the kernels need no particular
+// contents (split-K counters are tagged per call), and the allocator's stream
+// ordering keeps a later user of the block behind this call.
 at::Tensor workspace_for(const at::Tensor& like, size_t bytes) {
-    static std::mutex mu;
-    static auto* cache = new std::map<std::pair<int, qk_stream_t>, at::Tensor>();
-    const auto key = std::make_pair((int)like.device().index(), current_stream(like));
-    std::lock_guard<std::mutex> lock(mu);
-    at::Tensor& ws = (*cache)[key];
-    if (!ws.defined() || (size_t)ws.numel() < bytes) ws = at::zeros({(int64_t)bytes}, like.options().dtype(at::kByte));
-    return ws;
+    return at::empty({(int64_t)bytes}, like.options().dtype(at::kByte));
+}
+
+// Rows of an [..., K] operand: the product of the leading dims (also when K == 0).
+int64_t leading_rows(const at::Tensor& t) {
+    int64_t m = 1;
+    for (int64_t i = 0; i + 1 < t.dim(); ++i) m *= t.size(i);
+    return m;
 }
 
 // ---------------------------------------------------------------- npu_dynamic_quant
@@ -123,7 +121,7 @@ QmmPlan quant_matmul_plan(const at::Tensor& x1, const at::Tensor& x2, const at::
     const int64_t K = x1.size(-1);
     TORCH_CHECK(x2.size(0) == K, op, ": x1 last dim (", K, ") must equal x2 first dim (", x2.size(0), ")");
     const int64_t N = x2.size(1);
-    const int64_t M = K == 0 ? x1.numel() / std::max<int64_t>(1, x1.size(-1)) : x1.numel() / K;
+    const int64_t M = leading_rows(x1);
     const at::ScalarType out_type = output_dtype.value_or(at::kChar);
     TORCH_CHECK(out_type == at::kBFloat16 || out_type == at::kHalf || out_type == at::kChar ||
                     out_type == at::kInt || out_type == at::kFloat,
@@ -251,7 +249,7 @@ WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at
     }
     std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
     shape.back() = N;
-    const int64_t M = K == 0 ? 0 : x.numel() / K;
+    const int64_t M = leading_rows(x);
     return {M, N, K, group, int4, shape};
 }
 

@@ -5,11 +5,111 @@
 // aclGetRecentErrMsg() plays behind EXEC_NPU_CMD,
 // op_plugin/utils/op_api_common.h:544-555), and enqueues the kernels on the
 // caller's stream.  Nothing here allocates or synchronises.
+#include <atomic>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
+#include <unistd.h>
+
 #include "kernels/common.h"
+
+namespace qk {
+
+// Split-K counter tags: a process-wide call counter seeded from the clock and
+// the process id, scrambled by the splitmix64 output function (Steele, Lea and
+// Flood, "Fast splittable pseudorandom number generators", 2014) so that tags
+// look random against whatever data a fresh workspace holds, and cut to 48
+// bits; 0 and all ones are skipped, so a zero- or 0xFF-filled counter word
+// never carries a live tag.  A counter word left by an earlier call is zero
+// (its last arrival cleared it), so tags of different calls need not differ.
+uint64_t next_split_tag() {
+    static std::atomic<uint64_t> seq{(uint64_t)std::chrono::steady_clock::now().time_since_epoch().count() ^
+                                     ((uint64_t)getpid() << 32)};
+    constexpr uint64_t kMask = ((uint64_t)1 << (64 - kSplitCountBits)) - 1;
+    for (;;) {
+        uint64_t z = seq.fetch_add(0x9e3779b97f4a7c15ull, std::memory_order_relaxed);
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z ^= z >> 31;
+        const uint64_t tag = z & kMask;
+        if (tag != 0 && tag != kMask) return tag;
+    }
+}
+
+namespace {
+
+bool parse_plan(const char* spec, PlanOverride& o) {
+    PlanOverride r;
+    std::string s(spec ? spec : "");
+    size_t pos = 0;
+    while (pos < s.size()) {
+        size_t end = s.find(',', pos);
+        if (end == std::string::npos) end = s.size();
+        const std::string item = s.substr(pos, end - pos);
+        pos = end + 1;
+        if (item.empty()) continue;
+        const size_t eq = item.find('=');
+        if (eq == std::string::npos) return false;
+        const std::string k = item.substr(0, eq), v = item.substr(eq + 1);
+        int a = 0, b = 0, c = 0;
+        if (k == "w4_stream") {
+            if (v == "off") r.w4_stream_off = true;
+            else if (std::sscanf(v.c_str(), "%d:%d:%d", &a, &b, &c) == 3 && (a == 8 || a == 16) &&
+                     ((b == 4 && (c == 2 || c == 4)) || (a == 8 && b == 8 && (c == 2 || c == 3)))) {
+                r.w4_stream_nwave = a;
+                r.w4_stream_nkb = b;
+                r.w4_stream_pf = c;
+            } else return false;
+        } else if (k == "w4_gemm") {
+            if (v == "force") r.w4_gemm = 1;
+            else if (v == "nodma") r.w4_gemm = 2;
+            else if (v == "off") r.w4_gemm = 3;
+            else return false;
+        } else if (k == "w4_splits" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 4096) {
+            r.w4_splits = a;
+        } else if (k == "qmm_dma" && (v == "0" || v == "1")) {
+            r.qmm_dma = v == "1";
+        } else if (k == "skinny_splits" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 64 &&
+                   (a & (a - 1)) == 0) {
+            r.skinny_splits = a;
+        } else {
+            return false;
+        }
+    }
+    o = r;
+    return true;
+}
+
+// Snapshots are never freed: a planner may still read the previous one.
+std::atomic<const PlanOverride*>& plan_slot() {
+    static std::atomic<const PlanOverride*> slot{[] {
+        auto* o = new PlanOverride();
+        if (const char* e = std::getenv("QK_DEBUG_PLAN")) {
+            if (!parse_plan(e, *o)) std::fprintf(stderr, "libqk_hip: QK_DEBUG_PLAN=\"%s\" not understood, ignored\n", e);
+        }
+        return o;
+    }()};
+    return slot;
+}
+
+}  // namespace
+
+const PlanOverride& plan_override() { return *plan_slot().load(std::memory_order_acquire); }
+
+bool set_plan_override(const char* spec) {
+    auto* o = new PlanOverride();
+    if (!parse_plan(spec, *o)) {
+        delete o;
+        return false;
+    }
+    plan_slot().store(o, std::memory_order_release);
+    return true;
+}
+
+}  // namespace qk
 
 namespace {
 
@@ -42,7 +142,13 @@ extern "C" {
 
 const char* qk_last_error(void) { return g_last_error.c_str(); }
 
-int qk_abi_version(void) { return 2; }
+int qk_abi_version(void) { return 3; }
+
+int qk_debug_set_plan(const char* spec) {
+    g_last_error.clear();
+    if (!qk::set_plan_override(spec)) return fail(QK_ERR_ARG, "qk_debug_set_plan: \"%s\" not understood", spec ? spec : "");
+    return QK_OK;
+}
 
 int qk_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t K, const float* smooth_scales, int8_t* y,
                      float* scale, qk_stream_t stream) {

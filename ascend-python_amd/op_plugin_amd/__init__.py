@@ -56,7 +56,7 @@ QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32 = 1, 2, 3, 4, 5
 QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, -2, -3, -4
 
 ABI_SYMBOLS = (
-    "qk_last_error", "qk_abi_version", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",
+    "qk_last_error", "qk_abi_version", "qk_debug_set_plan", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",
     "qk_quant_matmul", "qk_weight_quant_bmm_workspace_size", "qk_weight_quant_bmm", "qk_int4_pack",
     "qk_rms_norm", "qk_rms_norm_quant", "qk_swiglu", "qk_swiglu_quant",
 )
@@ -73,6 +73,7 @@ def abi() -> ctypes.CDLL:
         L.qk_last_error.restype = ctypes.c_char_p
         L.qk_last_error.argtypes = []
         L.qk_abi_version.restype = I
+        L.qk_debug_set_plan.argtypes = [ctypes.c_char_p]
         L.qk_dynamic_quant.argtypes = [P, I, I64, I64, P, P, P, P]
         L.qk_quant_matmul_workspace_size.argtypes = [I64, I64, I64, I, ctypes.POINTER(SZ)]
         L.qk_quant_matmul.argtypes = [P, I64, P, I64, I64, I64, I64, I64, P, I64, P, I64, P, P, I, P, I, P, SZ, P]
@@ -94,8 +95,18 @@ def last_error() -> str:
     return abi().qk_last_error().decode()
 
 
+def debug_set_plan(spec: str = "") -> None:
+    """Force kernel choices of the planners (tests and tuning only; "" restores the planners' choices).
+
+    Spec grammar: see PlanOverride in csrc/kernels/common.h, e.g. "w4_gemm=force" or
+    "w4_stream=8:4:2,skinny_splits=4"."""
+    rc = abi().qk_debug_set_plan(spec.encode())
+    if rc != 0:
+        raise ValueError(last_error())
+
+
 __all__ = [
     "npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
     "npu_convert_weight_to_int4pack", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
-    "npu_swiglu_dynamic_quant", "abi", "last_error", "LIB_PATH", "OPS_PATH",
+    "npu_swiglu_dynamic_quant", "abi", "last_error", "debug_set_plan", "LIB_PATH", "OPS_PATH",
 ]

@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--no-configs", action="store_true", help="skip timing the other BASELINE configs")
     ap.add_argument("--configs-only", action="store_true",
                     help="time only the other BASELINE configs (for a kernel trace of them alone)")
-    ap.add_argument("--config-reps", type=int, default=20, help="timed launches per other config")
+    ap.add_argument("--min-launches", type=int, default=100,
+                    help="launches timed per kernel (median over runs of back-to-back launches)")
     return ap.parse_args()
 
 
@@ -74,62 +75,117 @@ def hbm_traffic() -> dict:
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it (model name, family / model / stepping)."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                if ":" in ln:
+                    k, v = (t.strip() for t in ln.split(":", 1))
+                    if k in ("model name", "cpu family", "model", "stepping") and k not in fields:
+                        fields[k] = v
+                if not ln.strip() and fields:
+                    break
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    name = fields.get("model name") or platform.processor() or "unknown"
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ids})" if ids else name
 
 
 def cpu_baseline(target_s: float) -> dict:
-    """The oracle (single-threaded C) on a bounded row sample of cfg4, timed on this host."""
+    """The CPU reference path of BASELINE.md section 3 on cfg1, on all host cores.
+
+    One step = npu_dynamic_quant (torch CPU fp32: absmax / 127, IEEE division, round-half-even, clamp)
+    + the exact int32 GEMM (float64 BLAS on int8-valued operands) + the fused epilogue and bf16 cast
+    (the C oracle).  The first step's output is checked bit for bit against the oracle's whole path;
+    the reported rate is the median over the steps of a ~target_s sample.  A one-step cfg4 figure by
+    the same method is reported beside it."""
     import numpy as np
+    import torch
 
     from oracle import oracle
     from op_plugin_amd import workloads as W
 
-    d = W.w8a8_inputs(W.CFG4)
-    xb = W.bits(d["x"])
-    w = d["w"].numpy()
-    ws = d["w_scale"].numpy()
-    b = W.bits(d["bias"])
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
 
-    def run(rows):
+    def prepare(case):
+        d = W.w8a8_inputs(case, seed=0)
+        return d["x"], d["w"].double(), d["w_scale"].numpy(), W.bits(d["bias"])
+
+    def step(x, w64, ws, b):
+        xf = x.float()
+        s = xf.abs().amax(dim=-1) / 127.0
+        q = torch.where(s[:, None] > 0, torch.round(xf / s[:, None]), torch.zeros_like(xf)).clamp_(-128, 127)
+        acc = (q.double() @ w64).to(torch.int32).numpy()
+        return q.to(torch.int8).numpy(), s.numpy(), oracle.quant_matmul_epilogue(
+            acc, ws, pertoken=s.numpy(), bias=b, bias_dtype=oracle.BF16, out_dtype=oracle.BF16)
+
+    c1 = W.CFG1
+    x, w64, ws, b = prepare(c1)
+    q, s, out = step(x, w64, ws, b)                       # warm-up, and the parity check
+    rq, rs = oracle.dynamic_quant(W.bits(x), oracle.F16)
+    ok = bool(np.array_equal(q, rq) and np.array_equal(s, rs) and np.array_equal(
+        out, oracle.quant_matmul(rq, W.w8a8_inputs(c1, seed=0)["w"].numpy(), ws, pertoken=rs, bias=b,
+                                 bias_dtype=oracle.BF16, out_dtype=oracle.BF16)))
+    times = []
+    t_end = time.perf_counter() + target_s
+    while time.perf_counter() < t_end or len(times) < 5:
         t0 = time.perf_counter()
-        q, s = oracle.dynamic_quant(xb[:rows], oracle.F16)
-        oracle.quant_matmul(q, w, ws, pertoken=s, bias=b, bias_dtype=oracle.BF16, out_dtype=oracle.BF16)
-        return time.perf_counter() - t0
+        step(x, w64, ws, b)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    ops1 = 2.0 * c1.M * c1.N * c1.K
 
-    t8 = run(8)
-    rows = int(max(8, min(W.CFG4.M, 8 * target_s / max(t8, 1e-6))))
-    t = run(rows)
-    ops = 2.0 * rows * W.CFG4.N * W.CFG4.K
-    return {"value": ops / t / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
-            "sample": f"cfg4 W8A8 path (dynamic quant + int32 GEMM + epilogue) on rows 0..{rows - 1} of 4096, "
-                      f"K=N=8192, {t:.2f} s, oracle/qk_oracle.c single-threaded",
-            "cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
+    c4 = W.CFG4
+    x4, w4, ws4, b4 = prepare(c4)
+    t0 = time.perf_counter()
+    step(x4, w4, ws4, b4)
+    t4 = time.perf_counter() - t0
+    return {"value": round(ops1 / t / 1e12, 4), "unit": "TOPS", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"cfg1 W8A8 path (dynamic quant [128,4096] + exact int32 GEMM x [4096,4096] + epilogue, "
+                      f"bf16 out): median of {len(times)} steps over {sum(times):.1f} s, "
+                      f"{t * 1e3:.2f} ms per step; bit-exact vs the oracle: {ok}",
+            "cpu_model": cpu_model(), "host_cpus": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "cfg4_one_step": {"s": round(t4, 3), "TOPS": round(2.0 * c4.M * c4.N * c4.K / t4 / 1e12, 4)}}
 
 
-def _timed(fn, reps: int, warm: int = 3) -> float:
-    """Mean seconds per call of fn(i), from events recorded on the current stream around each call."""
+def launch_runs(fn, per_run: int, min_launches: int, prime) -> dict:
+    """Per-launch kernel time of fn(i) as the median over runs of back-to-back launches.
+
+    Each run enqueues prime() (about half a millisecond of other GPU work, so that every launch of the
+    run is queued before the GPU reaches it), then per_run launches of fn between two HIP events on the
+    current stream; the run's figure is the event interval / per_run.  Runs repeat until at least
+    min_launches launches are timed.  Returns the median (seconds) and the spread of the run figures."""
+    import numpy as np
     import torch
-    for i in range(warm):
+    for i in range(3):
         fn(i)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    torch.cuda.synchronize()
-    for i in range(reps):
-        ev[i][0].record()
-        fn(i)
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in ev) / reps * 1e-3
+    runs = []
+    k = 0
+    while k < min_launches:
+        prime()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(per_run):
+            fn(k + i)
+        b.record()
+        torch.cuda.synchronize()
+        runs.append(a.elapsed_time(b) * 1e-3 / per_run)
+        k += per_run
+    r = np.array(runs)
+    return {"s": float(np.median(r)), "min_s": float(r.min()), "max_s": float(r.max()), "launches": k,
+            "runs": len(runs), "per_run": per_run}
 
 
-def other_configs(q, W, dev, reps: int) -> dict:
-    """The remaining BASELINE configs, each timed on its own (kernel time per launch).
+def timing_note(t: dict) -> str:
+    return (f"median over {t['runs']} runs of {t['per_run']} back-to-back launches ({t['launches']} launches); "
+            f"run range {t['min_s'] * 1e6:.2f}-{t['max_s'] * 1e6:.2f} us")
+
+
+def other_configs(q, W, dev, min_launches: int) -> dict:
+    """The remaining BASELINE configs, each timed on its own (time per op call, every kernel of the call).
 
     Weights rotate over enough operand sets to exceed the 256 MB Infinity Cache where the
     shape is bandwidth-bound; operands come from seeded device generators."""
@@ -138,6 +194,14 @@ def other_configs(q, W, dev, reps: int) -> dict:
 
     res = {}
     g = torch.Generator(device=dev).manual_seed(7)
+    pa = torch.randn((4096, 4096), generator=g, device=dev).bfloat16()
+
+    def prime():  # ~0.5 ms of bf16 GEMMs (hipBLASLt) ahead of each timed run
+        for _ in range(4):
+            torch.mm(pa, pa)
+
+    def timed(fn, per_run):
+        return launch_runs(fn, per_run, min_launches, prime)["s"]
 
     def i8(shape):
         return torch.randint(-127, 128, shape, generator=g, device=dev, dtype=torch.int8)
@@ -151,8 +215,8 @@ def other_configs(q, W, dev, reps: int) -> dict:
     x = torch.randn((c.M, c.K), generator=g, device=dev).half()
     xq, xs = q.npu_dynamic_quant(x)
     sc, b = u((c.N,), 1e-3, 1e-2), (0.1 * torch.randn(c.N, generator=g, device=dev)).bfloat16()
-    t = _timed(lambda i: q.npu_quant_matmul(xq, ws[i % 32], sc, pertoken_scale=xs, bias=b,
-                                            output_dtype=torch.bfloat16), reps)
+    t = timed(lambda i: q.npu_quant_matmul(xq, ws[i % 32], sc, pertoken_scale=xs, bias=b,
+                                           output_dtype=torch.bfloat16), 32)
     res["cfg1_w8a8_m128_k4096_n4096"] = {"avg_us": round(t * 1e6, 2), "TOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1),
                                          "mfma_frac": round(2 * c.M * c.N * c.K / t / 1e12 / PEAK_I8_TOPS, 4)}
     del ws
@@ -164,8 +228,8 @@ def other_configs(q, W, dev, reps: int) -> dict:
     for c in W.CFG2:
         x = torch.randn((c.M, c.K), generator=g, device=dev).half()
         xq, xs = q.npu_dynamic_quant(x)
-        t = _timed(lambda i: q.npu_quant_matmul(xq, ws[i % 3], sc, pertoken_scale=xs, output_dtype=torch.bfloat16),
-                   reps)
+        t = timed(lambda i: q.npu_quant_matmul(xq, ws[i % 3], sc, pertoken_scale=xs, output_dtype=torch.bfloat16),
+                  12)
         nb = c.K * c.N + c.M * c.K + 4 * c.M + 4 * c.N + 2 * c.M * c.N
         res[f"cfg2_w8a8_m{c.M}_k8192_n28672"] = {"avg_us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
                                                  "hbm_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4)}
@@ -177,7 +241,7 @@ def other_configs(q, W, dev, reps: int) -> dict:
     s = u((c.K // c.group, c.N), 5e-3, 2e-2).half()
     o = u((c.K // c.group, c.N), -1.0, 1.0).half()
     x = torch.randn((c.M, c.K), generator=g, device=dev).bfloat16()
-    t = _timed(lambda i: q.npu_weight_quant_batchmatmul(x, wp, s, o, antiquant_group_size=c.group), reps)
+    t = timed(lambda i: q.npu_weight_quant_batchmatmul(x, wp, s, o, antiquant_group_size=c.group), 8)
     res["cfg3_w4a16_m2048_k4096_n11008"] = {"avg_us": round(t * 1e6, 2),
                                             "TFLOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1),
                                             "mfma_frac_bf16": round(2 * c.M * c.N * c.K / t / 1e12 / 2500.0, 4)}
@@ -188,7 +252,7 @@ def other_configs(q, W, dev, reps: int) -> dict:
     gamma = (1 + 0.02 * torch.randn(H, generator=g, device=dev)).bfloat16()
     wgu, sgu = i8((H, 2 * I)), u((2 * I,), 1e-3, 1e-2)
     wd, sd = i8((I, H)), u((H,), 1e-3, 1e-2)
-    t = _timed(lambda i: quant_mlp(x, gamma, wgu, sgu, wd, sd, eps=W.CFG5["eps"]), reps)
+    t = timed(lambda i: quant_mlp(x, gamma, wgu, sgu, wd, sd, eps=W.CFG5["eps"]), 8)
     ops = 2 * T * H * 2 * I + 2 * T * I * H
     res["cfg5_quant_mlp_t512_h4096_i14336"] = {"avg_us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 1),
                                                "mfma_frac": round(ops / t / 1e12 / PEAK_I8_TOPS, 4)}
@@ -211,7 +275,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.configs_only:
-        print(json.dumps({"other_configs": other_configs(q, W, dev, args.config_reps)}), flush=True)
+        print(json.dumps({"other_configs": other_configs(q, W, dev, args.min_launches)}), flush=True)
         return
 
     # ---------------- cfg4 operands (set 0 = the seeded config inputs)
@@ -282,32 +346,26 @@ def main():
 
     # Per-launch kernel durations.  An event pair around one launch also counts the event packets
     # and the launch gap (several us here), so every kernel is timed as runs of back-to-back
-    # launches between two events, queued behind three cfg4 GEMMs so that every launch is
-    # enqueued before the GPU reaches it (no host gaps inside the run).  The per-step event-pair
-    # figures are reported beside them.
-    def run_rate(fn, reps):
+    # launches between two events, each run queued behind three cfg4 GEMMs so that every launch is
+    # enqueued before the GPU reaches it (no host gaps inside the run); the figure is the median over
+    # the runs, at least --min-launches launches per kernel.  The per-step event-pair figures are
+    # reported beside them.
+    xq0, xs0 = q.npu_dynamic_quant(xs4[0])
+
+    def prime():
         for i in range(3):
             q.npu_quant_matmul(xq0, ws4[i % W8A8_SETS], scale4, pertoken_scale=xs0, bias=bias4,
                                output_dtype=torch.bfloat16)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for i in range(reps):
-            fn(i)
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) * 1e-3 / reps
 
-    xq0, xs0 = q.npu_dynamic_quant(xs4[0])
     xq_sets = [q.npu_dynamic_quant(xs4[s]) for s in range(W8A8_SETS)]
-    gemm_rates = [run_rate(lambda i: q.npu_quant_matmul(xq_sets[i % W8A8_SETS][0], ws4[i % W8A8_SETS], scale4,
-                                                        pertoken_scale=xq_sets[i % W8A8_SETS][1], bias=bias4,
-                                                        output_dtype=torch.bfloat16), 8)
-                  for _ in range(3)]
+    gemm_t = launch_runs(lambda i: q.npu_quant_matmul(xq_sets[i % W8A8_SETS][0], ws4[i % W8A8_SETS], scale4,
+                                                      pertoken_scale=xq_sets[i % W8A8_SETS][1], bias=bias4,
+                                                      output_dtype=torch.bfloat16), 8, args.min_launches, prime)
     del xq_sets
-    w4_rates = [run_rate(lambda i: q.npu_weight_quant_batchmatmul(x3, wp3[i % W4_SETS], sc3[i % W4_SETS],
-                                                                  of3[i % W4_SETS], antiquant_group_size=128), 24)
-                for _ in range(3)]
-    dq_rates = [run_rate(lambda i: q.npu_dynamic_quant(xs4[i % W8A8_SETS]), 12) for _ in range(3)]
+    w4_t = launch_runs(lambda i: q.npu_weight_quant_batchmatmul(x3, wp3[i % W4_SETS], sc3[i % W4_SETS],
+                                                                of3[i % W4_SETS], antiquant_group_size=128),
+                       W4_SETS, args.min_launches, prime)
+    dq_t = launch_runs(lambda i: q.npu_dynamic_quant(xs4[i % W8A8_SETS]), 12, args.min_launches, prime)
 
     # ---------------- parity spot check of set 0 against the oracle (rows 0..7)
     parity = None
@@ -328,17 +386,17 @@ def main():
 
     ops4 = 2.0 * c4.M * c4.N * c4.K
     gemm_step_s = float(np.mean(t_gemm))
-    gemm_s = float(np.mean(gemm_rates))
+    gemm_s = gemm_t["s"]
     tops = ops4 / gemm_s / 1e12
     bytes4 = c4.M * c4.K + c4.K * c4.N + 4 * c4.M + 4 * c4.N + 2 * c4.N + 2 * c4.M * c4.N
     ng = c3.K // c3.group
     bytes3 = c3.M * c3.K * 2 + c3.K * c3.N // 2 + 2 * 2 * ng * c3.N + c3.M * c3.N * 2
     w4_step_s = float(np.mean(t_w4))
-    w4_s = float(np.mean(w4_rates))
+    w4_s = w4_t["s"]
     gbs3 = bytes3 / w4_s / 1e9
     qbytes = c4.M * c4.K * 3 + 4 * c4.M
     q_step_s = float(np.mean(t_quant))
-    q_s = float(np.mean(dq_rates))
+    q_s = dq_t["s"]
 
     traffic = hbm_traffic()
     t_w4 = traffic.get("w4_stream")
@@ -366,23 +424,23 @@ def main():
                      "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": t_gemm_traffic,
                      "kernel": "qmm (W8A8 GEMM)", "avg_us": round(gemm_s * 1e6, 2),
                      "algorithmic": f"2*M*N*K = {ops4:.0f} int8 ops per launch",
-                     "timing": "back-to-back launches over the 4 operand sets (8 per run, 3 runs)",
+                     "timing": timing_note(gemm_t) + ", rotating over the 4 operand sets",
                      "avg_us_event_pair_in_step": round(gemm_step_s * 1e6, 2)},
         "secondary": {
             "metric": "W4A16 decode GB/s (M=16)", "value": round(gbs3, 1), "unit": "GB/s",
             "roofline": {"bound": "hbm", "achieved": round(gbs3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(gbs3 / PEAK_HBM_GBS, 4), "traffic": t_w4,
                          "avg_us": round(w4_s * 1e6, 3), "algorithmic_bytes": bytes3,
-                         "timing": "back-to-back launches (24 per run, 3 runs)",
+                         "timing": timing_note(w4_t) + f", rotating over the {W4_SETS} operand sets",
                          "avg_us_event_pair_in_step": round(w4_step_s * 1e6, 3)}},
         "dynamic_quant": {"avg_us": round(q_s * 1e6, 2), "GB/s": round(qbytes / q_s / 1e9, 1),
                           "hbm_frac": round(qbytes / q_s / 1e9 / PEAK_HBM_GBS, 4),
-                          "timing": "back-to-back launches (12 per run, 3 runs)",
+                          "timing": timing_note(dq_t),
                           "avg_us_event_pair_in_step": round(q_step_s * 1e6, 2)},
         "parity": parity,
     }
     if not args.no_configs:
-        line["other_configs"] = other_configs(q, W, dev, args.config_reps)
+        line["other_configs"] = other_configs(q, W, dev, args.min_launches)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

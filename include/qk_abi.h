@@ -23,15 +23,20 @@
  *     op_plugin/utils/op_api_common.h:546, 555).
  * All functions are thread-safe; calls on one stream execute in order.
  *
- * Workspaces (this build's one departure from the reference's per-call
- * scratch): a non-empty workspace begins with QK_SPLIT_COUNTER_BYTES of
- * split-K arrival counters, followed by the partial sums (split-K shapes) or
- * by the activations' per-group sums (weight-quant matmul at large M).  The
- * counters must be zero the first time a workspace is used -- allocate it
- * once, zero it (hipMemset), and keep reusing it; every call leaves them zero
- * again.  The workgroup that completes a tile's splits adds them up itself,
- * so no second kernel runs.  Calls that may be in flight at the same time
- * need distinct workspaces.
+ * Workspaces, as the reference's per-call scratch
+ * (op_plugin/utils/op_api_common.h:547-551, unsafe_empty_workspace): the
+ * caller passes at least *_workspace_size() bytes, 256-byte aligned, of any
+ * contents -- uninitialised memory is fine.  A non-empty workspace begins with
+ * QK_SPLIT_COUNTER_BYTES of split-K arrival counters, followed by the partial
+ * sums (split-K shapes) or by the activations' per-group sums (weight-quant
+ * matmul at large M).  Each counter carries the tag of the call that counts
+ * into it (48 bits drawn per call, never 0 or all ones), so what an earlier
+ * call or another user left there is not mistaken for arrivals of this call;
+ * the one exception is memory whose counter words happen to hold this call's
+ * random 48-bit tag (odds 2^-48 per counter word for random contents, zero for
+ * zero- or 0xFF-filled memory).  The workgroup that completes a tile's splits
+ * adds them up itself, so no second kernel runs.  Calls that may be in flight
+ * at the same time need distinct workspaces.
  */
 #ifndef QK_ABI_H
 #define QK_ABI_H
@@ -68,8 +73,17 @@ enum {
 const char* qk_last_error(void);
 
 /* ABI revision; bumped on any incompatible signature or contract change
- * (2: the split-K counters at the head of a workspace). */
+ * (2: the split-K counters at the head of a workspace; 3: the counters are
+ * tagged per call, so a workspace needs no initialisation). */
 int qk_abi_version(void);
+
+/* Debug and test hook, no counterpart in the reference: forces kernel choices
+ * of the planners (spec grammar in csrc/kernels/common.h, "PlanOverride"; NULL
+ * or "" restores the planners' own choices).  The library reads the
+ * QK_DEBUG_PLAN environment variable once at first use; this call replaces
+ * that for the rest of the process.  Not meant for production callers.
+ * Returns QK_ERR_ARG (override unchanged) for a spec it does not understand. */
+int qk_debug_set_plan(const char* spec);
 
 /* Bytes of split-K counters at the start of every non-empty workspace. */
 #define QK_SPLIT_COUNTER_BYTES 4096

@@ -28,7 +28,19 @@ def test_abi_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), f"{n} declared in qk_abi.h but not exported"
     assert set(names) == set(q.ABI_SYMBOLS)
-    assert q.abi().qk_abi_version() == 2
+    assert q.abi().qk_abi_version() == 3
+
+
+def test_debug_plan_override_parsing():
+    """The planners' one debug override: accepted specs, and refusal (with the override unchanged) of
+    specs it does not understand.  Nothing is launched."""
+    for spec in ("", "w4_stream=16:4:4", "w4_stream=off", "w4_gemm=force,skinny_splits=4", "qmm_dma=0",
+                 "w4_splits=8,w4_gemm=nodma"):
+        q.debug_set_plan(spec)
+    for bad in ("w4_stream=12:4:2", "w4_gemm=maybe", "skinny_splits=3", "nonsense", "qmm_dma=2"):
+        with pytest.raises(ValueError, match="not understood"):
+            q.debug_set_plan(bad)
+    q.debug_set_plan("")
 
 
 def test_abi_refuses_bad_arguments_without_launch():
