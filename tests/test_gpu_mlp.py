@@ -5,7 +5,7 @@ Bar: RMSNorm / SwiGLU outputs are floating point, within rtol 1e-2 / atol 1e-2 o
 oracle (and in practice within one unit in the last place); rstd within 1e-6 relative.  The fused
 kernels' int8 rows and scales are bit-exact against the oracle's dynamic quantization of the same
 kernel's unfused 16-bit output, so the fusion itself changes no bit.  The block is checked on all
-512 rows against the oracle chain.
+512 rows, stage by stage.
 """
 import ctypes
 
@@ -39,12 +39,15 @@ def close(got, ref_bits, dtype, rtol=1e-2, atol=1e-2):
     g = got.cpu().float()
     r = W.from_bits(ref_bits, dtype).float().reshape(g.shape)
     torch.testing.assert_close(g, r, rtol=rtol, atol=atol)
-    # diagnostic bar: the fp32 kernel and the float64 oracle differ by at most one rounding step
-    # (signed zeros compare equal: results far below the 16-bit range may come out as -0 or +0)
+    # diagnostic bar: the fp32 kernel and the float64 oracle differ by at most one rounding step.
+    # Results of magnitude below 2^-100 count as zero (signed zeros compare equal): there the fp32
+    # formula's intermediates underflow where float64's do not -- SwiGLU's exp(-a) overflows fp32 for
+    # a < -88.7, so the kernel returns +-0 where the oracle keeps a value of order 1e-35.
     gb = W.bits(got.cpu()).astype(np.int32)
     rb = np.asarray(ref_bits).astype(np.int32).reshape(g.shape)
-    gb[(gb & 0x7fff) == 0] = 0
-    rb[(rb & 0x7fff) == 0] = 0
+    tiny = (g.abs() < 2.0**-100).numpy() & (r.abs() < 2.0**-100).numpy()
+    gb[tiny] = 0
+    rb[tiny] = 0
     assert np.abs(gb - rb).max() <= 1
 
 
@@ -177,28 +180,67 @@ def test_abi_rms_norm_and_swiglu(ops, oracle):
 
 
 def test_quant_mlp_block_cfg5(ops, oracle):
-    """cfg5 end to end: fused and unfused chains give identical bits, and all 512 rows match the oracle
-    chain (RMSNorm -> quant -> W8A8 -> SwiGLU -> quant -> W8A8) within 1e-2.  The two GEMMs of the chain
-    take their exact int32 accumulators from float64 GEMMs (pinned against qo_w8a8_acc on two rows each)
-    and the oracle's epilogue."""
+    """cfg5, all 512 rows, every stage against the oracle on the GPU's own inputs to that stage:
+    RMSNorm within one ulp; its fused quantization bit-exact (= qo_dynamic_quant of the GPU's RMSNorm
+    output); the gate_up W8A8 bit-exact (exact float64 accumulator, pinned to qo_w8a8_acc, plus
+    qo_quant_matmul_epilogue); SwiGLU within one ulp and its fused quantization bit-exact; the down W8A8
+    bit-exact.  quant_mlp (fused) and the unfused chain give the same bits as these stages.
+    End to end against the independent oracle chain: RMSNorm and SwiGLU may differ by one ulp, and a
+    one-ulp change of a row's absmax rescales that row's int8 activations, so rows whose quantized
+    activations differ from the oracle chain's are counted (a few are expected; bounded at 5 %); every
+    other row must match within rtol = atol = 1e-2."""
     from op_plugin_amd.mlp import quant_mlp
     c = W.CFG5
-    say(f"quant_mlp cfg5 T={c['tokens']} H={c['hidden']} I={c['intermediate']} (all rows)")
-    d = W.mlp_inputs(c["tokens"], c["hidden"], c["intermediate"], seed=0)
+    T = c["tokens"]
+    say(f"quant_mlp cfg5 T={T} H={c['hidden']} I={c['intermediate']} (all rows, every stage)")
+    d = W.mlp_inputs(T, c["hidden"], c["intermediate"], seed=0)
     dev = {k: v.to(DEV) for k, v in d.items()}
     out = quant_mlp(dev["x"], dev["gamma"], dev["w_gu"], dev["s_gu"], dev["w_d"], dev["s_d"], eps=c["eps"])
     out_u = quant_mlp(dev["x"], dev["gamma"], dev["w_gu"], dev["s_gu"], dev["w_d"], dev["s_d"], eps=c["eps"],
                       fused=False)
-    assert out.shape == (c["tokens"], c["hidden"]) and out.dtype == torch.bfloat16
+    assert out.shape == (T, c["hidden"]) and out.dtype == torch.bfloat16
     assert torch.equal(out, out_u)
-    pin = np.r_[0, c["tokens"] - 1]
-    y, _ = oracle.rms_norm(W.bits(d["x"]), BF16, W.bits(d["gamma"]), c["eps"])
-    q1, s1 = oracle.dynamic_quant(y, BF16)
-    acc1 = exact.w8a8_acc(q1, d["w_gu"].numpy())
-    exact.pin_acc(oracle, q1, d["w_gu"].numpy(), acc1, pin)
-    h = oracle.quant_matmul_epilogue(acc1, d["s_gu"].numpy(), pertoken=s1, out_dtype=BF16)
-    q2, s2 = oracle.dynamic_quant(oracle.swiglu(h, BF16), BF16)
-    acc2 = exact.w8a8_acc(q2, d["w_d"].numpy())
-    exact.pin_acc(oracle, q2, d["w_d"].numpy(), acc2, pin)
-    ref = oracle.quant_matmul_epilogue(acc2, d["s_d"].numpy(), pertoken=s2, out_dtype=BF16)
-    torch.testing.assert_close(out.cpu().float(), W.from_bits(ref, torch.bfloat16).float(), rtol=1e-2, atol=1e-2)
+    # the block's stages, op by op
+    y = ops.npu_rms_norm(dev["x"], dev["gamma"], c["eps"])[0]
+    q1, s1, _ = ops.npu_rms_norm_dynamic_quant(dev["x"], dev["gamma"], c["eps"])
+    h = ops.npu_quant_matmul(q1, dev["w_gu"], dev["s_gu"], pertoken_scale=s1, output_dtype=torch.bfloat16)
+    sw = ops.npu_swiglu(h)
+    q2, s2 = ops.npu_swiglu_dynamic_quant(h)
+    o = ops.npu_quant_matmul(q2, dev["w_d"], dev["s_d"], pertoken_scale=s2, output_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(o, out)
+    pin = np.r_[0, T - 1]
+    # RMSNorm (one ulp) and its quantization (bit-exact on the GPU's y)
+    y_ref, _ = oracle.rms_norm(W.bits(d["x"]), BF16, W.bits(d["gamma"]), c["eps"])
+    close(y, y_ref, torch.bfloat16)
+    rq1, rs1 = oracle.dynamic_quant(W.bits(y.cpu()), BF16)
+    q1n, s1n = q1.cpu().numpy(), s1.cpu().numpy()
+    assert np.array_equal(q1n, rq1) and np.array_equal(s1n, rs1)
+    # gate_up W8A8, bit-exact on the GPU's q1
+    acc1 = exact.w8a8_acc(q1n, d["w_gu"].numpy())
+    exact.pin_acc(oracle, q1n, d["w_gu"].numpy(), acc1, pin)
+    h_ref = oracle.quant_matmul_epilogue(acc1, d["s_gu"].numpy(), pertoken=s1n, out_dtype=BF16)
+    assert np.array_equal(W.bits(h.cpu()), h_ref)
+    # SwiGLU (one ulp) and its quantization (bit-exact on the GPU's SwiGLU output)
+    close(sw, oracle.swiglu(h_ref, BF16), torch.bfloat16)
+    rq2, rs2 = oracle.dynamic_quant(W.bits(sw.cpu()), BF16)
+    q2n, s2n = q2.cpu().numpy(), s2.cpu().numpy()
+    assert np.array_equal(q2n, rq2) and np.array_equal(s2n, rs2)
+    # down W8A8, bit-exact on the GPU's q2
+    acc2 = exact.w8a8_acc(q2n, d["w_d"].numpy())
+    exact.pin_acc(oracle, q2n, d["w_d"].numpy(), acc2, pin)
+    o_ref = oracle.quant_matmul_epilogue(acc2, d["s_d"].numpy(), pertoken=s2n, out_dtype=BF16)
+    assert np.array_equal(W.bits(out.cpu()), o_ref)
+    # end to end against the independent oracle chain
+    iq1, is1 = oracle.dynamic_quant(y_ref, BF16)
+    ih = oracle.quant_matmul_epilogue(exact.w8a8_acc(iq1, d["w_gu"].numpy()), d["s_gu"].numpy(), pertoken=is1,
+                                      out_dtype=BF16)
+    iq2, is2 = oracle.dynamic_quant(oracle.swiglu(ih, BF16), BF16)
+    iref = oracle.quant_matmul_epilogue(exact.w8a8_acc(iq2, d["w_d"].numpy()), d["s_d"].numpy(), pertoken=is2,
+                                        out_dtype=BF16)
+    same = (q1n == iq1).all(axis=1) & (q2n == iq2).all(axis=1)
+    say(f"  rows whose int8 activations differ from the independent oracle chain: {int((~same).sum())} of {T}")
+    assert (~same).sum() <= T // 20
+    rows = torch.as_tensor(np.flatnonzero(same))
+    torch.testing.assert_close(out.cpu().float()[rows], W.from_bits(iref, torch.bfloat16).float()[rows],
+                               rtol=1e-2, atol=1e-2)
