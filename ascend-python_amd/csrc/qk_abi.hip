@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include <unistd.h>
@@ -242,12 +243,16 @@ int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weig
     return QK_OK;
 }
 
-int qk_weight_quant_bmm(const void* x, int x_dtype, const void* weight, int weight_dtype, const void* antiquant_scale,
-                        const void* antiquant_offset, int scale_dtype, int64_t M, int64_t N, int64_t K,
-                        int64_t group_size, const void* bias, int bias_dtype, void* out, int out_dtype,
-                        void* workspace, size_t workspace_bytes, qk_stream_t stream) {
-    g_last_error.clear();
-    const char* op = "npu_weight_quant_batchmatmul";
+}  // extern "C"
+
+namespace {
+
+// Checks shared by the two weight-quant entry points; `ws` of `ws_bytes` is the scratch the call may use.
+int weight_quant_bmm_run(const char* op, const void* x, int x_dtype, const void* weight, int weight_dtype,
+                         const void* antiquant_scale, const void* antiquant_offset, int scale_dtype, int64_t M,
+                         int64_t N, int64_t K, int64_t group_size, const void* bias, int bias_dtype, void* out,
+                         int out_dtype, void* (*scratch)(size_t need, size_t* bytes, int* rc), void* workspace,
+                         size_t workspace_bytes, qk_stream_t stream) {
     if (!is_half(x_dtype)) return fail(QK_ERR_ARG, "%s: x must be float16 or bfloat16", op);
     if (weight_dtype != QK_I32 && weight_dtype != QK_I8)
         return fail(QK_ERR_ARG, "%s: weight must be int32 (packed int4) or int8", op);
@@ -261,6 +266,11 @@ int qk_weight_quant_bmm(const void* x, int x_dtype, const void* weight, int weig
     if (M == 0 || N == 0) return QK_OK;
     if (!out || (K > 0 && (!x || !weight || !antiquant_scale))) return fail(QK_ERR_ARG, "%s: null pointer", op);
     const size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size);
+    if (scratch && need > 0) {
+        int rc = QK_OK;
+        workspace = scratch(need, &workspace_bytes, &rc);
+        if (rc != QK_OK) return rc;
+    }
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(QK_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, workspace_bytes);
     if (need > 0 && (uintptr_t)workspace % 256 != 0)
@@ -282,6 +292,73 @@ int qk_weight_quant_bmm(const void* x, int x_dtype, const void* weight, int weig
     p.out = out;
     p.out_dtype = out_dtype;
     return launched(qk::launch_weight_quant_bmm(p, workspace, workspace_bytes, (hipStream_t)stream), op);
+}
+
+// Scratch of qk_weight_quant_bmm_noalloc: one array per GPU, held by the
+// library until the process ends.  Its host-side name is only a handle: the
+// device address of the current GPU's copy comes from hipGetSymbolAddress,
+// looked up once per device (on that device's first call) and cached.  The
+// kernels need no particular contents in it (split-K counters are tagged per
+// call; partial and group sums are written before they are read), so nothing
+// is cleared.
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) static unsigned char scratch[QK_NOALLOC_SCRATCH_BYTES];
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+void* noalloc_scratch(size_t need, size_t* bytes, int* rc) {
+    const char* op = "npu_weight_quant_batchmatmul (no allocation)";
+    if (need > QK_NOALLOC_SCRATCH_BYTES) {
+        *rc = fail(QK_ERR_UNSUPPORTED, "%s: this shape needs %zu bytes of scratch, more than the %d the library holds",
+                   op, need, QK_NOALLOC_SCRATCH_BYTES);
+        return nullptr;
+    }
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        *rc = fail(QK_ERR_LAUNCH, "%s: no usable current device (%s)", op, hipGetErrorString(e));
+        return nullptr;
+    }
+    void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!ptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!ptr) {
+            e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !ptr) {
+                *rc = fail(QK_ERR_LAUNCH, "%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", op,
+                           dev, hipGetErrorString(e));
+                return nullptr;
+            }
+            g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+        }
+    }
+    *bytes = QK_NOALLOC_SCRATCH_BYTES;
+    return ptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qk_weight_quant_bmm(const void* x, int x_dtype, const void* weight, int weight_dtype, const void* antiquant_scale,
+                        const void* antiquant_offset, int scale_dtype, int64_t M, int64_t N, int64_t K,
+                        int64_t group_size, const void* bias, int bias_dtype, void* out, int out_dtype,
+                        void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+    g_last_error.clear();
+    return weight_quant_bmm_run("npu_weight_quant_batchmatmul", x, x_dtype, weight, weight_dtype, antiquant_scale,
+                                antiquant_offset, scale_dtype, M, N, K, group_size, bias, bias_dtype, out, out_dtype,
+                                nullptr, workspace, workspace_bytes, stream);
+}
+
+int qk_weight_quant_bmm_noalloc(const void* x, int x_dtype, const void* weight, int weight_dtype,
+                                const void* antiquant_scale, const void* antiquant_offset, int scale_dtype, int64_t M,
+                                int64_t N, int64_t K, int64_t group_size, const void* bias, int bias_dtype, void* out,
+                                int out_dtype, qk_stream_t stream) {
+    g_last_error.clear();
+    return weight_quant_bmm_run("npu_weight_quant_batchmatmul (no allocation)", x, x_dtype, weight, weight_dtype,
+                                antiquant_scale, antiquant_offset, scale_dtype, M, N, K, group_size, bias, bias_dtype,
+                                out, out_dtype, noalloc_scratch, nullptr, 0, stream);
 }
 
 int qk_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed, qk_stream_t stream) {

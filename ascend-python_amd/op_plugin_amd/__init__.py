@@ -57,7 +57,8 @@ QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, 
 
 ABI_SYMBOLS = (
     "qk_last_error", "qk_abi_version", "qk_debug_set_plan", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",
-    "qk_quant_matmul", "qk_weight_quant_bmm_workspace_size", "qk_weight_quant_bmm", "qk_int4_pack",
+    "qk_quant_matmul", "qk_weight_quant_bmm_workspace_size", "qk_weight_quant_bmm", "qk_weight_quant_bmm_noalloc",
+    "qk_int4_pack",
     "qk_rms_norm", "qk_rms_norm_quant", "qk_swiglu", "qk_swiglu_quant",
 )
 
@@ -79,6 +80,7 @@ def abi() -> ctypes.CDLL:
         L.qk_quant_matmul.argtypes = [P, I64, P, I64, I64, I64, I64, I64, P, I64, P, I64, P, P, I, P, I, P, SZ, P]
         L.qk_weight_quant_bmm_workspace_size.argtypes = [I64, I64, I64, I, I64, ctypes.POINTER(SZ)]
         L.qk_weight_quant_bmm.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P, SZ, P]
+        L.qk_weight_quant_bmm_noalloc.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P]
         L.qk_int4_pack.argtypes = [P, I, I64, I64, P, P]
         F = ctypes.c_float
         L.qk_rms_norm.argtypes = [P, I, P, I64, I64, F, P, P, P]

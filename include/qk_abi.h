@@ -162,6 +162,31 @@ int qk_weight_quant_bmm(const void* x, int x_dtype,
                         void* out, int out_dtype,
                         void* workspace, size_t workspace_bytes, qk_stream_t stream);
 
+/* Bytes of the library-held scratch that qk_weight_quant_bmm_noalloc uses on each GPU. */
+#define QK_NOALLOC_SCRATCH_BYTES (16 << 20)
+
+/*
+ * npu_weight_quant_batchmatmul without a workspace argument.  No counterpart
+ * in the reference (whose calls always take caller-allocated scratch): this
+ * entry point is for callers that cannot allocate device memory -- code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * Arguments and results are those of qk_weight_quant_bmm; the scratch the
+ * call needs (split-K partials, group sums) lives in a library-owned device
+ * array of QK_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, and
+ * the call allocates nothing.  A shape whose workspace
+ * (qk_weight_quant_bmm_workspace_size) exceeds that size is refused with
+ * QK_ERR_UNSUPPORTED.  The call uses the array of the current device, so
+ * `stream` must belong to it.  All calls on one GPU share that array: calls
+ * that may run at the same time on one GPU (several streams or threads) race
+ * on it and give wrong results, so serialise them (e.g. one stream).
+ */
+int qk_weight_quant_bmm_noalloc(const void* x, int x_dtype,
+                                const void* weight, int weight_dtype,
+                                const void* antiquant_scale, const void* antiquant_offset, int scale_dtype,
+                                int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                const void* bias, int bias_dtype,
+                                void* out, int out_dtype, qk_stream_t stream);
+
 /*
  * npu_convert_weight_to_int4pack -- packs int4 values held one per element
  * (int8 or int32 [K,N], values in [-8,7]) into int32 [K, N/8] in the layout
