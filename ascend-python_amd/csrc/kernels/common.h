@@ -16,6 +16,38 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// ---------------------------------------------------------------- 16-bit MFMA
+// v_mfma_f32_16x16x32 in the activations' 16-bit type, with the magic-exponent
+// constants of the int4 unpack: a nibble u in the low mantissa bits of MAGIC
+// reads as 128 + u (bf16) / 1024 + u (fp16) exactly, so a two's-complement
+// nibble w flipped to u = w + 8 is the operand w + BASE.
+template <int DT>
+struct Mfma;
+
+template <>
+struct Mfma<QK_BF16> {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    static constexpr uint32_t MAGIC = 0x43004300u;  // bf16 pair (128, 128)
+    static constexpr uint32_t ONES = 0x3f803f80u;   // bf16 pair (1, 1)
+    static constexpr float BASE = 136.0f;
+    static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0,
+                                                       0, 0);
+    }
+};
+
+template <>
+struct Mfma<QK_F16> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    static constexpr uint32_t MAGIC = 0x64006400u;  // fp16 pair (1024, 1024)
+    static constexpr uint32_t ONES = 0x3c003c00u;   // fp16 pair (1, 1)
+    static constexpr float BASE = 1032.0f;
+    static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0,
+                                                      0, 0);
+    }
+};
+
 // ---------------------------------------------------------------- conversions
 // fp16 -> fp32 is exact; bf16 -> fp32 is a shift.
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
@@ -251,6 +283,8 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   w4_splits=<n>                                   K splits of the 32-row-block decode kernel
 //   qmm_dma=0                                       W8A8 prefill: register-staged kernel instead of the DMA one
 //   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
+//   w4nz=off                                        NZ int4 weights: unpack to ND and take the row-major kernels
+//   w4nz_wg=<n>                                     NZ decode kernel: workgroups along N
 struct PlanOverride {
     int w4_stream_nwave = 0, w4_stream_nkb = 0, w4_stream_pf = 0;  // 0: the planner's choice
     bool w4_stream_off = false;
@@ -258,6 +292,8 @@ struct PlanOverride {
     int w4_splits = 0;
     bool qmm_dma = true;
     int skinny_splits = 0;
+    bool w4nz_off = false;
+    int w4nz_wg = 0;
 };
 const PlanOverride& plan_override();
 bool set_plan_override(const char* spec);  // false: spec not understood (override unchanged)
@@ -282,7 +318,7 @@ struct WqbmmArgs {
     const void* x;
     int x_dtype;
     const void* w;
-    int w_dtype;          // QK_I32 (int4 packed) or QK_I8
+    int w_dtype;          // QK_I32 (int4 packed), QK_I8 or QK_I4_NZ
     const void* scale;
     const void* offset;
     int s_dtype;
@@ -294,6 +330,11 @@ struct WqbmmArgs {
 };
 hipError_t launch_weight_quant_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group);
+
+// NZ int4 weights (w4a16_nz.hip): the ND <-> NZ casts and the matmul on NZ weights.
+hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t N, int32_t* dst, hipStream_t stream);
+size_t w4_nz_workspace(const WqbmmArgs& args);
+hipError_t launch_w4_nz_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 
 hipError_t launch_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed,
                             hipStream_t stream);

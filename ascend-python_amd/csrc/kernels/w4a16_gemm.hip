@@ -40,33 +40,6 @@ constexpr int kThreads = 256;
 constexpr int CHUNK = 128;  // K rows per streamed chunk (4 MFMA K-blocks)
 constexpr int STRIP = 32;   // packed words per workgroup
 
-template <int DT>
-struct Mfma;
-
-template <>
-struct Mfma<QK_BF16> {
-    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
-    static constexpr uint32_t MAGIC = 0x43004300u;  // bf16 pair (128, 128)
-    static constexpr uint32_t ONES = 0x3f803f80u;   // bf16 pair (1, 1)
-    static constexpr float BASE = 136.0f;
-    static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0,
-                                                       0, 0);
-    }
-};
-
-template <>
-struct Mfma<QK_F16> {
-    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
-    static constexpr uint32_t MAGIC = 0x64006400u;  // fp16 pair (1024, 1024)
-    static constexpr uint32_t ONES = 0x3c003c00u;   // fp16 pair (1, 1)
-    static constexpr float BASE = 1032.0f;
-    static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0,
-                                                      0, 0);
-    }
-};
-
 // B operand of MFMA tile j: nibble j of 8 offset-binary words (rows 0..7),
 // packed as 16-bit magic values, two rows per dword.
 template <uint32_t MAGIC, int J>
@@ -1633,6 +1606,7 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     p.x = p.scale = p.offset = p.out = (void*)(uintptr_t)256;
     p.w = (void*)(uintptr_t)256;
     if (p.group == 0) p.group = p.K;
+    if (w_dtype == QK_I4_NZ) return w4_nz_workspace(p);
     // [split-K counters][fp32 partials [nsplit][M][N]]
     const StreamPlan s = stream_plan(p);
     if (s.ok) return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
@@ -1647,6 +1621,7 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
     if (a.M == 0 || a.N == 0) return hipSuccess;
     WqbmmArgs p = a;
     if (p.group == 0) p.group = p.K;  // per channel == one group spanning K
+    if (p.w_dtype == QK_I4_NZ) return launch_w4_nz_bmm(p, workspace, ws_bytes, stream);
     // a split workspace is [counters][partials]: the stream kernel finishes each strip in its last
     // split's workgroup (one counter per strip); the decode kernel uses the reduce kernel
     char* ws = static_cast<char*>(workspace);

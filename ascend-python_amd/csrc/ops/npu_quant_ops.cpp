@@ -204,9 +204,15 @@ at::Tensor npu_quant_matmul_meta(const at::Tensor& x1, const at::Tensor& x2, con
 
 struct WqPlan {
     int64_t M, N, K, group;
-    bool int4;
+    bool int4, nz;
     std::vector<int64_t> out_shape;
 };
+
+// An int4 weight in the NZ layout written by npu_format_cast(w, 29): int32
+// [N/16, K/128, 64, 4] (the shape carries the format; see qk_weight_format_cast).
+bool is_w4_nz(const at::Tensor& w) {
+    return w.scalar_type() == at::kInt && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 4;
+}
 
 WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at::Tensor& antiquant_scale,
                          const std::optional<at::Tensor>& antiquant_offset,
@@ -216,15 +222,18 @@ WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at
     TORCH_CHECK(x.scalar_type() == at::kHalf || x.scalar_type() == at::kBFloat16, op,
                 ": x must be float16 or bfloat16, got ", x.scalar_type());
     TORCH_CHECK(x.dim() >= 2, op, ": x must be at least 2-D, got ", x.dim());
-    TORCH_CHECK(weight.dim() == 2, op, ": weight must be 2-D, got ", weight.dim());
+    const bool nz = is_w4_nz(weight);
+    TORCH_CHECK(weight.dim() == 2 || nz, op, ": weight must be 2-D (ND) or an int4 NZ weight [N/16, K/128, 64, 4], got ",
+                weight.sizes());
     TORCH_CHECK(weight.scalar_type() == at::kInt || weight.scalar_type() == at::kChar, op,
                 ": weight must be int32 (int4 packed 8 per element) or int8, got ", weight.scalar_type());
     TORCH_CHECK(!quant_scale.has_value() && !quant_offset.has_value(), op,
                 ": quant_scale/quant_offset (int8 output) are not supported by this build");
     const bool int4 = weight.scalar_type() == at::kInt;
     const int64_t K = x.size(-1);
-    TORCH_CHECK(weight.size(0) == K, op, ": x last dim (", K, ") must equal weight first dim (", weight.size(0), ")");
-    const int64_t N = int4 ? weight.size(1) * 8 : weight.size(1);
+    const int64_t wk = nz ? weight.size(1) * 128 : weight.size(0);
+    TORCH_CHECK(wk == K, op, ": x last dim (", K, ") must equal the weight's K (", wk, ")");
+    const int64_t N = nz ? weight.size(0) * 16 : (int4 ? weight.size(1) * 8 : weight.size(1));
     TORCH_CHECK(group >= 0, op, ": antiquant_group_size must be >= 0");
     TORCH_CHECK(group == 0 || K % group == 0, op, ": K=", K, " must be a multiple of antiquant_group_size=", group);
     const auto st = antiquant_scale.scalar_type();
@@ -250,7 +259,7 @@ WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at
     std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
     shape.back() = N;
     const int64_t M = leading_rows(x);
-    return {M, N, K, group, int4, shape};
+    return {M, N, K, group, int4, nz, shape};
 }
 
 at::Tensor npu_weight_quant_batchmatmul(const at::Tensor& x_in, const at::Tensor& weight_in,
@@ -270,7 +279,7 @@ at::Tensor npu_weight_quant_batchmatmul(const at::Tensor& x_in, const at::Tensor
     at::Tensor off, b;
     if (antiquant_offset.has_value()) off = antiquant_offset->contiguous();
     if (bias.has_value()) b = bias->contiguous();
-    const int wdt = pl.int4 ? QK_I32 : QK_I8;
+    const int wdt = pl.nz ? QK_I4_NZ : (pl.int4 ? QK_I32 : QK_I8);
     size_t ws_bytes = 0;
     check_rc(qk_weight_quant_bmm_workspace_size(pl.M, pl.N, pl.K, wdt, pl.group, &ws_bytes),
              "npu_weight_quant_batchmatmul");
@@ -306,21 +315,91 @@ std::vector<int64_t> int4pack_shape(const at::Tensor& w) {
     return {w.size(0), w.size(1) / 8};
 }
 
+// inner_k_tiles: 0 packs along N in the ND layout [K, N/8]; 4 writes the NZ
+// layout [N/16, K/128, 64, 4] directly, whose lanes each hold 4 MFMA K-tiles
+// of 32 (what npu_format_cast(npu_convert_weight_to_int4pack(w), 29) gives).
+void int4pack_check_tiles(const at::Tensor& w, int64_t inner_k_tiles) {
+    const char* op = "npu_convert_weight_to_int4pack";
+    TORCH_CHECK(inner_k_tiles == 0 || inner_k_tiles == 4, op,
+                ": inner_k_tiles must be 0 (ND) or 4 (the NZ layout's four 32-row K tiles per lane), got ",
+                inner_k_tiles);
+    if (inner_k_tiles == 4)
+        TORCH_CHECK(w.size(0) % 128 == 0 && w.size(1) % 16 == 0, op,
+                    ": the NZ layout needs K % 128 == 0 and N % 16 == 0, got ", w.sizes());
+}
+
+std::vector<int64_t> nz_shape(int64_t K, int64_t N) { return {N / 16, K / 128, 64, 4}; }
+
 at::Tensor npu_convert_weight_to_int4pack(const at::Tensor& weight, int64_t inner_k_tiles) {
-    (void)inner_k_tiles;
     auto shape = int4pack_shape(weight);
+    int4pack_check_tiles(weight, inner_k_tiles);
     const c10::DeviceGuard guard(weight.device());
     auto w = weight.contiguous();
     auto out = at::empty(shape, w.options().dtype(at::kInt));
     check_rc(qk_int4_pack(w.data_ptr(), qk_dtype_of(w.scalar_type()), w.size(0), w.size(1), out.data_ptr<int32_t>(),
                           current_stream(w)),
              "npu_convert_weight_to_int4pack");
-    return out;
+    if (inner_k_tiles == 0) return out;
+    auto nz = at::empty(nz_shape(w.size(0), w.size(1)), w.options().dtype(at::kInt));
+    check_rc(qk_weight_format_cast(out.data_ptr(), QK_FORMAT_ND, nz.data_ptr(), QK_FORMAT_FRACTAL_NZ, QK_I32,
+                                   w.size(0), w.size(1), current_stream(w)),
+             "npu_convert_weight_to_int4pack");
+    return nz;
 }
 
 at::Tensor npu_convert_weight_to_int4pack_meta(const at::Tensor& weight, int64_t inner_k_tiles) {
-    (void)inner_k_tiles;
-    return at::empty(int4pack_shape(weight), weight.options().dtype(at::kInt));
+    auto shape = int4pack_shape(weight);
+    int4pack_check_tiles(weight, inner_k_tiles);
+    if (inner_k_tiles == 4) shape = nz_shape(weight.size(0), weight.size(1));
+    return at::empty(shape, weight.options().dtype(at::kInt));
+}
+
+// ---------------------------------------------------------------- npu_format_cast
+
+// npu_format_cast(self, acl_format) for matmul weights: ND (2) <-> FRACTAL_NZ (29)
+// of an int4-packed int32 weight, the casts the reference applies to matmul
+// operands (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:303-316,
+// op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:103-107).  A tensor
+// already in the requested format is returned as is.
+std::vector<int64_t> format_cast_shape(const at::Tensor& self, int64_t acl_format, bool* to_nz) {
+    const char* op = "npu_format_cast";
+    TORCH_CHECK(acl_format == QK_FORMAT_ND || acl_format == QK_FORMAT_FRACTAL_NZ, op,
+                ": only ND (2) and FRACTAL_NZ (29) are supported, got ", acl_format);
+    TORCH_CHECK(self.scalar_type() == at::kInt, op,
+                ": only int4-packed int32 weights ([K, N/8] in ND) have an NZ layout, got ", self.scalar_type());
+    const bool nz = is_w4_nz(self);
+    TORCH_CHECK(nz || self.dim() == 2, op, ": expected an ND weight [K, N/8] or an NZ weight [N/16, K/128, 64, 4], got ",
+                self.sizes());
+    *to_nz = !nz && acl_format == QK_FORMAT_FRACTAL_NZ;
+    if (nz == (acl_format == QK_FORMAT_FRACTAL_NZ)) return self.sizes().vec();
+    if (*to_nz) {
+        TORCH_CHECK(self.size(0) % 128 == 0 && (self.size(1) * 8) % 16 == 0, op,
+                    ": FRACTAL_NZ needs K % 128 == 0 and N % 16 == 0, got [K, N/8] = ", self.sizes());
+        return nz_shape(self.size(0), self.size(1) * 8);
+    }
+    return {self.size(1) * 128, self.size(0) * 2};
+}
+
+at::Tensor npu_format_cast(const at::Tensor& self, int64_t acl_format) {
+    bool to_nz = false;
+    auto shape = format_cast_shape(self, acl_format, &to_nz);
+    if (is_w4_nz(self) == (acl_format == QK_FORMAT_FRACTAL_NZ)) return self;
+    const c10::DeviceGuard guard(self.device());
+    auto src = self.contiguous();
+    auto out = at::empty(shape, src.options());
+    const int64_t K = to_nz ? src.size(0) : src.size(1) * 128;
+    const int64_t N = to_nz ? src.size(1) * 8 : src.size(0) * 16;
+    check_rc(qk_weight_format_cast(src.data_ptr(), to_nz ? QK_FORMAT_ND : QK_FORMAT_FRACTAL_NZ, out.data_ptr(),
+                                   to_nz ? QK_FORMAT_FRACTAL_NZ : QK_FORMAT_ND, QK_I32, K, N, current_stream(src)),
+             "npu_format_cast");
+    return out;
+}
+
+at::Tensor npu_format_cast_meta(const at::Tensor& self, int64_t acl_format) {
+    bool to_nz = false;
+    auto shape = format_cast_shape(self, acl_format, &to_nz);
+    if (is_w4_nz(self) == (acl_format == QK_FORMAT_FRACTAL_NZ)) return self;
+    return at::empty(shape, self.options());
 }
 
 // ---------------------------------------------------------------- npu_rms_norm (+ dynamic quant)
@@ -460,6 +539,7 @@ TORCH_LIBRARY(npu, m) {
         "npu_weight_quant_batchmatmul(Tensor x, Tensor weight, Tensor antiquant_scale, Tensor? antiquant_offset=None, "
         "Tensor? quant_scale=None, Tensor? quant_offset=None, Tensor? bias=None, int antiquant_group_size=0) -> Tensor");
     m.def("npu_convert_weight_to_int4pack(Tensor weight, int inner_k_tiles=0) -> Tensor");
+    m.def("npu_format_cast(Tensor self, int acl_format) -> Tensor");
     // schema as op_plugin/config/v2r2/op_plugin_functions.yaml:2047
     m.def("npu_rms_norm(Tensor self, Tensor gamma, float epsilon=1e-06) -> (Tensor, Tensor)");
     m.def("npu_swiglu(Tensor self, int dim=-1) -> Tensor");
@@ -473,6 +553,7 @@ TORCH_LIBRARY_IMPL(npu, CUDA, m) {
     m.impl("npu_quant_matmul", &npu_quant_matmul);
     m.impl("npu_weight_quant_batchmatmul", &npu_weight_quant_batchmatmul);
     m.impl("npu_convert_weight_to_int4pack", &npu_convert_weight_to_int4pack);
+    m.impl("npu_format_cast", &npu_format_cast);
     m.impl("npu_rms_norm", &npu_rms_norm);
     m.impl("npu_swiglu", &npu_swiglu);
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant);
@@ -484,6 +565,7 @@ TORCH_LIBRARY_IMPL(npu, Meta, m) {
     m.impl("npu_quant_matmul", &npu_quant_matmul_meta);
     m.impl("npu_weight_quant_batchmatmul", &npu_weight_quant_batchmatmul_meta);
     m.impl("npu_convert_weight_to_int4pack", &npu_convert_weight_to_int4pack_meta);
+    m.impl("npu_format_cast", &npu_format_cast_meta);
     m.impl("npu_rms_norm", &npu_rms_norm_meta);
     m.impl("npu_swiglu", &npu_swiglu_meta);
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant_meta);

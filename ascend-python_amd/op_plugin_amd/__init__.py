@@ -9,6 +9,9 @@ Importing this package loads ``_npu_ops.so``, which registers
   antiquant_offset=None, quant_scale=None, quant_offset=None, bias=None,
   antiquant_group_size=0) -> Tensor``  (W4A16 / W8A16)
 * ``torch.ops.npu.npu_convert_weight_to_int4pack(weight, inner_k_tiles=0) -> Tensor``
+  (``inner_k_tiles=4``: straight to the NZ layout)
+* ``torch.ops.npu.npu_format_cast(self, acl_format) -> Tensor``: an int4-packed weight between ND (2) and
+  FRACTAL_NZ (29), the MFMA-tiled layout ``npu_weight_quant_batchmatmul`` streams fastest
 * ``torch.ops.npu.npu_rms_norm(self, gamma, epsilon=1e-6) -> (y, fp32 rstd)``
 * ``torch.ops.npu.npu_swiglu(self, dim=-1) -> Tensor``
 * ``torch.ops.npu.npu_rms_norm_dynamic_quant(self, gamma, epsilon=1e-6) -> (int8 q, fp32 scale, fp32 rstd)``
@@ -46,19 +49,21 @@ npu_dynamic_quant = torch.ops.npu.npu_dynamic_quant
 npu_quant_matmul = torch.ops.npu.npu_quant_matmul
 npu_weight_quant_batchmatmul = torch.ops.npu.npu_weight_quant_batchmatmul
 npu_convert_weight_to_int4pack = torch.ops.npu.npu_convert_weight_to_int4pack
+npu_format_cast = torch.ops.npu.npu_format_cast
 npu_rms_norm = torch.ops.npu.npu_rms_norm
 npu_swiglu = torch.ops.npu.npu_swiglu
 npu_rms_norm_dynamic_quant = torch.ops.npu.npu_rms_norm_dynamic_quant
 npu_swiglu_dynamic_quant = torch.ops.npu.npu_swiglu_dynamic_quant
 
 # qk_abi.h constants
-QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32 = 1, 2, 3, 4, 5
+QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_I4_NZ = 1, 2, 3, 4, 5, 16
+ACL_FORMAT_ND, ACL_FORMAT_FRACTAL_NZ = 2, 29
 QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, -2, -3, -4
 
 ABI_SYMBOLS = (
     "qk_last_error", "qk_abi_version", "qk_debug_set_plan", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",
     "qk_quant_matmul", "qk_weight_quant_bmm_workspace_size", "qk_weight_quant_bmm", "qk_weight_quant_bmm_noalloc",
-    "qk_int4_pack",
+    "qk_int4_pack", "qk_weight_format_cast",
     "qk_rms_norm", "qk_rms_norm_quant", "qk_swiglu", "qk_swiglu_quant",
 )
 
@@ -82,6 +87,7 @@ def abi() -> ctypes.CDLL:
         L.qk_weight_quant_bmm.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P, SZ, P]
         L.qk_weight_quant_bmm_noalloc.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P]
         L.qk_int4_pack.argtypes = [P, I, I64, I64, P, P]
+        L.qk_weight_format_cast.argtypes = [P, I, P, I, I, I64, I64, P]
         F = ctypes.c_float
         L.qk_rms_norm.argtypes = [P, I, P, I64, I64, F, P, P, P]
         L.qk_rms_norm_quant.argtypes = [P, I, P, I64, I64, F, P, P, P, P]
@@ -91,6 +97,13 @@ def abi() -> ctypes.CDLL:
             getattr(L, name).restype = I if name != "qk_last_error" else ctypes.c_char_p
         _abi = L
     return _abi
+
+
+def get_npu_format(t: torch.Tensor) -> int:
+    """Storage format of a matmul weight, as torch_npu.get_npu_format reports it:
+    FRACTAL_NZ (29) for an int4 NZ weight [N/16, K/128, 64, 4], ND (2) otherwise."""
+    nz = t.dtype == torch.int32 and t.dim() == 4 and t.shape[2] == 64 and t.shape[3] == 4
+    return ACL_FORMAT_FRACTAL_NZ if nz else ACL_FORMAT_ND
 
 
 def last_error() -> str:
@@ -109,6 +122,6 @@ def debug_set_plan(spec: str = "") -> None:
 
 __all__ = [
     "npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
-    "npu_convert_weight_to_int4pack", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
+    "npu_convert_weight_to_int4pack", "npu_format_cast", "get_npu_format", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
     "npu_swiglu_dynamic_quant", "abi", "last_error", "debug_set_plan", "LIB_PATH", "OPS_PATH",
 ]

@@ -57,8 +57,16 @@ typedef enum {
     QK_BF16 = 2,
     QK_F32 = 3,
     QK_I8 = 4,
-    QK_I32 = 5
+    QK_I32 = 5,
+    /* weight code of qk_weight_quant_bmm: an int4 weight in the MFMA-tiled
+     * NZ layout that qk_weight_format_cast writes (int32 [N/16][K/128][64][4]) */
+    QK_I4_NZ = 16
 } qk_dtype;
+
+/* Weight storage formats: the reference's aclFormat numbers for ND and
+ * FRACTAL_NZ (op_plugin/third_party/acl/inc/graph/types.h:111, 138). */
+#define QK_FORMAT_ND 2
+#define QK_FORMAT_FRACTAL_NZ 29
 
 /* Return codes. */
 enum {
@@ -74,7 +82,8 @@ const char* qk_last_error(void);
 
 /* ABI revision; bumped on any incompatible signature or contract change
  * (2: the split-K counters at the head of a workspace; 3: the counters are
- * tagged per call, so a workspace needs no initialisation). */
+ * tagged per call, so a workspace needs no initialisation; 4: NZ weights,
+ * qk_weight_format_cast). */
 int qk_abi_version(void);
 
 /* Debug and test hook, no counterpart in the reference: forces kernel choices
@@ -147,7 +156,9 @@ int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weig
  * aclnnWeightQuantBatchMatmul* behind EXEC_NPU_CMD; the nearest reference op
  * is bmm (op_plugin/ops/base_ops/opapi/BmmKernelNpuOpApi.cpp:24-52).
  * x: [M,K] fp16/bf16 row-major.  weight: QK_I32 -> int4 packed [K, N/8]
- * (nibble i of word j is column 8j+i, two's complement); QK_I8 -> int8 [K,N].
+ * (nibble i of word j is column 8j+i, two's complement); QK_I8 -> int8 [K,N];
+ * QK_I4_NZ -> int4 in the NZ layout of qk_weight_format_cast (N % 16 == 0,
+ * K % 128 == 0).
  * antiquant_scale / antiquant_offset: [K/group, N] (group_size > 0) or [N]
  * (group_size == 0, per channel), of scale_dtype (fp16/bf16); offset may be NULL.
  * bias: [N] or NULL.  out: [M,N] of out_dtype (fp16/bf16).
@@ -186,6 +197,24 @@ int qk_weight_quant_bmm_noalloc(const void* x, int x_dtype,
                                 int64_t M, int64_t N, int64_t K, int64_t group_size,
                                 const void* bias, int bias_dtype,
                                 void* out, int out_dtype, qk_stream_t stream);
+
+/*
+ * npu_format_cast for an int4 matmul weight -- the MI355X counterpart of the
+ * FRACTAL_NZ casts the reference applies to matmul operands
+ * (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:303-316,
+ * op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:103-107), done once when
+ * weights are loaded.  weight_dtype must be QK_I32 (int4 packed, [K, N/8] in
+ * ND).  src_format -> dst_format is QK_FORMAT_ND -> QK_FORMAT_FRACTAL_NZ or
+ * back; N % 16 == 0 and K % 128 == 0; src and dst must not overlap.
+ * NZ layout, int32 [N/16][K/128][64][4]: element (k, n) is in word
+ *   ((n/16 * (K/128) + k/128) * 64 + lane) * 4 + j,
+ *   c = (k%128)/8, lane = n%16 + 16*(c%4), j = c/4,
+ * at nibble i/2 for even i = k%8 and 4 + i/2 for odd i (two's complement).
+ * One 1 KB block (16 columns x 128 k) is read by a wave as one 16-byte load
+ * per lane, each word being one MFMA operand.  No workspace.
+ */
+int qk_weight_format_cast(const void* src, int src_format, void* dst, int dst_format, int weight_dtype,
+                          int64_t K, int64_t N, qk_stream_t stream);
 
 /*
  * npu_convert_weight_to_int4pack -- packs int4 values held one per element

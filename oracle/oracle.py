@@ -44,6 +44,8 @@ def lib() -> ctypes.CDLL:
         L.qo_quant_matmul_epilogue.argtypes = [P, I64, I64, P, I64, P, I64, P, P, I, P, I]
         L.qo_int4_pack.argtypes = [P, I64, I64, P]
         L.qo_int4_unpack.argtypes = [P, I64, I64, P]
+        L.qo_w4_nz_pack.argtypes = [P, I64, I64, P]
+        L.qo_w4_nz_unpack.argtypes = [P, I64, I64, P]
         L.qo_weight_quant_bmm.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P]
         L.qo_rms_norm.argtypes = [P, I, P, I64, I64, ctypes.c_double, P, P]
         L.qo_swiglu.argtypes = [P, I, I64, I64, P]
@@ -148,6 +150,25 @@ def int4_unpack(packed: np.ndarray) -> np.ndarray:
     K, NW = packed.shape
     out = np.empty((K, NW * 8), dtype=np.int8)
     lib().qo_int4_unpack(_p(packed), K, NW * 8, _p(out))
+    return out
+
+
+def w4_nz_pack(packed: np.ndarray) -> np.ndarray:
+    """int32 [K, N/8] (ND int4) -> int32 [N/16, K/128, 64, 4] (MFMA-tiled NZ layout)."""
+    nd = _c(packed, np.int32)
+    K, NW = nd.shape
+    N = NW * 8
+    out = np.empty((N // 16, K // 128, 64, 4), dtype=np.int32)
+    lib().qo_w4_nz_pack(_p(nd), K, N, _p(out))
+    return out
+
+
+def w4_nz_unpack(nz: np.ndarray) -> np.ndarray:
+    """int32 [N/16, K/128, 64, 4] -> int32 [K, N/8] (ND int4)."""
+    t = _c(nz, np.int32)
+    N, K = t.shape[0] * 16, t.shape[1] * 128
+    out = np.empty((K, N // 8), dtype=np.int32)
+    lib().qo_w4_nz_unpack(_p(t), K, N, _p(out))
     return out
 
 

@@ -35,6 +35,10 @@
  *       before the output cast; bf16 cast pinned as above.
  *   qo_int4_pack / unpack: hand-computed packed words, round trip over all
  *       16 nibble values at every position.
+ *   qo_w4_nz_pack / unpack: round trip on random weights (a bijection of
+ *       words), hand-computed word/nibble positions of single nonzero
+ *       elements, and the MFMA operand property the kernels rely on (the 8
+ *       nibbles of one word are 8 consecutive k of one column, even k low).
  *   qo_weight_quant_bmm: scale=1/offset=0 reduces to torch.matmul in float64;
  *       a hand-computed 1x2x128 example; linearity in x.
  *   qo_rms_norm: the reference's numpy closed form, restated in float64.
@@ -266,6 +270,53 @@ void qo_int4_unpack(const int32_t* packed, int64_t K, int64_t N, int8_t* w) {
                 int v = (int)((word >> (4 * i)) & 0xfu);
                 w[k * N + 8 * j + i] = (int8_t)(v >= 8 ? v - 16 : v);
             }
+        }
+}
+
+/* ------------------------------------------------------------------ */
+/* MFMA-tiled ("NZ") int4 weight layout                                */
+/* ------------------------------------------------------------------ */
+/*
+ * npu_format_cast(weight, FRACTAL_NZ) for an int4 weight: this build's
+ * device-native counterpart of the FRACTAL_NZ weight casts the reference
+ * applies before matmuls (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:303-316,
+ * op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:103-107; format number 29,
+ * op_plugin/third_party/acl/inc/graph/types.h:138).  The tiled tensor is
+ * int32 [N/16][K/128][64][4].  Weight element (k, n) lives in word
+ *   ((n/16 * (K/128) + k/128) * 64 + lane) * 4 + j,
+ *   c = (k%128) / 8, lane = n%16 + 16*(c%4), j = c/4,
+ * at nibble p = i/2 for even i = k%8 and p = 4 + i/2 for odd i (two's
+ * complement, bits 4p..4p+3).  Both directions are plain gathers over (k, n).
+ */
+static inline int64_t nz4_word(int64_t k, int64_t n, int64_t K, int *nibble) {
+    int64_t c = (k % 128) / 8, i = k % 8;
+    int64_t lane = n % 16 + 16 * (c % 4), j = c / 4;
+    *nibble = (int)((i % 2 == 0) ? i / 2 : 4 + i / 2);
+    return (((n / 16) * (K / 128) + k / 128) * 64 + lane) * 4 + j;
+}
+
+/* nd: int32 [K, N/8] as qo_int4_pack writes it; nz: int32 [N/16][K/128][64][4]. */
+void qo_w4_nz_pack(const int32_t* nd, int64_t K, int64_t N, int32_t* nz) {
+    int64_t NW = N / 8;
+    memset(nz, 0, (size_t)(K * N / 8) * sizeof(int32_t));
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) {
+            uint32_t v = ((uint32_t)nd[k * NW + n / 8] >> (4 * (n % 8))) & 0xfu;
+            int p;
+            int64_t w = nz4_word(k, n, K, &p);
+            nz[w] = (int32_t)((uint32_t)nz[w] | (v << (4 * p)));
+        }
+}
+
+void qo_w4_nz_unpack(const int32_t* nz, int64_t K, int64_t N, int32_t* nd) {
+    int64_t NW = N / 8;
+    memset(nd, 0, (size_t)(K * NW) * sizeof(int32_t));
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) {
+            int p;
+            int64_t w = nz4_word(k, n, K, &p);
+            uint32_t v = ((uint32_t)nz[w] >> (4 * p)) & 0xfu;
+            nd[k * NW + n / 8] = (int32_t)((uint32_t)nd[k * NW + n / 8] | (v << (4 * (n % 8))));
         }
 }
 

@@ -1,0 +1,182 @@
+"""GPU parity of the NZ (MFMA-tiled) int4 weight path against the CPU oracle.
+
+* npu_format_cast / npu_convert_weight_to_int4pack(inner_k_tiles=4) on the
+  device: bit-exact against the oracle's NZ restatement, both directions.
+* npu_weight_quant_batchmatmul on NZ weights: within rtol 1e-2 / atol 1e-2
+  of the float64 oracle on the same seeded inputs (the bar of the row-major
+  path), through the NZ decode kernel and through the unpack-to-ND fallback
+  (short groups, K with no even wave split, M > 64, forced off).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from op_plugin_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16 = 1, 2
+CODE = {torch.float16: F16, torch.bfloat16: BF16}
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import op_plugin_amd
+    return op_plugin_amd
+
+
+@pytest.fixture
+def plan(ops):
+    yield ops.debug_set_plan
+    ops.debug_set_plan("")
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _ref(oracle, d, group, bias=None, x_dtype=torch.bfloat16):
+    return oracle.weight_quant_bmm(W.bits(d["x"]), CODE[x_dtype], d["w_packed"].numpy(), W.bits(d["scale"]),
+                                   None if d["offset"] is None else W.bits(d["offset"]), F16, group,
+                                   bias=None if bias is None else W.bits(bias), bias_dtype=CODE[x_dtype],
+                                   out_dtype=CODE[x_dtype])
+
+
+def _close(out, ref_bits, dtype):
+    torch.testing.assert_close(out.cpu().float(), W.from_bits(ref_bits, dtype).float(), rtol=1e-2, atol=1e-2)
+
+
+def _inputs(M, N, K, group, offset, x_dtype, seed):
+    d = W.w4a16_inputs(W.W4A16Case(M=M, N=N, K=K, group=group, x_dtype=x_dtype, offset=offset), seed=seed)
+    if group == 0:
+        d = dict(d, scale=d["scale"].reshape(-1), offset=None if d["offset"] is None else d["offset"].reshape(-1))
+    return d
+
+
+def _run(ops, d, group, nz, bias=None):
+    return ops.npu_weight_quant_batchmatmul(
+        d["x"].to(DEV), nz, d["scale"].to(DEV), None if d["offset"] is None else d["offset"].to(DEV),
+        bias=None if bias is None else bias.to(DEV), antiquant_group_size=group)
+
+
+def test_format_cast_device_matches_oracle(ops, oracle):
+    say("npu_format_cast ND <-> NZ, K=384 N=80")
+    g = torch.Generator().manual_seed(11)
+    w = torch.randint(-8, 8, (384, 80), generator=g, dtype=torch.int8)
+    nd = oracle.int4_pack(w.numpy())
+    ref = oracle.w4_nz_pack(nd)
+    got = ops.npu_format_cast(torch.from_numpy(nd).to(DEV), 29)
+    assert ops.get_npu_format(got) == 29
+    assert np.array_equal(got.cpu().numpy(), ref)
+    back = ops.npu_format_cast(got, 2)
+    assert np.array_equal(back.cpu().numpy(), nd)
+    direct = ops.npu_convert_weight_to_int4pack(w.to(torch.int32).to(DEV), inner_k_tiles=4)
+    assert np.array_equal(direct.cpu().numpy(), ref)
+
+
+def test_format_cast_cfg3_round_trip(ops, oracle):
+    say("npu_format_cast cfg3 weight [4096, 1376] round trip")
+    d = W.w4a16_inputs(W.CFG3[0])
+    nd = d["w_packed"].to(DEV)
+    nz = ops.npu_format_cast(nd, 29)
+    assert nz.shape == (688, 32, 64, 4)
+    assert torch.equal(ops.npu_format_cast(nz, 2), nd)
+    # spot blocks against the oracle on a column slice (the oracle restates any slice of 16-column blocks)
+    ref = oracle.w4_nz_pack(d["w_packed"][:, :64].numpy())
+    assert np.array_equal(nz[:32].cpu().numpy(), ref)
+
+
+def test_w4a16_nz_cfg3_decode(ops, oracle):
+    c = W.CFG3[0]
+    say(f"w4a16 NZ cfg3 M={c.M} 4096x11008 (whole output)")
+    d = W.w4a16_inputs(c)
+    nz = ops.npu_format_cast(d["w_packed"].to(DEV), 29)
+    out = _run(ops, d, 128, nz)
+    _close(out, _ref(oracle, d, 128), torch.bfloat16)
+    nd_out = _run(ops, d, 128, d["w_packed"].to(DEV))
+    torch.testing.assert_close(out.float(), nd_out.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,bias", [
+    (1, 11008, 4096, 128, True, torch.bfloat16, False),
+    (4, 11008, 4096, 128, True, torch.bfloat16, True),
+    (16, 256, 512, 128, False, torch.bfloat16, False),      # 4 waves, one superblock each
+    (7, 1008, 1024, 256, True, torch.float16, True),        # fp16, 256-row groups
+    (16, 4096, 4096, 0, True, torch.bfloat16, True),        # per channel
+    (33, 512, 2048, 128, True, torch.bfloat16, False),      # three 16-row blocks, clamped rows
+    (64, 144, 8192, 128, True, torch.bfloat16, True),       # four superblocks per wave (two in flight)
+    (2, 48, 14336, 128, True, torch.bfloat16, False),       # seven superblocks per wave
+    (3, 16, 128, 128, True, torch.float16, False),          # one wave, one block
+    (5, 4112, 640, 128, False, torch.bfloat16, True),       # 257 blocks: some workgroups own one fewer
+    # fallbacks: the weight is unpacked to ND in the workspace and the row-major kernels run
+    (16, 256, 2176, 128, True, torch.bfloat16, False),      # 17 superblocks: no even wave split
+    (8, 512, 1024, 64, True, torch.bfloat16, True),         # 64-row groups
+    (100, 256, 1024, 128, True, torch.float16, False),      # M > 64
+])
+def test_w4a16_nz_shapes(ops, oracle, M, N, K, group, offset, x_dtype, bias):
+    say(f"w4a16 NZ M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    d = _inputs(M, N, K, group, offset, x_dtype, seed=M + N + K)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(5)).to(x_dtype) if bias else None
+    nz = ops.npu_format_cast(d["w_packed"].to(DEV), 29)
+    out = _run(ops, d, group, nz, bias=b)
+    _close(out, _ref(oracle, d, group, bias=b, x_dtype=x_dtype), x_dtype)
+
+
+@pytest.mark.parametrize("spec", ["w4nz_wg=344", "w4nz_wg=688", "w4nz_wg=100", "w4nz=off"])
+def test_w4a16_nz_plans(ops, oracle, plan, spec):
+    """The cfg3 M=16 shape with other workgroup counts (344 and 688 give 2 and 1 blocks per workgroup; 100
+    asks for 7, capped at the 4 a wave of two superblocks holds, so 172 workgroups) and with the NZ kernel
+    switched off (unpack + row-major stream)."""
+    c = W.CFG3[0]
+    say(f"w4a16 NZ cfg3 M=16 plan {spec}")
+    plan(spec)
+    d = W.w4a16_inputs(c, seed=4)
+    nz = ops.npu_format_cast(d["w_packed"].to(DEV), 29)
+    out = _run(ops, d, 128, nz)
+    _close(out, _ref(oracle, d, 128), torch.bfloat16)
+
+
+def test_w4a16_nz_prefill_fallback(ops, oracle):
+    """M = 512 on NZ weights: unpacked to ND, then the DMA prefill kernel (forced onto this small shape)."""
+    say("w4a16 NZ prefill M=512 N=1024 K=1024")
+    ops.debug_set_plan("w4_gemm=force")
+    try:
+        d = _inputs(512, 1024, 1024, 128, True, torch.bfloat16, seed=21)
+        nz = ops.npu_format_cast(d["w_packed"].to(DEV), 29)
+        out = _run(ops, d, 128, nz)
+    finally:
+        ops.debug_set_plan("")
+    _close(out, _ref(oracle, d, 128), torch.bfloat16)
+
+
+def test_abi_nz_and_noalloc(ops, oracle):
+    """qk_weight_quant_bmm with QK_I4_NZ through the C ABI (no workspace needed), and the no-allocation entry
+    point on the same NZ weight, against the oracle."""
+    say("ABI qk_weight_quant_bmm QK_I4_NZ M=16 N=2048 K=4096")
+    L = ops.abi()
+    d = _inputs(16, 2048, 4096, 128, True, torch.bfloat16, seed=9)
+    nz = ops.npu_format_cast(d["w_packed"].to(DEV), 29)
+    x, sc, off = d["x"].to(DEV), d["scale"].to(DEV), d["offset"].to(DEV)
+    ws = ctypes.c_size_t(1)
+    assert L.qk_weight_quant_bmm_workspace_size(16, 2048, 4096, ops.QK_I4_NZ, 128, ctypes.byref(ws)) == 0
+    assert ws.value == 0
+    ref = _ref(oracle, d, 128)
+    s = torch.cuda.current_stream().cuda_stream
+    for entry in ("ws", "noalloc"):
+        out = torch.empty(16, 2048, dtype=torch.bfloat16, device=DEV)
+        if entry == "ws":
+            rc = L.qk_weight_quant_bmm(x.data_ptr(), BF16, nz.data_ptr(), ops.QK_I4_NZ, sc.data_ptr(),
+                                       off.data_ptr(), F16, 16, 2048, 4096, 128, None, 0, out.data_ptr(), BF16,
+                                       None, 0, s)
+        else:
+            rc = L.qk_weight_quant_bmm_noalloc(x.data_ptr(), BF16, nz.data_ptr(), ops.QK_I4_NZ, sc.data_ptr(),
+                                               off.data_ptr(), F16, 16, 2048, 4096, 128, None, 0, out.data_ptr(),
+                                               BF16, s)
+        assert rc == 0, ops.last_error()
+        torch.cuda.synchronize()
+        _close(out, ref, torch.bfloat16)

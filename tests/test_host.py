@@ -28,16 +28,17 @@ def test_abi_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), f"{n} declared in qk_abi.h but not exported"
     assert set(names) == set(q.ABI_SYMBOLS)
-    assert q.abi().qk_abi_version() == 3
+    assert q.abi().qk_abi_version() == 4
 
 
 def test_debug_plan_override_parsing():
     """The planners' one debug override: accepted specs, and refusal (with the override unchanged) of
     specs it does not understand.  Nothing is launched."""
     for spec in ("", "w4_stream=16:4:4", "w4_stream=off", "w4_gemm=force,skinny_splits=4", "qmm_dma=0",
-                 "w4_splits=8,w4_gemm=nodma"):
+                 "w4_splits=8,w4_gemm=nodma", "w4nz=off", "w4nz_wg=172"):
         q.debug_set_plan(spec)
-    for bad in ("w4_stream=12:4:2", "w4_gemm=maybe", "skinny_splits=3", "nonsense", "qmm_dma=2"):
+    for bad in ("w4_stream=12:4:2", "w4_gemm=maybe", "skinny_splits=3", "nonsense", "qmm_dma=2", "w4nz=on",
+                "w4nz_wg=0"):
         with pytest.raises(ValueError, match="not understood"):
             q.debug_set_plan(bad)
     q.debug_set_plan("")
@@ -71,6 +72,21 @@ def test_abi_refuses_bad_arguments_without_launch():
     ws = ctypes.c_size_t(123)
     assert L.qk_weight_quant_bmm_workspace_size(16, 11008, 4096, I32, 128, ctypes.byref(ws)) == 0
     assert L.qk_int4_pack(fake, I8, 4, 12, fake, None) == q.QK_ERR_ARG
+    # NZ weights: shape rules, supported casts, overlap
+    rc = L.qk_weight_quant_bmm(fake, BF16, fake, q.QK_I4_NZ, fake, None, F16, 4, 24, 128, 128, None, 0, fake, BF16,
+                               None, 0, None)
+    assert rc == q.QK_ERR_ARG and "N % 16" in q.last_error()
+    nd, nz = q.ACL_FORMAT_ND, q.ACL_FORMAT_FRACTAL_NZ
+    assert L.qk_weight_format_cast(fake, nd, fake, nz, I8, 128, 16, None) == q.QK_ERR_UNSUPPORTED
+    assert L.qk_weight_format_cast(fake, nd, fake, 3, I32, 128, 16, None) == q.QK_ERR_UNSUPPORTED
+    assert L.qk_weight_format_cast(fake, nd, fake, nz, I32, 100, 16, None) == q.QK_ERR_ARG
+    assert L.qk_weight_format_cast(ctypes.c_void_p(4096), nd, ctypes.c_void_p(4096 + 512), nz, I32, 128, 16,
+                                   None) == q.QK_ERR_ARG and "overlap" in q.last_error()
+    assert L.qk_weight_format_cast(None, nz, None, nd, I32, 0, 16, None) == q.QK_OK
+    assert L.qk_weight_quant_bmm_workspace_size(16, 11008, 4096, q.QK_I4_NZ, 128, ctypes.byref(ws)) == 0
+    assert ws.value == 0   # the NZ decode kernel needs no workspace
+    assert L.qk_weight_quant_bmm_workspace_size(16, 11008, 4096, q.QK_I4_NZ, 64, ctypes.byref(ws)) == 0
+    assert ws.value >= 4096 + 4096 * 11008 // 2   # short groups: the ND weight is rebuilt in the workspace
     assert L.qk_rms_norm(fake, 9, fake, 4, 64, 1e-6, fake, None, None) == q.QK_ERR_ARG
     assert "float16 or bfloat16" in q.last_error()
     assert L.qk_rms_norm(fake, BF16, fake, 4, 0, 1e-6, fake, None, None) == q.QK_ERR_ARG and "D > 0" in q.last_error()
@@ -89,7 +105,7 @@ def _m(shape, dtype):
 
 def test_schemas_registered():
     for name in ("npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
-                 "npu_convert_weight_to_int4pack", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
+                 "npu_convert_weight_to_int4pack", "npu_format_cast", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
                  "npu_swiglu_dynamic_quant"):
         assert hasattr(torch.ops.npu, name)
     s = str(torch.ops.npu.npu_quant_matmul.default._schema)
@@ -110,6 +126,13 @@ def test_meta_shapes():
                                          antiquant_group_size=128)
     assert out.shape == (16, 11008) and out.dtype == torch.bfloat16
     assert q.npu_convert_weight_to_int4pack(_m((64, 96), torch.int32)).shape == (64, 12)
+    assert q.npu_convert_weight_to_int4pack(_m((256, 96), torch.int32), inner_k_tiles=4).shape == (6, 2, 64, 4)
+    nzw = q.npu_format_cast(_m((4096, 1376), torch.int32), 29)
+    assert nzw.shape == (688, 32, 64, 4) and q.get_npu_format(nzw) == 29
+    assert q.npu_format_cast(nzw, 2).shape == (4096, 1376) and q.npu_format_cast(nzw, 29) is nzw
+    out = q.npu_weight_quant_batchmatmul(_m((16, 4096), torch.bfloat16), nzw, _m((32, 11008), torch.float16),
+                                         _m((32, 11008), torch.float16), antiquant_group_size=128)
+    assert out.shape == (16, 11008) and out.dtype == torch.bfloat16
     y, rstd = q.npu_rms_norm(_m((2, 7, 4096), torch.bfloat16), _m((4096,), torch.bfloat16))
     assert y.shape == (2, 7, 4096) and y.dtype == torch.bfloat16 and rstd.shape == (2, 7, 1) \
         and rstd.dtype == torch.float32
@@ -141,6 +164,13 @@ def test_meta_shapes():
                                             _m((1, 16), torch.float16), quant_scale=_m((16,), torch.float32),
                                             antiquant_group_size=128), "not supported"),
     (lambda: q.npu_convert_weight_to_int4pack(_m((4, 12), torch.int32)), "multiple of 8"),
+    (lambda: q.npu_convert_weight_to_int4pack(_m((128, 16), torch.int32), inner_k_tiles=2), "inner_k_tiles"),
+    (lambda: q.npu_convert_weight_to_int4pack(_m((64, 16), torch.int32), inner_k_tiles=4), "K % 128"),
+    (lambda: q.npu_format_cast(_m((100, 2), torch.int32), 29), "K % 128"),
+    (lambda: q.npu_format_cast(_m((128, 2), torch.int32), 3), "only ND"),
+    (lambda: q.npu_format_cast(_m((128, 16), torch.int8), 29), "int4-packed"),
+    (lambda: q.npu_weight_quant_batchmatmul(_m((2, 256), torch.bfloat16), _m((1, 1, 64, 4), torch.int32),
+                                            _m((1, 16), torch.float16), antiquant_group_size=128), "weight's K"),
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((64,), torch.float16)), "dtype of self"),
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((32,), torch.bfloat16)), "trailing dims"),
     (lambda: q.npu_rms_norm_dynamic_quant(_m((4, 8, 8), torch.bfloat16), _m((8, 8), torch.bfloat16)), "1-D gamma"),

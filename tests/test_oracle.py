@@ -184,6 +184,66 @@ def test_int4_round_trip_all_positions(oracle):
     assert np.array_equal(W.int4_pack_cpu(tw).numpy(), oracle.int4_pack(w))
 
 
+def _nz_word_and_nibble_by_hand(k, n, K):
+    """Word index and nibble of element (k, n) in the NZ layout, spelled out step by step."""
+    S = K // 128
+    block, sup = n // 16, k // 128
+    chunk, within = (k % 128) // 8, k % 8
+    lane = n % 16 + 16 * (chunk % 4)
+    word_in_lane = chunk // 4
+    nibble = within // 2 if within % 2 == 0 else 4 + within // 2
+    return ((block * S + sup) * 64 + lane) * 4 + word_in_lane, nibble
+
+
+@pytest.mark.parametrize("k,n,word,nibble", [
+    (0, 0, 0, 0), (1, 0, 0, 4), (2, 0, 0, 1), (7, 0, 0, 7),      # one 8-k chunk: even k low, odd k high
+    (8, 0, 64, 0),                                                # chunk 1 -> lane 16
+    (32, 0, 1, 0),                                                # chunk 4 -> word 1 of lane 0
+    (2, 3, 12, 1),                                                # column 3 -> lane 3
+    (127, 15, 255, 7),                                            # last element of the first 1 KB block
+    (128, 0, 256, 0),                                             # next 128 k: next block of the same columns
+    (0, 16, 512, 0),                                              # next 16 columns, after all of K (K = 256)
+    (200, 37, ((2 * 2 + 1) * 64 + 5 + 16 * 1) * 4 + 2, 0),       # k%128 = 72: chunk 9 -> g 1, word 2
+])
+def test_w4_nz_known_positions(oracle, k, n, word, nibble):
+    """A single nonzero weight lands in exactly one word at the hand-computed position (K=256, N=48)."""
+    K, N = 256, 48
+    assert _nz_word_and_nibble_by_hand(k, n, K) == (word, nibble)
+    w = np.zeros((K, N), dtype=np.int8)
+    w[k, n] = -3   # 0xd as a nibble
+    nz = oracle.w4_nz_pack(oracle.int4_pack(w)).ravel().view(np.uint32)
+    assert np.count_nonzero(nz) == 1
+    assert nz[word] == np.uint32(0xD) << np.uint32(4 * nibble)
+
+
+def test_w4_nz_round_trip_and_operand_property(oracle):
+    """NZ is a bijection of the packed words (round trip on random weights), and each NZ word is the MFMA
+    operand the kernels assume: after (word >> 4q) & 0x000f000f, the low half is w[k0+2q, n] and the high half
+    w[k0+2q+1, n], k0 = 128*s + 8*(4*j + lane//16), n = 16*b + lane%16."""
+    g = np.random.default_rng(3)
+    K, N = 384, 80
+    w = g.integers(-8, 8, size=(K, N), dtype=np.int8)
+    nd = oracle.int4_pack(w)
+    nz = oracle.w4_nz_pack(nd)
+    assert nz.shape == (N // 16, K // 128, 64, 4)
+    assert np.array_equal(oracle.w4_nz_unpack(nz), nd)
+    u = nz.view(np.uint32)
+
+    def s4(v):
+        return ((v.astype(np.int32) + 8) % 16) - 8
+
+    for b in range(N // 16):
+        for s in range(K // 128):
+            for lane in range(64):
+                for j in range(4):
+                    k0, n = 128 * s + 8 * (4 * j + lane // 16), 16 * b + lane % 16
+                    word = u[b, s, lane, j]
+                    for q in range(4):
+                        d = (word >> np.uint32(4 * q)) & np.uint32(0x000F000F)
+                        assert s4(d & 0xF) == w[k0 + 2 * q, n]
+                        assert s4(d >> 16) == w[k0 + 2 * q + 1, n]
+
+
 def test_w4a16_identity_scale_is_plain_matmul(oracle):
     g = torch.Generator().manual_seed(5)
     M, K, N, G = 3, 256, 16, 128
