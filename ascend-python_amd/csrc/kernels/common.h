@@ -336,6 +336,12 @@ hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t 
 size_t w4_nz_workspace(const WqbmmArgs& args);
 hipError_t launch_w4_nz_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 
+// Static quantization (static_quant.hip): x [outer][C][inner] (fp32/fp16/bf16) -> q (int8/uint8/int32);
+// scales == nullptr: per tensor with scale0 / zp0.
+hipError_t launch_quantize(const void* x, int x_dtype, int64_t outer, int64_t C, int64_t inner, const float* scales,
+                           const int64_t* zps, float scale0, int64_t zp0, void* q, int q_dtype, hipStream_t stream);
+hipError_t launch_dequantize(const void* q, int q_dtype, int64_t n, float* out, hipStream_t stream);
+
 hipError_t launch_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed,
                             hipStream_t stream);
 

@@ -19,6 +19,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <cmath>
 #include <map>
 #include <mutex>
 #include <optional>
@@ -402,6 +403,118 @@ at::Tensor npu_format_cast_meta(const at::Tensor& self, int64_t acl_format) {
     return at::empty(shape, self.options());
 }
 
+// ---------------------------------------------------------------- quantize_per_tensor / _per_channel / dequantize
+
+// The reference's NPU quantize ops return plain integer tensors, QInt8 -> kChar, QUInt8 -> kByte,
+// QInt32 -> kInt (op_plugin/ops/base_ops/aclops/QuantizePerTensorKernelNpu.cpp:60-67,
+// op_plugin/ops/base_ops/aclops/QuantizePerChannelKernelNpu.cpp:81-88), not torch quantized tensors.
+std::pair<at::ScalarType, int> quant_out_type(const char* op, at::ScalarType dtype) {
+    switch (dtype) {
+    case at::kQInt8: return {at::kChar, QK_I8};
+    case at::kQUInt8: return {at::kByte, QK_U8};
+    case at::kQInt32: return {at::kInt, QK_I32};
+    default: TORCH_CHECK(false, op, ": dtype must be torch.qint8, torch.quint8 or torch.qint32, got ", dtype);
+    }
+}
+
+void quant_input_check(const char* op, const at::Tensor& self) {
+    const auto t = self.scalar_type();
+    TORCH_CHECK(t == at::kFloat || t == at::kHalf || t == at::kBFloat16, op,
+                ": self must be float32, float16 or bfloat16, got ", t);
+}
+
+at::Tensor quantize_per_tensor_meta(const at::Tensor& self, double scale, int64_t zero_point, at::ScalarType dtype) {
+    const char* op = "quantize_per_tensor";
+    quant_input_check(op, self);
+    TORCH_CHECK(scale > 0.0 && std::isfinite((float)scale), op, ": scale must be positive and finite, got ", scale);
+    (void)zero_point;
+    return at::empty(self.sizes(), self.options().dtype(quant_out_type(op, dtype).first));
+}
+
+at::Tensor quantize_per_tensor(const at::Tensor& self, double scale, int64_t zero_point, at::ScalarType dtype) {
+    const char* op = "quantize_per_tensor";
+    auto out = quantize_per_tensor_meta(self, scale, zero_point, dtype);
+    const c10::DeviceGuard guard(self.device());
+    auto x = self.contiguous();
+    out = at::empty(self.sizes(), self.options().dtype(out.scalar_type()));
+    check_rc(qk_quantize_per_tensor(x.data_ptr(), qk_dtype_of(x.scalar_type()), x.numel(), (float)scale, zero_point,
+                                    out.data_ptr(), quant_out_type(op, dtype).second, current_stream(x)),
+             op);
+    return out;
+}
+
+// axis wrapped as the reference does (make_warp_dim); the checks of
+// op_plugin/ops/base_ops/aclops/QuantizePerChannelKernelNpu.cpp:75-80
+int64_t quantize_per_channel_check(const at::Tensor& self, const at::Tensor& scales, const at::Tensor& zero_points,
+                                   int64_t axis) {
+    const char* op = "quantize_per_channel";
+    quant_input_check(op, self);
+    TORCH_CHECK(self.dim() >= 1, op, ": self must have at least one dimension");
+    if (axis < 0) axis += self.dim();
+    TORCH_CHECK(axis >= 0 && axis < self.dim(), op, ": axis out of range for a ", self.dim(), "-d input");
+    TORCH_CHECK(scales.dim() == 1, op, ": scales must be 1-D");
+    TORCH_CHECK(zero_points.dim() == 1, op, ": zero_points must be 1-D");
+    TORCH_CHECK(scales.size(0) == zero_points.size(0), op, ": scales and zero_points must have the same length");
+    TORCH_CHECK(scales.size(0) == self.size(axis), op, ": scales must have as many elements as dimension ", axis,
+                " of self (", self.size(axis), "), got ", scales.size(0));
+    TORCH_CHECK(scales.is_floating_point(), op, ": scales must be a floating-point tensor");
+    TORCH_CHECK(!zero_points.is_floating_point() && !zero_points.is_complex(), op,
+                ": zero_points must be an integer tensor");
+    return axis;
+}
+
+at::Tensor quantize_per_channel_meta(const at::Tensor& self, const at::Tensor& scales, const at::Tensor& zero_points,
+                                     int64_t axis, at::ScalarType dtype) {
+    quantize_per_channel_check(self, scales, zero_points, axis);
+    return at::empty(self.sizes(), self.options().dtype(quant_out_type("quantize_per_channel", dtype).first));
+}
+
+at::Tensor quantize_per_channel(const at::Tensor& self, const at::Tensor& scales, const at::Tensor& zero_points,
+                                int64_t axis, at::ScalarType dtype) {
+    const char* op = "quantize_per_channel";
+    axis = quantize_per_channel_check(self, scales, zero_points, axis);
+    const auto qt = quant_out_type(op, dtype);
+    const c10::DeviceGuard guard(self.device());
+    auto x = self.contiguous();
+    auto out = at::empty(self.sizes(), self.options().dtype(qt.first));
+    // the scales are rounded to float32 (as torch's quantizer does with its double scales), the zero points widened
+    auto sc = scales.to(self.device(), at::kFloat).contiguous();
+    auto zp = zero_points.to(self.device(), at::kLong).contiguous();
+    int64_t outer = 1, inner = 1;
+    for (int64_t i = 0; i < axis; ++i) outer *= x.size(i);
+    for (int64_t i = axis + 1; i < x.dim(); ++i) inner *= x.size(i);
+    check_rc(qk_quantize_per_channel(x.data_ptr(), qk_dtype_of(x.scalar_type()), outer, x.size(axis), inner,
+                                     sc.data_ptr<float>(), zp.data_ptr<int64_t>(), out.data_ptr(), qt.second,
+                                     current_stream(x)),
+             op);
+    return out;
+}
+
+// dequantize.self: the integers as float32 (op_plugin/ops/v1r11/opapi/DequantizeKernelNpuOpApi.cpp:22-24)
+int dequant_code(const at::Tensor& self) {
+    switch (self.scalar_type()) {
+    case at::kChar: return QK_I8;
+    case at::kByte: return QK_U8;
+    case at::kInt: return QK_I32;
+    default: TORCH_CHECK(false, "dequantize: self must be int8, uint8 or int32 (a quantized NPU tensor), got ",
+                         self.scalar_type());
+    }
+}
+
+at::Tensor dequantize_meta(const at::Tensor& self) {
+    dequant_code(self);
+    return at::empty(self.sizes(), self.options().dtype(at::kFloat));
+}
+
+at::Tensor dequantize(const at::Tensor& self) {
+    const int code = dequant_code(self);
+    const c10::DeviceGuard guard(self.device());
+    auto q = self.contiguous();
+    auto out = at::empty(self.sizes(), self.options().dtype(at::kFloat));
+    check_rc(qk_dequantize(q.data_ptr(), code, q.numel(), out.data_ptr<float>(), current_stream(q)), "dequantize");
+    return out;
+}
+
 // ---------------------------------------------------------------- npu_rms_norm (+ dynamic quant)
 
 // Normalized size D = gamma.numel() over the trailing gamma.dim() dims of self;
@@ -540,6 +653,11 @@ TORCH_LIBRARY(npu, m) {
         "Tensor? quant_scale=None, Tensor? quant_offset=None, Tensor? bias=None, int antiquant_group_size=0) -> Tensor");
     m.def("npu_convert_weight_to_int4pack(Tensor weight, int inner_k_tiles=0) -> Tensor");
     m.def("npu_format_cast(Tensor self, int acl_format) -> Tensor");
+    // static quantization: op_plugin/config/v2r2/op_plugin_functions.yaml:1231, 1233 and
+    // op_plugin/config/v1r11/op_plugin_functions.yaml:127
+    m.def("quantize_per_channel(Tensor self, Tensor scales, Tensor zero_points, int axis, ScalarType dtype) -> Tensor");
+    m.def("quantize_per_tensor(Tensor self, float scale, int zero_point, ScalarType dtype) -> Tensor");
+    m.def("dequantize.self(Tensor self) -> Tensor");
     // schema as op_plugin/config/v2r2/op_plugin_functions.yaml:2047
     m.def("npu_rms_norm(Tensor self, Tensor gamma, float epsilon=1e-06) -> (Tensor, Tensor)");
     m.def("npu_swiglu(Tensor self, int dim=-1) -> Tensor");
@@ -554,6 +672,9 @@ TORCH_LIBRARY_IMPL(npu, CUDA, m) {
     m.impl("npu_weight_quant_batchmatmul", &npu_weight_quant_batchmatmul);
     m.impl("npu_convert_weight_to_int4pack", &npu_convert_weight_to_int4pack);
     m.impl("npu_format_cast", &npu_format_cast);
+    m.impl("quantize_per_channel", &quantize_per_channel);
+    m.impl("quantize_per_tensor", &quantize_per_tensor);
+    m.impl("dequantize.self", &dequantize);
     m.impl("npu_rms_norm", &npu_rms_norm);
     m.impl("npu_swiglu", &npu_swiglu);
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant);
@@ -566,6 +687,9 @@ TORCH_LIBRARY_IMPL(npu, Meta, m) {
     m.impl("npu_weight_quant_batchmatmul", &npu_weight_quant_batchmatmul_meta);
     m.impl("npu_convert_weight_to_int4pack", &npu_convert_weight_to_int4pack_meta);
     m.impl("npu_format_cast", &npu_format_cast_meta);
+    m.impl("quantize_per_channel", &quantize_per_channel_meta);
+    m.impl("quantize_per_tensor", &quantize_per_tensor_meta);
+    m.impl("dequantize.self", &dequantize_meta);
     m.impl("npu_rms_norm", &npu_rms_norm_meta);
     m.impl("npu_swiglu", &npu_swiglu_meta);
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant_meta);

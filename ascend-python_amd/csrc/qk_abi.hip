@@ -6,6 +6,7 @@
 // op_plugin/utils/op_api_common.h:544-555), and enqueues the kernels on the
 // caller's stream.  Nothing here allocates or synchronises.
 #include <atomic>
+#include <cmath>
 #include <chrono>
 #include <cstdarg>
 #include <cstdio>
@@ -397,6 +398,52 @@ int qk_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* pack
     if (K * N == 0) return QK_OK;
     if (!w || !packed) return fail(QK_ERR_ARG, "%s: null pointer", op);
     return launched(qk::launch_int4_pack(w, w_dtype, K, N, packed, (hipStream_t)stream), op);
+}
+
+static int quant_common(const char* op, const void* x, int x_dtype, int64_t n, const void* q, int q_dtype) {
+    if (!(x_dtype == QK_F32 || is_half(x_dtype)))
+        return fail(QK_ERR_ARG, "%s: input must be float32, float16 or bfloat16 (got dtype %d)", op, x_dtype);
+    if (!(q_dtype == QK_I8 || q_dtype == QK_U8 || q_dtype == QK_I32))
+        return fail(QK_ERR_ARG, "%s: output must be int8 (qint8), uint8 (quint8) or int32 (qint32), got dtype %d", op,
+                    q_dtype);
+    if (n < 0) return fail(QK_ERR_ARG, "%s: negative size", op);
+    if (n > 0 && (!x || !q)) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    return QK_OK;
+}
+
+int qk_quantize_per_tensor(const void* x, int x_dtype, int64_t n, float scale, int64_t zero_point, void* q,
+                           int q_dtype, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "quantize_per_tensor";
+    if (int rc = quant_common(op, x, x_dtype, n, q, q_dtype)) return rc;
+    if (!(scale > 0.0f) || scale == INFINITY) return fail(QK_ERR_ARG, "%s: scale must be positive and finite", op);
+    if (n == 0) return QK_OK;
+    return launched(qk::launch_quantize(x, x_dtype, 1, 1, n, nullptr, nullptr, scale, zero_point, q, q_dtype,
+                                        (hipStream_t)stream), op);
+}
+
+int qk_quantize_per_channel(const void* x, int x_dtype, int64_t outer, int64_t C, int64_t inner, const float* scales,
+                            const int64_t* zero_points, void* q, int q_dtype, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "quantize_per_channel";
+    if (outer < 0 || C < 0 || inner < 0) return fail(QK_ERR_ARG, "%s: negative size", op);
+    const int64_t n = outer * C * inner;
+    if (int rc = quant_common(op, x, x_dtype, n, q, q_dtype)) return rc;
+    if (n == 0) return QK_OK;
+    if (!scales || !zero_points) return fail(QK_ERR_ARG, "%s: null scales or zero_points", op);
+    return launched(qk::launch_quantize(x, x_dtype, outer, C, inner, scales, zero_points, 1.0f, 0, q, q_dtype,
+                                        (hipStream_t)stream), op);
+}
+
+int qk_dequantize(const void* q, int q_dtype, int64_t n, float* out, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "dequantize";
+    if (!(q_dtype == QK_I8 || q_dtype == QK_U8 || q_dtype == QK_I32))
+        return fail(QK_ERR_ARG, "%s: input must be int8, uint8 or int32, got dtype %d", op, q_dtype);
+    if (n < 0) return fail(QK_ERR_ARG, "%s: negative size", op);
+    if (n == 0) return QK_OK;
+    if (!q || !out) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    return launched(qk::launch_dequantize(q, q_dtype, n, out, (hipStream_t)stream), op);
 }
 
 static int rms_common(const char* op, const void* x, int x_dtype, const void* gamma, int64_t rows, int64_t D,

@@ -12,6 +12,10 @@ Importing this package loads ``_npu_ops.so``, which registers
   (``inner_k_tiles=4``: straight to the NZ layout)
 * ``torch.ops.npu.npu_format_cast(self, acl_format) -> Tensor``: an int4-packed weight between ND (2) and
   FRACTAL_NZ (29), the MFMA-tiled layout ``npu_weight_quant_batchmatmul`` streams fastest
+* ``torch.ops.npu.quantize_per_tensor(self, scale, zero_point, dtype)``,
+  ``torch.ops.npu.quantize_per_channel(self, scales, zero_points, axis, dtype)`` and
+  ``torch.ops.npu.dequantize(self)``: the reference's static quantization ops (plain int8 / uint8 / int32
+  results for torch.qint8 / quint8 / qint32; dequantize is their cast to float32)
 * ``torch.ops.npu.npu_rms_norm(self, gamma, epsilon=1e-6) -> (y, fp32 rstd)``
 * ``torch.ops.npu.npu_swiglu(self, dim=-1) -> Tensor``
 * ``torch.ops.npu.npu_rms_norm_dynamic_quant(self, gamma, epsilon=1e-6) -> (int8 q, fp32 scale, fp32 rstd)``
@@ -50,20 +54,23 @@ npu_quant_matmul = torch.ops.npu.npu_quant_matmul
 npu_weight_quant_batchmatmul = torch.ops.npu.npu_weight_quant_batchmatmul
 npu_convert_weight_to_int4pack = torch.ops.npu.npu_convert_weight_to_int4pack
 npu_format_cast = torch.ops.npu.npu_format_cast
+quantize_per_tensor = torch.ops.npu.quantize_per_tensor
+quantize_per_channel = torch.ops.npu.quantize_per_channel
+dequantize = torch.ops.npu.dequantize
 npu_rms_norm = torch.ops.npu.npu_rms_norm
 npu_swiglu = torch.ops.npu.npu_swiglu
 npu_rms_norm_dynamic_quant = torch.ops.npu.npu_rms_norm_dynamic_quant
 npu_swiglu_dynamic_quant = torch.ops.npu.npu_swiglu_dynamic_quant
 
 # qk_abi.h constants
-QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_I4_NZ = 1, 2, 3, 4, 5, 16
+QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_U8, QK_I4_NZ = 1, 2, 3, 4, 5, 6, 16
 ACL_FORMAT_ND, ACL_FORMAT_FRACTAL_NZ = 2, 29
 QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, -2, -3, -4
 
 ABI_SYMBOLS = (
     "qk_last_error", "qk_abi_version", "qk_debug_set_plan", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",
     "qk_quant_matmul", "qk_weight_quant_bmm_workspace_size", "qk_weight_quant_bmm", "qk_weight_quant_bmm_noalloc",
-    "qk_int4_pack", "qk_weight_format_cast",
+    "qk_int4_pack", "qk_weight_format_cast", "qk_quantize_per_tensor", "qk_quantize_per_channel", "qk_dequantize",
     "qk_rms_norm", "qk_rms_norm_quant", "qk_swiglu", "qk_swiglu_quant",
 )
 
@@ -88,6 +95,9 @@ def abi() -> ctypes.CDLL:
         L.qk_weight_quant_bmm_noalloc.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P]
         L.qk_int4_pack.argtypes = [P, I, I64, I64, P, P]
         L.qk_weight_format_cast.argtypes = [P, I, P, I, I, I64, I64, P]
+        L.qk_quantize_per_tensor.argtypes = [P, I, I64, ctypes.c_float, I64, P, I, P]
+        L.qk_quantize_per_channel.argtypes = [P, I, I64, I64, I64, P, P, P, I, P]
+        L.qk_dequantize.argtypes = [P, I, I64, P, P]
         F = ctypes.c_float
         L.qk_rms_norm.argtypes = [P, I, P, I64, I64, F, P, P, P]
         L.qk_rms_norm_quant.argtypes = [P, I, P, I64, I64, F, P, P, P, P]
@@ -122,6 +132,7 @@ def debug_set_plan(spec: str = "") -> None:
 
 __all__ = [
     "npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
-    "npu_convert_weight_to_int4pack", "npu_format_cast", "get_npu_format", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
+    "npu_convert_weight_to_int4pack", "npu_format_cast", "get_npu_format", "quantize_per_tensor",
+    "quantize_per_channel", "dequantize", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
     "npu_swiglu_dynamic_quant", "abi", "last_error", "debug_set_plan", "LIB_PATH", "OPS_PATH",
 ]

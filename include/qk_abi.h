@@ -58,6 +58,7 @@ typedef enum {
     QK_F32 = 3,
     QK_I8 = 4,
     QK_I32 = 5,
+    QK_U8 = 6,
     /* weight code of qk_weight_quant_bmm: an int4 weight in the MFMA-tiled
      * NZ layout that qk_weight_format_cast writes (int32 [N/16][K/128][64][4]) */
     QK_I4_NZ = 16
@@ -83,7 +84,7 @@ const char* qk_last_error(void);
 /* ABI revision; bumped on any incompatible signature or contract change
  * (2: the split-K counters at the head of a workspace; 3: the counters are
  * tagged per call, so a workspace needs no initialisation; 4: NZ weights,
- * qk_weight_format_cast). */
+ * qk_weight_format_cast, static quantization). */
 int qk_abi_version(void);
 
 /* Debug and test hook, no counterpart in the reference: forces kernel choices
@@ -224,6 +225,38 @@ int qk_weight_format_cast(const void* src, int src_format, void* dst, int dst_fo
  */
 int qk_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed,
                  qk_stream_t stream);
+
+/*
+ * quantize_per_tensor -- replaces the CANN Quantize call of
+ * op_plugin/ops/base_ops/aclops/QuantizePerTensorKernelNpu.cpp:50-82 (schema
+ * op_plugin/config/v2r2/op_plugin_functions.yaml:1233).  x: n elements,
+ * fp32/fp16/bf16.  q: n elements of q_dtype QK_I8 (qint8), QK_U8 (quint8) or
+ * QK_I32 (qint32), the plain integer tensor the reference returns (dtype map
+ * :60-67).  Per element: q = clamp(RN(rint(x * RN(1/scale)) + float(zero_point)),
+ * qmin, qmax), ties to even, the zero point added in float32 (torch's affine
+ * quantizer); NaN gives qmin.  scale must be a positive finite float.
+ */
+int qk_quantize_per_tensor(const void* x, int x_dtype, int64_t n, float scale, int64_t zero_point, void* q,
+                           int q_dtype, qk_stream_t stream);
+
+/*
+ * quantize_per_channel -- replaces the CANN Quantize call of
+ * op_plugin/ops/base_ops/aclops/QuantizePerChannelKernelNpu.cpp:69-92 (schema
+ * op_plugin/config/v2r2/op_plugin_functions.yaml:1231).  x is viewed as
+ * [outer][C][inner] with C the quantized axis; scales: fp32 [C] (device);
+ * zero_points: int64 [C] (device).  Element rule as qk_quantize_per_tensor with
+ * the channel's scale and zero point.
+ */
+int qk_quantize_per_channel(const void* x, int x_dtype, int64_t outer, int64_t C, int64_t inner, const float* scales,
+                            const int64_t* zero_points, void* q, int q_dtype, qk_stream_t stream);
+
+/*
+ * dequantize -- the reference's op_plugin/ops/v1r11/opapi/DequantizeKernelNpuOpApi.cpp:22-24
+ * (schema op_plugin/config/v1r11/op_plugin_functions.yaml:127): the integers of
+ * q (QK_I8, QK_U8 or QK_I32, n elements) cast to float32 (round to nearest even
+ * past 2^24).
+ */
+int qk_dequantize(const void* q, int q_dtype, int64_t n, float* out, qk_stream_t stream);
 
 /*
  * npu_rms_norm -- replaces aclnnRmsNorm behind EXEC_NPU_CMD

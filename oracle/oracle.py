@@ -20,7 +20,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libqk_oracle.so")
 
-F16, BF16, F32, I8, I32 = 1, 2, 3, 4, 5
+F16, BF16, F32, I8, I32, U8 = 1, 2, 3, 4, 5, 6
 
 _lib = None
 
@@ -50,6 +50,8 @@ def lib() -> ctypes.CDLL:
         L.qo_rms_norm.argtypes = [P, I, P, I64, I64, ctypes.c_double, P, P]
         L.qo_swiglu.argtypes = [P, I, I64, I64, P]
         L.qo_cvt_array.argtypes = [P, I, P, I, I64]
+        L.qo_quantize.argtypes = [P, I, I64, I64, I64, P, P, P, I]
+        L.qo_dequantize.argtypes = [P, I, I64, P]
         L.qo_f32_to_bf16.argtypes = [ctypes.c_float]
         L.qo_f32_to_bf16.restype = ctypes.c_uint16
         L.qo_f32_to_f16.argtypes = [ctypes.c_float]
@@ -194,6 +196,34 @@ def weight_quant_bmm(x_bits, x_dtype, weight, scale_bits, offset_bits, scale_dty
     work = np.empty((M + 1) * N, dtype=np.float64)
     lib().qo_weight_quant_bmm(_p(x), x_dtype, _p(w), wdt, _p(sc), _p(off), scale_dtype, M, N, K,
                               group, _p(bias), bias_dtype, _p(out), out_dtype, _p(work))
+    return out
+
+
+_QNP = {I8: np.int8, U8: np.uint8, I32: np.int32}
+
+
+def quantize(x, x_dtype, scales, zero_points, axis=None, q_dtype=I8):
+    """quantize_per_tensor (axis None; scales / zero_points of one element) or quantize_per_channel along
+    `axis`.  x: float32 array (x_dtype F32) or uint16 bit patterns (F16 / BF16)."""
+    xa = np.ascontiguousarray(x, dtype=np.float32 if x_dtype == F32 else np.uint16)
+    sc = np.ascontiguousarray(scales, dtype=np.float32).ravel()
+    zp = np.ascontiguousarray(zero_points, dtype=np.int64).ravel()
+    if axis is None:
+        outer, C, inner = 1, 1, xa.size
+    else:
+        axis %= xa.ndim
+        C = xa.shape[axis]
+        outer = int(np.prod(xa.shape[:axis], dtype=np.int64))
+        inner = int(np.prod(xa.shape[axis + 1:], dtype=np.int64))
+    out = np.empty(xa.shape, dtype=_QNP[q_dtype])
+    lib().qo_quantize(_p(xa), x_dtype, outer, C, inner, _p(sc), _p(zp), _p(out), q_dtype)
+    return out
+
+
+def dequantize(q, q_dtype):
+    qa = np.ascontiguousarray(q, dtype=_QNP[q_dtype])
+    out = np.empty(qa.shape, dtype=np.float32)
+    lib().qo_dequantize(_p(qa), q_dtype, qa.size, _p(out))
     return out
 
 

@@ -43,6 +43,10 @@
  *       a hand-computed 1x2x128 example; linearity in x.
  *   qo_rms_norm: the reference's numpy closed form, restated in float64.
  *   qo_swiglu: torch.nn.functional.silu (a library routine) on float64.
+ *   qo_quantize: torch.quantize_per_tensor / quantize_per_channel on the CPU
+ *       (.int_repr(), library routines) for qint8 / quint8 / qint32 on random
+ *       data, planted exact ties and values past the clamp bounds; hand-computed
+ *       cases.  qo_dequantize: torch's integer -> float32 cast.
  */
 #include <math.h>
 #include <stdint.h>
@@ -102,7 +106,7 @@ uint16_t qo_f32_to_f16(float f) {
 }
 
 /* dtype codes shared with include/qk_abi.h */
-enum { QO_F16 = 1, QO_BF16 = 2, QO_F32 = 3, QO_I8 = 4, QO_I32 = 5 };
+enum { QO_F16 = 1, QO_BF16 = 2, QO_F32 = 3, QO_I8 = 4, QO_I32 = 5, QO_U8 = 6 };
 
 static inline float load_half(const uint16_t* p, int64_t i, int dt) {
     return dt == QO_BF16 ? qo_bf16_to_f32(p[i]) : qo_f16_to_f32(p[i]);
@@ -416,6 +420,56 @@ void qo_swiglu(const uint16_t* h, int dt, int64_t rows, int64_t I, uint16_t* out
 }
 
 /* Elementwise dtype conversion over an array (used to pin the scalar casts). */
+/* ------------------------------------------------------------------ */
+/* Static quantization: quantize_per_tensor / quantize_per_channel /   */
+/* dequantize                                                          */
+/* ------------------------------------------------------------------ */
+/*
+ * The reference's NPU quantize ops return plain integer tensors: QInt8 ->
+ * int8, QUInt8 -> uint8, QInt32 -> int32
+ * (op_plugin/ops/base_ops/aclops/QuantizePerTensorKernelNpu.cpp:60-67,
+ * op_plugin/ops/base_ops/aclops/QuantizePerChannelKernelNpu.cpp:81-88); the
+ * element rule is in CANN's closed Quantize op, so this restates torch's own
+ * affine quantizer for the same schema:
+ *   q = clamp(RN(rint(x * RN(1 / float(scale))) + float(zero_point)), qmin, qmax),
+ * one float32 multiply by the float32 reciprocal of the scale, ties to even,
+ * then the zero point added to the rounded value in float32 (torch's
+ * quantize_val adds its int64 zero point to a float, so past 2^24 the sum
+ * rounds: 2e9 - 7 stays 2e9 for qint32).  x is viewed as
+ * [outer][C][inner]; channel c uses scales[c], zero_points[c] (per tensor:
+ * C == 1).  A NaN input gives qmin.  dequantize is the reference's
+ * op_plugin/ops/v1r11/opapi/DequantizeKernelNpuOpApi.cpp:22-24: a plain cast of
+ * the integers to float32.
+ */
+void qo_quantize(const void* x, int x_dtype, int64_t outer, int64_t C, int64_t inner, const float* scales,
+                 const int64_t* zero_points, void* q, int q_dtype) {
+    const double qmin = q_dtype == QO_I8 ? -128.0 : q_dtype == QO_U8 ? 0.0 : -2147483648.0;
+    const double qmax = q_dtype == QO_I8 ? 127.0 : q_dtype == QO_U8 ? 255.0 : 2147483647.0;
+    for (int64_t o = 0; o < outer; ++o)
+        for (int64_t c = 0; c < C; ++c) {
+            const float r = 1.0f / scales[c];
+            for (int64_t i = 0; i < inner; ++i) {
+                const int64_t e = (o * C + c) * inner + i;
+                const float v = load_any(x, e, x_dtype);
+                const float t = v * r;
+                const float z = rintf(t) + (float)zero_points[c];  /* float32 add, as torch's quantize_val */
+                double d = isnan(z) ? qmin : (double)z;
+                d = d < qmin ? qmin : (d > qmax ? qmax : d);
+                if (q_dtype == QO_I8) ((int8_t*)q)[e] = (int8_t)d;
+                else if (q_dtype == QO_U8) ((uint8_t*)q)[e] = (uint8_t)d;
+                else ((int32_t*)q)[e] = (int32_t)d;
+            }
+        }
+}
+
+void qo_dequantize(const void* q, int q_dtype, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) {
+        if (q_dtype == QO_I8) out[i] = (float)((const int8_t*)q)[i];
+        else if (q_dtype == QO_U8) out[i] = (float)((const uint8_t*)q)[i];
+        else out[i] = (float)((const int32_t*)q)[i];
+    }
+}
+
 void qo_cvt_array(const void* in, int in_dt, void* out, int out_dt, int64_t n) {
     for (int64_t i = 0; i < n; ++i) {
         float v = load_any(in, i, in_dt);

@@ -72,6 +72,13 @@ def test_abi_refuses_bad_arguments_without_launch():
     ws = ctypes.c_size_t(123)
     assert L.qk_weight_quant_bmm_workspace_size(16, 11008, 4096, I32, 128, ctypes.byref(ws)) == 0
     assert L.qk_int4_pack(fake, I8, 4, 12, fake, None) == q.QK_ERR_ARG
+    assert L.qk_quantize_per_tensor(fake, I32, 4, 0.1, 0, fake, I8, None) == q.QK_ERR_ARG
+    assert L.qk_quantize_per_tensor(fake, F32, 4, -1.0, 0, fake, I8, None) == q.QK_ERR_ARG
+    assert L.qk_quantize_per_tensor(fake, F32, 4, 0.1, 0, fake, F16, None) == q.QK_ERR_ARG
+    assert L.qk_quantize_per_channel(fake, F32, 2, 3, 4, None, None, fake, I8, None) == q.QK_ERR_ARG
+    assert L.qk_quantize_per_channel(None, F32, 0, 3, 4, None, None, None, I8, None) == q.QK_OK
+    assert L.qk_dequantize(fake, F32, 4, fake, None) == q.QK_ERR_ARG
+    assert L.qk_dequantize(None, I8, 4, None, None) == q.QK_ERR_ARG and "null pointer" in q.last_error()
     # NZ weights: shape rules, supported casts, overlap
     rc = L.qk_weight_quant_bmm(fake, BF16, fake, q.QK_I4_NZ, fake, None, F16, 4, 24, 128, 128, None, 0, fake, BF16,
                                None, 0, None)
@@ -105,7 +112,8 @@ def _m(shape, dtype):
 
 def test_schemas_registered():
     for name in ("npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
-                 "npu_convert_weight_to_int4pack", "npu_format_cast", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
+                 "npu_convert_weight_to_int4pack", "npu_format_cast", "quantize_per_tensor", "quantize_per_channel",
+                 "dequantize", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
                  "npu_swiglu_dynamic_quant"):
         assert hasattr(torch.ops.npu, name)
     s = str(torch.ops.npu.npu_quant_matmul.default._schema)
@@ -130,6 +138,11 @@ def test_meta_shapes():
     nzw = q.npu_format_cast(_m((4096, 1376), torch.int32), 29)
     assert nzw.shape == (688, 32, 64, 4) and q.get_npu_format(nzw) == 29
     assert q.npu_format_cast(nzw, 2).shape == (4096, 1376) and q.npu_format_cast(nzw, 29) is nzw
+    assert q.quantize_per_tensor(_m((3, 8), torch.float16), 0.1, 2, torch.quint8).dtype == torch.uint8
+    qq = q.quantize_per_channel(_m((3, 8), torch.bfloat16), _m((8,), torch.float64), _m((8,), torch.int64), -1,
+                                torch.qint32)
+    assert qq.shape == (3, 8) and qq.dtype == torch.int32
+    assert q.dequantize(_m((2, 2), torch.uint8)).dtype == torch.float32
     out = q.npu_weight_quant_batchmatmul(_m((16, 4096), torch.bfloat16), nzw, _m((32, 11008), torch.float16),
                                          _m((32, 11008), torch.float16), antiquant_group_size=128)
     assert out.shape == (16, 11008) and out.dtype == torch.bfloat16
@@ -167,6 +180,18 @@ def test_meta_shapes():
     (lambda: q.npu_convert_weight_to_int4pack(_m((128, 16), torch.int32), inner_k_tiles=2), "inner_k_tiles"),
     (lambda: q.npu_convert_weight_to_int4pack(_m((64, 16), torch.int32), inner_k_tiles=4), "K % 128"),
     (lambda: q.npu_format_cast(_m((100, 2), torch.int32), 29), "K % 128"),
+    (lambda: q.quantize_per_tensor(_m((4,), torch.int32), 0.1, 0, torch.qint8), "float32, float16 or bfloat16"),
+    (lambda: q.quantize_per_tensor(_m((4,), torch.float32), 0.0, 0, torch.qint8), "positive"),
+    (lambda: q.quantize_per_tensor(_m((4,), torch.float32), 0.1, 0, torch.float16), "torch.qint8"),
+    (lambda: q.quantize_per_channel(_m((4, 3), torch.float32), _m((3,), torch.float32), _m((3,), torch.int64), 2,
+                                    torch.qint8), "axis out of range"),
+    (lambda: q.quantize_per_channel(_m((4, 3), torch.float32), _m((4,), torch.float32), _m((4,), torch.int64), 1,
+                                    torch.qint8), "as many elements"),
+    (lambda: q.quantize_per_channel(_m((4, 3), torch.float32), _m((3,), torch.float32), _m((2,), torch.int64), 1,
+                                    torch.qint8), "same length"),
+    (lambda: q.quantize_per_channel(_m((4, 3), torch.float32), _m((3, 1), torch.float32), _m((3,), torch.int64), 1,
+                                    torch.qint8), "1-D"),
+    (lambda: q.dequantize(_m((4,), torch.float32)), "int8, uint8 or int32"),
     (lambda: q.npu_format_cast(_m((128, 2), torch.int32), 3), "only ND"),
     (lambda: q.npu_format_cast(_m((128, 16), torch.int8), 29), "int4-packed"),
     (lambda: q.npu_weight_quant_batchmatmul(_m((2, 256), torch.bfloat16), _m((1, 1, 64, 4), torch.int32),

@@ -317,3 +317,72 @@ def test_swiglu_vs_torch_silu(oracle):
     a, b = h.double().chunk(2, dim=-1)
     ref = (torch.nn.functional.silu(a) * b).float().to(torch.bfloat16)
     assert np.array_equal(got, W.bits(ref))
+
+
+# ----------------------------------------------------------------------------- static quantization
+
+_QT = {"qint8": (torch.qint8, 4), "quint8": (torch.quint8, 6), "qint32": (torch.qint32, 5)}
+
+
+@pytest.mark.parametrize("qname", list(_QT))
+def test_quantize_per_tensor_vs_torch(oracle, qname):
+    """torch.quantize_per_tensor (CPU, .int_repr()) on random data, planted exact ties and values past the clamp
+    bounds.  Quotients beyond the int32 range are left out of the comparison: torch's vectorized CPU path wraps
+    them (-5e13 becomes +127 for qint8); the oracle saturates (test_quantize_hand_cases)."""
+    dt, code = _QT[qname]
+    g = torch.Generator().manual_seed(1)
+    for scale, zp in ((0.05, 0), (0.0173, 3), (1.0, 0), (0.5, -7), (3e-3, 101), (2e-5, 1234567)):
+        if dt == torch.quint8 and not 0 <= zp <= 255:
+            zp = 10
+        if dt == torch.qint8 and not -128 <= zp <= 127:
+            zp = -5
+        x = torch.randn(4096, generator=g) * 4
+        j = torch.randint(-300, 300, (512,), generator=g).float()
+        x[:512] = (j + 0.5) * scale                       # exact ties after the multiply by 1/scale
+        x[512:518] = torch.tensor([1e6, -1e6, 0.0, -0.0, 200.0, -200.0])
+        keep = (x.double() / scale).abs() < 2.0**31
+        t = torch.quantize_per_tensor(x, scale, zp, dt).int_repr().numpy()
+        r = oracle.quantize(x.numpy(), oracle.F32, np.array([scale]), np.array([zp]), None, code)
+        assert np.array_equal(t[keep.numpy()].astype(np.int64), r[keep.numpy()].astype(np.int64))
+
+
+@pytest.mark.parametrize("qname", list(_QT))
+@pytest.mark.parametrize("axis", [0, 1, 2, -1])
+def test_quantize_per_channel_vs_torch(oracle, qname, axis):
+    dt, code = _QT[qname]
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(6, 40, 7, generator=g) * 3
+    C = x.shape[axis]
+    sc = torch.rand(C, generator=g, dtype=torch.float64) * 0.1 + 1e-3
+    lo = 0 if dt == torch.quint8 else -20
+    zp = torch.randint(lo, 20, (C,), generator=g, dtype=torch.int64)
+    # the reference wraps a negative axis (op_plugin/ops/base_ops/aclops/QuantizePerChannelKernelNpu.cpp:75); torch
+    # takes only the wrapped one
+    t = torch.quantize_per_channel(x, sc, zp, axis % x.dim(), dt).int_repr().numpy()
+    r = oracle.quantize(x.numpy(), oracle.F32, sc.float().numpy(), zp.numpy(), axis, code)
+    assert np.array_equal(t.astype(np.int64), r.astype(np.int64))
+
+
+def test_quantize_hand_cases(oracle):
+    x = np.array([0.5, 1.5, 2.5, -0.5, -1.5, 1000.0, -1000.0, -1e9, 0.25], dtype=np.float32)
+    # scale 1, zero point 0: ties to even, clamp at the int8 bounds (-1e9 saturates)
+    assert oracle.quantize(x, oracle.F32, [1.0], [0], None, oracle.I8).tolist() == [0, 2, 2, 0, -2, 127, -128, -128, 0]
+    # zero point added after rounding: rint(0.5) + 3 = 3 (not rint(3.5) = 4)
+    assert oracle.quantize(x, oracle.F32, [1.0], [3], None, oracle.I8).tolist()[:3] == [3, 5, 5]
+    # uint8 clamps at 0 and 255; scale 0.25 -> 1/scale = 4 exactly
+    assert oracle.quantize(x, oracle.F32, [0.25], [128], None, 6).tolist() == [130, 134, 138, 126, 122, 255, 0, 0, 129]
+    # qint32: the zero point is added in float32 (torch's quantize_val), 2e9 - 7 rounds back to 2e9
+    assert oracle.quantize(np.array([1e9], np.float32), oracle.F32, [0.5], [-7], None, oracle.I32).tolist() \
+        == [2000000000]
+    assert oracle.quantize(np.array([3e9, -3e9], np.float32), oracle.F32, [1.0], [0], None, oracle.I32).tolist() \
+        == [2147483647, -2147483648]
+
+
+@pytest.mark.parametrize("code,npdt", [(4, np.int8), (6, np.uint8), (5, np.int32)])
+def test_dequantize_is_float_cast(oracle, code, npdt):
+    """The reference's dequantize is self.to(float) (op_plugin/ops/v1r11/opapi/DequantizeKernelNpuOpApi.cpp:22-24)."""
+    g = np.random.default_rng(4)
+    info = np.iinfo(npdt)
+    q = g.integers(info.min, info.max, size=3000, dtype=np.int64, endpoint=True).astype(npdt)
+    q[:4] = [info.min, info.max, 0, 1 if info.min == 0 else -1]
+    assert np.array_equal(oracle.dequantize(q, code), torch.from_numpy(q).float().numpy())
