@@ -318,7 +318,7 @@ struct WqbmmArgs {
     const void* x;
     int x_dtype;
     const void* w;
-    int w_dtype;          // QK_I32 (int4 packed), QK_I8 or QK_I4_NZ
+    int w_dtype;          // QK_I32 (int4 packed), QK_I8, QK_I4_NZ or QK_I8_NZ
     const void* scale;
     const void* offset;
     int s_dtype;
@@ -331,8 +331,9 @@ struct WqbmmArgs {
 hipError_t launch_weight_quant_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group);
 
-// NZ int4 weights (w4a16_nz.hip): the ND <-> NZ casts and the matmul on NZ weights.
+// NZ weights (nz_weights.hip): the ND <-> NZ casts (int4, int8) and the weight-quant matmul on NZ weights.
 hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t N, int32_t* dst, hipStream_t stream);
+hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N, int8_t* dst, hipStream_t stream);
 size_t w4_nz_workspace(const WqbmmArgs& args);
 hipError_t launch_w4_nz_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 

@@ -16,6 +16,11 @@
 // The matching A operand of lane (m, g) is x[m, 128s + 8*(4j+g) .. +8], 16
 // contiguous bytes.
 //
+// The int8 NZ layout (W8A16 and W8A8 weights) is int8 [N/16][K/64][64][16]:
+// lane l = n%16 + 16*g of a 16-column x 64-row block holds rows 16g..16g+15 of
+// its column, the B operand of one v_mfma_i32_16x16x64_i8, or two 8-row
+// operands of a 16-bit MFMA once the bytes are converted.
+//
 // Decode kernel (w4nz_decode), M <= 64: each workgroup owns a few n-blocks
 // over all of K, so no partial sums leave the workgroup.  Its waves split K
 // into equal runs of superblocks; every wave issues the loads of two
@@ -78,6 +83,37 @@ __global__ __launch_bounds__(kNzThreads) void w4_nz_unpack_kernel(const int32_t*
     }
 }
 
+// int8 ND [K, N] -> NZ: one thread per 16-byte lane chunk (16 rows of one column).
+__global__ __launch_bounds__(kNzThreads) void w8_nz_pack_kernel(const int8_t* __restrict__ nd, int64_t K, int64_t N,
+                                                                int8_t* __restrict__ nz) {
+    const int64_t total = K * N / 16, S = K / 64;
+    for (int64_t idx = (int64_t)blockIdx.x * kNzThreads + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * kNzThreads) {
+        const int64_t lane = idx & 63, sb = idx >> 6;
+        const int64_t s = sb % S, nb = sb / S;
+        const int64_t n = nb * 16 + (lane & 15), k0 = s * 64 + 16 * (lane >> 4);
+        u32x4 v = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i >> 2] |= (uint32_t)(uint8_t)nd[(k0 + i) * N + n] << (8 * (i & 3));
+        reinterpret_cast<u32x4*>(nz)[idx] = v;
+    }
+}
+
+// int8 NZ -> ND: one thread per 16-byte lane chunk, scattered back to its 16 rows.
+__global__ __launch_bounds__(kNzThreads) void w8_nz_unpack_kernel(const int8_t* __restrict__ nz, int64_t K, int64_t N,
+                                                                  int8_t* __restrict__ nd) {
+    const int64_t total = K * N / 16, S = K / 64;
+    for (int64_t idx = (int64_t)blockIdx.x * kNzThreads + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * kNzThreads) {
+        const int64_t lane = idx & 63, sb = idx >> 6;
+        const int64_t s = sb % S, nb = sb / S;
+        const int64_t n = nb * 16 + (lane & 15), k0 = s * 64 + 16 * (lane >> 4);
+        const u32x4 v = reinterpret_cast<const u32x4*>(nz)[idx];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) nd[(k0 + i) * N + n] = (int8_t)(v[i >> 2] >> (8 * (i & 3)));
+    }
+}
+
 // The B operand held in one NZ word: dword q takes nibbles q (k = 2q, low
 // half) and 4 + q (k = 2q + 1, high half) as magic values 128 + (w + 8)
 // (bf16) or 1024 + (w + 8) (fp16): one shift and one and-xor each.
@@ -93,15 +129,41 @@ __device__ __forceinline__ u32x4 nz_operand(uint32_t w) {
     return b;
 }
 
+// Eight int8 weights (two dwords, 8 consecutive rows of one column) as a
+// 16-bit MFMA operand of offset-binary values u = w + 128 (BASE 128): each
+// byte converts exactly to float (v_cvt_f32_ubyte) and from there to
+// bf16 (the upper half: u <= 255 fits 8 significant bits) or fp16.
+template <int DT>
+__device__ __forceinline__ u32x4 nz8_operand(uint32_t lo, uint32_t hi) {
+    const uint32_t flip = __builtin_amdgcn_readfirstlane(0x80808080u);
+    const uint32_t w[2] = {lo ^ flip, hi ^ flip};
+    u32x4 b;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t src = w[q >> 1];
+        const float f0 = (float)((src >> (16 * (q & 1))) & 0xffu);
+        const float f1 = (float)((src >> (16 * (q & 1) + 8)) & 0xffu);
+        if constexpr (DT == QK_BF16)
+            b[q] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+        else
+            b[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f0, f1));
+    }
+    return b;
+}
+
 // NB: n-blocks per workgroup (the last workgroups may own one fewer: their
 // extra block repeats a real one and is not stored).  NIT: superblocks per
 // wave.  The grid is (workgroups along N) x (16-row blocks of M); a
 // workgroup has K / (128 * NIT) waves.  A superblock's scale and offset rows
 // (the workgroup's NB*16 columns of one group) come in with one 16-byte load
 // per fetching lane and reach the other lanes through the wave's own LDS slot.
-template <int DT, int NB, int NIT, bool HAS_OFF>
+// W8: int8 NZ weights (two 1 KB blocks per 128 rows; the operand of 16-bit MFMA
+// step j is rows 16g + 8*(j&1) .. +8 of block j>>1, and its A operand is
+// x[m, 128s + 64*(j>>1) + 16g + 8*(j&1) ..]).
+template <int DT, int NB, int NIT, bool HAS_OFF, bool W8>
 __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int nwg, int nrb) {
     typedef Mfma<DT> MM;
+    constexpr int WL = W8 ? 2 : 1;         // weight loads per block and superblock
     constexpr int PF = NIT < 2 ? NIT : 2;  // superblocks in flight per wave
     constexpr int SL = PF;                 // register slots
     constexpr int NT = HAS_OFF ? 2 : 1;    // scale rows per superblock (scale, offset)
@@ -125,8 +187,8 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
     const int m = rb * 16 + c < M ? rb * 16 + c : M - 1;
 
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
-    const uint32_t x_lane = ((uint32_t)m * (uint32_t)K + 8u * (uint32_t)g) * 2u;
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (uint32_t)K * (uint32_t)N / 2u);
+    const uint32_t x_lane = ((uint32_t)m * (uint32_t)K + (W8 ? 16u : 8u) * (uint32_t)g) * 2u;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (uint32_t)K * (uint32_t)N / (W8 ? 1u : 2u));
     const uint32_t w_lane = (uint32_t)lane * 16u;
     // lane l < NT*RL fetches 16 bytes of row l / RL (scale, offset) of a superblock's group: columns
     // 16*b0 + 8*(l % RL) .. +8, clamped into the row (the clamped columns belong to no block of this
@@ -140,28 +202,31 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
 #pragma unroll
     for (int b = 0; b < NB; ++b) blk[b] = b0 + b < b1 ? b0 + b : b1 - 1;
 
-    u32x4 xa[SL][4], wv[SL][NB], sa[SL];
+    u32x4 xa[SL][4], wv[SL][NB][WL], sa[SL];
     auto issue = [&](int it) {
         __builtin_amdgcn_sched_barrier(0);
         const int s = s0 + it, sl = it % SL;
         const uint32_t grp = (uint32_t)(s * 128) / (uint32_t)G;
         sa[sl] = *reinterpret_cast<const u32x4*>(sl_base + (size_t)grp * (uint32_t)N);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            xa[sl][j] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, x_lane, (uint32_t)(s * 256 + 64 * j), 0));
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t xo = W8 ? (uint32_t)(s * 256 + 128 * (j >> 1) + 16 * (j & 1)) : (uint32_t)(s * 256 + 64 * j);
+            xa[sl][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, x_lane, xo, 0));
+        }
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-            wv[sl][b] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           wr, w_lane, ((uint32_t)blk[b] * (uint32_t)S + (uint32_t)s) * 1024u, 0));
+#pragma unroll
+            for (int h = 0; h < WL; ++h)
+                wv[sl][b][h] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               wr, w_lane, ((uint32_t)blk[b] * (uint32_t)(WL * S) + (uint32_t)(WL * s + h)) * 1024u, 0));
         __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
     for (int it = 0; it < PF; ++it) issue(it);
 
     const u32x4 ones = {MM::ONES, MM::ONES, MM::ONES, MM::ONES};
-    constexpr float BASE = MM::BASE;
+    constexpr float BASE = W8 ? 128.0f : MM::BASE;
     f32x4 acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -171,11 +236,13 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
         const int sl = it % SL;
         // this superblock's scale rows through the wave's LDS slot
         if (lane < NT * RL) *reinterpret_cast<u32x4*>(&srow[wave][sl][0][0] + 8 * lane) = sa[sl];
-        u32x4 xk[4], wk[NB];
+        u32x4 xk[4], wk[NB][WL];
 #pragma unroll
         for (int j = 0; j < 4; ++j) xk[j] = xa[sl][j];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) wk[b] = wv[sl][b];
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int h = 0; h < WL; ++h) wk[b][h] = wv[sl][b][h];
         f32x4 xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) xs = MM::mma(xk[j], ones, xs);
@@ -183,7 +250,13 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
         for (int b = 0; b < NB; ++b) {
             f32x4 ag = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) ag = MM::mma(xk[j], nz_operand<MM::MAGIC>(wk[b][j]), ag);
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (W8)
+                    ag = MM::mma(xk[j], nz8_operand<DT>(wk[b][j >> 1][2 * (j & 1)], wk[b][j >> 1][2 * (j & 1) + 1]),
+                                 ag);
+                else
+                    ag = MM::mma(xk[j], nz_operand<MM::MAGIC>(wk[b][0][j]), ag);
+            }
             const float sf = load_half_bits(srow[wave][sl][0][16 * b + c], p.s_dtype);
             const float of = HAS_OFF ? load_half_bits(srow[wave][sl][NT - 1][16 * b + c], p.s_dtype) : 0.0f;
             const float sx = sf * (of - BASE);
@@ -227,9 +300,12 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
 }
 
 // The most blocks per workgroup that a wave of `nit` superblocks holds in registers without
-// spilling (two superblocks in flight, NB accumulators): 4 up to 3 superblocks, 3 for 4, 2 for 5,
-// 1 beyond.  Only these (NB, NIT) pairs are built.
-constexpr int nz_max_blocks(int nit) { return nit <= 3 ? 4 : nit == 4 ? 3 : nit == 5 ? 2 : 1; }
+// spilling (two superblocks in flight, NB accumulators): int4, 4 up to 3 superblocks, 3 for 4, 2 for 5,
+// 1 beyond; int8 (two loads per block), 3 up to 2 superblocks, 2 for 3, 1 beyond.  Only these
+// (NB, NIT) pairs are built.
+constexpr int nz_max_blocks(int nit, bool w8) {
+    return w8 ? (nit <= 2 ? 3 : nit == 3 ? 2 : 1) : (nit <= 3 ? 4 : nit == 4 ? 3 : nit == 5 ? 2 : 1);
+}
 
 struct NzPlan {
     bool ok;
@@ -239,10 +315,11 @@ struct NzPlan {
 NzPlan nz_plan(const WqbmmArgs& p) {
     NzPlan z{false, 0, 0, 0, 0, 0};
     const int64_t G = p.group == 0 ? p.K : p.group;
-    if (p.w_dtype != QK_I4_NZ || p.M <= 0 || p.M > 64 || p.N <= 0 || p.K <= 0) return z;
+    const bool w8 = p.w_dtype == QK_I8_NZ;
+    if (!(p.w_dtype == QK_I4_NZ || w8) || p.M <= 0 || p.M > 64 || p.N <= 0 || p.K <= 0) return z;
     if (p.N % 16 != 0 || p.K % 128 != 0 || G <= 0 || G % 128 != 0 || p.K % G != 0) return z;
     // 32-bit buffer offsets
-    if (p.K * p.N / 2 >= ((int64_t)1 << 31) || p.M * p.K * 2 >= ((int64_t)1 << 31) ||
+    if (p.K * p.N >= ((int64_t)1 << 31) || p.M * p.K * 2 >= ((int64_t)1 << 31) ||
         (p.K / G) * p.N * 2 >= ((int64_t)1 << 31))
         return z;
     if ((uintptr_t)p.x % 16 != 0 || (uintptr_t)p.w % 16 != 0 || (uintptr_t)p.scale % 16 != 0 ||
@@ -262,7 +339,7 @@ NzPlan nz_plan(const WqbmmArgs& p) {
     z.nrb = (int)((p.M + 15) / 16);
     // blocks per workgroup: what one workgroup per CU needs, within what fits the wave's registers
     // (nz_max_blocks); then as few workgroups as give no workgroup more blocks than that
-    const int cap = nz_max_blocks(nit);
+    const int cap = nz_max_blocks(nit, w8);
     int64_t nb = (NBT + 255) / 256;
     if (const int f = plan_override().w4nz_wg) nb = (NBT + f - 1) / f;  // debug override: a workgroup count
     if (nb > cap) nb = cap;
@@ -272,43 +349,45 @@ NzPlan nz_plan(const WqbmmArgs& p) {
     return z;
 }
 
-template <int DT, int NB, int NIT, bool OFF>
+template <int DT, int NB, int NIT, bool OFF, bool W8>
 hipError_t launch_nz_k(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
-    if constexpr (NB <= nz_max_blocks(NIT)) {
+    if constexpr (NB <= nz_max_blocks(NIT, W8)) {
         const dim3 grid((uint32_t)(z.nwg * z.nrb)), block((uint32_t)(64 * z.nwave));
-        w4nz_decode<DT, NB, NIT, OFF><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
+        w4nz_decode<DT, NB, NIT, OFF, W8><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;  // not planned (nz_plan caps NB by nz_max_blocks)
 }
 
-template <int DT, int NB, bool OFF>
+template <int DT, int NB, bool OFF, bool W8>
 hipError_t launch_nz_nit(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
     switch (z.nit) {
-    case 1: return launch_nz_k<DT, NB, 1, OFF>(p, z, stream);
-    case 2: return launch_nz_k<DT, NB, 2, OFF>(p, z, stream);
-    case 3: return launch_nz_k<DT, NB, 3, OFF>(p, z, stream);
-    case 4: return launch_nz_k<DT, NB, 4, OFF>(p, z, stream);
-    case 5: return launch_nz_k<DT, NB, 5, OFF>(p, z, stream);
-    case 6: return launch_nz_k<DT, NB, 6, OFF>(p, z, stream);
-    case 7: return launch_nz_k<DT, NB, 7, OFF>(p, z, stream);
-    default: return launch_nz_k<DT, NB, 8, OFF>(p, z, stream);
+    case 1: return launch_nz_k<DT, NB, 1, OFF, W8>(p, z, stream);
+    case 2: return launch_nz_k<DT, NB, 2, OFF, W8>(p, z, stream);
+    case 3: return launch_nz_k<DT, NB, 3, OFF, W8>(p, z, stream);
+    case 4: return launch_nz_k<DT, NB, 4, OFF, W8>(p, z, stream);
+    case 5: return launch_nz_k<DT, NB, 5, OFF, W8>(p, z, stream);
+    case 6: return launch_nz_k<DT, NB, 6, OFF, W8>(p, z, stream);
+    case 7: return launch_nz_k<DT, NB, 7, OFF, W8>(p, z, stream);
+    default: return launch_nz_k<DT, NB, 8, OFF, W8>(p, z, stream);
     }
 }
 
-template <int DT, bool OFF>
+template <int DT, bool OFF, bool W8>
 hipError_t launch_nz_nb(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
     switch (z.nb) {
-    case 1: return launch_nz_nit<DT, 1, OFF>(p, z, stream);
-    case 2: return launch_nz_nit<DT, 2, OFF>(p, z, stream);
-    case 3: return launch_nz_nit<DT, 3, OFF>(p, z, stream);
-    default: return launch_nz_nit<DT, 4, OFF>(p, z, stream);
+    case 1: return launch_nz_nit<DT, 1, OFF, W8>(p, z, stream);
+    case 2: return launch_nz_nit<DT, 2, OFF, W8>(p, z, stream);
+    case 3: return launch_nz_nit<DT, 3, OFF, W8>(p, z, stream);
+    default: return launch_nz_nit<DT, 4, OFF, W8>(p, z, stream);
     }
 }
 
 template <int DT>
 hipError_t launch_nz_dt(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
-    return p.offset ? launch_nz_nb<DT, true>(p, z, stream) : launch_nz_nb<DT, false>(p, z, stream);
+    if (p.w_dtype == QK_I8_NZ)
+        return p.offset ? launch_nz_nb<DT, true, true>(p, z, stream) : launch_nz_nb<DT, false, true>(p, z, stream);
+    return p.offset ? launch_nz_nb<DT, true, false>(p, z, stream) : launch_nz_nb<DT, false, false>(p, z, stream);
 }
 
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -317,6 +396,9 @@ int64_t grid_for(int64_t total) {
     int64_t blocks = (total + kNzThreads - 1) / kNzThreads;
     return blocks > 65536 ? 65536 : (blocks < 1 ? 1 : blocks);
 }
+
+// bytes of the ND form of an NZ weight
+size_t nd_weight_bytes(const WqbmmArgs& p) { return (size_t)(p.w_dtype == QK_I8_NZ ? p.K * p.N : p.K * p.N / 2); }
 
 }  // namespace
 
@@ -330,30 +412,46 @@ hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t 
     return hipGetLastError();
 }
 
-// NZ weights: the decode kernel where it applies (no workspace); otherwise the
-// weight is unpacked into the workspace and the row-major kernels run on it:
-// [QK_SPLIT_COUNTER_BYTES, unused][ND weight, K*N/2 B][row-major call's workspace].
+hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N, int8_t* dst, hipStream_t stream) {
+    const int64_t total = K * N / 16;
+    if (total == 0) return hipSuccess;
+    if (to_nz)
+        w8_nz_pack_kernel<<<dim3((uint32_t)grid_for(total)), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
+    else
+        w8_nz_unpack_kernel<<<dim3((uint32_t)grid_for(total)), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
+    return hipGetLastError();
+}
+
+// NZ weights (int4 QK_I4_NZ, int8 QK_I8_NZ): the decode kernel where it applies (no workspace);
+// otherwise the weight is unpacked into the workspace and the row-major kernels run on it:
+// [QK_SPLIT_COUNTER_BYTES, unused][ND weight][row-major call's workspace].
 size_t w4_nz_workspace(const WqbmmArgs& p) {
     if (!plan_override().w4nz_off && nz_plan(p).ok) return 0;
-    return QK_SPLIT_COUNTER_BYTES + round256((size_t)(p.K * p.N / 2)) +
-           weight_quant_bmm_workspace(p.M, p.N, p.K, QK_I32, p.group);
+    const int nd_dtype = p.w_dtype == QK_I8_NZ ? QK_I8 : QK_I32;
+    return QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(p)) +
+           weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group);
 }
 
 hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes, hipStream_t stream) {
     const NzPlan z = plan_override().w4nz_off ? NzPlan{false, 0, 0, 0, 0, 0} : nz_plan(p);
     if (z.ok)
         return p.x_dtype == QK_BF16 ? launch_nz_dt<QK_BF16>(p, z, stream) : launch_nz_dt<QK_F16>(p, z, stream);
-    const size_t nd_bytes = round256((size_t)(p.K * p.N / 2));
-    const size_t rest = weight_quant_bmm_workspace(p.M, p.N, p.K, QK_I32, p.group);
+    const bool w8 = p.w_dtype == QK_I8_NZ;
+    const int nd_dtype = w8 ? QK_I8 : QK_I32;
+    const size_t nd_bytes = round256(nd_weight_bytes(p));
+    const size_t rest = weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group);
     if (!workspace || ws_bytes < QK_SPLIT_COUNTER_BYTES + nd_bytes + rest || (uintptr_t)workspace % 256 != 0)
         return hipErrorInvalidValue;
     char* ws = static_cast<char*>(workspace);
-    int32_t* nd = reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES);
-    hipError_t e = launch_w4_nz_cast(static_cast<const int32_t*>(p.w), false, p.K, p.N, nd, stream);
+    void* nd = ws + QK_SPLIT_COUNTER_BYTES;
+    hipError_t e = w8 ? launch_w8_nz_cast(static_cast<const int8_t*>(p.w), false, p.K, p.N, static_cast<int8_t*>(nd),
+                                          stream)
+                      : launch_w4_nz_cast(static_cast<const int32_t*>(p.w), false, p.K, p.N, static_cast<int32_t*>(nd),
+                                          stream);
     if (e != hipSuccess) return e;
     WqbmmArgs q = p;
     q.w = nd;
-    q.w_dtype = QK_I32;
+    q.w_dtype = nd_dtype;
     return launch_weight_quant_bmm(q, rest ? ws + QK_SPLIT_COUNTER_BYTES + nd_bytes : nullptr, rest, stream);
 }
 

@@ -1606,7 +1606,7 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     p.x = p.scale = p.offset = p.out = (void*)(uintptr_t)256;
     p.w = (void*)(uintptr_t)256;
     if (p.group == 0) p.group = p.K;
-    if (w_dtype == QK_I4_NZ) return w4_nz_workspace(p);
+    if (w_dtype == QK_I4_NZ || w_dtype == QK_I8_NZ) return w4_nz_workspace(p);
     // [split-K counters][fp32 partials [nsplit][M][N]]
     const StreamPlan s = stream_plan(p);
     if (s.ok) return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
@@ -1621,7 +1621,7 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
     if (a.M == 0 || a.N == 0) return hipSuccess;
     WqbmmArgs p = a;
     if (p.group == 0) p.group = p.K;  // per channel == one group spanning K
-    if (p.w_dtype == QK_I4_NZ) return launch_w4_nz_bmm(p, workspace, ws_bytes, stream);
+    if (p.w_dtype == QK_I4_NZ || p.w_dtype == QK_I8_NZ) return launch_w4_nz_bmm(p, workspace, ws_bytes, stream);
     // a split workspace is [counters][partials]: the stream kernel finishes each strip in its last
     // split's workgroup (one counter per strip); the decode kernel uses the reduce kernel
     char* ws = static_cast<char*>(workspace);

@@ -215,6 +215,13 @@ bool is_w4_nz(const at::Tensor& w) {
     return w.scalar_type() == at::kInt && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 4;
 }
 
+// An int8 weight in the NZ layout: int8 [N/16, K/64, 64, 16].
+bool is_w8_nz(const at::Tensor& w) {
+    return w.scalar_type() == at::kChar && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 16;
+}
+
+bool is_nz(const at::Tensor& w) { return is_w4_nz(w) || is_w8_nz(w); }
+
 WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at::Tensor& antiquant_scale,
                          const std::optional<at::Tensor>& antiquant_offset,
                          const std::optional<at::Tensor>& quant_scale, const std::optional<at::Tensor>& quant_offset,
@@ -223,8 +230,9 @@ WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at
     TORCH_CHECK(x.scalar_type() == at::kHalf || x.scalar_type() == at::kBFloat16, op,
                 ": x must be float16 or bfloat16, got ", x.scalar_type());
     TORCH_CHECK(x.dim() >= 2, op, ": x must be at least 2-D, got ", x.dim());
-    const bool nz = is_w4_nz(weight);
-    TORCH_CHECK(weight.dim() == 2 || nz, op, ": weight must be 2-D (ND) or an int4 NZ weight [N/16, K/128, 64, 4], got ",
+    const bool nz = is_nz(weight);
+    TORCH_CHECK(weight.dim() == 2 || nz, op,
+                ": weight must be 2-D (ND) or an NZ weight (int4 [N/16, K/128, 64, 4], int8 [N/16, K/64, 64, 16]), got ",
                 weight.sizes());
     TORCH_CHECK(weight.scalar_type() == at::kInt || weight.scalar_type() == at::kChar, op,
                 ": weight must be int32 (int4 packed 8 per element) or int8, got ", weight.scalar_type());
@@ -232,7 +240,7 @@ WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at
                 ": quant_scale/quant_offset (int8 output) are not supported by this build");
     const bool int4 = weight.scalar_type() == at::kInt;
     const int64_t K = x.size(-1);
-    const int64_t wk = nz ? weight.size(1) * 128 : weight.size(0);
+    const int64_t wk = nz ? weight.size(1) * (int4 ? 128 : 64) : weight.size(0);
     TORCH_CHECK(wk == K, op, ": x last dim (", K, ") must equal the weight's K (", wk, ")");
     const int64_t N = nz ? weight.size(0) * 16 : (int4 ? weight.size(1) * 8 : weight.size(1));
     TORCH_CHECK(group >= 0, op, ": antiquant_group_size must be >= 0");
@@ -280,7 +288,7 @@ at::Tensor npu_weight_quant_batchmatmul(const at::Tensor& x_in, const at::Tensor
     at::Tensor off, b;
     if (antiquant_offset.has_value()) off = antiquant_offset->contiguous();
     if (bias.has_value()) b = bias->contiguous();
-    const int wdt = pl.nz ? QK_I4_NZ : (pl.int4 ? QK_I32 : QK_I8);
+    const int wdt = pl.nz ? (pl.int4 ? QK_I4_NZ : QK_I8_NZ) : (pl.int4 ? QK_I32 : QK_I8);
     size_t ws_bytes = 0;
     check_rc(qk_weight_quant_bmm_workspace_size(pl.M, pl.N, pl.K, wdt, pl.group, &ws_bytes),
              "npu_weight_quant_batchmatmul");
@@ -358,49 +366,64 @@ at::Tensor npu_convert_weight_to_int4pack_meta(const at::Tensor& weight, int64_t
 // ---------------------------------------------------------------- npu_format_cast
 
 // npu_format_cast(self, acl_format) for matmul weights: ND (2) <-> FRACTAL_NZ (29)
-// of an int4-packed int32 weight, the casts the reference applies to matmul
-// operands (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:303-316,
+// of an int4-packed int32 weight or an int8 weight, the casts the reference
+// applies to matmul operands (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:303-316,
 // op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:103-107).  A tensor
 // already in the requested format is returned as is.
-std::vector<int64_t> format_cast_shape(const at::Tensor& self, int64_t acl_format, bool* to_nz) {
+struct CastPlan {
+    bool identity, to_nz, int4;
+    int64_t K, N;
+    std::vector<int64_t> shape;
+};
+
+CastPlan format_cast_plan(const at::Tensor& self, int64_t acl_format) {
     const char* op = "npu_format_cast";
     TORCH_CHECK(acl_format == QK_FORMAT_ND || acl_format == QK_FORMAT_FRACTAL_NZ, op,
                 ": only ND (2) and FRACTAL_NZ (29) are supported, got ", acl_format);
-    TORCH_CHECK(self.scalar_type() == at::kInt, op,
-                ": only int4-packed int32 weights ([K, N/8] in ND) have an NZ layout, got ", self.scalar_type());
-    const bool nz = is_w4_nz(self);
-    TORCH_CHECK(nz || self.dim() == 2, op, ": expected an ND weight [K, N/8] or an NZ weight [N/16, K/128, 64, 4], got ",
-                self.sizes());
-    *to_nz = !nz && acl_format == QK_FORMAT_FRACTAL_NZ;
-    if (nz == (acl_format == QK_FORMAT_FRACTAL_NZ)) return self.sizes().vec();
-    if (*to_nz) {
-        TORCH_CHECK(self.size(0) % 128 == 0 && (self.size(1) * 8) % 16 == 0, op,
-                    ": FRACTAL_NZ needs K % 128 == 0 and N % 16 == 0, got [K, N/8] = ", self.sizes());
-        return nz_shape(self.size(0), self.size(1) * 8);
+    const bool int4 = self.scalar_type() == at::kInt;
+    TORCH_CHECK(int4 || self.scalar_type() == at::kChar, op,
+                ": only int4-packed int32 ([K, N/8]) and int8 ([K, N]) weights have an NZ layout, got ",
+                self.scalar_type());
+    const bool nz = is_nz(self);
+    TORCH_CHECK(nz || self.dim() == 2, op, ": expected an ND weight (2-D) or an NZ weight (4-D), got ", self.sizes());
+    CastPlan c{nz == (acl_format == QK_FORMAT_FRACTAL_NZ), !nz && acl_format == QK_FORMAT_FRACTAL_NZ, int4, 0, 0,
+               self.sizes().vec()};
+    const int64_t kq = int4 ? 128 : 64;
+    if (nz) {
+        c.N = self.size(0) * 16;
+        c.K = self.size(1) * kq;
+    } else {
+        c.K = self.size(0);
+        c.N = int4 ? self.size(1) * 8 : self.size(1);
     }
-    return {self.size(1) * 128, self.size(0) * 2};
+    if (c.identity) return c;
+    if (c.to_nz) {
+        TORCH_CHECK(c.K % kq == 0 && c.N % 16 == 0, op, ": FRACTAL_NZ needs K % ", kq, " == 0 and N % 16 == 0, got ",
+                    int4 ? "[K, N/8] = " : "[K, N] = ", self.sizes());
+        c.shape = int4 ? nz_shape(c.K, c.N) : std::vector<int64_t>{c.N / 16, c.K / 64, 64, 16};
+    } else {
+        c.shape = int4 ? std::vector<int64_t>{c.K, c.N / 8} : std::vector<int64_t>{c.K, c.N};
+    }
+    return c;
 }
 
 at::Tensor npu_format_cast(const at::Tensor& self, int64_t acl_format) {
-    bool to_nz = false;
-    auto shape = format_cast_shape(self, acl_format, &to_nz);
-    if (is_w4_nz(self) == (acl_format == QK_FORMAT_FRACTAL_NZ)) return self;
+    const CastPlan c = format_cast_plan(self, acl_format);
+    if (c.identity) return self;
     const c10::DeviceGuard guard(self.device());
     auto src = self.contiguous();
-    auto out = at::empty(shape, src.options());
-    const int64_t K = to_nz ? src.size(0) : src.size(1) * 128;
-    const int64_t N = to_nz ? src.size(1) * 8 : src.size(0) * 16;
-    check_rc(qk_weight_format_cast(src.data_ptr(), to_nz ? QK_FORMAT_ND : QK_FORMAT_FRACTAL_NZ, out.data_ptr(),
-                                   to_nz ? QK_FORMAT_FRACTAL_NZ : QK_FORMAT_ND, QK_I32, K, N, current_stream(src)),
+    auto out = at::empty(c.shape, src.options());
+    check_rc(qk_weight_format_cast(src.data_ptr(), c.to_nz ? QK_FORMAT_ND : QK_FORMAT_FRACTAL_NZ, out.data_ptr(),
+                                   c.to_nz ? QK_FORMAT_FRACTAL_NZ : QK_FORMAT_ND, c.int4 ? QK_I32 : QK_I8, c.K, c.N,
+                                   current_stream(src)),
              "npu_format_cast");
     return out;
 }
 
 at::Tensor npu_format_cast_meta(const at::Tensor& self, int64_t acl_format) {
-    bool to_nz = false;
-    auto shape = format_cast_shape(self, acl_format, &to_nz);
-    if (is_w4_nz(self) == (acl_format == QK_FORMAT_FRACTAL_NZ)) return self;
-    return at::empty(shape, self.options());
+    const CastPlan c = format_cast_plan(self, acl_format);
+    if (c.identity) return self;
+    return at::empty(c.shape, self.options());
 }
 
 // ---------------------------------------------------------------- quantize_per_tensor / _per_channel / dequantize

@@ -259,13 +259,13 @@ int weight_quant_bmm_run(const char* op, const void* x, int x_dtype, const void*
                          int out_dtype, void* (*scratch)(size_t need, size_t* bytes, int* rc), void* workspace,
                          size_t workspace_bytes, qk_stream_t stream) {
     if (!is_half(x_dtype)) return fail(QK_ERR_ARG, "%s: x must be float16 or bfloat16", op);
-    if (weight_dtype != QK_I32 && weight_dtype != QK_I8 && weight_dtype != QK_I4_NZ)
-        return fail(QK_ERR_ARG, "%s: weight must be int32 (packed int4), int8 or NZ int4", op);
+    if (weight_dtype != QK_I32 && weight_dtype != QK_I8 && weight_dtype != QK_I4_NZ && weight_dtype != QK_I8_NZ)
+        return fail(QK_ERR_ARG, "%s: weight must be int32 (packed int4), int8, or NZ int4 / int8", op);
     if (!is_half(scale_dtype)) return fail(QK_ERR_ARG, "%s: antiquant_scale must be float16 or bfloat16", op);
     if (!is_half(out_dtype)) return fail(QK_ERR_ARG, "%s: output must be float16 or bfloat16", op);
     if (M < 0 || N < 0 || K < 0 || group_size < 0) return fail(QK_ERR_ARG, "%s: negative size", op);
     if (weight_dtype == QK_I32 && N % 8 != 0) return fail(QK_ERR_ARG, "%s: int4 packing needs N %% 8 == 0 (N=%lld)", op, (long long)N);
-    if (weight_dtype == QK_I4_NZ && (N % 16 != 0 || K % 128 != 0))
+    if ((weight_dtype == QK_I4_NZ || weight_dtype == QK_I8_NZ) && (N % 16 != 0 || K % 128 != 0))
         return fail(QK_ERR_ARG, "%s: an NZ weight needs N %% 16 == 0 and K %% 128 == 0 (N=%lld K=%lld)", op,
                     (long long)N, (long long)K);
     if (group_size > 0 && K % group_size != 0)
@@ -373,21 +373,31 @@ int qk_weight_format_cast(const void* src, int src_format, void* dst, int dst_fo
                           int64_t N, qk_stream_t stream) {
     g_last_error.clear();
     const char* op = "npu_format_cast";
-    if (weight_dtype != QK_I32) return fail(QK_ERR_UNSUPPORTED, "%s: only int4-packed (int32) weights have an NZ layout", op);
+    if (weight_dtype != QK_I32 && weight_dtype != QK_I8)
+        return fail(QK_ERR_UNSUPPORTED, "%s: only int4-packed (int32) and int8 weights have an NZ layout", op);
     const bool to_nz = src_format == QK_FORMAT_ND && dst_format == QK_FORMAT_FRACTAL_NZ;
     const bool to_nd = src_format == QK_FORMAT_FRACTAL_NZ && dst_format == QK_FORMAT_ND;
     if (!to_nz && !to_nd)
         return fail(QK_ERR_UNSUPPORTED, "%s: cast %d -> %d is not supported (ND = %d <-> FRACTAL_NZ = %d)", op,
                     src_format, dst_format, QK_FORMAT_ND, QK_FORMAT_FRACTAL_NZ);
-    if (K < 0 || N < 0 || N % 16 != 0 || K % 128 != 0)
-        return fail(QK_ERR_ARG, "%s: NZ needs N %% 16 == 0 and K %% 128 == 0 (K=%lld N=%lld)", op, (long long)K, (long long)N);
+    const int64_t kq = weight_dtype == QK_I32 ? 128 : 64;
+    if (K < 0 || N < 0 || N % 16 != 0 || K % kq != 0)
+        return fail(QK_ERR_ARG, "%s: NZ needs N %% 16 == 0 and K %% %lld == 0 (K=%lld N=%lld)", op, (long long)kq,
+                    (long long)K, (long long)N);
     if (K * N == 0) return QK_OK;
     if (!src || !dst) return fail(QK_ERR_ARG, "%s: null pointer", op);
-    const uintptr_t bytes = (uintptr_t)(K * N / 2);
+    const uintptr_t bytes = (uintptr_t)(weight_dtype == QK_I32 ? K * N / 2 : K * N);
     if ((uintptr_t)src < (uintptr_t)dst + bytes && (uintptr_t)dst < (uintptr_t)src + bytes)
         return fail(QK_ERR_ARG, "%s: src and dst overlap", op);
-    return launched(qk::launch_w4_nz_cast(static_cast<const int32_t*>(src), to_nz, K, N, static_cast<int32_t*>(dst),
-                                          (hipStream_t)stream), op);
+    if (weight_dtype == QK_I8 && ((uintptr_t)src | (uintptr_t)dst) % 16 != 0)
+        return fail(QK_ERR_ARG, "%s: int8 weights must be 16-byte aligned", op);
+    const hipError_t e =
+        weight_dtype == QK_I32
+            ? qk::launch_w4_nz_cast(static_cast<const int32_t*>(src), to_nz, K, N, static_cast<int32_t*>(dst),
+                                    (hipStream_t)stream)
+            : qk::launch_w8_nz_cast(static_cast<const int8_t*>(src), to_nz, K, N, static_cast<int8_t*>(dst),
+                                    (hipStream_t)stream);
+    return launched(e, op);
 }
 
 int qk_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed, qk_stream_t stream) {

@@ -10,8 +10,8 @@ Importing this package loads ``_npu_ops.so``, which registers
   antiquant_group_size=0) -> Tensor``  (W4A16 / W8A16)
 * ``torch.ops.npu.npu_convert_weight_to_int4pack(weight, inner_k_tiles=0) -> Tensor``
   (``inner_k_tiles=4``: straight to the NZ layout)
-* ``torch.ops.npu.npu_format_cast(self, acl_format) -> Tensor``: an int4-packed weight between ND (2) and
-  FRACTAL_NZ (29), the MFMA-tiled layout ``npu_weight_quant_batchmatmul`` streams fastest
+* ``torch.ops.npu.npu_format_cast(self, acl_format) -> Tensor``: an int4-packed or int8 weight between ND (2)
+  and FRACTAL_NZ (29), the MFMA-tiled layouts ``npu_weight_quant_batchmatmul`` streams fastest
 * ``torch.ops.npu.quantize_per_tensor(self, scale, zero_point, dtype)``,
   ``torch.ops.npu.quantize_per_channel(self, scales, zero_points, axis, dtype)`` and
   ``torch.ops.npu.dequantize(self)``: the reference's static quantization ops (plain int8 / uint8 / int32
@@ -63,7 +63,7 @@ npu_rms_norm_dynamic_quant = torch.ops.npu.npu_rms_norm_dynamic_quant
 npu_swiglu_dynamic_quant = torch.ops.npu.npu_swiglu_dynamic_quant
 
 # qk_abi.h constants
-QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_U8, QK_I4_NZ = 1, 2, 3, 4, 5, 6, 16
+QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_U8, QK_I4_NZ, QK_I8_NZ = 1, 2, 3, 4, 5, 6, 16, 17
 ACL_FORMAT_ND, ACL_FORMAT_FRACTAL_NZ = 2, 29
 QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, -2, -3, -4
 
@@ -111,8 +111,10 @@ def abi() -> ctypes.CDLL:
 
 def get_npu_format(t: torch.Tensor) -> int:
     """Storage format of a matmul weight, as torch_npu.get_npu_format reports it:
-    FRACTAL_NZ (29) for an int4 NZ weight [N/16, K/128, 64, 4], ND (2) otherwise."""
-    nz = t.dtype == torch.int32 and t.dim() == 4 and t.shape[2] == 64 and t.shape[3] == 4
+    FRACTAL_NZ (29) for an NZ weight (int4 int32 [N/16, K/128, 64, 4], int8 [N/16, K/64, 64, 16]), ND (2)
+    otherwise."""
+    nz = t.dim() == 4 and t.shape[2] == 64 and ((t.dtype == torch.int32 and t.shape[3] == 4) or
+                                                 (t.dtype == torch.int8 and t.shape[3] == 16))
     return ACL_FORMAT_FRACTAL_NZ if nz else ACL_FORMAT_ND
 
 

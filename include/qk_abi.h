@@ -59,9 +59,11 @@ typedef enum {
     QK_I8 = 4,
     QK_I32 = 5,
     QK_U8 = 6,
-    /* weight code of qk_weight_quant_bmm: an int4 weight in the MFMA-tiled
-     * NZ layout that qk_weight_format_cast writes (int32 [N/16][K/128][64][4]) */
-    QK_I4_NZ = 16
+    /* weight codes of qk_weight_quant_bmm for weights in the MFMA-tiled NZ
+     * layouts that qk_weight_format_cast writes: int4, int32 [N/16][K/128][64][4];
+     * int8, int8 [N/16][K/64][64][16] */
+    QK_I4_NZ = 16,
+    QK_I8_NZ = 17
 } qk_dtype;
 
 /* Weight storage formats: the reference's aclFormat numbers for ND and
@@ -158,8 +160,8 @@ int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weig
  * is bmm (op_plugin/ops/base_ops/opapi/BmmKernelNpuOpApi.cpp:24-52).
  * x: [M,K] fp16/bf16 row-major.  weight: QK_I32 -> int4 packed [K, N/8]
  * (nibble i of word j is column 8j+i, two's complement); QK_I8 -> int8 [K,N];
- * QK_I4_NZ -> int4 in the NZ layout of qk_weight_format_cast (N % 16 == 0,
- * K % 128 == 0).
+ * QK_I4_NZ / QK_I8_NZ -> int4 / int8 in the NZ layouts of qk_weight_format_cast
+ * (N % 16 == 0, K % 128 == 0).
  * antiquant_scale / antiquant_offset: [K/group, N] (group_size > 0) or [N]
  * (group_size == 0, per channel), of scale_dtype (fp16/bf16); offset may be NULL.
  * bias: [N] or NULL.  out: [M,N] of out_dtype (fp16/bf16).
@@ -200,19 +202,21 @@ int qk_weight_quant_bmm_noalloc(const void* x, int x_dtype,
                                 void* out, int out_dtype, qk_stream_t stream);
 
 /*
- * npu_format_cast for an int4 matmul weight -- the MI355X counterpart of the
+ * npu_format_cast for a matmul weight -- the MI355X counterpart of the
  * FRACTAL_NZ casts the reference applies to matmul operands
  * (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:303-316,
  * op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:103-107), done once when
- * weights are loaded.  weight_dtype must be QK_I32 (int4 packed, [K, N/8] in
- * ND).  src_format -> dst_format is QK_FORMAT_ND -> QK_FORMAT_FRACTAL_NZ or
- * back; N % 16 == 0 and K % 128 == 0; src and dst must not overlap.
- * NZ layout, int32 [N/16][K/128][64][4]: element (k, n) is in word
+ * weights are loaded.  src_format -> dst_format is QK_FORMAT_ND ->
+ * QK_FORMAT_FRACTAL_NZ or back; N % 16 == 0; src and dst must not overlap.
+ * weight_dtype QK_I32 (int4 packed, [K, N/8] in ND; K % 128 == 0): NZ is int32
+ * [N/16][K/128][64][4]; element (k, n) is in word
  *   ((n/16 * (K/128) + k/128) * 64 + lane) * 4 + j,
  *   c = (k%128)/8, lane = n%16 + 16*(c%4), j = c/4,
  * at nibble i/2 for even i = k%8 and 4 + i/2 for odd i (two's complement).
- * One 1 KB block (16 columns x 128 k) is read by a wave as one 16-byte load
- * per lane, each word being one MFMA operand.  No workspace.
+ * weight_dtype QK_I8 ([K, N] in ND; K % 64 == 0): NZ is int8 [N/16][K/64][64][16];
+ * element (k, n) is byte ((n/16 * (K/64) + k/64) * 64 + n%16 + 16*((k%64)/16)) * 16 + k%16.
+ * Either way a 1 KB block (16 columns) is read by a wave as one 16-byte load
+ * per lane, each lane's bytes being its MFMA B operands.  No workspace.
  */
 int qk_weight_format_cast(const void* src, int src_format, void* dst, int dst_format, int weight_dtype,
                           int64_t K, int64_t N, qk_stream_t stream);

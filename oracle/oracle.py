@@ -46,6 +46,8 @@ def lib() -> ctypes.CDLL:
         L.qo_int4_unpack.argtypes = [P, I64, I64, P]
         L.qo_w4_nz_pack.argtypes = [P, I64, I64, P]
         L.qo_w4_nz_unpack.argtypes = [P, I64, I64, P]
+        L.qo_w8_nz_pack.argtypes = [P, I64, I64, P]
+        L.qo_w8_nz_unpack.argtypes = [P, I64, I64, P]
         L.qo_weight_quant_bmm.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P]
         L.qo_rms_norm.argtypes = [P, I, P, I64, I64, ctypes.c_double, P, P]
         L.qo_swiglu.argtypes = [P, I, I64, I64, P]
@@ -171,6 +173,23 @@ def w4_nz_unpack(nz: np.ndarray) -> np.ndarray:
     N, K = t.shape[0] * 16, t.shape[1] * 128
     out = np.empty((K, N // 8), dtype=np.int32)
     lib().qo_w4_nz_unpack(_p(t), K, N, _p(out))
+    return out
+
+
+def w8_nz_pack(w: np.ndarray) -> np.ndarray:
+    """int8 [K, N] -> int8 [N/16, K/64, 64, 16] (the int8 NZ layout)."""
+    nd = _c(w, np.int8)
+    K, N = nd.shape
+    out = np.empty((N // 16, K // 64, 64, 16), dtype=np.int8)
+    lib().qo_w8_nz_pack(_p(nd), K, N, _p(out))
+    return out
+
+
+def w8_nz_unpack(nz: np.ndarray) -> np.ndarray:
+    t = _c(nz, np.int8)
+    N, K = t.shape[0] * 16, t.shape[1] * 64
+    out = np.empty((K, N), dtype=np.int8)
+    lib().qo_w8_nz_unpack(_p(t), K, N, _p(out))
     return out
 
 

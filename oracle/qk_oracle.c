@@ -39,6 +39,8 @@
  *       words), hand-computed word/nibble positions of single nonzero
  *       elements, and the MFMA operand property the kernels rely on (the 8
  *       nibbles of one word are 8 consecutive k of one column, even k low).
+ *   qo_w8_nz_pack / unpack: round trip, hand-computed byte positions, and the
+ *       int8-MFMA operand property (a lane's 16 bytes are 16 consecutive k).
  *   qo_weight_quant_bmm: scale=1/offset=0 reduces to torch.matmul in float64;
  *       a hand-computed 1x2x128 example; linearity in x.
  *   qo_rms_norm: the reference's numpy closed form, restated in float64.
@@ -322,6 +324,29 @@ void qo_w4_nz_unpack(const int32_t* nz, int64_t K, int64_t N, int32_t* nd) {
             uint32_t v = ((uint32_t)nz[w] >> (4 * p)) & 0xfu;
             nd[k * NW + n / 8] = (int32_t)((uint32_t)nd[k * NW + n / 8] | (v << (4 * (n % 8))));
         }
+}
+
+/*
+ * The int8 counterpart (W8A8 and W8A16 weights): int8 [N/16][K/64][64][16].
+ * Weight element (k, n) is byte
+ *   ((n/16 * (K/64) + k/64) * 64 + lane) * 16 + k%16,  lane = n%16 + 16*((k%64)/16),
+ * so each lane's 16 bytes are 16 consecutive k of one column: the B operand of
+ * one v_mfma_i32_16x16x64_i8, or two 8-row bf16 MFMA operands.
+ */
+static inline int64_t nz8_byte(int64_t k, int64_t n, int64_t K) {
+    int64_t lane = n % 16 + 16 * ((k % 64) / 16);
+    return (((n / 16) * (K / 64) + k / 64) * 64 + lane) * 16 + k % 16;
+}
+
+/* nd: int8 [K, N] row-major; nz: int8 [N/16][K/64][64][16]. */
+void qo_w8_nz_pack(const int8_t* nd, int64_t K, int64_t N, int8_t* nz) {
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) nz[nz8_byte(k, n, K)] = nd[k * N + n];
+}
+
+void qo_w8_nz_unpack(const int8_t* nz, int64_t K, int64_t N, int8_t* nd) {
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) nd[k * N + n] = nz[nz8_byte(k, n, K)];
 }
 
 /* ------------------------------------------------------------------ */

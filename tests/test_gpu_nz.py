@@ -180,3 +180,75 @@ def test_abi_nz_and_noalloc(ops, oracle):
         assert rc == 0, ops.last_error()
         torch.cuda.synchronize()
         _close(out, ref, torch.bfloat16)
+
+
+# ----------------------------------------------------------------------------- int8 NZ (W8A16)
+
+def _w8(M, N, K, group, offset, x_dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((M, K), generator=g).to(x_dtype)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    ng = K // group if group > 0 else 1
+    scale = (5e-4 + 2.5e-3 * torch.rand((ng, N), generator=g)).to(torch.float16)
+    off = (8 * torch.rand((ng, N), generator=g) - 4).to(torch.float16) if offset else None
+    if group == 0:
+        scale = scale.reshape(-1)
+        off = None if off is None else off.reshape(-1)
+    return dict(x=x, w=w, scale=scale, offset=off)
+
+
+def _w8_ref(oracle, d, group, x_dtype, bias=None):
+    return oracle.weight_quant_bmm(W.bits(d["x"]), CODE[x_dtype], d["w"].numpy(), W.bits(d["scale"]),
+                                   None if d["offset"] is None else W.bits(d["offset"]), F16, group,
+                                   bias=None if bias is None else W.bits(bias), bias_dtype=CODE[x_dtype],
+                                   out_dtype=CODE[x_dtype])
+
+
+def test_format_cast_int8_device_matches_oracle(ops, oracle):
+    say("npu_format_cast int8 ND <-> NZ, K=192 N=80")
+    g = torch.Generator().manual_seed(12)
+    w = torch.randint(-128, 128, (192, 80), generator=g, dtype=torch.int8)
+    got = ops.npu_format_cast(w.to(DEV), 29)
+    assert got.shape == (5, 3, 64, 16) and ops.get_npu_format(got) == 29
+    assert np.array_equal(got.cpu().numpy(), oracle.w8_nz_pack(w.numpy()))
+    assert torch.equal(ops.npu_format_cast(got, 2).cpu(), w)
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,bias", [
+    (16, 11008, 4096, 128, True, torch.bfloat16, False),   # the cfg3 shape with int8 weights
+    (1, 4096, 4096, 128, True, torch.float16, True),
+    (16, 768, 512, 0, True, torch.bfloat16, True),         # per channel
+    (33, 512, 1024, 256, False, torch.bfloat16, False),    # three row blocks, 256-row groups
+    (4, 144, 8192, 128, True, torch.float16, False),       # four superblocks per wave: one block per workgroup
+    (3, 48, 384, 128, True, torch.bfloat16, True),         # three waves
+    # fallbacks (unpacked to ND in the workspace)
+    (7, 2048, 1024, 64, False, torch.bfloat16, False),     # 64-row groups
+    (80, 256, 512, 128, True, torch.float16, False),       # M > 64
+])
+def test_w8a16_nz_shapes(ops, oracle, M, N, K, group, offset, x_dtype, bias):
+    say(f"w8a16 NZ M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    d = _w8(M, N, K, group, offset, x_dtype, seed=M + N + K)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(6)).to(x_dtype) if bias else None
+    nz = ops.npu_format_cast(d["w"].to(DEV), 29)
+    out = ops.npu_weight_quant_batchmatmul(
+        d["x"].to(DEV), nz, d["scale"].to(DEV), None if d["offset"] is None else d["offset"].to(DEV),
+        bias=None if b is None else b.to(DEV), antiquant_group_size=group)
+    _close(out, _w8_ref(oracle, d, group, x_dtype, bias=b), x_dtype)
+
+
+def test_abi_w8_nz(ops, oracle):
+    say("ABI qk_weight_quant_bmm QK_I8_NZ M=16 N=1024 K=2048")
+    L = ops.abi()
+    d = _w8(16, 1024, 2048, 128, True, torch.bfloat16, seed=13)
+    nz = ops.npu_format_cast(d["w"].to(DEV), 29)
+    x, sc, off = d["x"].to(DEV), d["scale"].to(DEV), d["offset"].to(DEV)
+    ws = ctypes.c_size_t(1)
+    assert L.qk_weight_quant_bmm_workspace_size(16, 1024, 2048, ops.QK_I8_NZ, 128, ctypes.byref(ws)) == 0
+    assert ws.value == 0
+    out = torch.empty(16, 1024, dtype=torch.bfloat16, device=DEV)
+    rc = L.qk_weight_quant_bmm(x.data_ptr(), BF16, nz.data_ptr(), ops.QK_I8_NZ, sc.data_ptr(), off.data_ptr(), F16,
+                               16, 1024, 2048, 128, None, 0, out.data_ptr(), BF16, None, 0,
+                               torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ops.last_error()
+    torch.cuda.synchronize()
+    _close(out, _w8_ref(oracle, d, 128, torch.bfloat16), torch.bfloat16)

@@ -84,7 +84,8 @@ def test_abi_refuses_bad_arguments_without_launch():
                                None, 0, None)
     assert rc == q.QK_ERR_ARG and "N % 16" in q.last_error()
     nd, nz = q.ACL_FORMAT_ND, q.ACL_FORMAT_FRACTAL_NZ
-    assert L.qk_weight_format_cast(fake, nd, fake, nz, I8, 128, 16, None) == q.QK_ERR_UNSUPPORTED
+    assert L.qk_weight_format_cast(fake, nd, fake, nz, F16, 128, 16, None) == q.QK_ERR_UNSUPPORTED
+    assert L.qk_weight_format_cast(fake, nd, fake, nz, I8, 96, 16, None) == q.QK_ERR_ARG
     assert L.qk_weight_format_cast(fake, nd, fake, 3, I32, 128, 16, None) == q.QK_ERR_UNSUPPORTED
     assert L.qk_weight_format_cast(fake, nd, fake, nz, I32, 100, 16, None) == q.QK_ERR_ARG
     assert L.qk_weight_format_cast(ctypes.c_void_p(4096), nd, ctypes.c_void_p(4096 + 512), nz, I32, 128, 16,
@@ -138,6 +139,10 @@ def test_meta_shapes():
     nzw = q.npu_format_cast(_m((4096, 1376), torch.int32), 29)
     assert nzw.shape == (688, 32, 64, 4) and q.get_npu_format(nzw) == 29
     assert q.npu_format_cast(nzw, 2).shape == (4096, 1376) and q.npu_format_cast(nzw, 29) is nzw
+    w8z = q.npu_format_cast(_m((4096, 11008), torch.int8), 29)
+    assert w8z.shape == (688, 64, 64, 16) and q.get_npu_format(w8z) == 29
+    assert q.npu_weight_quant_batchmatmul(_m((16, 4096), torch.bfloat16), w8z, _m((32, 11008), torch.float16),
+                                          antiquant_group_size=128).shape == (16, 11008)
     assert q.quantize_per_tensor(_m((3, 8), torch.float16), 0.1, 2, torch.quint8).dtype == torch.uint8
     qq = q.quantize_per_channel(_m((3, 8), torch.bfloat16), _m((8,), torch.float64), _m((8,), torch.int64), -1,
                                 torch.qint32)
@@ -193,7 +198,8 @@ def test_meta_shapes():
                                     torch.qint8), "1-D"),
     (lambda: q.dequantize(_m((4,), torch.float32)), "int8, uint8 or int32"),
     (lambda: q.npu_format_cast(_m((128, 2), torch.int32), 3), "only ND"),
-    (lambda: q.npu_format_cast(_m((128, 16), torch.int8), 29), "int4-packed"),
+    (lambda: q.npu_format_cast(_m((128, 16), torch.float16), 29), "int4-packed"),
+    (lambda: q.npu_format_cast(_m((96, 16), torch.int8), 29), "K % 64"),
     (lambda: q.npu_weight_quant_batchmatmul(_m((2, 256), torch.bfloat16), _m((1, 1, 64, 4), torch.int32),
                                             _m((1, 16), torch.float16), antiquant_group_size=128), "weight's K"),
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((64,), torch.float16)), "dtype of self"),

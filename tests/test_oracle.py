@@ -244,6 +244,36 @@ def test_w4_nz_round_trip_and_operand_property(oracle):
                         assert s4(d >> 16) == w[k0 + 2 * q + 1, n]
 
 
+@pytest.mark.parametrize("k,n,byte", [
+    (0, 0, 0), (15, 0, 15),                 # one lane's 16 consecutive k
+    (16, 0, 16 * 16),                       # next 16 k: lane 16
+    (63, 15, 63 * 16 + 15),                 # last byte of the first 1 KB block
+    (64, 0, 1024),                          # next 64 k: next block of the same columns (K = 192)
+    (0, 16, 3 * 1024),                      # next 16 columns after all of K
+    (100, 21, ((1 * 3 + 1) * 64 + 5 + 16 * 2) * 16 + 4),   # k%64 = 36: g 2, byte 4
+])
+def test_w8_nz_known_positions(oracle, k, n, byte):
+    K, N = 192, 32
+    w = np.zeros((K, N), dtype=np.int8)
+    w[k, n] = -77
+    nz = oracle.w8_nz_pack(w).ravel()
+    assert np.count_nonzero(nz) == 1 and nz[byte] == -77
+
+
+def test_w8_nz_round_trip_and_operand_property(oracle):
+    g = np.random.default_rng(5)
+    K, N = 256, 48
+    w = g.integers(-128, 128, size=(K, N), dtype=np.int8)
+    nz = oracle.w8_nz_pack(w)
+    assert nz.shape == (N // 16, K // 64, 64, 16)
+    assert np.array_equal(oracle.w8_nz_unpack(nz), w)
+    for b in range(N // 16):
+        for s in range(K // 64):
+            for lane in range(64):
+                k0, n = 64 * s + 16 * (lane // 16), 16 * b + lane % 16
+                assert np.array_equal(nz[b, s, lane], w[k0:k0 + 16, n])
+
+
 def test_w4a16_identity_scale_is_plain_matmul(oracle):
     g = torch.Generator().manual_seed(5)
     M, K, N, G = 3, 256, 16, 128
