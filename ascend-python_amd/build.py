@@ -1,10 +1,14 @@
 """Build recipe for the native parts of op_plugin_amd (run in-tree, no JIT cache).
 
-1. Every ``csrc/**/*.hip`` file is compiled for gfx950 with hipcc and linked
-   into ``op_plugin_amd/libqk_hip.so`` -- the C ABI of ``include/qk_abi.h``.
+1. Every ``csrc/**/*.hip`` file outside ``csrc/calib`` is compiled for gfx950
+   with hipcc and linked into ``op_plugin_amd/libqk_hip.so`` -- the C ABI of
+   ``include/qk_abi.h``.
 2. ``csrc/ops/npu_quant_ops.cpp`` (torch.ops.npu.* registration) is compiled
    with the host C++ compiler against torch's headers and linked against
    ``libqk_hip.so`` into ``op_plugin_amd/_npu_ops.so``.
+3. ``csrc/calib/calibrate.hip`` (roofline calibration kernels for
+   ``bench.py --calibrate``; not part of the op path) becomes
+   ``op_plugin_amd/libqk_calib.so``.
 
 Usage: ``python ascend-python_amd/build.py`` (or ``__graft_entry__.build()``).
 """
@@ -54,7 +58,8 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 def build_hip(verbose: bool = False, jobs: int = 8) -> str:
     os.makedirs(OBJ, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "**", "*.hip"), recursive=True))
+    srcs = sorted(s for s in glob.glob(os.path.join(CSRC, "**", "*.hip"), recursive=True)
+                  if os.sep + "calib" + os.sep not in s)
     objs = [os.path.join(OBJ, os.path.relpath(s, CSRC).replace(os.sep, "_") + ".o") for s in srcs]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-c", s, "-o", o], verbose) for s, o in zip(srcs, objs)]
@@ -87,9 +92,18 @@ def build_ops(verbose: bool = False) -> str:
     return out
 
 
+def build_calib(verbose: bool = False) -> str:
+    lib = os.path.join(PKG, "libqk_calib.so")
+    tmp = lib + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-o", tmp, os.path.join(CSRC, "calib", "calibrate.hip")], verbose)
+    os.replace(tmp, lib)
+    return lib
+
+
 def build(verbose: bool = False) -> None:
     build_hip(verbose)
     build_ops(verbose)
+    build_calib(verbose)
 
 
 if __name__ == "__main__":

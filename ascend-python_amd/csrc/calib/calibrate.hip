@@ -1,0 +1,92 @@
+// Roofline calibration kernels (measurement only; not part of the op path or
+// of libqk_hip.so's C ABI).  bench.py --calibrate times them to give the
+// ceilings the kernels of this library are judged against on the same box:
+//
+//  calib_mfma_i8     the int8 MFMA issue ceiling: every wave issues
+//                    v_mfma_i32_16x16x64_i8 back to back on register
+//                    operands (8 independent accumulators, no memory
+//                    traffic), with constant or pseudo-random operand bits
+//                    (the clock of this part is power-limited by the bits
+//                    the MFMA unit toggles).
+//  calib_stream_read the HBM read ceiling of one launch: every thread issues
+//                    its 16-byte loads of a buffer up front and folds them
+//                    into one word (so the loads are not removed).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t mix(uint32_t x) {  // a 32-bit integer hash (xorshift-multiply)
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+__global__ __launch_bounds__(512) void calib_mfma_i8(int64_t iters, int random, int32_t* out) {
+    const uint32_t seed = (blockIdx.x * blockDim.x + threadIdx.x) * 16u + 1u;
+    i32x4 a[4], b[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[i][e] = random ? (int32_t)mix(seed + 4 * i + e) : 0x01010101;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b[i][e] = random ? (int32_t)mix(seed + 100 + 4 * i + e) : 0x01010101;
+    i32x4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = (i32x4){0, 0, 0, 0};
+    for (int64_t it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[j & 3], b[j >> 2], acc[j], 0, 0, 0);
+    }
+    int32_t s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s ^= acc[j][0] ^ acc[j][1] ^ acc[j][2] ^ acc[j][3];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// PER: 16-byte loads per thread, all issued before the first use.
+template <int PER>
+__global__ __launch_bounds__(1024) void calib_stream_read(const u32x4* __restrict__ buf, int64_t n16,
+                                                          uint32_t* out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    u32x4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int64_t idx = t + i * stride;
+        v[i] = idx < n16 ? buf[idx] : (u32x4){0u, 0u, 0u, 0u};
+    }
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) s ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+    out[t] = s;
+}
+
+}  // namespace
+
+extern "C" {
+
+// grid x 512 threads, each wave issuing iters x 8 MFMAs; out holds grid*512 words.
+int qk_calib_mfma_i8(int grid, int64_t iters, int random, int32_t* out, hipStream_t stream) {
+    calib_mfma_i8<<<dim3((uint32_t)grid), dim3(512), 0, stream>>>(iters, random, out);
+    return (int)hipGetLastError();
+}
+
+// bytes (a multiple of 16) read by `grid` workgroups of 1024 threads, 8 loads each in flight
+// (the grid must cover the buffer: grid * 1024 * 8 * 16 >= bytes); out holds grid*1024 words.
+int qk_calib_stream_read(const void* buf, int64_t bytes, int grid, uint32_t* out, hipStream_t stream) {
+    const int64_t n16 = bytes / 16;
+    if ((int64_t)grid * 1024 * 8 < n16) return -1;
+    calib_stream_read<8><<<dim3((uint32_t)grid), dim3(1024), 0, stream>>>(static_cast<const u32x4*>(buf), n16, out);
+    return (int)hipGetLastError();
+}
+
+}  // extern "C"

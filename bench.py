@@ -53,6 +53,9 @@ def parse():
     ap.add_argument("--no-configs", action="store_true", help="skip timing the other BASELINE configs")
     ap.add_argument("--configs-only", action="store_true",
                     help="time only the other BASELINE configs (for a kernel trace of them alone)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="time only the roofline calibration kernels (int8 MFMA issue ceiling with constant and "
+                         "random operands, streaming read of 24 MB) and the launch floor, and print them")
     ap.add_argument("--min-launches", type=int, default=100,
                     help="launches timed per kernel (median over runs of back-to-back launches)")
     return ap.parse_args()
@@ -187,6 +190,53 @@ def timing_note(t: dict) -> str:
             f"run range {t['min_s'] * 1e6:.2f}-{t['max_s'] * 1e6:.2f} us")
 
 
+def calibrate(dev, min_launches: int) -> dict:
+    """Ceilings of this box for the roofline figures: the int8 MFMA issue rate with register operands (constant
+    and pseudo-random bits: the clock is power-limited by the bits the MFMA unit toggles), the read rate of
+    one launch streaming a buffer of the cfg3 decode weight's size, a device copy, and the launch-to-launch
+    floor of an empty kernel.  Kernels: op_plugin_amd/libqk_calib.so (measurement only)."""
+    import ctypes
+    import torch
+    from op_plugin_amd import LIB_PATH
+    L = ctypes.CDLL(os.path.join(os.path.dirname(LIB_PATH), "libqk_calib.so"))
+    L.qk_calib_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    L.qk_calib_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    st = torch.cuda.current_stream().cuda_stream
+    pa = torch.randn((4096, 4096), device=dev).bfloat16()
+
+    def prime():
+        for _ in range(4):
+            torch.mm(pa, pa)
+
+    res = {}
+    grid, iters = 256, 2048  # 256 x 8 waves x 2048 x 8 MFMAs = 268M ops per wave-iteration set
+    out = torch.empty(grid * 512, dtype=torch.int32, device=dev)
+    ops = grid * 8 * iters * 8 * 2 * 16 * 16 * 64
+    for name, rnd in (("mfma_i8_constant", 0), ("mfma_i8_random", 1)):
+        t = launch_runs(lambda i: L.qk_calib_mfma_i8(grid, iters, rnd, out.data_ptr(), st), 4, 16, prime)
+        res[name] = {"TOPS": round(ops / t["s"] / 1e12, 1), "frac_of_5000": round(ops / t["s"] / 1e12 / PEAK_I8_TOPS, 4),
+                     "us": round(t["s"] * 1e6, 1)}
+    nbytes = 24436736 // 16 * 16
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(24)]
+    for b in bufs:
+        b.random_(0, 256)
+    sgrid = (nbytes // 16 + 1024 * 8 - 1) // (1024 * 8)
+    sout = torch.empty(sgrid * 1024, dtype=torch.int32, device=dev)
+    t = launch_runs(lambda i: L.qk_calib_stream_read(bufs[i % 24].data_ptr(), nbytes, sgrid, sout.data_ptr(), st),
+                    24, min_launches, prime)
+    res["stream_read_24MB"] = {"us": round(t["s"] * 1e6, 2), "GB/s": round(nbytes / t["s"] / 1e9, 1),
+                               "frac_of_8000": round(nbytes / t["s"] / 1e9 / PEAK_HBM_GBS, 4),
+                               "grid": f"{sgrid} x 1024 threads, 8 x 16-byte loads each in flight"}
+    dst = [torch.empty_like(bufs[0]) for _ in range(2)]
+    t = launch_runs(lambda i: dst[i % 2].copy_(bufs[i % 24]), 24, min_launches, prime)
+    res["device_copy_24MB"] = {"us": round(t["s"] * 1e6, 2), "GB/s_read_plus_write": round(2 * nbytes / t["s"] / 1e9, 1)}
+    one = torch.zeros(1, device=dev)
+    t = launch_runs(lambda i: one.fill_(i), 24, min_launches, prime)
+    res["launch_floor_us"] = round(t["s"] * 1e6, 2)
+    return res
+
+
 def other_configs(q, W, dev, min_launches: int) -> dict:
     """The remaining BASELINE configs, each timed on its own (time per op call, every kernel of the call).
 
@@ -279,6 +329,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.configs_only:
         print(json.dumps({"other_configs": other_configs(q, W, dev, args.min_launches)}), flush=True)
+        return
+    if args.calibrate:
+        print(json.dumps({"calibration": calibrate(dev, args.min_launches)}), flush=True)
         return
 
     # ---------------- cfg4 operands (set 0 = the seeded config inputs)
