@@ -346,7 +346,8 @@ hipError_t launch_dequantize(const void* q, int q_dtype, int64_t n, float* out, 
 hipError_t launch_int4_pack(const void* w, int w_dtype, int64_t K, int64_t N, int32_t* packed,
                             hipStream_t stream);
 
-// Quantized MLP block neighbours (x, gamma, h, y in the 16-bit dtype `dt`).
+// Quantized MLP block neighbours (x, gamma, h, y in the 16-bit dtype `dt`; launch_rms_norm also
+// takes QK_F32 without q).
 hipError_t launch_rms_norm(const void* x, int dt, const void* gamma, int64_t rows, int64_t D, float eps, void* y,
                            int8_t* q, float* scale, float* rstd, hipStream_t stream);
 hipError_t launch_swiglu(const void* h, int dt, int64_t rows, int64_t I, void* y, int8_t* q, float* scale,

@@ -1,5 +1,5 @@
 // RMSNorm and SwiGLU for the quantized MLP block, each alone or fused with
-// npu_dynamic_quant, on gfx950.
+// npu_dynamic_quant, on gfx950 (RMSNorm also in float32, unfused).
 //
 // One 256-thread workgroup (4 wave64) per row.  The row is read once with
 // 128-bit loads and kept in registers; row reductions (sum of squares,
@@ -155,6 +155,59 @@ __global__ __launch_bounds__(kThreads) void rms_norm_generic(const uint16_t* __r
         q[row * D + d] = (int8_t)quant_row(load_half_bits(yat(d), DT), rq);
 }
 
+// ---------------------------------------------------------------- RMSNorm, float32
+// The reference's golden case (fp32 x, gamma, y).  y = (x * rstd) * gamma stays
+// fp32.  Vector path: D % 4 == 0, 16-byte aligned rows, D <= 4 * 256 * VPT.
+template <int VPT>
+__global__ __launch_bounds__(kThreads) void rms_norm_f32_vec(const float* __restrict__ x,
+                                                             const float* __restrict__ gamma, int64_t D, float eps,
+                                                             float* __restrict__ y, float* __restrict__ rstd) {
+    const int64_t row = blockIdx.x;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * D);
+    const f32x4* gr = reinterpret_cast<const f32x4*>(gamma);
+    const int nv = (int)(D >> 2);
+    f32x4 v[VPT];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        if (idx < nv) {
+            v[i] = xr[idx];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(v[i][e], v[i][e], ss);
+        }
+    }
+    ss = block_sum(ss);
+    const float rs = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+    if (threadIdx.x == 0 && rstd) rstd[row] = rs;
+    f32x4* yr = reinterpret_cast<f32x4*>(y + row * D);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        if (idx < nv) {
+            const f32x4 g = gr[idx];
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = (v[i][e] * rs) * g[e];
+            yr[idx] = o;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void rms_norm_f32_generic(const float* __restrict__ x,
+                                                                 const float* __restrict__ gamma, int64_t D,
+                                                                 float eps, float* __restrict__ y,
+                                                                 float* __restrict__ rstd) {
+    const int64_t row = blockIdx.x;
+    const float* xr = x + row * D;
+    float ss = 0.0f;
+    for (int64_t d = threadIdx.x; d < D; d += kThreads) ss = __builtin_fmaf(xr[d], xr[d], ss);
+    ss = block_sum(ss);
+    const float rs = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+    if (threadIdx.x == 0 && rstd) rstd[row] = rs;
+    for (int64_t d = threadIdx.x; d < D; d += kThreads) y[row * D + d] = (xr[d] * rs) * gamma[d];
+}
+
 // ---------------------------------------------------------------- SwiGLU
 __device__ __forceinline__ float silu_mul(float a, float b) { return a / (1.0f + expf(-a)) * b; }
 
@@ -247,6 +300,21 @@ hipError_t rms_dispatch(const uint16_t* x, const uint16_t* g, int64_t rows, int6
     return hipGetLastError();
 }
 
+hipError_t rms_f32_dispatch(const float* x, const float* g, int64_t rows, int64_t D, float eps, float* y,
+                            float* rstd, hipStream_t stream) {
+    const dim3 grid((uint32_t)rows), block(kThreads);
+    const bool aligned = D % 4 == 0 && ((uintptr_t)x | (uintptr_t)g | (uintptr_t)y) % 16 == 0;
+    const int64_t per_thread = (D / 4 + kThreads - 1) / kThreads;
+    if (aligned && per_thread <= 16) {
+        if (per_thread <= 4) rms_norm_f32_vec<4><<<grid, block, 0, stream>>>(x, g, D, eps, y, rstd);
+        else if (per_thread <= 8) rms_norm_f32_vec<8><<<grid, block, 0, stream>>>(x, g, D, eps, y, rstd);
+        else rms_norm_f32_vec<16><<<grid, block, 0, stream>>>(x, g, D, eps, y, rstd);
+    } else {
+        rms_norm_f32_generic<<<grid, block, 0, stream>>>(x, g, D, eps, y, rstd);
+    }
+    return hipGetLastError();
+}
+
 template <int DT, int VPT>
 hipError_t swi_vec(const uint16_t* h, int64_t rows, int64_t I, uint16_t* y, int8_t* q, float* scale,
                    hipStream_t stream) {
@@ -277,6 +345,10 @@ hipError_t swi_dispatch(const uint16_t* h, int64_t rows, int64_t I, uint16_t* y,
 hipError_t launch_rms_norm(const void* x, int dt, const void* gamma, int64_t rows, int64_t D, float eps, void* y,
                            int8_t* q, float* scale, float* rstd, hipStream_t stream) {
     if (rows == 0) return hipSuccess;
+    if (dt == QK_F32)  // unfused only: the fused quantization takes 16-bit rows
+        return q ? hipErrorInvalidValue
+                 : rms_f32_dispatch(static_cast<const float*>(x), static_cast<const float*>(gamma), rows, D, eps,
+                                    static_cast<float*>(y), rstd, stream);
     const uint16_t* xh = static_cast<const uint16_t*>(x);
     const uint16_t* gh = static_cast<const uint16_t*>(gamma);
     uint16_t* yh = static_cast<uint16_t*>(y);

@@ -544,8 +544,9 @@ at::Tensor dequantize(const at::Tensor& self) {
 // rstd keeps the batch dims and has size 1 in the normalized ones
 // (op_plugin/utils/KernelNpuOutputSize.cpp:1514-1530).
 int64_t rms_norm_check(const char* op, const at::Tensor& self, const at::Tensor& gamma, bool quant) {
-    TORCH_CHECK(self.scalar_type() == at::kHalf || self.scalar_type() == at::kBFloat16, op,
-                ": self must be float16 or bfloat16, got ", self.scalar_type());
+    const auto st = self.scalar_type();
+    TORCH_CHECK(st == at::kHalf || st == at::kBFloat16 || (!quant && st == at::kFloat), op, ": self must be ",
+                quant ? "float16 or bfloat16" : "float16, bfloat16 or float32", ", got ", st);
     TORCH_CHECK(gamma.scalar_type() == self.scalar_type(), op, ": gamma must have the dtype of self (",
                 self.scalar_type(), "), got ", gamma.scalar_type());
     TORCH_CHECK(gamma.dim() >= 1 && gamma.dim() <= self.dim(), op, ": gamma must have 1..", self.dim(),

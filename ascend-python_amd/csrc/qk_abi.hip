@@ -457,8 +457,10 @@ int qk_dequantize(const void* q, int q_dtype, int64_t n, float* out, qk_stream_t
 }
 
 static int rms_common(const char* op, const void* x, int x_dtype, const void* gamma, int64_t rows, int64_t D,
-                      float eps, const void* out) {
-    if (!is_half(x_dtype)) return fail(QK_ERR_ARG, "%s: x must be float16 or bfloat16 (got dtype %d)", op, x_dtype);
+                      float eps, const void* out, bool allow_f32) {
+    if (!(is_half(x_dtype) || (allow_f32 && x_dtype == QK_F32)))
+        return fail(QK_ERR_ARG, "%s: x must be float16 or bfloat16%s (got dtype %d)", op, allow_f32 ? " or float32" : "",
+                    x_dtype);
     if (rows < 0 || D <= 0) return fail(QK_ERR_ARG, "%s: need rows >= 0 and D > 0 (rows=%lld D=%lld)", op, (long long)rows, (long long)D);
     if (!(eps >= 0.0f)) return fail(QK_ERR_ARG, "%s: epsilon must be >= 0", op);
     if (rows > 0 && (!x || !gamma || !out)) return fail(QK_ERR_ARG, "%s: null pointer", op);
@@ -470,7 +472,7 @@ int qk_rms_norm(const void* x, int x_dtype, const void* gamma, int64_t rows, int
                 float* rstd, qk_stream_t stream) {
     g_last_error.clear();
     const char* op = "npu_rms_norm";
-    if (int rc = rms_common(op, x, x_dtype, gamma, rows, D, eps, y)) return rc;
+    if (int rc = rms_common(op, x, x_dtype, gamma, rows, D, eps, y, true)) return rc;
     if (rows == 0) return QK_OK;
     return launched(qk::launch_rms_norm(x, x_dtype, gamma, rows, D, eps, y, nullptr, nullptr, rstd, (hipStream_t)stream), op);
 }
@@ -479,7 +481,7 @@ int qk_rms_norm_quant(const void* x, int x_dtype, const void* gamma, int64_t row
                       float* scale, float* rstd, qk_stream_t stream) {
     g_last_error.clear();
     const char* op = "npu_rms_norm_dynamic_quant";
-    if (int rc = rms_common(op, x, x_dtype, gamma, rows, D, eps, q)) return rc;
+    if (int rc = rms_common(op, x, x_dtype, gamma, rows, D, eps, q, false)) return rc;
     if (rows == 0) return QK_OK;
     if (!scale) return fail(QK_ERR_ARG, "%s: null pointer", op);
     return launched(qk::launch_rms_norm(x, x_dtype, gamma, rows, D, eps, nullptr, q, scale, rstd, (hipStream_t)stream), op);

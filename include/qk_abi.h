@@ -266,7 +266,8 @@ int qk_dequantize(const void* q, int q_dtype, int64_t n, float* out, qk_stream_t
  * npu_rms_norm -- replaces aclnnRmsNorm behind EXEC_NPU_CMD
  * (op_plugin/ops/base_ops/opapi/RmsNormKernelOpApi.cpp:24-35: y has the dtype
  * of x, :31; rstd is fp32, :32; schema op_plugin/config/v2r2/op_plugin_functions.yaml:2047).
- * x: [rows, D] fp16/bf16.  gamma: [D], same dtype.  y: [rows, D], x's dtype.
+ * x: [rows, D] fp16/bf16/fp32 (fp32 is the reference's golden case).  gamma:
+ * [D], same dtype.  y: [rows, D], x's dtype.
  * rstd: [rows] fp32 or NULL.  rstd = 1/sqrt(mean(x^2) + eps); y = x * rstd * gamma
  * (golden test/test_custom_ops/test_npu_rms_norm.py:10-17), fp32 arithmetic.
  */
@@ -277,7 +278,8 @@ int qk_rms_norm(const void* x, int x_dtype, const void* gamma, int64_t rows, int
  * RMSNorm followed by npu_dynamic_quant of its 16-bit output, in one pass
  * (the first two steps of the quantized MLP block).  No single reference op:
  * the unfused chain is qk_rms_norm then qk_dynamic_quant, and q / scale are
- * bit-identical to it.  q: [rows, D] int8.  scale: [rows] fp32.  rstd as above.
+ * bit-identical to it.  x: fp16/bf16 only (npu_dynamic_quant takes no fp32).
+ * q: [rows, D] int8.  scale: [rows] fp32.  rstd as above.
  */
 int qk_rms_norm_quant(const void* x, int x_dtype, const void* gamma, int64_t rows, int64_t D, float eps,
                       int8_t* q, float* scale, float* rstd, qk_stream_t stream);

@@ -50,6 +50,7 @@ def lib() -> ctypes.CDLL:
         L.qo_w8_nz_unpack.argtypes = [P, I64, I64, P]
         L.qo_weight_quant_bmm.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P]
         L.qo_rms_norm.argtypes = [P, I, P, I64, I64, ctypes.c_double, P, P]
+        L.qo_rms_norm_f32.argtypes = [P, P, I64, I64, ctypes.c_double, P, P]
         L.qo_swiglu.argtypes = [P, I, I64, I64, P]
         L.qo_cvt_array.argtypes = [P, I, P, I, I64]
         L.qo_quantize.argtypes = [P, I, I64, I64, I64, P, P, P, I]
@@ -253,6 +254,17 @@ def rms_norm(x_bits, x_dtype, gamma_bits, eps=1e-6):
     y = np.empty(x.shape, dtype=np.uint16)
     rstd = np.empty(x.shape[:-1] + (1,), dtype=np.float32)
     lib().qo_rms_norm(_p(x), x_dtype, _p(_c(gamma_bits, np.uint16)), rows, D, eps, _p(y), _p(rstd))
+    return y, rstd
+
+
+def rms_norm_f32(x, gamma, eps=1e-6):
+    """float32 RMSNorm (the reference's golden case): y float32 like x, rstd [..., 1] float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    D = x.shape[-1]
+    rows = x.size // D
+    y = np.empty(x.shape, dtype=np.float32)
+    rstd = np.empty(x.shape[:-1] + (1,), dtype=np.float32)
+    lib().qo_rms_norm_f32(_p(x), _p(np.ascontiguousarray(gamma, dtype=np.float32)), rows, D, eps, _p(y), _p(rstd))
     return y, rstd
 
 

@@ -43,7 +43,9 @@
  *       int8-MFMA operand property (a lane's 16 bytes are 16 consecutive k).
  *   qo_weight_quant_bmm: scale=1/offset=0 reduces to torch.matmul in float64;
  *       a hand-computed 1x2x128 example; linearity in x.
- *   qo_rms_norm: the reference's numpy closed form, restated in float64.
+ *   qo_rms_norm / qo_rms_norm_f32: the reference's numpy closed form, restated
+ *       in float64; pinned against torch.nn.functional.rms_norm (a library
+ *       routine) in float64 and a hand-computed row.
  *   qo_swiglu: torch.nn.functional.silu (a library routine) on float64.
  *   qo_quantize: torch.quantize_per_tensor / quantize_per_channel on the CPU
  *       (.int_repr(), library routines) for qint8 / quint8 / qint32 on random
@@ -409,6 +411,18 @@ void qo_weight_quant_bmm(const uint16_t* x, int x_dtype, const void* weight, int
  * golden in test/test_custom_ops/test_npu_rms_norm.py:10-17; carried in
  * float64 here, y rounded to the activation dtype, rstd to float32.
  */
+/* float32 x, gamma, y (the reference's golden case, test_npu_rms_norm.py:24-33), float64 arithmetic. */
+void qo_rms_norm_f32(const float* x, const float* gamma, int64_t rows, int64_t D, double eps, float* y,
+                     float* rstd) {
+    for (int64_t r = 0; r < rows; ++r) {
+        double ss = 0.0;
+        for (int64_t d = 0; d < D; ++d) ss += (double)x[r * D + d] * (double)x[r * D + d];
+        double rs = 1.0 / sqrt(ss / (double)D + eps);
+        rstd[r] = (float)rs;
+        for (int64_t d = 0; d < D; ++d) y[r * D + d] = (float)((double)x[r * D + d] * rs * (double)gamma[d]);
+    }
+}
+
 void qo_rms_norm(const uint16_t* x, int x_dtype, const uint16_t* gamma, int64_t rows, int64_t D,
                  double eps, uint16_t* y, float* rstd) {
     for (int64_t r = 0; r < rows; ++r) {

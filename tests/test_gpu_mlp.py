@@ -79,6 +79,29 @@ def test_rms_norm(ops, oracle, rows, D, dtype):
     np.testing.assert_allclose(rstd.cpu().numpy(), rr, rtol=1e-6)
 
 
+@pytest.mark.parametrize("rows,D,dist", [
+    (1024, 12288, "golden"),   # the reference's golden test shape and distribution
+    (7, 4096, "normal"),       # vector path, 4 per thread
+    (3, 1002, "normal"),       # D % 4 != 0: generic path
+    (2, 20000, "normal"),      # beyond the vector path
+])
+def test_rms_norm_f32(ops, oracle, rows, D, dist):
+    """float32 x / gamma / y (test/test_custom_ops/test_npu_rms_norm.py:24-33 runs float32, uniform(0, 100)).
+    Bar: rtol 1e-5 against the float64 oracle (the reference's assertRtolEqual allows 1e-4)."""
+    say(f"rms_norm float32 rows={rows} D={D} {dist}")
+    rng = np.random.default_rng(rows + D)
+    if dist == "golden":
+        x, gm = rng.uniform(0, 100, (rows, D)), rng.uniform(0, 100, D)
+    else:
+        x, gm = 3 * rng.standard_normal((rows, D)), 1 + 0.02 * rng.standard_normal(D)
+    x, gm = x.astype(np.float32), gm.astype(np.float32)
+    y, rstd = ops.npu_rms_norm(torch.from_numpy(x).to(DEV), torch.from_numpy(gm).to(DEV), 1e-6)
+    assert y.dtype == torch.float32 and rstd.dtype == torch.float32 and rstd.shape == (rows, 1)
+    ry, rr = oracle.rms_norm_f32(x, gm, 1e-6)
+    np.testing.assert_allclose(y.cpu().numpy(), ry, rtol=1e-5, atol=1e-30)
+    np.testing.assert_allclose(rstd.cpu().numpy(), rr, rtol=1e-6)
+
+
 def test_rms_norm_special_rows(ops, oracle):
     say("rms_norm zero row, huge row, 3-D input with 2-D gamma")
     x = torch.zeros((4, 64), dtype=torch.bfloat16)

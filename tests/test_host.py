@@ -102,6 +102,8 @@ def test_abi_refuses_bad_arguments_without_launch():
     assert L.qk_rms_norm(None, BF16, fake, 4, 64, 1e-6, fake, None, None) == q.QK_ERR_ARG
     assert L.qk_rms_norm(None, BF16, None, 0, 64, 1e-6, None, None, None) == q.QK_OK
     assert L.qk_rms_norm_quant(fake, BF16, fake, 4, 64, 1e-6, fake, None, None, None) == q.QK_ERR_ARG
+    assert L.qk_rms_norm_quant(fake, 3, fake, 4, 64, 1e-6, fake, fake, None, None) == q.QK_ERR_ARG
+    assert "float16 or bfloat16 (got" in q.last_error()   # float32 x: the fused quantization takes 16-bit rows
     assert L.qk_swiglu(fake, F16, -1, 8, fake, None) == q.QK_ERR_ARG
     assert L.qk_swiglu(None, F16, 3, 8, None, None) == q.QK_ERR_ARG and "null pointer" in q.last_error()
     assert L.qk_swiglu_quant(fake, BF16, 3, 0, fake, fake, None) == q.QK_ERR_ARG and "empty" in q.last_error()
@@ -156,6 +158,8 @@ def test_meta_shapes():
         and rstd.dtype == torch.float32
     y, rstd = q.npu_rms_norm(_m((3, 4, 8), torch.float16), _m((4, 8), torch.float16))   # 2-D gamma
     assert y.shape == (3, 4, 8) and rstd.shape == (3, 1, 1)
+    y, rstd = q.npu_rms_norm(_m((1024, 12288), torch.float32), _m((12288,), torch.float32))
+    assert y.dtype == torch.float32 and rstd.shape == (1024, 1)
     qq, sc, rstd = q.npu_rms_norm_dynamic_quant(_m((512, 4096), torch.bfloat16), _m((4096,), torch.bfloat16))
     assert qq.dtype == torch.int8 and qq.shape == (512, 4096) and sc.shape == (512,) and rstd.shape == (512, 1)
     assert q.npu_swiglu(_m((512, 28672), torch.bfloat16)).shape == (512, 14336)
@@ -205,6 +209,7 @@ def test_meta_shapes():
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((64,), torch.float16)), "dtype of self"),
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((32,), torch.bfloat16)), "trailing dims"),
     (lambda: q.npu_rms_norm_dynamic_quant(_m((4, 8, 8), torch.bfloat16), _m((8, 8), torch.bfloat16)), "1-D gamma"),
+    (lambda: q.npu_rms_norm_dynamic_quant(_m((4, 8), torch.float32), _m((8,), torch.float32)), "float16 or bfloat16"),
     (lambda: q.npu_swiglu(_m((4, 63), torch.bfloat16)), "even"),
     (lambda: q.npu_swiglu(_m((4, 64), torch.bfloat16), dim=0), "last dimension"),
     (lambda: q.npu_swiglu(_m((4, 64), torch.float32)), "float16 or bfloat16"),

@@ -340,6 +340,26 @@ def test_rms_norm_reference_closed_form(oracle):
     assert np.array_equal(y, W.bits(torch.from_numpy(ref).float().to(torch.bfloat16)))
 
 
+def test_rms_norm_f32_vs_torch_rms_norm(oracle):
+    """float32 RMSNorm against torch.nn.functional.rms_norm (a library routine) in float64, on the
+    reference's golden distribution (uniform(0, 100) x and gamma) and on signed data; and a row of
+    three values worked by hand: x = (3, 4, 0), mean(x^2) = 25/3, rstd = sqrt(3)/5."""
+    rng = np.random.default_rng(1)
+    for x, gm in [(rng.uniform(0, 100, (6, 384)), rng.uniform(0, 100, 384)),
+                  (rng.standard_normal((5, 96)) * 3, 1 + 0.02 * rng.standard_normal(96))]:
+        x, gm = x.astype(np.float32), gm.astype(np.float32)
+        y, rstd = oracle.rms_norm_f32(x, gm, 1e-6)
+        ref = torch.nn.functional.rms_norm(torch.from_numpy(x).double(), (x.shape[-1],),
+                                           torch.from_numpy(gm).double(), eps=1e-6)
+        assert np.array_equal(y, ref.float().numpy())
+        ms = (torch.from_numpy(x).double() ** 2).mean(-1, keepdim=True)
+        assert np.allclose(rstd, (1 / torch.sqrt(ms + 1e-6)).numpy(), rtol=1e-7)
+    y, rstd = oracle.rms_norm_f32(np.array([[3.0, 4.0, 0.0]], np.float32), np.array([1.0, 2.0, 5.0], np.float32), 0.0)
+    r = np.sqrt(3.0) / 5.0
+    assert rstd[0, 0] == np.float32(r)
+    assert np.array_equal(y[0], np.array([3 * r, 8 * r, 0.0], np.float32))
+
+
 def test_swiglu_vs_torch_silu(oracle):
     g = torch.Generator().manual_seed(9)
     h = (3 * torch.randn((4, 64), generator=g)).to(torch.bfloat16)
