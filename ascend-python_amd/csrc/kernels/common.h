@@ -282,6 +282,7 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   w4_gemm=force | nodma | off                     prefill kernels on few tiles / register-staged only / never
 //   w4_splits=<n>                                   K splits of the 32-row-block decode kernel
 //   qmm_dma=0                                       W8A8 prefill: register-staged kernel instead of the DMA one
+//   qmm_mid=0                                       W8A8 16 < M <= 256: split stream / tiled kernels instead of qmm_mid
 //   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
 //   w4nz=off                                        NZ int4 weights: unpack to ND and take the row-major kernels
 //   w4nz_wg=<n>                                     NZ decode kernel: workgroups along N
@@ -291,6 +292,7 @@ struct PlanOverride {
     int w4_gemm = 0;  // 0 planner, 1 force, 2 nodma, 3 off
     int w4_splits = 0;
     bool qmm_dma = true;
+    bool qmm_mid = true;
     int skinny_splits = 0;
     bool w4nz_off = false;
     int w4nz_wg = 0;

@@ -244,15 +244,51 @@ __device__ __forceinline__ void store_elem(void* out, int64_t o, int32_t acc, fl
 }
 }  // namespace big
 
+// The epilogue's per-column (scale, offset, bias) and per-row (per-token
+// scale) operands of one lane: columns n0 + wn*128 + 16j + (lane&15), rows
+// m0 + wm*16*TM + 16i + 4(lane>>4) + r.  bias holds the int32 bias, or the
+// fp32 bits of a float bias (0 = +0.0f when there is none).  Loaded apart from
+// the epilogue so a kernel can issue the loads long before the tile ends.
+template <int TM>
+struct EpiOps {
+    float sc[8], of[8];
+    uint32_t bias[8];
+    float pt[TM][4];
+};
+
+template <int TM>
+__device__ __forceinline__ void load_epi_ops(const QmmArgs& p, EpiOps<TM>& o, int64_t m0, int64_t n0, int wm,
+                                             int wn, int lane) {
+    const QmmEpilogue& e = p.epi;
+    const int fr = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t n = n0 + wn * 128 + 16 * j + fr;
+        const bool ok = n < p.N;
+        o.sc[j] = (ok && e.scale) ? e.scale[e.scale_per_ch ? n : 0] : 0.0f;
+        o.of[j] = (ok && e.offset) ? e.offset[e.offset_per_ch ? n : 0] : 0.0f;
+        o.bias[j] = 0u;
+        if (ok && e.bias_dtype == QK_I32) o.bias[j] = (uint32_t)((const int32_t*)e.bias)[n];
+        else if (ok && e.bias_dtype) o.bias[j] = __builtin_bit_cast(uint32_t, load_scalar(e.bias, n, e.bias_dtype));
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = m0 + wm * 16 * TM + 16 * i + 4 * g + r;
+            o.pt[i][r] = (e.pertoken && m < p.M) ? e.pertoken[m] : 1.0f;  // multiplying by 1.0 is exact
+        }
+}
+
 // The end of a 256x256 tile: exact int32 partials of a K split (FULL only), or
 // the fused epilogue; FULL 16-bit tiles are staged through LDS (smem must
 // hold BM x (2*BN + 16) bytes) so the global stores are 16-byte and
 // row-contiguous.  acc[i][j] holds rows wm*WMR + 16i + 4(lane>>4) + r, column
 // wn*128 + 16j + (lane&15) of the tile (the MFMA 16x16 output layout).
 template <int OUT, int TM, int NT, bool FULL>
-__device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc)[TM][8], int8_t* smem, int64_t m0,
-                                             int64_t n0, int wm, int wn, int lane, int tid, int split, int nsplit,
-                                             int32_t* __restrict__ partial) {
+__device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc)[TM][8], const EpiOps<TM>& ops,
+                                             int8_t* smem, int64_t m0, int64_t n0, int wm, int wn, int lane, int tid,
+                                             int split, int nsplit, int32_t* __restrict__ partial) {
     using namespace big;
     constexpr int WMR = 16 * TM;
     const int fr = lane & 15, g = lane >> 4;
@@ -269,20 +305,17 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
         return;
     }
 
-    // ---- epilogue: per-column and per-row operands loaded once per lane
+    // ---- epilogue
     const QmmEpilogue& e = p.epi;
-    float sc[8], bf[8], of[8];
+    const bool ibias = e.bias_dtype == QK_I32;
+    const float* sc = ops.sc;
+    const float* of = ops.of;
+    float bf[8];
     int32_t bi[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int64_t n = n0 + wn * 128 + 16 * j + fr;
-        const bool ok = n < p.N;
-        sc[j] = (ok && e.scale) ? e.scale[e.scale_per_ch ? n : 0] : 0.0f;
-        of[j] = (ok && e.offset) ? e.offset[e.offset_per_ch ? n : 0] : 0.0f;
-        bf[j] = 0.0f;
-        bi[j] = 0;
-        if (ok && e.bias_dtype == QK_I32) bi[j] = ((const int32_t*)e.bias)[n];
-        else if (ok && e.bias_dtype) bf[j] = load_scalar(e.bias, n, e.bias_dtype);
+        bi[j] = ibias ? (int32_t)ops.bias[j] : 0;
+        bf[j] = ibias ? 0.0f : __builtin_bit_cast(float, ops.bias[j]);
     }
     if constexpr (FULL && (OUT == QK_BF16 || OUT == QK_F16)) {
         // 16-bit outputs of a full tile are staged through LDS (the operand
@@ -296,7 +329,7 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = wm * WMR + 16 * i + 4 * g + r;
-                const float pt = e.pertoken ? e.pertoken[m0 + row] : 1.0f;
+                const float pt = ops.pt[i][r];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int32_t a = (int32_t)((uint32_t)acc[i][j][r] + (uint32_t)bi[j]);
@@ -326,8 +359,7 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
         for (int r = 0; r < 4; ++r) {
             const int64_t m = m0 + wm * WMR + 16 * i + 4 * g + r;
             const bool row_ok = m < p.M;
-            // pertoken multiply by 1.0 is exact, so "no pertoken" needs no branch
-            const float pt = (e.pertoken && row_ok) ? e.pertoken[m] : 1.0f;
+            const float pt = ops.pt[i][r];
             const int64_t ro = m * e.ldo + n0 + wn * 128 + fr;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -497,7 +529,9 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
         }
     }
 
-    big_epilogue<OUT, TM, NT, FULL>(p, acc, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
+    EpiOps<TM> ops;
+    if (!(FULL && nsplit > 1)) load_epi_ops<TM>(p, ops, m0, n0, wm, wn, lane);
+    big_epilogue<OUT, TM, NT, FULL>(p, acc, ops, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -686,8 +720,24 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
         __builtin_amdgcn_s_waitcnt(LGKM0);
     }
     bar();
+    // Some stages before the tile ends, each wave touches the cache lines of its epilogue operands
+    // (per-column scale and bias, per-row per-token scale) so the epilogue's loads of them hit the L2.
+    // The loaded word is only kept live to the end (no wait inside the loop).
+    float warm = 0.0f;
+    auto warm_up = [&]() {
+        if (nsplit != 1) return;
+        const QmmEpilogue& e = p.epi;
+        const int64_t n = n0 + 4 * lane, m = m0 + 4 * lane;  // 64 lanes x 16 B: 256 columns or rows
+        if (wave == 0 && e.scale && e.scale_per_ch) warm = e.scale[n];
+        else if (wave == 1 && e.pertoken) warm = e.pertoken[m];
+        else if (wave == 2 && e.bias_dtype) {
+            const int es = (e.bias_dtype == QK_F32 || e.bias_dtype == QK_I32) ? 4 : 2;
+            if (16 * lane < 256 * es) warm = *(const float*)((const char*)e.bias + n0 * es + 16 * lane);
+        }
+    };
     if (pg == 0) {
         for (int t0 = 0; t0 < nk; t0 += NST) {
+            if (t0 == nk - NST) warm_up();
 #pragma unroll
             for (int u = 0; u < NST; ++u) {
                 const int t = t0 + u;
@@ -717,7 +767,10 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     }
     // the trailing DMAs (past the last stage) land before the LDS is reused or released
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    big_epilogue<OUT, TM, NT, true>(p, acc, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
+    asm volatile("" ::"v"(warm));
+    EpiOps<TM> ops;
+    if (nsplit == 1) load_epi_ops<TM>(p, ops, m0, n0, wm, wn, lane);
+    big_epilogue<OUT, TM, NT, true>(p, acc, ops, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -852,6 +905,275 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
                 if (FINAL) qmm_store(p.epi, m, n, acc[i][j][r]);
                 else partial[((int64_t)split * p.M + m) * p.N + n] = acc[i][j][r];
             }
+}
+
+// ---------------------------------------------------------------------------
+// Mid-M kernel (16 < M <= 256, every K in one workgroup, no split partials):
+// a BM x BN output tile per workgroup of NW waves (BM = 16, 32 or 64; BN = 64,
+// or 128 for a [K,N] weight so each of its k rows is one whole 128-byte line),
+// so a few thousand output columns already give hundreds of workgroups.  K
+// goes in stages of 256 bytes through a ring of NST LDS stages filled by
+// direct global->LDS loads (buffer_load_dwordx4 ... lds), NST-1 stages in
+// flight; every wave issues a share of each stage's 1 KB load instructions
+// (a CU's fill rate from L2 grows with the number of waves issuing them).
+// Wave w multiplies K bytes 64(w%4)..64(w%4)+63 of every stage for column
+// group w/4 (BN/(NW/4) columns) into its own accumulators, and the four K
+// partials of each column group are added (exact int32) through LDS before
+// the epilogue.  Rows past M read as zeros (buffer range checks) and are not
+// stored.
+//   A stage [BM rows][256 B]:      chunk c of row r at r*256 + 16*(c ^ (r & 15))
+//   [N,K] weight [BN n][256 B]:    as A
+//   [K,N] weight [256 k][BN B]:    chunk c of row k at k*BN + 16*(c ^ h(k)),
+//       BN = 64:  h(k) = ((k>>2)&1) | ((k>>4)&1)<<1
+//       BN = 128: h(k) = ((k>>1)&3) | ((k>>4)&1)<<2
+// so the 16 rows of a fragment read (A, [N,K]) and the 16 k rows that two
+// 16-lane groups of one ds_read_b64_tr_b8 address ([K,N]) fall in distinct
+// banks.
+namespace md {
+constexpr int KS = 256;
+template <int BM, int BN, int NW, int RES>
+struct Cfg {  // RES: LDS bytes kept apart from the ring
+    static constexpr int NT = 64 * NW;
+    static constexpr int A_BYTES = BM * KS;
+    static constexpr int B_BYTES = BN * KS;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int NST = ((160 * 1024 - RES) / STAGE) > 8 ? 8 : ((160 * 1024 - RES) / STAGE);
+    static constexpr int A_DMA = BM / 4;              // 1 KB DMA instructions per stage (4 rows of A each)
+    static constexpr int DMA = A_DMA + BN / 4;        // + the weight's
+    static constexpr int PW_LO = DMA / NW;            // instructions per wave per stage: waves below
+    static constexpr int PW_HI = PW_LO + 1;           // DMA % NW issue PW_HI, the others PW_LO
+    static constexpr int NG = NW / 4;                 // column groups
+    static constexpr int NTJ = BN / 16 / NG;          // MFMA column tiles per wave
+    static constexpr int RED_ROW = BN + 4;            // int32 reduction rows, padded
+    static constexpr int RED_BYTES = 4 * BM * RED_ROW * 4;
+    static_assert(NW % 4 == 0 && NTJ >= 1 && NTJ * 16 * NG == BN, "waves cover the columns");
+    static_assert(NST >= 3, "at least two stages in flight");
+    static_assert(RED_BYTES <= NST * STAGE, "the reduction fits the ring");
+};
+template <int BN>
+__device__ __forceinline__ int hkn(int k) {
+    if constexpr (BN == 64) return ((k >> 2) & 1) | (((k >> 4) & 1) << 1);
+    else return ((k >> 1) & 3) | (((k >> 4) & 1) << 2);
+}
+}  // namespace md
+
+// 8 consecutive outputs of one row: the same float operations, in the same order, as qmm_store.
+template <int OUT>
+__device__ __forceinline__ void store8(const QmmEpilogue& e, int64_t m, int64_t n, const uint32_t (&s)[8]) {
+    float pt = 1.0f;
+    if (e.pertoken) pt = e.pertoken[m];
+    uint32_t q[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int64_t c = n + t;
+        int32_t acc = (int32_t)s[t];
+        float bf = 0.0f;
+        if (e.bias_dtype == QK_I32) acc = (int32_t)((uint32_t)acc + (uint32_t)((const int32_t*)e.bias)[c]);
+        else if (e.bias_dtype) bf = load_scalar(e.bias, c, e.bias_dtype);
+        const float sc = e.scale ? e.scale[e.scale_per_ch ? c : 0] : 0.0f;
+        if constexpr (OUT == QK_I32) {
+            q[t] = (uint32_t)acc;
+        } else if constexpr (OUT == QK_I8) {
+            const float off = e.offset ? e.offset[e.offset_per_ch ? c : 0] : 0.0f;
+            float v = __builtin_rintf(__builtin_fmaf((float)acc, sc, off));
+            v = fminf(fmaxf(v, -128.0f), 127.0f);
+            q[t] = (uint32_t)(uint8_t)(int8_t)(int)v;
+        } else {
+            const float v = __builtin_fmaf((float)acc * pt, sc, bf);
+            if constexpr (OUT == QK_BF16) q[t] = f32_to_bf16_bits(v);
+            else if constexpr (OUT == QK_F16) q[t] = f32_to_f16_bits(v);
+            else q[t] = __builtin_bit_cast(uint32_t, v);
+        }
+    }
+    const int64_t o = m * e.ldo + n;
+    if constexpr (OUT == QK_BF16 || OUT == QK_F16) {
+        *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(e.out) + o) =
+            (i32x4){(int32_t)(q[0] | q[1] << 16), (int32_t)(q[2] | q[3] << 16), (int32_t)(q[4] | q[5] << 16),
+                    (int32_t)(q[6] | q[7] << 16)};
+    } else if constexpr (OUT == QK_I8) {
+        *reinterpret_cast<u32x2*>(static_cast<int8_t*>(e.out) + o) =
+            (u32x2){q[0] | q[1] << 8 | q[2] << 16 | q[3] << 24, q[4] | q[5] << 8 | q[6] << 16 | q[7] << 24};
+    } else {
+        i32x4* d = reinterpret_cast<i32x4*>(static_cast<int32_t*>(e.out) + o);
+        d[0] = (i32x4){(int32_t)q[0], (int32_t)q[1], (int32_t)q[2], (int32_t)q[3]};
+        d[1] = (i32x4){(int32_t)q[4], (int32_t)q[5], (int32_t)q[6], (int32_t)q[7]};
+    }
+}
+
+template <bool B_KN, int BM, int BN, int NW, int PD, int OUT>
+__global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p, int tiles_m) {
+    constexpr int SCRATCH = PD > 0 ? 1024 : 0;  // the prefetch wave's landing block
+    using C = md::Cfg<BM, BN, NW, SCRATCH>;
+    constexpr int NST = C::NST, TMI = BM / 16, NTJ = C::NTJ, NT = C::NT;
+    static_assert(NST * C::STAGE + SCRATCH <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) int8_t smem[NST * C::STAGE + SCRATCH];
+
+    // logical tile id: consecutive ids (one XCD) share a column block, so the weight's lines are
+    // fetched once per XCD; the row blocks of a column block run side by side
+    const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int tm = bid % tiles_m, tn = bid / tiles_m;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int rows = (int)((p.M - m0) < BM ? (p.M - m0) : BM);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kq = wave & 3, cg = wave >> 2;  // K quarter of each stage, column group
+    const int fr = lane & 15, g = lane >> 4;
+
+    const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem;
+    const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)(B_KN ? p.sbk : p.sbn);
+    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.a + m0 * p.lda, (uint32_t)((rows - 1) * p.lda + p.K));
+    const __amdgpu_buffer_rsrc_t rsB = B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
+                                            : make_rsrc(p.b + n0 * p.sbn, (uint32_t)((BN - 1) * p.sbn + p.K));
+    // [row][256 B] DMA (A, [N,K] weight): an instruction covers rows 4b..4b+3; lane l -> row 4b + (l>>4),
+    // LDS chunk l&15, global chunk (l&15) ^ (row&15)
+    auto voff_rk = [&](int b, uint32_t ld) {
+        const int row = 4 * b + (lane >> 4);
+        return (uint32_t)row * ld + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+    };
+    // [k][BN B] DMA ([K,N] weight): an instruction covers 1024/BN k rows; lane l -> row b*(1024/BN) + l/(BN/16),
+    // LDS chunk l%(BN/16), global chunk (l%(BN/16)) ^ h(row)
+    auto voff_kn = [&](int b) {
+        constexpr int CPR = BN / 16;
+        const int row = b * (1024 / BN) + lane / CPR;
+        return (uint32_t)row * ldb + 16u * (uint32_t)((lane % CPR) ^ md::hkn<BN>(row));
+    };
+    const int nk = (int)(p.K / md::KS);
+    const bool hi = wave < C::DMA % NW;  // this wave issues PW_HI instructions per stage
+    auto issue = [&](int s) {  // stage s into buffer s % NST: instructions wave, wave+NW, ...
+        const uint32_t lds = sbase + (uint32_t)(s % NST) * C::STAGE;
+        const uint32_t k0 = (uint32_t)s * md::KS;
+#pragma unroll
+        for (int u = 0; u < C::PW_HI; ++u) {
+            const int q = wave + NW * u;
+            if (q >= C::DMA) break;
+            if (q < C::A_DMA) {
+                dma16(rsA, lds + q * 1024, voff_rk(q, lda), k0);
+            } else {
+                const int b = q - C::A_DMA;
+                if constexpr (B_KN) dma16(rsB, lds + C::A_BYTES + b * 1024, voff_kn(b), k0 * ldb);
+                else dma16(rsB, lds + C::A_BYTES + b * 1024, voff_rk(b, ldb), k0);
+            }
+        }
+    };
+
+    i32x4 acc[TMI][NTJ];
+#pragma unroll
+    for (int i = 0; i < TMI; ++i)
+#pragma unroll
+        for (int j = 0; j < NTJ; ++j) acc[i][j] = (i32x4){0, 0, 0, 0};
+
+    const int ck = 4 * kq + g;  // this lane's 16-byte K chunk of a stage row
+    // PD > 0: wave NW only runs ahead of the ring, loading stage s + PD of this workgroup's rows of A
+    // and its share (1 / tiles_m) of the weight block into one scratch KB of LDS nobody reads, so the
+    // ring's own loads of those lines later hit the L2.  It waits on nothing but its own loads at the end.
+    // The A rows are prefetched only by the workgroups of the first column block an XCD runs (the first
+    // tiles_m logical ids of each XCD's range), the weight block's rows split over its tiles_m row blocks.  The lead pd keeps the wave's outstanding loads under the 63 vmcnt can count,
+    // so it never stalls at an issue while the other waves wait for it at a barrier.
+    const bool pf_wave = PD > 0 && wave == NW;
+    const int per_xcd = (int)(gridDim.x >> 3);
+    const bool pf_a = per_xcd > 0 && (bid % per_xcd) < tiles_m;
+    const int pf_cnt = (pf_a ? C::A_DMA : 0) + (BN / 4 + tiles_m - 1) / tiles_m;
+    const int pd = min(PD, 56 / pf_cnt);
+    auto prefetch = [&](int s) {
+        const uint32_t lds = sbase + (uint32_t)(NST * C::STAGE);
+        const uint32_t k0 = (uint32_t)s * md::KS;
+        if (pf_a)
+            for (int q = 0; q < C::A_DMA; ++q) dma16(rsA, lds, voff_rk(q, lda), k0);
+        for (int b = tm; b < BN / 4; b += tiles_m) {
+            if constexpr (B_KN) dma16(rsB, lds, voff_kn(b), k0 * ldb);
+            else dma16(rsB, lds, voff_rk(b, ldb), k0);
+        }
+    };
+    if (pf_wave) {
+        for (int s = NST - 1; s < NST - 1 + pd && s < nk; ++s) prefetch(s);
+    } else {
+        for (int s = 0; s < NST - 1 && s < nk; ++s) issue(s);
+    }
+    for (int s = 0; s < nk; ++s) {
+        // stage s has landed once at most the later stages' instructions are outstanding
+        if (pf_wave) {
+        } else if (s + NST - 2 < nk) {
+            if (hi) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * C::PW_HI));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * C::PW_LO));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // stage s visible to every wave; every wave is done with stage s-1
+        __builtin_amdgcn_sched_barrier(0);
+        if (pf_wave) {
+            if (s + NST - 1 + pd < nk) prefetch(s + NST - 1 + pd);
+            continue;
+        }
+        if (s + NST - 1 < nk) issue(s + NST - 1);  // into the buffer of stage s-1
+        const int8_t* As = smem + (s % NST) * C::STAGE;
+        const int8_t* Bs = As + C::A_BYTES;
+        i32x4 af[TMI], bf[NTJ];
+#pragma unroll
+        for (int i = 0; i < TMI; ++i) {
+            const int r = 16 * i + fr;
+            af[i] = *reinterpret_cast<const i32x4*>(As + r * md::KS + 16 * (ck ^ (r & 15)));
+        }
+#pragma unroll
+        for (int jj = 0; jj < NTJ; ++jj) {
+            const int j = cg * NTJ + jj;  // column tile of the block
+            if constexpr (!B_KN) {
+                const int r = 16 * j + fr;
+                bf[jj] = *reinterpret_cast<const i32x4*>(Bs + r * md::KS + 16 * (ck ^ (r & 15)));
+            } else {
+                // lanes 2b / 2b+1 of each 16-lane group address k row 64kq + 16g + b (and +8), columns
+                // 16j..16j+7 / 16j+8..16j+15
+                const int k = 64 * kq + 16 * g + (fr >> 1);
+                const big::v2i lo = big::lds_tr8(Bs + k * BN + 16 * (j ^ md::hkn<BN>(k)) + 8 * (fr & 1));
+                const big::v2i hi8 = big::lds_tr8(Bs + (k + 8) * BN + 16 * (j ^ md::hkn<BN>(k + 8)) + 8 * (fr & 1));
+                bf[jj] = (i32x4){lo[0], lo[1], hi8[0], hi8[1]};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TMI; ++i)
+#pragma unroll
+            for (int jj = 0; jj < NTJ; ++jj)
+                acc[i][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[jj], acc[i][jj], 0, 0, 0);
+    }
+
+    // the four K partials of each column group -> LDS (the ring is free once every wave is past its
+    // last reads)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+    if (pf_wave) {  // the prefetch wave still passes the one barrier below
+        __syncthreads();
+        return;
+    }
+    int32_t* red = reinterpret_cast<int32_t*>(smem);
+#pragma unroll
+    for (int i = 0; i < TMI; ++i)
+#pragma unroll
+        for (int jj = 0; jj < NTJ; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[(kq * BM + 16 * i + 4 * g + r) * C::RED_ROW + 16 * (cg * NTJ + jj) + fr] = acc[i][jj][r];
+    __syncthreads();
+    // 8 consecutive outputs per thread-step: exact int32 sum of the four partials, then the epilogue
+    for (int q = tid; q < BM * BN / 8; q += NT) {
+        const int row = q / (BN / 8), c8 = 8 * (q % (BN / 8));
+        if (row >= rows) continue;
+        uint32_t s8[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s8[t] = 0u;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int32_t* src = red + (w * BM + row) * C::RED_ROW + c8;
+            const i32x4 a = *reinterpret_cast<const i32x4*>(src);
+            const i32x4 b = *reinterpret_cast<const i32x4*>(src + 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                s8[t] += (uint32_t)a[t];
+                s8[4 + t] += (uint32_t)b[t];
+            }
+        }
+        store8<OUT>(p.epi, m0 + row, n0 + c8, s8);
+    }
 }
 
 // Exact int32 sum of the split partials, then the common epilogue.
@@ -1045,8 +1367,89 @@ hipError_t launch_skinny(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial
 
 }  // namespace
 
+// Mid-M shapes (16 < M <= 128, or M <= 256 with N <= 8192 -- beyond that the 256x256 tiles move fewer
+// bytes per CU; N % 64 == 0, K % 256 == 0): qmm_mid, no workspace.  Column blocks of 128 for a [K,N]
+// weight whose N allows it (whole-line k rows), else 64; the row block (64, 32 or 16; 32 at most with
+// 128 columns) that moves the fewest operand bytes per CU.  A [K,N] weight with M <= 32 keeps the split
+// stream (measured faster there), so for M <= 32 the workspace query still reports the split stream's
+// workspace, which a [N,K] weight's qmm_mid launch leaves unused.  Eligibility from sizes only, so the
+// workspace query and the launch agree.
+struct MidPlan {
+    int bm = 0, bn = 0, tiles_m = 0, tiles = 0;
+};
+
+
+MidPlan mid_plan(int64_t M, int64_t N, int64_t K, bool b_kn) {
+    MidPlan m;
+    if (!plan_override().qmm_mid) return m;  // debug override: the split stream / tiled kernels instead
+    if (M <= 16 || M > 256 || (M > 128 && N > 8192) || N <= 0 || N % 64 != 0 || K <= 0 || K % md::KS != 0)
+        return m;
+    const int bn = (b_kn && N % 128 == 0) ? 128 : 64;
+    const int64_t tn = N / bn;
+    if (tn * ((M + 15) / 16) >= ((int64_t)1 << 30)) return m;
+    // the row block with the fewest operand bytes per CU: rounds of workgroups over the 256 CUs times
+    // each workgroup's (BM + BN) bytes per K byte (ties to the larger block)
+    int bm = 16;
+    int64_t best = -1;
+    for (int c : {64, 32, 16}) {
+        if (bn == 128 && c == 64) continue;
+        const int64_t rounds = (((M + c - 1) / c) * tn + 255) / 256;
+        const int64_t cost = rounds * (c + bn);
+        if (best < 0 || cost < best) {
+            best = cost;
+            bm = c;
+        }
+    }
+    m.bm = bm;
+    m.bn = bn;
+    m.tiles_m = (int)((M + bm - 1) / bm);
+    m.tiles = (int)(m.tiles_m * tn);
+    return m;
+}
+
+template <bool B_KN, int BM, int BN>
+hipError_t launch_mid_t(const QmmArgs& p, const MidPlan& mp, hipStream_t stream) {
+    // 8 waves; a prefetch wave 12 stages ahead for a [K,N] weight (measured: it shortens the [K,N]
+    // cfg1 shape by a sixth and lengthens the [N,K] one, whose 256-byte rows stream well without it)
+    constexpr int NW = 8, PD = B_KN ? 12 : 0;
+    const dim3 grid((uint32_t)mp.tiles), block(64 * NW + (PD > 0 ? 64 : 0));
+    switch (p.epi.out_dtype) {
+    case QK_BF16: qmm_mid<B_KN, BM, BN, NW, PD, QK_BF16><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
+    case QK_F16: qmm_mid<B_KN, BM, BN, NW, PD, QK_F16><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
+    case QK_F32: qmm_mid<B_KN, BM, BN, NW, PD, QK_F32><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
+    case QK_I8: qmm_mid<B_KN, BM, BN, NW, PD, QK_I8><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
+    default: qmm_mid<B_KN, BM, BN, NW, PD, QK_I32><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
+    }
+    return hipGetLastError();
+}
+
+template <bool B_KN>
+hipError_t launch_mid(const QmmArgs& p, const MidPlan& mp, hipStream_t stream) {
+    if constexpr (B_KN) {  // 128-column blocks only for a [K,N] weight
+        if (mp.bn == 128) {
+            if (mp.bm == 32) return launch_mid_t<B_KN, 32, 128>(p, mp, stream);
+            return launch_mid_t<B_KN, 16, 128>(p, mp, stream);
+        }
+    }
+    if (mp.bm == 64) return launch_mid_t<B_KN, 64, 64>(p, mp, stream);
+    if (mp.bm == 32) return launch_mid_t<B_KN, 32, 64>(p, mp, stream);
+    return launch_mid_t<B_KN, 16, 64>(p, mp, stream);
+}
+
+// The kernels that need no workspace and no alignment beyond the tiled kernels' (or none at all).
+hipError_t launch_qmm_fallback(const QmmArgs& p, bool a_ok, bool b_kn, bool b_nk, hipStream_t stream) {
+    if (p.K > 0 && a_ok && b_kn) return launch_by_m<true>(p, stream);
+    if (p.K > 0 && a_ok && b_nk) return launch_by_m<false>(p, stream);
+    const int64_t total = p.M * p.N;
+    int64_t blocks = (total + kThreads - 1) / kThreads;
+    if (blocks > 65536) blocks = 65536;
+    qmm_generic<<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(p);
+    return hipGetLastError();
+}
+
 // A split workspace is [split-K counters][int32 partials [nsplit][M][N]].
 size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K) {
+    if (mid_plan(M, N, K, false).bm != 0 && M > 32) return 0;  // the column block does not change eligibility
     const SkinnyPlan s = skinny_plan(M, N, K);
     if (s.mt != 0)
         return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
@@ -1063,6 +1466,18 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
     const bool b_kn16 = b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0;
     char* ws = static_cast<char*>(workspace);
     int32_t* partial = ws ? reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES) : nullptr;
+    const MidPlan mp = mid_plan(p.M, p.N, p.K, b_kn16);
+    if (mp.bm != 0 && (p.M > 32 || !b_kn16)) {
+        // direct-to-LDS loads need 16-byte aligned rows and 32-bit buffer offsets; the 8-output epilogue
+        // stores need 16-byte aligned output rows.  Otherwise the tiled kernels (no workspace) take it.
+        const int osz = p.epi.out_dtype == QK_I8 ? 1 : ((p.epi.out_dtype == QK_BF16 || p.epi.out_dtype == QK_F16) ? 2 : 4);
+        const bool ok = a_ok && (uint64_t)mp.bm * (uint64_t)p.lda < (1ull << 31) &&
+                        (uintptr_t)p.epi.out % 16 == 0 && (p.epi.ldo * osz) % 16 == 0 &&
+                        (b_kn16 ? (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32)
+                                : (b_nk && (uint64_t)mp.bn * (uint64_t)p.sbn < (1ull << 32)));
+        if (ok) return b_kn16 ? launch_mid<true>(p, mp, stream) : launch_mid<false>(p, mp, stream);
+        return launch_qmm_fallback(p, a_ok, b_kn, b_nk, stream);
+    }
     const SkinnyPlan sp = skinny_plan(p.M, p.N, p.K);
     if (sp.mt != 0 && a_ok && (b_nk || b_kn16)) {
         const size_t need = sp.nsplit > 1 ? QK_SPLIT_COUNTER_BYTES + (size_t)sp.nsplit * p.M * p.N * sizeof(int32_t) : 0;
@@ -1095,13 +1510,7 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
         default: return launch_big<QK_I32>(p, b_kn, tm, tn, 1, nullptr, stream);
         }
     }
-    if (p.K > 0 && a_ok && b_kn) return launch_by_m<true>(p, stream);
-    if (p.K > 0 && a_ok && b_nk) return launch_by_m<false>(p, stream);
-    const int64_t total = p.M * p.N;
-    int64_t blocks = (total + kThreads - 1) / kThreads;
-    if (blocks > 65536) blocks = 65536;
-    qmm_generic<<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(p);
-    return hipGetLastError();
+    return launch_qmm_fallback(p, a_ok, b_kn, b_nk, stream);
 }
 
 }  // namespace qk

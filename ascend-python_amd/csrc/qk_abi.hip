@@ -74,6 +74,8 @@ bool parse_plan(const char* spec, PlanOverride& o) {
             r.w4_splits = a;
         } else if (k == "qmm_dma" && (v == "0" || v == "1")) {
             r.qmm_dma = v == "1";
+        } else if (k == "qmm_mid" && (v == "0" || v == "1")) {
+            r.qmm_mid = v == "1";
         } else if (k == "w4nz" && v == "off") {
             r.w4nz_off = true;
         } else if (k == "w4nz_wg" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 65536) {

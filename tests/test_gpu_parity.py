@@ -217,6 +217,95 @@ def test_quant_matmul_big_tiles_and_split_k(ops, oracle, M, N, K, kn):
     assert np.array_equal(to_bits(out)[rows], ref)
 
 
+@pytest.mark.parametrize("M,N,K,kn,out_dtype,bias_dtype", [
+    (17, 64, 256, False, torch.bfloat16, torch.bfloat16),    # [N,K]: 16 x 64 blocks, one K stage, a 1-row last block
+    (48, 4096, 512, False, torch.float16, torch.float32),    # 16-row blocks, [N,K] weight view
+    (128, 4096, 4096, True, torch.bfloat16, torch.bfloat16),  # cfg1: 16 x 128 blocks ([K,N]), 16 K stages
+    (200, 4096, 1024, True, torch.float32, torch.int32),     # 16 x 128 blocks, last block 8 rows
+    (256, 2048, 768, False, torch.int8, torch.int32),        # 32-row blocks, 3 K stages (fewer than the ring)
+    (96, 1024, 2304, True, torch.int32, None),               # 16-row blocks, 9 K stages
+    (256, 4096, 512, True, torch.bfloat16, torch.bfloat16),  # [K,N]: 32 x 128 blocks
+    (64, 192, 256, True, torch.float16, None),               # [K,N] with N % 128 != 0: 64-column blocks
+])
+def test_quant_matmul_mid_m(ops, oracle, M, N, K, kn, out_dtype, bias_dtype):
+    """16 < M <= 256 with N % 64 == 0 and K % 256 == 0 (a [K,N] weight from M = 33): the no-split mid-M
+    kernel (waves splitting each K stage, exact int32 reduction in LDS; for a [K,N] weight, with the L2
+    prefetch wave).  Every int32 accumulator through exact row and column checksums;
+    first, middle and last rows of the fused output bit-exact against the oracle."""
+    say(f"quant_matmul mid-M M={M} N={N} K={K} {'[K,N]' if kn else '[N,K] view'} out={out_dtype} bias={bias_dtype}")
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    ad = a.to(DEV)
+    wd = w.to(DEV) if kn else w.t().contiguous().to(DEV).t()
+    acc = ops.npu_quant_matmul(ad, wd, torch.ones(1, device=DEV), output_dtype=torch.int32)
+    a64, w64, acc64 = a.to(torch.int64), w.to(torch.int64), acc.cpu().to(torch.int64)
+    assert torch.equal(acc64.sum(0), a64.sum(0) @ w64)
+    assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
+    integer_out = out_dtype in (torch.int8, torch.int32)
+    s = (1e-4 + 1e-3 * torch.rand(N, generator=g)) if out_dtype is torch.int8 else 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    pt = 1e-2 * torch.rand(M, generator=g)
+    off = torch.randn(N, generator=g) if out_dtype is torch.int8 else None
+    b = None
+    if bias_dtype is torch.int32:
+        b = torch.randint(-1000, 1000, (N,), generator=g, dtype=torch.int32)
+    elif bias_dtype is not None:
+        b = torch.randn(N, generator=g).to(bias_dtype)
+    kw = dict(bias=None if b is None else b.to(DEV), output_dtype=out_dtype)
+    if out_dtype is torch.int8:
+        kw["offset"] = off.to(DEV)
+    elif not integer_out:
+        kw["pertoken_scale"] = pt.to(DEV)
+    out = ops.npu_quant_matmul(ad, wd, s.to(DEV), **kw).cpu()
+    rows = np.unique(np.r_[0:4, M // 2 - 2:M // 2 + 2, M - 4:M])
+    bias_np = None if b is None else (b.numpy() if b.dtype in (torch.int32, torch.float32) else W.bits(b))
+    ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(),
+                              pertoken=None if integer_out else pt[rows].numpy(),
+                              offset=None if off is None else off.numpy(), bias=bias_np,
+                              bias_dtype=CODE[b.dtype] if b is not None else BF16, out_dtype=CODE[out_dtype])
+    got = out[rows]
+    got_np = got.numpy() if out_dtype in (torch.float32, torch.int32, torch.int8) else W.bits(got)
+    bad = np.argwhere(got_np != ref)
+    assert bad.size == 0, (f"{len(bad)} mismatches, first at (row {rows[bad[0][0]]}, col {bad[0][1]}): "
+                           f"{got_np[tuple(bad[0])]} vs {ref[tuple(bad[0])]}")
+
+
+def test_quant_matmul_mid_m_against_split_plan(ops, plan):
+    """The mid-M kernel and the split stream it replaced (debug override qmm_mid=0) give the same bf16 bits."""
+    say("quant_matmul mid-M vs split stream, M=100 N=2048 K=4096")
+    g = torch.Generator().manual_seed(11)
+    M, N, K = 100, 2048, 4096
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(DEV)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8).to(DEV)
+    s = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(DEV)
+    pt = (1e-2 * torch.rand(M, generator=g)).to(DEV)
+    b = torch.randn(N, generator=g).to(torch.bfloat16).to(DEV)
+    mid = ops.npu_quant_matmul(a, w, s, pertoken_scale=pt, bias=b, output_dtype=torch.bfloat16)
+    plan("qmm_mid=0")
+    split = ops.npu_quant_matmul(a, w, s, pertoken_scale=pt, bias=b, output_dtype=torch.bfloat16)
+    assert torch.equal(mid.view(torch.int16), split.view(torch.int16))
+
+
+def test_abi_quant_matmul_mid_m_unaligned_rows(ops, oracle):
+    """A mid-M shape whose x1 rows are not 16-byte aligned (lda = K + 8) cannot take the direct-to-LDS
+    kernel: the library falls back to the tiled kernels (no workspace) with the same results."""
+    say("ABI qk_quant_matmul mid-M, lda = K + 8")
+    L = ops.abi()
+    M, N, K = 64, 128, 512
+    g = torch.Generator().manual_seed(12)
+    a_wide = torch.randint(-127, 128, (M, K + 8), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    s = 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    ad, wd, sd = a_wide.to(DEV), w.to(DEV), s.to(DEV)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    rc = L.qk_quant_matmul(ad.data_ptr(), K + 8, wd.data_ptr(), N, 1, M, N, K, sd.data_ptr(), N, None, 0, None, None,
+                           0, out.data_ptr(), BF16, None, 0, _stream())
+    assert rc == 0, ops.last_error()
+    torch.cuda.synchronize()
+    ref = oracle.quant_matmul(a_wide[:, :K].contiguous().numpy(), w.numpy(), s.numpy(), out_dtype=BF16)
+    assert np.array_equal(to_bits(out), ref)
+
+
 @pytest.mark.parametrize("K,out_dtype,bias_dtype,kn", [
     (256, torch.bfloat16, torch.bfloat16, True),   # 192 whole 256x256 tiles, direct-to-LDS kernel (one ring)
     (256, torch.float16, torch.float32, False),
@@ -731,7 +820,7 @@ def test_abi_w8a8_split_workspace_reuse(ops, oracle):
     say("ABI qk_quant_matmul split workspace reuse")
     import ctypes
     L = ops.abi()
-    cases = [(16, 4096, 8192, BF16), (512, 4096, 14336, BF16), (100, 2048, 4096, I8), (512, 1024, 8192, I32),
+    cases = [(16, 4096, 8192, BF16), (512, 4096, 14336, BF16), (16, 2048, 4096, I8), (512, 1024, 8192, I32),
              (16, 4096, 8192, F16)]
     need = []
     for (M, N, K, od) in cases:
