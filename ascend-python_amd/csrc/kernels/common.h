@@ -331,6 +331,8 @@ struct WqbmmArgs {
     int out_dtype;
 };
 hipError_t launch_weight_quant_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
+// xsum[g][m] = fp32 sum of x[m][k] over group g (G a multiple of 64), for the prefill kernels' group algebra
+hipError_t launch_w4_xsum(const WqbmmArgs& p, float* xsum, hipStream_t stream);
 size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group);
 
 // NZ weights (nz_weights.hip): the ND <-> NZ casts (int4, int8) and the weight-quant matmul on NZ weights.

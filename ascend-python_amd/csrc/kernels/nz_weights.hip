@@ -299,6 +299,227 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill on an int4 NZ weight (M > 64): a 128 x 256 output tile per 512-thread
+// workgroup, K in steps of 128 (one NZ block row).  Per step, DMAs
+// (buffer_load_dwordx4 ... lds, counted with each wave's own vmcnt waits) bring
+// the tile's 128 activation rows ([row][256 B], chunk c of row r at
+// r*256 + 16*(c ^ (r & 15))), its 16 NZ weight blocks (1 KB each, copied as
+// they are: a lane's 16 bytes of a block are its B operands for the step's
+// four MFMA k-steps) and the step's group rows (scale and offset of the 256
+// columns, x group sums of the 128 rows) into a ring of three LDS stages, two
+// ahead.  Wave w owns all 128 rows and columns 32w..32w+31 (its two NZ blocks,
+// unpacked once, in registers, by the magic-number conversion): 8 x 2 MFMA
+// tiles accumulate the group's raw sums ag, and at each group's end
+// acc += s * ag + s * (offset - BASE) * xsum (the decode kernel's algebra).
+// The output tile is staged through LDS for 16-byte row stores.
+namespace nzg {
+constexpr int BM = 128, BN = 256, KS = 128, NT = 512, NSTG = 3;
+constexpr int X_BYTES = BM * KS * 2;          // 32 KB
+constexpr int W_BYTES = (BN / 16) * 1024;     // 16 KB
+constexpr int SC_BYTES = 3072;                // scale row, offset row, x group sums
+constexpr int STAGE = X_BYTES + W_BYTES + SC_BYTES;
+constexpr int RING = NSTG * STAGE;            // 153 KB
+constexpr int OROWB = 2 * BN + 16;            // padded output staging row (bytes)
+constexpr int SMEM = RING > BM * OROWB ? RING : BM * OROWB;
+static_assert(SMEM <= 160 * 1024, "LDS");
+}  // namespace nzg
+
+// G1: the group is one step (G == 128), so every step starts a group: its first MFMAs take a zero
+// accumulator and each row tile is folded right after its last MFMAs, between the later tiles' MFMAs.
+template <int DT, bool HAS_OFF, bool G1>
+__global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, int tiles_n,
+                                                     const float* __restrict__ xsum) {
+    typedef Mfma<DT> MM;
+    using namespace nzg;
+    constexpr int TM = 8, TN = 2;
+    constexpr int NSC = HAS_OFF ? 3 : 2;  // group-row DMAs per step: waves 0 .. NSC-1 issue one each
+    __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+
+    const int bid = xcd_swizzle(blockIdx.x, tiles_m * tiles_n);
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int grp = bid / per_group;
+    const int first_m = grp * GM;
+    const int gm = min(tiles_m - first_m, GM);
+    const int tm = first_m + (bid % per_group) % gm;
+    const int tn = (bid % per_group) / gm;
+    const int M = (int)p.M, N = (int)p.N, K = (int)p.K, G = (int)p.group;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int rows = M - m0 < BM ? M - m0 : BM;
+    const int nk = K / KS, kb_n = K / KS;  // steps; NZ blocks along K per column block
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int fr = lane & 15, g4 = lane >> 4;
+    const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+
+    // activations: rows past M read as zeros (range-checked offsets), K*2 bytes per row
+    const uint32_t ldx = (uint32_t)K * 2u;
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(static_cast<const char*>(p.x) + (size_t)m0 * ldx, (uint32_t)(rows - 1) * ldx + ldx);
+    // an instruction covers rows 4q..4q+3: lane l -> row 4q + (l>>4), LDS chunk l&15, k chunk (l&15) ^ (row&15)
+    auto vx = [&](int q) {
+        const int row = 4 * q + (lane >> 4);
+        return (uint32_t)row * ldx + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+    };
+    // the 16 NZ blocks of the column block: block i of step s at ((n0/16 + i) * kb_n + s) KB
+    const __amdgpu_buffer_rsrc_t rw =
+        make_rsrc(static_cast<const char*>(p.w) + (size_t)(n0 / 16) * kb_n * 1024, (uint32_t)(16 * kb_n * 1024));
+    // group rows: 512 bytes each (lanes 32..63 repeat 0..31 into the unused upper half of the KB)
+    const uint32_t nsb = (uint32_t)(K / G) * (uint32_t)N * 2u;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scale, nsb);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(HAS_OFF ? p.offset : p.scale, nsb);
+    const __amdgpu_buffer_rsrc_t rxs = make_rsrc(xsum, (uint32_t)(K / G) * (uint32_t)M * 4u);
+    const uint32_t l32 = 16u * (uint32_t)(lane & 31);
+
+    auto issue = [&](int s) {
+        const uint32_t base = sbase + (uint32_t)(s % NSTG) * STAGE;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = wave + 8 * u;
+            dma16(rx, base + (uint32_t)q * 1024u, vx(q), (uint32_t)s * (uint32_t)(KS * 2));
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = wave + 8 * u;
+            dma16(rw, base + X_BYTES + (uint32_t)i * 1024u, (uint32_t)i * (uint32_t)kb_n * 1024u + 16u * lane,
+                  (uint32_t)s * 1024u);
+        }
+        const uint32_t g = (uint32_t)(s * KS / G);
+        const uint32_t sdst = base + X_BYTES + W_BYTES;
+        if (wave == 0) dma16(rs, sdst, (g * (uint32_t)N + (uint32_t)n0) * 2u + l32, 0);
+        if (HAS_OFF && wave == 1) dma16(ro, sdst + 1024u, (g * (uint32_t)N + (uint32_t)n0) * 2u + l32, 0);
+        if (wave == NSC - 1) dma16(rxs, sdst + 2048u, (g * (uint32_t)M + (uint32_t)m0) * 4u + l32, 0);
+    };
+
+    f32x4 acc[TM][TN], ag[TM][TN];
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = ag[i][j] = zero4;
+
+    const bool more = wave < NSC;  // this wave issues one more DMA per step
+    for (int s = 0; s < 2 && s < nk; ++s) issue(s);
+    for (int s = 0; s < nk; ++s) {
+        // stage s has landed once at most stage s+1's DMAs are outstanding
+        if (s + 1 < nk) {
+            if (more) __builtin_amdgcn_s_waitcnt(vmcnt_imm(7));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(6));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // stage s visible to every wave; every wave is done with stage s-1
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 2 < nk) issue(s + 2);  // into the buffer of stage s-1
+        const char* As = smem + (s % NSTG) * STAGE;
+        const char* Bs = As + X_BYTES;
+        u32x4 bw[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const u32x4*>(Bs + (2 * wave + j) * 1024 + 16 * lane);
+        const char* sc = As + X_BYTES + W_BYTES;
+        // the group's per-column factors s and s * (offset - BASE) of this wave's columns
+        auto col_factors = [&](float (&sf)[TN], float (&sx)[TN]) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = 32 * wave + 16 * j + fr;
+                sf[j] = load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 2 * col), p.s_dtype);
+                const float of =
+                    HAS_OFF ? load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 1024 + 2 * col), p.s_dtype) : 0.0f;
+                sx[j] = sf[j] * (of - MM::BASE);
+            }
+        };
+        auto fold_row = [&](int i, const float (&sf)[TN], const float (&sx)[TN]) {
+            const f32x4 xs = *reinterpret_cast<const f32x4*>(sc + 2048 + 4 * (16 * i + 4 * g4));
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[i][j][r] = __builtin_fmaf(sf[j], ag[i][j][r], __builtin_fmaf(sx[j], xs[r], acc[i][j][r]));
+        };
+        if constexpr (G1) {
+            float sf[TN], sx[TN];
+            col_factors(sf, sx);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                u32x4 af[TM], b[TN];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int r = 16 * i + fr;
+                    af[i] = *reinterpret_cast<const u32x4*>(As + r * 256 + 16 * ((4 * t + g4) ^ (r & 15)));
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j) b[j] = nz_operand<MM::MAGIC>(bw[j][t]);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], b[j], t == 0 ? zero4 : ag[i][j]);
+                    if (t == 3 && i >= 2) fold_row(i - 2, sf, sx);  // two row tiles behind the MFMAs
+                }
+            }
+            fold_row(TM - 2, sf, sx);
+            fold_row(TM - 1, sf, sx);
+            continue;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            u32x4 af[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int r = 16 * i + fr;
+                af[i] = *reinterpret_cast<const u32x4*>(As + r * 256 + 16 * ((4 * t + g4) ^ (r & 15)));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[j] = nz_operand<MM::MAGIC>(bw[j][t]);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], b[j], ag[i][j]);
+        }
+        if (((s + 1) * KS) % G == 0) {  // the group ends with this step: fold it into acc
+            float sf[TN], sx[TN];
+            col_factors(sf, sx);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                fold_row(i, sf, sx);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) ag[i][j] = zero4;
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();  // every wave is past its last reads of the ring
+
+    // ---- epilogue: + bias, cast, staged through LDS for 16-byte row stores
+    float bv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+        bv[j] = p.bias_dtype ? load_scalar(p.bias, n0 + 32 * wave + 16 * j + fr, p.bias_dtype) : 0.0f;
+    uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * i + 4 * g4 + r;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const float v = acc[i][j][r] + bv[j];
+                ot[row * (OROWB / 2) + 32 * wave + 16 * j + fr] =
+                    (uint16_t)(p.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+            }
+        }
+    __syncthreads();
+    constexpr int CPRO = 2 * BN / 16;  // 16-byte chunks per output row
+    for (int q = tid; q < BM * CPRO; q += NT) {
+        const int row = q / CPRO, c = q % CPRO;
+        if (row >= rows) break;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * OROWB + 16 * c);
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N + n0 + 8 * c) = v;
+    }
+}
+
 // The most blocks per workgroup that a wave of `nit` superblocks holds in registers without
 // spilling (two superblocks in flight, NB accumulators): int4, 4 up to 3 superblocks, 3 for 4, 2 for 5,
 // 1 beyond; int8 (two loads per block), 3 up to 2 superblocks, 2 for 3, 1 beyond.  Only these
@@ -400,6 +621,54 @@ int64_t grid_for(int64_t total) {
 // bytes of the ND form of an NZ weight
 size_t nd_weight_bytes(const WqbmmArgs& p) { return (size_t)(p.w_dtype == QK_I8_NZ ? p.K * p.N : p.K * p.N / 2); }
 
+// Prefill plan on an int4 NZ weight: M > 64 with at least 96 tiles of 128 x 256, N % 256 == 0, groups of
+// whole 128-row NZ blocks, 16-byte aligned operands and 32-bit buffer offsets.  The workspace holds the x
+// group sums ([split counters, unused][fp32 [K/G][M]]).
+struct NzGemmPlan {
+    bool ok;
+    int tiles_m, tiles_n;
+};
+
+NzGemmPlan nzg_plan(const WqbmmArgs& p) {
+    NzGemmPlan g{false, 0, 0};
+    const int64_t G = p.group == 0 ? p.K : p.group;
+    if (p.w_dtype != QK_I4_NZ || p.M <= 64 || p.N <= 0 || p.N % nzg::BN != 0 || p.K <= 0 || p.K % nzg::KS != 0)
+        return g;
+    if (G <= 0 || G % nzg::KS != 0 || p.K % G != 0) return g;
+    if (p.M * p.K * 2 >= ((int64_t)1 << 31) || p.K * p.N / 2 >= ((int64_t)1 << 31) ||
+        (p.K / G) * p.N * 2 >= ((int64_t)1 << 31) || (p.K / G) * p.M * 4 >= ((int64_t)1 << 31) ||
+        p.M * p.N >= ((int64_t)1 << 31))
+        return g;
+    if (((uintptr_t)p.x | (uintptr_t)p.w | (uintptr_t)p.scale | (uintptr_t)p.out |
+         (uintptr_t)(p.offset ? p.offset : p.scale)) % 16 != 0)
+        return g;
+    g.tiles_m = (int)((p.M + nzg::BM - 1) / nzg::BM);
+    g.tiles_n = (int)(p.N / nzg::BN);
+    if ((int64_t)g.tiles_m * g.tiles_n < 96) return g;  // too few tiles to fill the CUs
+    g.ok = true;
+    return g;
+}
+
+size_t nzg_workspace(const WqbmmArgs& p) {
+    const int64_t G = p.group == 0 ? p.K : p.group;
+    return QK_SPLIT_COUNTER_BYTES + (size_t)(p.K / G) * (size_t)p.M * sizeof(float);
+}
+
+template <int DT>
+hipError_t launch_nzg_dt(const WqbmmArgs& p, const NzGemmPlan& g, float* xsum, hipStream_t stream) {
+    hipError_t e = launch_w4_xsum(p, xsum, stream);
+    if (e != hipSuccess) return e;
+    const dim3 grid((uint32_t)(g.tiles_m * g.tiles_n)), block(nzg::NT);
+    if (p.group == nzg::KS) {
+        if (p.offset) w4nz_gemm<DT, true, true><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+        else w4nz_gemm<DT, false, true><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+    } else {
+        if (p.offset) w4nz_gemm<DT, true, false><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+        else w4nz_gemm<DT, false, false><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t N, int32_t* dst, hipStream_t stream) {
@@ -427,6 +696,7 @@ hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N
 // [QK_SPLIT_COUNTER_BYTES, unused][ND weight][row-major call's workspace].
 size_t w4_nz_workspace(const WqbmmArgs& p) {
     if (!plan_override().w4nz_off && nz_plan(p).ok) return 0;
+    if (!plan_override().w4nz_off && nzg_plan(p).ok) return nzg_workspace(p);
     const int nd_dtype = p.w_dtype == QK_I8_NZ ? QK_I8 : QK_I32;
     return QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(p)) +
            weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group);
@@ -436,6 +706,12 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
     const NzPlan z = plan_override().w4nz_off ? NzPlan{false, 0, 0, 0, 0, 0} : nz_plan(p);
     if (z.ok)
         return p.x_dtype == QK_BF16 ? launch_nz_dt<QK_BF16>(p, z, stream) : launch_nz_dt<QK_F16>(p, z, stream);
+    const NzGemmPlan g = plan_override().w4nz_off ? NzGemmPlan{false, 0, 0} : nzg_plan(p);
+    if (g.ok) {
+        if (!workspace || ws_bytes < nzg_workspace(p) || (uintptr_t)workspace % 16 != 0) return hipErrorInvalidValue;
+        float* xs = reinterpret_cast<float*>(static_cast<char*>(workspace) + QK_SPLIT_COUNTER_BYTES);
+        return p.x_dtype == QK_BF16 ? launch_nzg_dt<QK_BF16>(p, g, xs, stream) : launch_nzg_dt<QK_F16>(p, g, xs, stream);
+    }
     const bool w8 = p.w_dtype == QK_I8_NZ;
     const int nd_dtype = w8 ? QK_I8 : QK_I32;
     const size_t nd_bytes = round256(nd_weight_bytes(p));

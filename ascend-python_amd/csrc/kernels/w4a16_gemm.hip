@@ -1595,6 +1595,12 @@ hipError_t launch_reduce(const WqbmmArgs& p, int nsplit, const float* partial, h
 
 }  // namespace
 
+hipError_t launch_w4_xsum(const WqbmmArgs& p, float* xsum, hipStream_t stream) {
+    const int64_t sums = p.M * (p.K / p.group);
+    w4_xsum<<<dim3((uint32_t)((sums + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream>>>(p, xsum);
+    return hipGetLastError();
+}
+
 size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group) {
     WqbmmArgs p{};
     p.M = M;

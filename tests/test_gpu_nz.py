@@ -4,8 +4,9 @@
   device: bit-exact against the oracle's NZ restatement, both directions.
 * npu_weight_quant_batchmatmul on NZ weights: within rtol 1e-2 / atol 1e-2
   of the float64 oracle on the same seeded inputs (the bar of the row-major
-  path), through the NZ decode kernel and through the unpack-to-ND fallback
-  (short groups, K with no even wave split, M > 64, forced off).
+  path), through the NZ decode kernel (M <= 64), the NZ prefill kernel (M > 64
+  with enough 128 x 256 tiles) and through the unpack-to-ND fallback (short
+  groups, K with no even wave split, few prefill tiles, forced off).
 """
 import ctypes
 
@@ -13,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+import exact
 from op_plugin_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -152,6 +154,31 @@ def test_w4a16_nz_prefill_fallback(ops, oracle):
     finally:
         ops.debug_set_plan("")
     _close(out, _ref(oracle, d, 128), torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,bias", [
+    (2048, 11008, 4096, 128, True, torch.bfloat16, False),   # cfg3 prefill: 16 x 43 tiles
+    (320, 8192, 1024, 256, False, torch.float16, True),      # two steps per group, last row tile half full
+    (512, 6144, 768, 0, True, torch.bfloat16, False),        # per channel: one group of 768 rows
+    (1000, 4096, 2048, 128, True, torch.bfloat16, True),     # last row tile of 104 rows
+])
+def test_w4a16_nz_prefill_kernel(ops, oracle, M, N, K, group, offset, x_dtype, bias):
+    """The NZ prefill kernel (M > 64, at least 96 tiles of 128 x 256): every output element within
+    rtol/atol 1e-2 of the float64 dequant-matmul, which is pinned against the C oracle on four rows; and
+    against the row-major path on the same weight."""
+    say(f"w4a16 NZ prefill M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    d = _inputs(M, N, K, group, offset, x_dtype, seed=M + N + K + 1)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(6)).to(x_dtype) if bias else None
+    nz = ops.npu_format_cast(d["w_packed"].to(DEV), 29)
+    out = _run(ops, d, group, nz, bias=b)
+    ref64 = exact.wq_dequant_matmul(d["x"], d["w"], d["scale"], d["offset"], group, bias=b)
+    rows = np.r_[0:2, M - 2:M]
+    pin = _ref(oracle, dict(d, x=d["x"][rows]), group, bias=b, x_dtype=x_dtype)
+    pin_diff = (W.from_bits(pin, x_dtype).float() - ref64[rows].float()).abs()
+    assert pin_diff.max().item() <= 2.0**-7 * ref64[rows].abs().max().item() + 1e-3
+    torch.testing.assert_close(out.cpu().float(), ref64.float(), rtol=1e-2, atol=1e-2)
+    nd_out = _run(ops, d, group, d["w_packed"].to(DEV), bias=b)
+    torch.testing.assert_close(out.float(), nd_out.float(), rtol=1e-2, atol=1e-2)
 
 
 def test_abi_nz_and_noalloc(ops, oracle):
