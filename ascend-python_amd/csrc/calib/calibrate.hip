@@ -11,6 +11,13 @@
 //  calib_stream_read the HBM read ceiling of one launch: every thread issues
 //                    its 16-byte loads of a buffer up front and folds them
 //                    into one word (so the loads are not removed).
+//  calib_dma_fill    the rate at which one CU fills its LDS by direct
+//                    global->LDS loads (buffer_load_dwordx4 ... lds, as the
+//                    GEMM kernels stage operands): NW waves each keep 16 such
+//                    1 KB loads in flight, from a span that stays in L2 or one
+//                    that streams from HBM, in row pieces of PIECE contiguous
+//                    bytes (the rest of each 1 KB load from rows `rowstride`
+//                    apart, as a [K,N] weight's column block is read).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -70,6 +77,43 @@ __global__ __launch_bounds__(1024) void calib_stream_read(const u32x4* __restric
     out[t] = s;
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes per lane into LDS bytes [lds + 16*lane, +16); the kernel counts vmcnt itself
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds));
+}
+
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
+
+// Workgroup b streams n_instr 1 KB loads per wave from offset (b * stride_wg + row block) % span into a
+// 128 KB LDS ring (which nothing reads: only the fill rate is measured); the buffer must hold span bytes
+// plus 64 rows of rowstride.
+template <int NW, int PIECE>
+__global__ __launch_bounds__(64 * NW) void calib_dma_fill(const int8_t* buf, uint32_t span, uint32_t rowstride,
+                                                          int n_instr, uint32_t stride_wg, int32_t* out) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[128 * 1024];
+    constexpr int DEPTH = 16;
+    const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(buf, span + 64u * rowstride);
+    constexpr int LPR = PIECE / 16;  // lanes per row piece
+    constexpr int RPI = 64 / LPR;    // rows per load
+    const uint32_t voff = (uint32_t)(lane / LPR) * rowstride + 16u * (uint32_t)(lane % LPR);
+    const uint32_t base = (uint32_t)blockIdx.x * stride_wg;
+    for (int i = 0; i < n_instr; ++i) {
+        const uint32_t blk = (uint32_t)(i * NW + wave);
+        const uint32_t soff = (base + blk * (uint32_t)RPI * rowstride) % span;
+        dma16(rs, sbase + (blk % 128u) * 1024u, voff, soff);
+        if (i >= DEPTH) __builtin_amdgcn_s_waitcnt(vmcnt_imm(DEPTH));
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = smem[blockIdx.x & 1023];
+}
+
 }  // namespace
 
 extern "C" {
@@ -86,6 +130,22 @@ int qk_calib_stream_read(const void* buf, int64_t bytes, int grid, uint32_t* out
     const int64_t n16 = bytes / 16;
     if ((int64_t)grid * 1024 * 8 < n16) return -1;
     calib_stream_read<8><<<dim3((uint32_t)grid), dim3(1024), 0, stream>>>(static_cast<const u32x4*>(buf), n16, out);
+    return (int)hipGetLastError();
+}
+
+// variant: 0 = 4 waves, 1 = 8 waves, 2 = 16 waves (256-byte pieces); 3 = 8 waves, 128-byte pieces;
+// 4 = 8 waves, 64-byte pieces.  buf holds span + 64 * rowstride bytes; out holds grid words.
+int qk_calib_dma_fill(int variant, int grid, const void* buf, uint32_t span, uint32_t rowstride, int n_instr,
+                      uint32_t stride_wg, int32_t* out, hipStream_t stream) {
+    const int8_t* b = static_cast<const int8_t*>(buf);
+    switch (variant) {
+    case 0: calib_dma_fill<4, 256><<<grid, 256, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
+    case 1: calib_dma_fill<8, 256><<<grid, 512, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
+    case 2: calib_dma_fill<16, 256><<<grid, 1024, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
+    case 3: calib_dma_fill<8, 128><<<grid, 512, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
+    case 4: calib_dma_fill<8, 64><<<grid, 512, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
+    default: return -1;
+    }
     return (int)hipGetLastError();
 }
 

@@ -234,6 +234,27 @@ def calibrate(dev, min_launches: int) -> dict:
     one = torch.zeros(1, device=dev)
     t = launch_runs(lambda i: one.fill_(i), 24, min_launches, prime)
     res["launch_floor_us"] = round(t["s"] * 1e6, 2)
+    del bufs, dst
+    # per-CU fill rate of direct global->LDS loads: 256 workgroups, 2 MB each, 16 loads in flight per wave,
+    # from a 2 MB span every XCD keeps in its L2 (contiguous rows) and from a 510 MB span that streams from
+    # HBM (rows 4096 B apart, as a [K,N] weight's column block is read)
+    L.qk_calib_dma_fill.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                    ctypes.c_int, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    big = torch.empty((511 << 20), dtype=torch.int8, device=dev)
+    fout = torch.empty(256, dtype=torch.int32, device=dev)
+    fill = {}
+    for where, span, stride_wg, cases in (("l2_2MB", 2 << 20, 8192, ((0, 4, 256), (1, 8, 256), (2, 16, 256))),
+                                         ("hbm_510MB_rowstride4096", 510 << 20, 2 << 20,
+                                          ((1, 8, 256), (3, 8, 128), (4, 8, 64)))):
+        for v, nw, piece in cases:
+            rowstride = piece if where.startswith("l2") else 4096
+            n_instr = 2048 // nw
+            t = launch_runs(lambda i: L.qk_calib_dma_fill(v, 256, big.data_ptr(), span, rowstride, n_instr, stride_wg,
+                                                          fout.data_ptr(), st), 2, 8, prime)
+            nb = 256 * nw * n_instr * 1024
+            fill[f"{where}_{nw}waves_{piece}B"] = {"us": round(t["s"] * 1e6, 1), "TB/s": round(nb / t["s"] / 1e12, 2),
+                                                   "GB/s_per_CU": round(nb / t["s"] / 256 / 1e9, 1)}
+    res["dma_fill"] = fill
     return res
 
 
@@ -272,7 +293,15 @@ def other_configs(q, W, dev, min_launches: int) -> dict:
                                            output_dtype=torch.bfloat16), 32)
     res["cfg1_w8a8_m128_k4096_n4096"] = {"avg_us": round(t * 1e6, 2), "TOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1),
                                          "mfma_frac": round(2 * c.M * c.N * c.K / t / 1e12 / PEAK_I8_TOPS, 4)}
+    # the same weights stored [N,K] (nn.Linear layout) and passed as their [K,N] transposed view: whole 256-byte
+    # K rows per weight row stream better than the [K,N] rows' 128-byte column blocks
+    wt = [w.t().contiguous().t() for w in ws]
     del ws
+    t = timed(lambda i: q.npu_quant_matmul(xq, wt[i % 32], sc, pertoken_scale=xs, bias=b,
+                                           output_dtype=torch.bfloat16), 32)
+    res["cfg1_w8a8_m128_k4096_n4096_nk_view"] = {"avg_us": round(t * 1e6, 2),
+                                                 "TOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1)}
+    del wt
 
     # cfg2: decode-shaped W8A8, K=8192, N=28672, M in {1,4,16}; W 235 MB per set, 3 sets
     c0 = W.CFG2[0]
@@ -298,6 +327,13 @@ def other_configs(q, W, dev, min_launches: int) -> dict:
     res["cfg3_w4a16_m2048_k4096_n11008"] = {"avg_us": round(t * 1e6, 2),
                                             "TFLOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1),
                                             "mfma_frac_bf16": round(2 * c.M * c.N * c.K / t / 1e12 / 2500.0, 4)}
+    # the same weight cast once (untimed) to the NZ layout: the NZ prefill kernel
+    wz = q.npu_format_cast(wp, q.ACL_FORMAT_FRACTAL_NZ)
+    t = timed(lambda i: q.npu_weight_quant_batchmatmul(x, wz, s, o, antiquant_group_size=c.group), 8)
+    res["cfg3_w4a16_m2048_k4096_n11008_nz"] = {"avg_us": round(t * 1e6, 2),
+                                               "TFLOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1),
+                                               "mfma_frac_bf16": round(2 * c.M * c.N * c.K / t / 1e12 / 2500.0, 4)}
+    del wz
 
     # cfg5: quantized MLP block, 512 tokens, hidden 4096, intermediate 14336 (whole block)
     T, H, I = W.CFG5["tokens"], W.CFG5["hidden"], W.CFG5["intermediate"]
