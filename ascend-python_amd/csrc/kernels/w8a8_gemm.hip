@@ -908,7 +908,7 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
 }
 
 // ---------------------------------------------------------------------------
-// Mid-M kernel (16 < M <= 256, every K in one workgroup, no split partials):
+// Mid-M kernel (M <= 256, every K in one workgroup, no split partials):
 // a BM x BN output tile per workgroup of NW waves (BM = 16, 32 or 64; BN = 64,
 // or 128 for a [K,N] weight so each of its k rows is one whole 128-byte line),
 // so a few thousand output columns already give hundreds of workgroups.  K
@@ -1367,8 +1367,8 @@ hipError_t launch_skinny(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial
 
 }  // namespace
 
-// Mid-M shapes (16 < M <= 128, or M <= 256 with N <= 8192 -- beyond that the 256x256 tiles move fewer
-// bytes per CU; N % 64 == 0, K % 256 == 0): qmm_mid, no workspace.  Column blocks of 128 for a [K,N]
+// Mid-M shapes (M <= 128, or M <= 256 with N <= 8192 -- beyond that the 256x256 tiles move fewer bytes
+// per CU; N % 64 == 0, K % 256 == 0): qmm_mid, no workspace.  Column blocks of 128 for a [K,N]
 // weight whose N allows it (whole-line k rows), else 64; the row block (64, 32 or 16; 32 at most with
 // 128 columns) that moves the fewest operand bytes per CU.  A [K,N] weight with M <= 32 keeps the split
 // stream (measured faster there), so for M <= 32 the workspace query still reports the split stream's
@@ -1382,7 +1382,7 @@ struct MidPlan {
 MidPlan mid_plan(int64_t M, int64_t N, int64_t K, bool b_kn) {
     MidPlan m;
     if (!plan_override().qmm_mid) return m;  // debug override: the split stream / tiled kernels instead
-    if (M <= 16 || M > 256 || (M > 128 && N > 8192) || N <= 0 || N % 64 != 0 || K <= 0 || K % md::KS != 0)
+    if (M <= 0 || M > 256 || (M > 128 && N > 8192) || N <= 0 || N % 64 != 0 || K <= 0 || K % md::KS != 0)
         return m;
     const int bn = (b_kn && N % 128 == 0) ? 128 : 64;
     const int64_t tn = N / bn;

@@ -226,9 +226,11 @@ def test_quant_matmul_big_tiles_and_split_k(ops, oracle, M, N, K, kn):
     (96, 1024, 2304, True, torch.int32, None),               # 16-row blocks, 9 K stages
     (256, 4096, 512, True, torch.bfloat16, torch.bfloat16),  # [K,N]: 32 x 128 blocks
     (64, 192, 256, True, torch.float16, None),               # [K,N] with N % 128 != 0: 64-column blocks
+    (1, 28672, 1024, False, torch.bfloat16, torch.bfloat16), # decode rows on an [N,K] weight: one row of 16
+    (7, 4096, 2048, False, torch.float16, None),             # 7 of 16 rows
 ])
 def test_quant_matmul_mid_m(ops, oracle, M, N, K, kn, out_dtype, bias_dtype):
-    """16 < M <= 256 with N % 64 == 0 and K % 256 == 0 (a [K,N] weight from M = 33): the no-split mid-M
+    """M <= 256 with N % 64 == 0 and K % 256 == 0 (a [K,N] weight from M = 33): the no-split mid-M
     kernel (waves splitting each K stage, exact int32 reduction in LDS; for a [K,N] weight, with the L2
     prefetch wave).  Every int32 accumulator through exact row and column checksums;
     first, middle and last rows of the fused output bit-exact against the oracle."""
@@ -257,7 +259,7 @@ def test_quant_matmul_mid_m(ops, oracle, M, N, K, kn, out_dtype, bias_dtype):
     elif not integer_out:
         kw["pertoken_scale"] = pt.to(DEV)
     out = ops.npu_quant_matmul(ad, wd, s.to(DEV), **kw).cpu()
-    rows = np.unique(np.r_[0:4, M // 2 - 2:M // 2 + 2, M - 4:M])
+    rows = np.unique(np.clip(np.r_[0:4, M // 2 - 2:M // 2 + 2, M - 4:M], 0, M - 1))
     bias_np = None if b is None else (b.numpy() if b.dtype in (torch.int32, torch.float32) else W.bits(b))
     ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(),
                               pertoken=None if integer_out else pt[rows].numpy(),
