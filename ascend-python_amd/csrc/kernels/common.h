@@ -282,7 +282,8 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   w4_gemm=force | nodma | off                     prefill kernels on few tiles / register-staged only / never
 //   w4_splits=<n>                                   K splits of the 32-row-block decode kernel
 //   qmm_dma=0                                       W8A8 prefill: register-staged kernel instead of the DMA one
-//   qmm_mid=0                                       W8A8 16 < M <= 256: split stream / tiled kernels instead of qmm_mid
+//   qmm_mid=0                                       W8A8 M <= 256: split stream / tiled kernels instead of qmm_mid
+//   mid_bm=<16|32|64>, mid_split=<1|2>              qmm_mid: row block and K split (where the shape allows them)
 //   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
 //   w4nz=off                                        NZ int4 weights: unpack to ND and take the row-major kernels
 //   w4nz_wg=<n>                                     NZ decode kernel: workgroups along N
@@ -293,6 +294,7 @@ struct PlanOverride {
     int w4_splits = 0;
     bool qmm_dma = true;
     bool qmm_mid = true;
+    int mid_bm = 0, mid_split = 0;
     int skinny_splits = 0;
     bool w4nz_off = false;
     int w4nz_wg = 0;

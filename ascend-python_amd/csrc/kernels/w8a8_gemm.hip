@@ -1000,18 +1000,25 @@ __device__ __forceinline__ void store8(const QmmEpilogue& e, int64_t m, int64_t 
     }
 }
 
-template <bool B_KN, int BM, int BN, int NW, int PD, int OUT>
-__global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p, int tiles_m) {
+// SPLIT: the grid holds nsplit workgroups per tile, each over K / nsplit; each stores its exact int32 tile
+// sums device-coherently to partial[tile][split], and the last to arrive (splitk_last) adds the splits in
+// split order and applies the epilogue.
+template <bool B_KN, int BM, int BN, int NW, int PD, int OUT, bool SPLIT>
+__global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p, int tiles_m, int nsplit,
+                                                                     int32_t* __restrict__ partial,
+                                                                     uint64_t* __restrict__ ctr, uint64_t tag) {
     constexpr int SCRATCH = PD > 0 ? 1024 : 0;  // the prefetch wave's landing block
     using C = md::Cfg<BM, BN, NW, SCRATCH>;
     constexpr int NST = C::NST, TMI = BM / 16, NTJ = C::NTJ, NT = C::NT;
     static_assert(NST * C::STAGE + SCRATCH <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) int8_t smem[NST * C::STAGE + SCRATCH];
 
-    // logical tile id: consecutive ids (one XCD) share a column block, so the weight's lines are
-    // fetched once per XCD; the row blocks of a column block run side by side
+    // logical id: consecutive ids (one XCD) share a column block, so the weight's lines are fetched once
+    // per XCD; the splits of a tile, then the row blocks of a column block, run side by side
     const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-    const int tm = bid % tiles_m, tn = bid / tiles_m;
+    const int split = SPLIT ? bid % nsplit : 0;
+    const int tile = SPLIT ? bid / nsplit : bid;
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int rows = (int)((p.M - m0) < BM ? (p.M - m0) : BM);
 
@@ -1038,11 +1045,12 @@ __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p
         const int row = b * (1024 / BN) + lane / CPR;
         return (uint32_t)row * ldb + 16u * (uint32_t)((lane % CPR) ^ md::hkn<BN>(row));
     };
-    const int nk = (int)(p.K / md::KS);
+    const int nk = (int)(p.K / md::KS / (SPLIT ? nsplit : 1));  // stages of this workgroup's K range
+    const uint32_t kbeg = (uint32_t)(split * nk * md::KS);
     const bool hi = wave < C::DMA % NW;  // this wave issues PW_HI instructions per stage
     auto issue = [&](int s) {  // stage s into buffer s % NST: instructions wave, wave+NW, ...
         const uint32_t lds = sbase + (uint32_t)(s % NST) * C::STAGE;
-        const uint32_t k0 = (uint32_t)s * md::KS;
+        const uint32_t k0 = kbeg + (uint32_t)s * md::KS;
 #pragma unroll
         for (int u = 0; u < C::PW_HI; ++u) {
             const int q = wave + NW * u;
@@ -1077,7 +1085,7 @@ __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p
     const int pd = min(PD, 56 / pf_cnt);
     auto prefetch = [&](int s) {
         const uint32_t lds = sbase + (uint32_t)(NST * C::STAGE);
-        const uint32_t k0 = (uint32_t)s * md::KS;
+        const uint32_t k0 = kbeg + (uint32_t)s * md::KS;
         if (pf_a)
             for (int q = 0; q < C::A_DMA; ++q) dma16(rsA, lds, voff_rk(q, lda), k0);
         for (int b = tm; b < BN / 4; b += tiles_m) {
@@ -1141,26 +1149,26 @@ __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p
     // last reads)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
-    if (pf_wave) {  // the prefetch wave still passes the one barrier below
-        __syncthreads();
-        return;
-    }
     int32_t* red = reinterpret_cast<int32_t*>(smem);
+    if (!pf_wave) {
 #pragma unroll
-    for (int i = 0; i < TMI; ++i)
+        for (int i = 0; i < TMI; ++i)
 #pragma unroll
-        for (int jj = 0; jj < NTJ; ++jj)
+            for (int jj = 0; jj < NTJ; ++jj)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                red[(kq * BM + 16 * i + 4 * g + r) * C::RED_ROW + 16 * (cg * NTJ + jj) + fr] = acc[i][jj][r];
+                for (int r = 0; r < 4; ++r)
+                    red[(kq * BM + 16 * i + 4 * g + r) * C::RED_ROW + 16 * (cg * NTJ + jj) + fr] = acc[i][jj][r];
+    }
     __syncthreads();
-    // 8 consecutive outputs per thread-step: exact int32 sum of the four partials, then the epilogue
-    for (int q = tid; q < BM * BN / 8; q += NT) {
-        const int row = q / (BN / 8), c8 = 8 * (q % (BN / 8));
-        if (row >= rows) continue;
-        uint32_t s8[8];
+    // thread tid finishes 8 consecutive outputs of one row (tiles have at most 8 * NT outputs): the exact
+    // int32 sum of the four K partials, then (this split's share of) the epilogue
+    static_assert(BM * BN / 8 <= NT, "one group of 8 outputs per thread");
+    const int row = tid / (BN / 8), c8 = 8 * (tid % (BN / 8));
+    const bool has = !pf_wave && tid < BM * BN / 8 && row < rows;
+    uint32_t s8[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) s8[t] = 0u;
+    for (int t = 0; t < 8; ++t) s8[t] = 0u;
+    if (has) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const int32_t* src = red + (w * BM + row) * C::RED_ROW + c8;
@@ -1172,7 +1180,42 @@ __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p
                 s8[4 + t] += (uint32_t)b[t];
             }
         }
-        store8<OUT>(p.epi, m0 + row, n0 + c8, s8);
+    }
+    if constexpr (!SPLIT) {
+        if (has) store8<OUT>(p.epi, m0 + row, n0 + c8, s8);
+    } else {
+        // partial[tile][split][BM][BN], written through the L2 (device-coherent) and read back by the last split
+        const __amdgpu_buffer_rsrc_t prs =
+            make_rsrc(partial, (uint32_t)((int64_t)gridDim.x * BM * BN * 4));
+        const uint32_t own_off = (uint32_t)((((int64_t)tile * nsplit + split) * BM + row) * BN + c8) * 4u;
+        if (has) {
+            __builtin_amdgcn_raw_buffer_store_b128((u32x4){s8[0], s8[1], s8[2], s8[3]}, prs, own_off, 0, kCoherent);
+            __builtin_amdgcn_raw_buffer_store_b128((u32x4){s8[4], s8[5], s8[6], s8[7]}, prs, own_off + 16u, 0,
+                                                   kCoherent);
+        }
+        if (!splitk_last(ctr + tile, (uint32_t)nsplit, tag)) return;
+        if (has) {
+            uint32_t t8[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) t8[t] = 0u;
+            for (int sp = 0; sp < nsplit; ++sp) {  // in split order (integer sums: any order is exact)
+                u32x4 lo, hi;
+                if (sp == split) {
+                    lo = (u32x4){s8[0], s8[1], s8[2], s8[3]};
+                    hi = (u32x4){s8[4], s8[5], s8[6], s8[7]};
+                } else {
+                    const uint32_t off = (uint32_t)((((int64_t)tile * nsplit + sp) * BM + row) * BN + c8) * 4u;
+                    lo = __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kCoherent);
+                    hi = __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16u, 0, kCoherent);
+                }
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    t8[t] += lo[t];
+                    t8[4 + t] += hi[t];
+                }
+            }
+            store8<OUT>(p.epi, m0 + row, n0 + c8, t8);
+        }
     }
 }
 
@@ -1372,10 +1415,13 @@ hipError_t launch_skinny(const QmmArgs& p, const SkinnyPlan& s, int32_t* partial
 // weight whose N allows it (whole-line k rows), else 64; the row block (64, 32 or 16; 32 at most with
 // 128 columns) that moves the fewest operand bytes per CU.  A [K,N] weight with M <= 32 keeps the split
 // stream (measured faster there), so for M <= 32 the workspace query still reports the split stream's
-// workspace, which a [N,K] weight's qmm_mid launch leaves unused.  Eligibility from sizes only, so the
-// workspace query and the launch agree.
+// workspace, which a [N,K] weight's qmm_mid launch leaves unused.  With 128 columns the plan may split K
+// in two (each split finishing through device-coherent int32 partials and a tagged counter per tile, the
+// last split applying the epilogue) when that moves fewer bytes per CU; the workspace query reports that
+// [K,N] plan's workspace for every mid shape, and a launch given less runs unsplit.  Eligibility from
+// sizes only, so the workspace query and the launch agree.
 struct MidPlan {
-    int bm = 0, bn = 0, tiles_m = 0, tiles = 0;
+    int bm = 0, bn = 0, tiles_m = 0, tiles = 0, nsplit = 1;
 };
 
 
@@ -1387,53 +1433,88 @@ MidPlan mid_plan(int64_t M, int64_t N, int64_t K, bool b_kn) {
     const int bn = (b_kn && N % 128 == 0) ? 128 : 64;
     const int64_t tn = N / bn;
     if (tn * ((M + 15) / 16) >= ((int64_t)1 << 30)) return m;
-    // the row block with the fewest operand bytes per CU: rounds of workgroups over the 256 CUs times
-    // each workgroup's (BM + BN) bytes per K byte (ties to the larger block)
-    int bm = 16;
+    // the row block (and, with 128 columns, K split) with the fewest bytes per CU: rounds of workgroups over
+    // the 256 CUs times each workgroup's (BM + BN) * K / nsplit operand bytes, plus a split's partial tile
+    // written and read (ties to the larger block, then to no split)
+    int bm = 16, ns = 1;
     int64_t best = -1;
+    const PlanOverride& ov = plan_override();  // debug override: a row block and / or a split count
     for (int c : {64, 32, 16}) {
         if (bn == 128 && c == 64) continue;
-        const int64_t rounds = (((M + c - 1) / c) * tn + 255) / 256;
-        const int64_t cost = rounds * (c + bn);
-        if (best < 0 || cost < best) {
-            best = cost;
-            bm = c;
+        if (ov.mid_bm && c != ov.mid_bm) continue;
+        const int64_t tiles = ((M + c - 1) / c) * tn;
+        for (int sp : {1, 2}) {
+            if (ov.mid_split && sp != ov.mid_split) continue;
+            // a split only while it keeps one round of workgroups and at least three stages in flight
+            // (measured: a second round, or a split K range behind a two-stage ring, costs more than the
+            // halved bytes save)
+            const int nst = (160 * 1024 - 1024) / ((c + bn) * md::KS);
+            if (sp > 1 && (bn != 128 || tiles * sp > 256 || nst < 4 || K % ((int64_t)sp * md::KS) != 0 ||
+                           tiles > (int64_t)(QK_SPLIT_COUNTER_BYTES / sizeof(uint64_t)) ||
+                           tiles * sp * c * bn * 4 >= ((int64_t)1 << 31)))
+                continue;
+            const int64_t rounds = (tiles * sp + 255) / 256;
+            const int64_t cost = rounds * (c + bn) * (K / sp) + (sp > 1 ? (int64_t)c * bn * 8 : 0);
+            if (best < 0 || cost < best) {
+                best = cost;
+                bm = c;
+                ns = sp;
+            }
         }
     }
+    if (best < 0) return m;  // the override asked for a block or split the shape does not allow
     m.bm = bm;
     m.bn = bn;
+    m.nsplit = ns;
     m.tiles_m = (int)((M + bm - 1) / bm);
     m.tiles = (int)(m.tiles_m * tn);
     return m;
 }
 
-template <bool B_KN, int BM, int BN>
-hipError_t launch_mid_t(const QmmArgs& p, const MidPlan& mp, hipStream_t stream) {
+size_t mid_workspace(const MidPlan& m) {
+    return m.nsplit > 1 ? QK_SPLIT_COUNTER_BYTES + (size_t)m.tiles * m.nsplit * m.bm * m.bn * sizeof(int32_t) : 0;
+}
+
+template <bool B_KN, int BM, int BN, int OUT>
+hipError_t launch_mid_o(const QmmArgs& p, const MidPlan& mp, int32_t* partial, uint64_t* ctr, hipStream_t stream) {
     // 8 waves; a prefetch wave 12 stages ahead for a [K,N] weight (measured: it shortens the [K,N]
     // cfg1 shape by a sixth and lengthens the [N,K] one, whose 256-byte rows stream well without it)
     constexpr int NW = 8, PD = B_KN ? 12 : 0;
-    const dim3 grid((uint32_t)mp.tiles), block(64 * NW + (PD > 0 ? 64 : 0));
-    switch (p.epi.out_dtype) {
-    case QK_BF16: qmm_mid<B_KN, BM, BN, NW, PD, QK_BF16><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
-    case QK_F16: qmm_mid<B_KN, BM, BN, NW, PD, QK_F16><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
-    case QK_F32: qmm_mid<B_KN, BM, BN, NW, PD, QK_F32><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
-    case QK_I8: qmm_mid<B_KN, BM, BN, NW, PD, QK_I8><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
-    default: qmm_mid<B_KN, BM, BN, NW, PD, QK_I32><<<grid, block, 0, stream>>>(p, mp.tiles_m); break;
+    const dim3 grid((uint32_t)(mp.tiles * mp.nsplit)), block(64 * NW + (PD > 0 ? 64 : 0));
+    if (mp.nsplit > 1) {
+        if constexpr (BN == 128)  // splits only with 128-column blocks
+            qmm_mid<B_KN, BM, BN, NW, PD, OUT, true><<<grid, block, 0, stream>>>(p, mp.tiles_m, mp.nsplit, partial,
+                                                                                ctr, next_split_tag());
+        else
+            return hipErrorInvalidValue;
+    } else {
+        qmm_mid<B_KN, BM, BN, NW, PD, OUT, false><<<grid, block, 0, stream>>>(p, mp.tiles_m, 1, nullptr, nullptr, 0);
     }
     return hipGetLastError();
 }
 
+template <bool B_KN, int BM, int BN>
+hipError_t launch_mid_t(const QmmArgs& p, const MidPlan& mp, int32_t* partial, uint64_t* ctr, hipStream_t stream) {
+    switch (p.epi.out_dtype) {
+    case QK_BF16: return launch_mid_o<B_KN, BM, BN, QK_BF16>(p, mp, partial, ctr, stream);
+    case QK_F16: return launch_mid_o<B_KN, BM, BN, QK_F16>(p, mp, partial, ctr, stream);
+    case QK_F32: return launch_mid_o<B_KN, BM, BN, QK_F32>(p, mp, partial, ctr, stream);
+    case QK_I8: return launch_mid_o<B_KN, BM, BN, QK_I8>(p, mp, partial, ctr, stream);
+    default: return launch_mid_o<B_KN, BM, BN, QK_I32>(p, mp, partial, ctr, stream);
+    }
+}
+
 template <bool B_KN>
-hipError_t launch_mid(const QmmArgs& p, const MidPlan& mp, hipStream_t stream) {
+hipError_t launch_mid(const QmmArgs& p, const MidPlan& mp, int32_t* partial, uint64_t* ctr, hipStream_t stream) {
     if constexpr (B_KN) {  // 128-column blocks only for a [K,N] weight
         if (mp.bn == 128) {
-            if (mp.bm == 32) return launch_mid_t<B_KN, 32, 128>(p, mp, stream);
-            return launch_mid_t<B_KN, 16, 128>(p, mp, stream);
+            if (mp.bm == 32) return launch_mid_t<B_KN, 32, 128>(p, mp, partial, ctr, stream);
+            return launch_mid_t<B_KN, 16, 128>(p, mp, partial, ctr, stream);
         }
     }
-    if (mp.bm == 64) return launch_mid_t<B_KN, 64, 64>(p, mp, stream);
-    if (mp.bm == 32) return launch_mid_t<B_KN, 32, 64>(p, mp, stream);
-    return launch_mid_t<B_KN, 16, 64>(p, mp, stream);
+    if (mp.bm == 64) return launch_mid_t<B_KN, 64, 64>(p, mp, partial, ctr, stream);
+    if (mp.bm == 32) return launch_mid_t<B_KN, 32, 64>(p, mp, partial, ctr, stream);
+    return launch_mid_t<B_KN, 16, 64>(p, mp, partial, ctr, stream);
 }
 
 // The kernels that need no workspace and no alignment beyond the tiled kernels' (or none at all).
@@ -1449,7 +1530,8 @@ hipError_t launch_qmm_fallback(const QmmArgs& p, bool a_ok, bool b_kn, bool b_nk
 
 // A split workspace is [split-K counters][int32 partials [nsplit][M][N]].
 size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K) {
-    if (mid_plan(M, N, K, false).bm != 0 && M > 32) return 0;  // the column block does not change eligibility
+    if (mid_plan(M, N, K, false).bm != 0 && M > 32)  // eligibility does not depend on the layout; the
+        return mid_workspace(mid_plan(M, N, K, true));  // [K,N] plan's split needs a workspace
     const SkinnyPlan s = skinny_plan(M, N, K);
     if (s.mt != 0)
         return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
@@ -1466,8 +1548,11 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
     const bool b_kn16 = b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0;
     char* ws = static_cast<char*>(workspace);
     int32_t* partial = ws ? reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES) : nullptr;
-    const MidPlan mp = mid_plan(p.M, p.N, p.K, b_kn16);
+    MidPlan mp = mid_plan(p.M, p.N, p.K, b_kn16);
     if (mp.bm != 0 && (p.M > 32 || !b_kn16)) {
+        // a split plan needs its partials and counters; with less workspace the same blocks run unsplit
+        const size_t need = mid_workspace(mp);
+        if (need && (!ws || ws_bytes < need || (uintptr_t)ws % 16 != 0)) mp.nsplit = 1;
         // direct-to-LDS loads need 16-byte aligned rows and 32-bit buffer offsets; the 8-output epilogue
         // stores need 16-byte aligned output rows.  Otherwise the tiled kernels (no workspace) take it.
         const int osz = p.epi.out_dtype == QK_I8 ? 1 : ((p.epi.out_dtype == QK_BF16 || p.epi.out_dtype == QK_F16) ? 2 : 4);
@@ -1475,7 +1560,8 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
                         (uintptr_t)p.epi.out % 16 == 0 && (p.epi.ldo * osz) % 16 == 0 &&
                         (b_kn16 ? (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32)
                                 : (b_nk && (uint64_t)mp.bn * (uint64_t)p.sbn < (1ull << 32)));
-        if (ok) return b_kn16 ? launch_mid<true>(p, mp, stream) : launch_mid<false>(p, mp, stream);
+        uint64_t* ctr = mp.nsplit > 1 ? reinterpret_cast<uint64_t*>(ws) : nullptr;
+        if (ok) return b_kn16 ? launch_mid<true>(p, mp, partial, ctr, stream) : launch_mid<false>(p, mp, partial, ctr, stream);
         return launch_qmm_fallback(p, a_ok, b_kn, b_nk, stream);
     }
     const SkinnyPlan sp = skinny_plan(p.M, p.N, p.K);

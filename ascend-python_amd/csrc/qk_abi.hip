@@ -76,6 +76,10 @@ bool parse_plan(const char* spec, PlanOverride& o) {
             r.qmm_dma = v == "1";
         } else if (k == "qmm_mid" && (v == "0" || v == "1")) {
             r.qmm_mid = v == "1";
+        } else if (k == "mid_bm" && (v == "16" || v == "32" || v == "64")) {
+            r.mid_bm = std::atoi(v.c_str());
+        } else if (k == "mid_split" && (v == "1" || v == "2")) {
+            r.mid_split = std::atoi(v.c_str());
         } else if (k == "w4nz" && v == "off") {
             r.w4nz_off = true;
         } else if (k == "w4nz_wg" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 65536) {

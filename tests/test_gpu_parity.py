@@ -7,6 +7,8 @@ rtol 1e-2 / atol 1e-2; W4A16 outputs within rtol 1e-2 / atol 1e-2 of the
 float64 oracle.  Full-size shapes the oracle cannot finish in seconds are
 checked on a row subset plus exact checksums of the whole int32 output.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -226,6 +228,7 @@ def test_quant_matmul_big_tiles_and_split_k(ops, oracle, M, N, K, kn):
     (96, 1024, 2304, True, torch.int32, None),               # 16-row blocks, 9 K stages
     (256, 4096, 512, True, torch.bfloat16, torch.bfloat16),  # [K,N]: 32 x 128 blocks
     (64, 192, 256, True, torch.float16, None),               # [K,N] with N % 128 != 0: 64-column blocks
+    (64, 4096, 8192, True, torch.int8, torch.int32),         # [K,N]: 16 x 128 blocks, K split in two
     (1, 28672, 1024, False, torch.bfloat16, torch.bfloat16), # decode rows on an [N,K] weight: one row of 16
     (7, 4096, 2048, False, torch.float16, None),             # 7 of 16 rows
 ])
@@ -288,6 +291,45 @@ def test_quant_matmul_mid_m_against_split_plan(ops, plan):
     assert torch.equal(mid.view(torch.int16), split.view(torch.int16))
 
 
+def test_abi_quant_matmul_mid_m_split_workspace(ops, oracle):
+    """M = 64 on a [K,N] weight plans a K split finished in-kernel (16 x 128 blocks, device-coherent partials
+    and a tagged counter per tile in the workspace).  The ABI refuses a call without the queried workspace; on a
+    0xFF-filled one every tile is finished once: bit-exact against the oracle on a row subset, and the same
+    on a second call over the same workspace."""
+    say("ABI qk_quant_matmul mid-M split, 0xFF workspace")
+    L = ops.abi()
+    M, N, K = 64, 4096, 4096
+    n = ctypes.c_size_t(0)
+    assert L.qk_quant_matmul_workspace_size(M, N, K, BF16, ctypes.byref(n)) == 0
+    assert n.value > 0, "the [K,N] plan splits K"
+    g = torch.Generator().manual_seed(13)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    s = 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    pt = 1e-2 * torch.rand(M, generator=g)
+    b = torch.randn(N, generator=g).to(torch.bfloat16)
+    ad, wd, sd, ptd, bd = a.to(DEV), w.to(DEV), s.to(DEV), pt.to(DEV), b.to(DEV)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    rc = L.qk_quant_matmul(ad.data_ptr(), K, wd.data_ptr(), N, 1, M, N, K, sd.data_ptr(), N, None, 0,
+                           ptd.data_ptr(), bd.data_ptr(), BF16, out.data_ptr(), BF16, None, 0, _stream())
+    assert rc != 0 and "workspace" in ops.last_error()
+    wsbuf = torch.full((n.value,), 0xFF, dtype=torch.uint8, device=DEV)
+    outs = []
+    for rep in range(2):  # twice on the same workspace: the counters must be reusable
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+        rc = L.qk_quant_matmul(ad.data_ptr(), K, wd.data_ptr(), N, 1, M, N, K, sd.data_ptr(), N, None, 0,
+                               ptd.data_ptr(), bd.data_ptr(), BF16, out.data_ptr(), BF16, wsbuf.data_ptr(),
+                               n.value, _stream())
+        assert rc == 0, ops.last_error()
+        torch.cuda.synchronize()
+        outs.append(out)
+    rows = np.r_[0:4, 30:34, M - 4:M]
+    ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(), pertoken=pt[rows].numpy(), bias=W.bits(b),
+                              bias_dtype=BF16, out_dtype=BF16)
+    assert np.array_equal(to_bits(outs[0])[rows], ref)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 def test_abi_quant_matmul_mid_m_unaligned_rows(ops, oracle):
     """A mid-M shape whose x1 rows are not 16-byte aligned (lda = K + 8) cannot take the direct-to-LDS
     kernel: the library falls back to the tiled kernels (no workspace) with the same results."""
@@ -300,8 +342,11 @@ def test_abi_quant_matmul_mid_m_unaligned_rows(ops, oracle):
     s = 1e-3 + 9e-3 * torch.rand(N, generator=g)
     ad, wd, sd = a_wide.to(DEV), w.to(DEV), s.to(DEV)
     out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    n = ctypes.c_size_t(0)
+    assert L.qk_quant_matmul_workspace_size(M, N, K, BF16, ctypes.byref(n)) == 0
+    wsbuf = torch.empty(max(n.value, 1), dtype=torch.uint8, device=DEV)
     rc = L.qk_quant_matmul(ad.data_ptr(), K + 8, wd.data_ptr(), N, 1, M, N, K, sd.data_ptr(), N, None, 0, None, None,
-                           0, out.data_ptr(), BF16, None, 0, _stream())
+                           0, out.data_ptr(), BF16, wsbuf.data_ptr(), n.value, _stream())
     assert rc == 0, ops.last_error()
     torch.cuda.synchronize()
     ref = oracle.quant_matmul(a_wide[:, :K].contiguous().numpy(), w.numpy(), s.numpy(), out_dtype=BF16)
