@@ -284,6 +284,7 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   qmm_dma=0                                       W8A8 prefill: register-staged kernel instead of the DMA one
 //   qmm_mid=0                                       W8A8 M <= 256: split stream / tiled kernels instead of qmm_mid
 //   mid_bm=<16|32|64>, mid_split=<1|2>              qmm_mid: row block and K split (where the shape allows them)
+//   mid_bn=<64|128>                                 qmm_mid: column block (128 only for a [K,N] weight)
 //   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
 //   w4nz=off                                        NZ int4 weights: unpack to ND and take the row-major kernels
 //   w4nz_wg=<n>                                     NZ decode kernel: workgroups along N
@@ -294,7 +295,7 @@ struct PlanOverride {
     int w4_splits = 0;
     bool qmm_dma = true;
     bool qmm_mid = true;
-    int mid_bm = 0, mid_split = 0;
+    int mid_bm = 0, mid_split = 0, mid_bn = 0;
     int skinny_splits = 0;
     bool w4nz_off = false;
     int w4nz_wg = 0;
@@ -317,6 +318,9 @@ struct QmmArgs {
 };
 hipError_t launch_quant_matmul(const QmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K);
+// the same op on an int8 NZ weight (args.b: [N/16][K/64][64][16]; args.sbk / args.sbn unused)
+hipError_t launch_quant_matmul_nz(const QmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
+size_t quant_matmul_nz_workspace(int64_t M, int64_t N, int64_t K);
 
 struct WqbmmArgs {
     const void* x;

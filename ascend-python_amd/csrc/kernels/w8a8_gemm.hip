@@ -21,6 +21,11 @@ constexpr int kThreads = 256;
 constexpr int BK = 64;        // K bytes per step == K of one i8 MFMA
 constexpr int LDS_ROW = 80;   // padded row stride (bytes) of the LDS tiles
 
+// Weight layouts of the direct-to-LDS kernels: the transposed view of an [N,K] tensor, a [K,N] tensor, and
+// the int8 NZ layout [N/16][K/64][64][16] (1 KB blocks of 16 columns x 64 rows, lane l of a block holding
+// rows 16(l/16)..+15 of column l%16: one v_mfma_i32_16x16x64_i8 B operand per block).
+constexpr int kLayNK = 0, kLayKN = 1, kLayNZ = 2;
+
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
@@ -553,8 +558,11 @@ __global__ __launch_bounds__(64 * NW) void qmm_big(QmmArgs p, int tiles_m, int t
 //   [row][64 B] weight stages ([N,K]):   chunk c of row r at r*64 + 16*(c ^ ((r>>1)&3))
 //   [k][256 B]  weight stages ([K,N]):   chunk c of row k at k*256 + 16*(c ^ h(k)),
 //                                         h(k) = (k&7) | ((k>>4)&1)<<3
-// All three are free of LDS bank conflicts for the fragment reads (b128 row
-// reads; transpose reads for [K,N]), measured with SQ_LDS_BANK_CONFLICT.
+//   NZ weight stages:                    the column block's 16 NZ blocks of one K block, 1 KB each, as
+//                                         they are (fragment reads of 64 lanes x 16 contiguous bytes)
+// All four are free of LDS bank conflicts for the fragment reads (b128 row
+// reads; transpose reads for [K,N]; NZ by construction), the first three
+// measured with SQ_LDS_BANK_CONFLICT.
 namespace dm {
 constexpr int BM = 256, BN = 256, BK = 64, NST = 4, NW = 8, NT = 64 * NW;
 constexpr int TM = 4;                   // 64-row wave tiles: 4 x 8 MFMA tiles
@@ -568,10 +576,11 @@ constexpr int SMEM = RING > OUT_BYTES ? RING : OUT_BYTES;
 
 }  // namespace dm
 
-template <bool B_KN, int OUT>
+template <int BL, int OUT>
 __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int tiles_n, int nsplit,
                                                   int32_t* __restrict__ partial) {
     using namespace dm;
+    constexpr bool B_KN = BL == kLayKN, B_NZ = BL == kLayNZ;
     __shared__ __attribute__((aligned(1024))) int8_t smem[SMEM];
 
     const int tiles = tiles_m * tiles_n;
@@ -599,8 +608,11 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     // buffer views of this tile's operand rows (sizes checked on the host to fit 32 bits)
     const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem;
     const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.a + m0 * p.lda, (uint32_t)(BM * p.lda));
-    const __amdgpu_buffer_rsrc_t rsB = B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
-                                            : make_rsrc(p.b + n0 * p.sbn, (uint32_t)(BN * p.sbn));
+    // an NZ column block: BN/16 consecutive n-blocks of K/64 1 KB blocks, BN * K contiguous bytes
+    const __amdgpu_buffer_rsrc_t rsB = B_NZ   ? make_rsrc(p.b + n0 * p.K, (uint32_t)(BN * p.K))
+                                       : B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
+                                              : make_rsrc(p.b + n0 * p.sbn, (uint32_t)(BN * p.sbn));
+    const uint32_t kblocks = (uint32_t)(p.K >> 6);
     const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)(B_KN ? p.sbk : p.sbn);
     // A [row][128 B]: one instruction = 8 rows 8b..8b+7; lane l -> row l>>3, LDS chunk l&7, and
     // (r>>1)&7 = 4*(b&1) + (l>>4)
@@ -623,7 +635,9 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int b = 4 * gw + i;
-            if constexpr (B_KN)
+            if constexpr (B_NZ)  // n-block b of the column block, K block k0/64: one contiguous 1 KB block
+                dma16(rsB, sbase + st * B_ST + b * 1024, ((uint32_t)b * kblocks + (k0 >> 6)) * 1024u + 16u * lane, 0u);
+            else if constexpr (B_KN)
                 dma16(rsB, sbase + st * B_ST + b * 1024, (i & 1) ? vkn1 : vkn0, (k0 + 4u * b) * ldb);
             else
                 dma16(rsB, sbase + st * B_ST + b * 1024, vrk_b, (uint32_t)(16 * b) * ldb + k0);
@@ -659,7 +673,9 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
         for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i32x4*>(smem + ard + i * 16 * A_KB);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            if constexpr (!B_KN) {
+            if constexpr (B_NZ) {
+                bfr[j] = *reinterpret_cast<const i32x4*>(smem + st * B_ST + (8 * wn + j) * 1024 + 16 * lane);
+            } else if constexpr (!B_KN) {
                 bfr[j] = *reinterpret_cast<const i32x4*>(smem + b_rd + st * B_ST + j * 1024);
             } else {
                 const int8_t* t = smem + t_rd + st * B_ST + 16 * (j ^ xr);
@@ -926,9 +942,12 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
 //   [K,N] weight [256 k][BN B]:    chunk c of row k at k*BN + 16*(c ^ h(k)),
 //       BN = 64:  h(k) = ((k>>2)&1) | ((k>>4)&1)<<1
 //       BN = 128: h(k) = ((k>>1)&3) | ((k>>4)&1)<<2
+//   NZ weight [BN/16 n-blocks][4 K blocks][1 KB]: the weight's own 1 KB
+//       blocks, copied as they are (16 columns x 64 rows; lane l's 16 bytes
+//       are rows 16(l/16)..+15 of column l%16, its MFMA B operand)
 // so the 16 rows of a fragment read (A, [N,K]) and the 16 k rows that two
 // 16-lane groups of one ds_read_b64_tr_b8 address ([K,N]) fall in distinct
-// banks.
+// banks, and an NZ fragment read is 64 lanes x 16 contiguous bytes.
 namespace md {
 constexpr int KS = 256;
 template <int BM, int BN, int NW, int RES>
@@ -1003,10 +1022,12 @@ __device__ __forceinline__ void store8(const QmmEpilogue& e, int64_t m, int64_t 
 // SPLIT: the grid holds nsplit workgroups per tile, each over K / nsplit; each stores its exact int32 tile
 // sums device-coherently to partial[tile][split], and the last to arrive (splitk_last) adds the splits in
 // split order and applies the epilogue.
-template <bool B_KN, int BM, int BN, int NW, int PD, int OUT, bool SPLIT>
+template <int BL, int BM, int BN, int NW, int PD, int OUT, bool SPLIT>
 __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p, int tiles_m, int nsplit,
                                                                      int32_t* __restrict__ partial,
                                                                      uint64_t* __restrict__ ctr, uint64_t tag) {
+    constexpr bool B_KN = BL == kLayKN, B_NZ = BL == kLayNZ;
+    static_assert(!B_NZ || PD == 0, "NZ blocks stream as whole lines without the prefetch wave");
     constexpr int SCRATCH = PD > 0 ? 1024 : 0;  // the prefetch wave's landing block
     using C = md::Cfg<BM, BN, NW, SCRATCH>;
     constexpr int NST = C::NST, TMI = BM / 16, NTJ = C::NTJ, NT = C::NT;
@@ -1030,8 +1051,16 @@ __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p
     const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem;
     const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)(B_KN ? p.sbk : p.sbn);
     const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.a + m0 * p.lda, (uint32_t)((rows - 1) * p.lda + p.K));
-    const __amdgpu_buffer_rsrc_t rsB = B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
-                                            : make_rsrc(p.b + n0 * p.sbn, (uint32_t)((BN - 1) * p.sbn + p.K));
+    // an NZ column block is BN/16 consecutive n-blocks of K/64 blocks each: BN * K contiguous bytes
+    const __amdgpu_buffer_rsrc_t rsB = B_NZ   ? make_rsrc(p.b + n0 * p.K, (uint32_t)(BN * p.K))
+                                       : B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
+                                              : make_rsrc(p.b + n0 * p.sbn, (uint32_t)((BN - 1) * p.sbn + p.K));
+    const uint32_t kblocks = (uint32_t)(p.K >> 6);  // NZ: 1 KB blocks per n-block
+    // NZ DMA: instruction b copies block (n-block b/4 of the column block, K block 4*stage + b%4); the whole
+    // offset goes in voff
+    auto voff_nz = [&](int b, uint32_t k0) {
+        return ((uint32_t)(b >> 2) * kblocks + (k0 >> 6) + (uint32_t)(b & 3)) * 1024u + 16u * (uint32_t)lane;
+    };
     // [row][256 B] DMA (A, [N,K] weight): an instruction covers rows 4b..4b+3; lane l -> row 4b + (l>>4),
     // LDS chunk l&15, global chunk (l&15) ^ (row&15)
     auto voff_rk = [&](int b, uint32_t ld) {
@@ -1059,7 +1088,8 @@ __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p
                 dma16(rsA, lds + q * 1024, voff_rk(q, lda), k0);
             } else {
                 const int b = q - C::A_DMA;
-                if constexpr (B_KN) dma16(rsB, lds + C::A_BYTES + b * 1024, voff_kn(b), k0 * ldb);
+                if constexpr (B_NZ) dma16(rsB, lds + C::A_BYTES + b * 1024, voff_nz(b, k0), 0u);
+                else if constexpr (B_KN) dma16(rsB, lds + C::A_BYTES + b * 1024, voff_kn(b), k0 * ldb);
                 else dma16(rsB, lds + C::A_BYTES + b * 1024, voff_rk(b, ldb), k0);
             }
         }
@@ -1126,7 +1156,9 @@ __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p
 #pragma unroll
         for (int jj = 0; jj < NTJ; ++jj) {
             const int j = cg * NTJ + jj;  // column tile of the block
-            if constexpr (!B_KN) {
+            if constexpr (B_NZ) {
+                bf[jj] = *reinterpret_cast<const i32x4*>(Bs + (4 * j + kq) * 1024 + 16 * lane);
+            } else if constexpr (!B_KN) {
                 const int r = 16 * j + fr;
                 bf[jj] = *reinterpret_cast<const i32x4*>(Bs + r * md::KS + 16 * (ck ^ (r & 15)));
             } else {
@@ -1219,6 +1251,113 @@ __global__ __launch_bounds__(64 * NW + (PD > 0 ? 64 : 0)) void qmm_mid(QmmArgs p
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode on an int8 NZ weight (M <= 16): an HBM weight stream with no split
+// partials.  Workgroup wg owns n-blocks [b0, b1) (16 columns each, NB at most)
+// over all of K; wave w takes K blocks (64 rows) w, w + NW, w + 2NW, ... of
+// all of them.  Per K block a lane loads 16 bytes of x (lane (m, g): x[m,
+// 64kb + 16g .. +16], the A operand of v_mfma_i32_16x16x64_i8) and 16 bytes of
+// each of the NB weight blocks (its B operand as stored), PF K blocks ahead.
+// Loads past a wave's last K block are given an out-of-range buffer offset,
+// so they return zeros without touching memory and the loop needs no tail.
+// The waves' exact int32 sums are added through LDS, and each thread applies
+// the epilogue to 8 consecutive outputs of one row.  Rows past M load row
+// M-1 and are not stored.
+namespace nzd {
+// measured at M=16, K=8192, N=28672: 2 to 5 K blocks in flight, 4 to 16 waves and direct-to-LDS loads in place of
+// register loads all stream 5.0-5.3 TB/s; two blocks in flight were the fastest by a few percent
+constexpr int NW = 8, NT = 64 * NW, PF = 2, NBMAX = 8;
+constexpr int PITCH = 320;  // int32 per 16x16 tile: row r at 16*(r + r/4), so a wave's stores hit 64 banks
+constexpr uint32_t kOff = 0x80000000u;  // an offset past every buffer range
+}  // namespace nzd
+
+template <int NB>
+__global__ __launch_bounds__(nzd::NT) void qmm_nzd(QmmArgs p, int nwg) {
+    using namespace nzd;
+    __shared__ __attribute__((aligned(16))) int32_t red[NW][NB][PITCH];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int wg = blockIdx.x;
+    const int M = (int)p.M;
+    const int64_t NBT = p.N >> 4;
+    const uint32_t KB = (uint32_t)(p.K >> 6);
+    const int b0 = (int)((int64_t)wg * NBT / nwg), nb = (int)((int64_t)(wg + 1) * NBT / nwg) - b0;
+    const int m = c < M ? c : M - 1;
+
+    // sizes checked on the host: (M-1)*lda + K and NB * K * 16 fit in 31 bits
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.a, (uint32_t)((M - 1) * p.lda + p.K));
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.b + (int64_t)b0 * p.K * 16, (uint32_t)(nb * p.K * 16));
+    const uint32_t x_lane = (uint32_t)m * (uint32_t)p.lda + 16u * (uint32_t)g, w_lane = 16u * (uint32_t)lane;
+    uint32_t blk[NB];  // a workgroup with fewer blocks repeats its last one (not stored)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) blk[b] = (uint32_t)(b < nb ? b : nb - 1) * KB * 1024u;
+
+    const int nkb = KB > (uint32_t)wave ? (int)((KB - 1 - (uint32_t)wave) / NW) + 1 : 0;
+    i32x4 xa[PF], wv[PF][NB];
+    auto issue = [&](int it, int sl) {
+        const uint32_t kb = (uint32_t)(wave + it * NW);
+        const bool in = it < nkb;
+        __builtin_amdgcn_sched_barrier(0);
+        xa[sl] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, in ? x_lane + 64u * kb : kOff, 0, 0));
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            wv[sl][b] = __builtin_bit_cast(
+                i32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, in ? blk[b] + kb * 1024u + w_lane : kOff, 0, 0));
+        __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int u = 0; u < PF; ++u) issue(u, u);
+
+    i32x4 acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = (i32x4){0, 0, 0, 0};
+    for (int it0 = 0; it0 < nkb; it0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {  // slot u holds K block it0 + u (zeros past the wave's last one)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u], wv[u][b], acc[b], 0, 0, 0);
+            issue(it0 + u + PF, u);
+        }
+    }
+    // the (zero) loads issued past the end land before the wave leaves
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+    // lane (c, g) holds rows 4g..4g+3 of column c of each block
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][b][16 * (5 * g + r) + c] = acc[b][r];
+    __syncthreads();
+
+    // thread t < 32*NB: block t/32, row (t/2)%16, columns 8*(t%2)..+7; exact int32 sums over the waves
+    const int t = threadIdx.x;
+    if (t >= 32 * NB) return;
+    const int b = t >> 5, row = (t >> 1) & 15, c8 = 8 * (t & 1);
+    if (b >= nb || row >= M) return;
+    const int at = 16 * (row + (row >> 2)) + c8;
+    uint32_t s8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s8[e] = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(&red[w][b][at]);
+        const i32x4 hi = *reinterpret_cast<const i32x4*>(&red[w][b][at + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            s8[e] += (uint32_t)lo[e];
+            s8[4 + e] += (uint32_t)hi[e];
+        }
+    }
+    const int64_t n = ((int64_t)b0 + b) * 16 + c8;
+    switch (p.epi.out_dtype) {
+    case QK_BF16: store8<QK_BF16>(p.epi, row, n, s8); break;
+    case QK_F16: store8<QK_F16>(p.epi, row, n, s8); break;
+    case QK_F32: store8<QK_F32>(p.epi, row, n, s8); break;
+    case QK_I8: store8<QK_I8>(p.epi, row, n, s8); break;
+    default: store8<QK_I32>(p.epi, row, n, s8); break;
+    }
+}
+
 // Exact int32 sum of the split partials, then the common epilogue.
 __global__ __launch_bounds__(kThreads) void qmm_reduce(QmmArgs p, int nsplit, const int32_t* __restrict__ partial) {
     const int64_t total = p.M * p.N;
@@ -1302,8 +1441,8 @@ hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, int
                      (b_kn ? (p.sbk % 16 == 0 && (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32))
                            : (p.sbn % 16 == 0));
     if (dma) {
-        if (b_kn) qmm_dma<true, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
-        else qmm_dma<false, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
+        if (b_kn) qmm_dma<kLayKN, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
+        else qmm_dma<kLayNK, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
     } else if (full) {
         if (b_kn) qmm_big<true, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
         else qmm_big<false, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
@@ -1430,7 +1569,8 @@ MidPlan mid_plan(int64_t M, int64_t N, int64_t K, bool b_kn) {
     if (!plan_override().qmm_mid) return m;  // debug override: the split stream / tiled kernels instead
     if (M <= 0 || M > 256 || (M > 128 && N > 8192) || N <= 0 || N % 64 != 0 || K <= 0 || K % md::KS != 0)
         return m;
-    const int bn = (b_kn && N % 128 == 0) ? 128 : 64;
+    const PlanOverride& ov = plan_override();  // debug override: a row block, column block and / or split
+    const int bn = (b_kn && N % 128 == 0 && ov.mid_bn != 64) ? 128 : 64;
     const int64_t tn = N / bn;
     if (tn * ((M + 15) / 16) >= ((int64_t)1 << 30)) return m;
     // the row block (and, with 128 columns, K split) with the fewest bytes per CU: rounds of workgroups over
@@ -1438,7 +1578,6 @@ MidPlan mid_plan(int64_t M, int64_t N, int64_t K, bool b_kn) {
     // written and read (ties to the larger block, then to no split)
     int bm = 16, ns = 1;
     int64_t best = -1;
-    const PlanOverride& ov = plan_override();  // debug override: a row block and / or a split count
     for (int c : {64, 32, 16}) {
         if (bn == 128 && c == 64) continue;
         if (ov.mid_bm && c != ov.mid_bm) continue;
@@ -1475,46 +1614,46 @@ size_t mid_workspace(const MidPlan& m) {
     return m.nsplit > 1 ? QK_SPLIT_COUNTER_BYTES + (size_t)m.tiles * m.nsplit * m.bm * m.bn * sizeof(int32_t) : 0;
 }
 
-template <bool B_KN, int BM, int BN, int OUT>
+template <int BL, int BM, int BN, int OUT>
 hipError_t launch_mid_o(const QmmArgs& p, const MidPlan& mp, int32_t* partial, uint64_t* ctr, hipStream_t stream) {
     // 8 waves; a prefetch wave 12 stages ahead for a [K,N] weight (measured: it shortens the [K,N]
     // cfg1 shape by a sixth and lengthens the [N,K] one, whose 256-byte rows stream well without it)
-    constexpr int NW = 8, PD = B_KN ? 12 : 0;
+    constexpr int NW = 8, PD = BL == kLayKN ? 12 : 0;
     const dim3 grid((uint32_t)(mp.tiles * mp.nsplit)), block(64 * NW + (PD > 0 ? 64 : 0));
     if (mp.nsplit > 1) {
         if constexpr (BN == 128)  // splits only with 128-column blocks
-            qmm_mid<B_KN, BM, BN, NW, PD, OUT, true><<<grid, block, 0, stream>>>(p, mp.tiles_m, mp.nsplit, partial,
+            qmm_mid<BL, BM, BN, NW, PD, OUT, true><<<grid, block, 0, stream>>>(p, mp.tiles_m, mp.nsplit, partial,
                                                                                 ctr, next_split_tag());
         else
             return hipErrorInvalidValue;
     } else {
-        qmm_mid<B_KN, BM, BN, NW, PD, OUT, false><<<grid, block, 0, stream>>>(p, mp.tiles_m, 1, nullptr, nullptr, 0);
+        qmm_mid<BL, BM, BN, NW, PD, OUT, false><<<grid, block, 0, stream>>>(p, mp.tiles_m, 1, nullptr, nullptr, 0);
     }
     return hipGetLastError();
 }
 
-template <bool B_KN, int BM, int BN>
+template <int BL, int BM, int BN>
 hipError_t launch_mid_t(const QmmArgs& p, const MidPlan& mp, int32_t* partial, uint64_t* ctr, hipStream_t stream) {
     switch (p.epi.out_dtype) {
-    case QK_BF16: return launch_mid_o<B_KN, BM, BN, QK_BF16>(p, mp, partial, ctr, stream);
-    case QK_F16: return launch_mid_o<B_KN, BM, BN, QK_F16>(p, mp, partial, ctr, stream);
-    case QK_F32: return launch_mid_o<B_KN, BM, BN, QK_F32>(p, mp, partial, ctr, stream);
-    case QK_I8: return launch_mid_o<B_KN, BM, BN, QK_I8>(p, mp, partial, ctr, stream);
-    default: return launch_mid_o<B_KN, BM, BN, QK_I32>(p, mp, partial, ctr, stream);
+    case QK_BF16: return launch_mid_o<BL, BM, BN, QK_BF16>(p, mp, partial, ctr, stream);
+    case QK_F16: return launch_mid_o<BL, BM, BN, QK_F16>(p, mp, partial, ctr, stream);
+    case QK_F32: return launch_mid_o<BL, BM, BN, QK_F32>(p, mp, partial, ctr, stream);
+    case QK_I8: return launch_mid_o<BL, BM, BN, QK_I8>(p, mp, partial, ctr, stream);
+    default: return launch_mid_o<BL, BM, BN, QK_I32>(p, mp, partial, ctr, stream);
     }
 }
 
-template <bool B_KN>
+template <int BL>
 hipError_t launch_mid(const QmmArgs& p, const MidPlan& mp, int32_t* partial, uint64_t* ctr, hipStream_t stream) {
-    if constexpr (B_KN) {  // 128-column blocks only for a [K,N] weight
+    if constexpr (BL == kLayKN) {  // 128-column blocks only for a [K,N] weight
         if (mp.bn == 128) {
-            if (mp.bm == 32) return launch_mid_t<B_KN, 32, 128>(p, mp, partial, ctr, stream);
-            return launch_mid_t<B_KN, 16, 128>(p, mp, partial, ctr, stream);
+            if (mp.bm == 32) return launch_mid_t<BL, 32, 128>(p, mp, partial, ctr, stream);
+            return launch_mid_t<BL, 16, 128>(p, mp, partial, ctr, stream);
         }
     }
-    if (mp.bm == 64) return launch_mid_t<B_KN, 64, 64>(p, mp, partial, ctr, stream);
-    if (mp.bm == 32) return launch_mid_t<B_KN, 32, 64>(p, mp, partial, ctr, stream);
-    return launch_mid_t<B_KN, 16, 64>(p, mp, partial, ctr, stream);
+    if (mp.bm == 64) return launch_mid_t<BL, 64, 64>(p, mp, partial, ctr, stream);
+    if (mp.bm == 32) return launch_mid_t<BL, 32, 64>(p, mp, partial, ctr, stream);
+    return launch_mid_t<BL, 16, 64>(p, mp, partial, ctr, stream);
 }
 
 // The kernels that need no workspace and no alignment beyond the tiled kernels' (or none at all).
@@ -1561,7 +1700,7 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
                         (b_kn16 ? (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32)
                                 : (b_nk && (uint64_t)mp.bn * (uint64_t)p.sbn < (1ull << 32)));
         uint64_t* ctr = mp.nsplit > 1 ? reinterpret_cast<uint64_t*>(ws) : nullptr;
-        if (ok) return b_kn16 ? launch_mid<true>(p, mp, partial, ctr, stream) : launch_mid<false>(p, mp, partial, ctr, stream);
+        if (ok) return b_kn16 ? launch_mid<kLayKN>(p, mp, partial, ctr, stream) : launch_mid<kLayNK>(p, mp, partial, ctr, stream);
         return launch_qmm_fallback(p, a_ok, b_kn, b_nk, stream);
     }
     const SkinnyPlan sp = skinny_plan(p.M, p.N, p.K);
@@ -1597,6 +1736,117 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
         }
     }
     return launch_qmm_fallback(p, a_ok, b_kn, b_nk, stream);
+}
+
+// ---------------------------------------------------------------------------
+// W8A8 on an int8 NZ weight (p.b: [N/16][K/64][64][16]; p.sbk and p.sbn unused).  By shape: M <= 16 the
+// decode stream qmm_nzd (no workspace); the mid-M plan qmm_mid on NZ blocks (64-column blocks, no split);
+// whole 256 x 256 tiles qmm_dma on NZ blocks (a K split as planned for the row-major weight); any other
+// shape unpacks the weight to [K,N] in the workspace and runs the row-major kernels on it:
+// [ND weight, 256-byte rounded][that call's workspace].  The C ABI guarantees 16-byte aligned x1 rows
+// (row stride below 2^24), weight and output.
+namespace {
+
+struct NzdPlan {
+    int nb = 0, nwg = 0;
+};
+
+// every CU one workgroup of ceil(N/16 / 256) n-blocks (at most NBMAX), then as few workgroups as give
+// none more
+NzdPlan nzd_plan(int64_t M, int64_t N, int64_t K) {
+    NzdPlan z;
+    if (M < 1 || M > 16 || N < 16 || N % 16 != 0 || K <= 0 || K % 64 != 0) return z;
+    const int64_t nbt = N / 16;
+    int64_t nb = (nbt + 255) / 256;
+    if (nb > nzd::NBMAX) nb = nzd::NBMAX;
+    const int64_t nwg = (nbt + nb - 1) / nb;
+    if (nwg >= ((int64_t)1 << 30)) return z;
+    z.nb = (int)nb;
+    z.nwg = (int)nwg;
+    return z;
+}
+
+hipError_t launch_nzd(const QmmArgs& p, const NzdPlan& z, hipStream_t stream) {
+    const dim3 grid((uint32_t)z.nwg), block(nzd::NT);
+    switch (z.nb) {
+    case 1: qmm_nzd<1><<<grid, block, 0, stream>>>(p, z.nwg); break;
+    case 2: qmm_nzd<2><<<grid, block, 0, stream>>>(p, z.nwg); break;
+    case 3: qmm_nzd<3><<<grid, block, 0, stream>>>(p, z.nwg); break;
+    case 4: qmm_nzd<4><<<grid, block, 0, stream>>>(p, z.nwg); break;
+    case 5: qmm_nzd<5><<<grid, block, 0, stream>>>(p, z.nwg); break;
+    case 6: qmm_nzd<6><<<grid, block, 0, stream>>>(p, z.nwg); break;
+    case 7: qmm_nzd<7><<<grid, block, 0, stream>>>(p, z.nwg); break;
+    default: qmm_nzd<8><<<grid, block, 0, stream>>>(p, z.nwg); break;
+    }
+    return hipGetLastError();
+}
+
+// qmm_dma on NZ blocks: whole tiles and K ranges of whole four-stage rings
+bool nz_dma_ok(const BigPlan& b, int64_t M, int64_t N, int64_t K) {
+    return plan_override().qmm_dma && b.ok && M % dm::BM == 0 && N % dm::BN == 0 &&
+           K % ((int64_t)b.nsplit * dm::BK * dm::NST) == 0;
+}
+
+template <int OUT>
+hipError_t launch_dma_nz(const QmmArgs& p, const BigPlan& b, int32_t* partial, hipStream_t stream) {
+    qmm_dma<kLayNZ, OUT><<<dim3((uint32_t)(b.tiles_m * b.tiles_n * b.nsplit)), dim3(dm::NT), 0, stream>>>(
+        p, b.tiles_m, b.tiles_n, b.nsplit, partial);
+    return hipGetLastError();
+}
+
+size_t round_up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace
+
+size_t quant_matmul_nz_workspace(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    if (nzd_plan(M, N, K).nb) return 0;
+    if (mid_plan(M, N, K, false).bm) return 0;
+    const BigPlan b = big_plan(M, N, K);
+    if (nz_dma_ok(b, M, N, K))
+        return b.nsplit > 1 ? QK_SPLIT_COUNTER_BYTES + (size_t)b.nsplit * (size_t)M * (size_t)N * sizeof(int32_t) : 0;
+    return round_up256((size_t)K * (size_t)N) + quant_matmul_workspace(M, N, K);
+}
+
+hipError_t launch_quant_matmul_nz(const QmmArgs& p, void* workspace, size_t ws_bytes, hipStream_t stream) {
+    if (p.M == 0 || p.N == 0) return hipSuccess;
+    if (p.K == 0) return launch_qmm_fallback(p, false, false, false, stream);  // reads no weight
+    const NzdPlan z = nzd_plan(p.M, p.N, p.K);
+    if (z.nb) return launch_nzd(p, z, stream);
+    const MidPlan mp = mid_plan(p.M, p.N, p.K, false);
+    if (mp.bm) return launch_mid<kLayNZ>(p, mp, nullptr, nullptr, stream);
+    char* ws = static_cast<char*>(workspace);
+    const BigPlan b = big_plan(p.M, p.N, p.K);
+    if (nz_dma_ok(b, p.M, p.N, p.K)) {
+        if (b.nsplit == 1) {
+            switch (p.epi.out_dtype) {
+            case QK_BF16: return launch_dma_nz<QK_BF16>(p, b, nullptr, stream);
+            case QK_F16: return launch_dma_nz<QK_F16>(p, b, nullptr, stream);
+            case QK_F32: return launch_dma_nz<QK_F32>(p, b, nullptr, stream);
+            case QK_I8: return launch_dma_nz<QK_I8>(p, b, nullptr, stream);
+            default: return launch_dma_nz<QK_I32>(p, b, nullptr, stream);
+            }
+        }
+        const size_t need = QK_SPLIT_COUNTER_BYTES + (size_t)b.nsplit * (size_t)p.M * (size_t)p.N * sizeof(int32_t);
+        if (!ws || ws_bytes < need || (uintptr_t)ws % 16 != 0) return hipErrorInvalidValue;
+        int32_t* partial = reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES);
+        const hipError_t e = launch_dma_nz<QK_I32>(p, b, partial, stream);
+        if (e != hipSuccess) return e;
+        int64_t blocks = (p.M * p.N / 4 + kThreads - 1) / kThreads;
+        if (blocks > 65536) blocks = 65536;
+        qmm_reduce<<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(p, b.nsplit, partial);
+        return hipGetLastError();
+    }
+    const size_t nd = round_up256((size_t)p.K * (size_t)p.N);
+    const size_t rest = quant_matmul_workspace(p.M, p.N, p.K);
+    if (!ws || ws_bytes < nd + rest || (uintptr_t)ws % 256 != 0) return hipErrorInvalidValue;
+    const hipError_t e = launch_w8_nz_cast(p.b, false, p.K, p.N, reinterpret_cast<int8_t*>(ws), stream);
+    if (e != hipSuccess) return e;
+    QmmArgs q = p;
+    q.b = reinterpret_cast<const int8_t*>(ws);
+    q.sbk = p.N;
+    q.sbn = 1;
+    return launch_quant_matmul(q, rest ? ws + nd : nullptr, rest, stream);
 }
 
 }  // namespace qk

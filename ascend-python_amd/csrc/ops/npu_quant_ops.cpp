@@ -105,8 +105,22 @@ std::tuple<at::Tensor, at::Tensor> npu_dynamic_quant_meta(const at::Tensor& inpu
 
 // ---------------------------------------------------------------- npu_quant_matmul
 
+// An int4 weight in the NZ layout written by npu_format_cast(w, 29): int32
+// [N/16, K/128, 64, 4] (the shape carries the format; see qk_weight_format_cast).
+bool is_w4_nz(const at::Tensor& w) {
+    return w.scalar_type() == at::kInt && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 4;
+}
+
+// An int8 weight in the NZ layout: int8 [N/16, K/64, 64, 16].
+bool is_w8_nz(const at::Tensor& w) {
+    return w.scalar_type() == at::kChar && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 16;
+}
+
+bool is_nz(const at::Tensor& w) { return is_w4_nz(w) || is_w8_nz(w); }
+
 struct QmmPlan {
     int64_t M, N, K;
+    bool nz;  // x2 is an int8 NZ weight
     at::ScalarType out_type;
     std::vector<int64_t> out_shape;
 };
@@ -118,10 +132,14 @@ QmmPlan quant_matmul_plan(const at::Tensor& x1, const at::Tensor& x2, const at::
     TORCH_CHECK(x1.scalar_type() == at::kChar && x2.scalar_type() == at::kChar, op,
                 ": x1 and x2 must be int8, got ", x1.scalar_type(), " and ", x2.scalar_type());
     TORCH_CHECK(x1.dim() >= 2 && x1.dim() <= 6, op, ": x1 must have 2 to 6 dimensions, got ", x1.dim());
-    TORCH_CHECK(x2.dim() == 2, op, ": x2 must be 2-D [K, N], got ", x2.dim(), " dimensions");
+    // x2 is [K, N] (or the transposed view of [N, K]), or the int8 NZ weight npu_format_cast(x2, 29) writes
+    const bool nz = is_w8_nz(x2);
+    TORCH_CHECK(x2.dim() == 2 || nz, op, ": x2 must be 2-D [K, N] or an int8 NZ weight [N/16, K/64, 64, 16], got ",
+                x2.sizes());
     const int64_t K = x1.size(-1);
-    TORCH_CHECK(x2.size(0) == K, op, ": x1 last dim (", K, ") must equal x2 first dim (", x2.size(0), ")");
-    const int64_t N = x2.size(1);
+    const int64_t x2_k = nz ? x2.size(1) * 64 : x2.size(0);
+    TORCH_CHECK(x2_k == K, op, ": x1 last dim (", K, ") must equal the weight's K (", x2_k, ")");
+    const int64_t N = nz ? x2.size(0) * 16 : x2.size(1);
     const int64_t M = leading_rows(x1);
     const at::ScalarType out_type = output_dtype.value_or(at::kChar);
     TORCH_CHECK(out_type == at::kBFloat16 || out_type == at::kHalf || out_type == at::kChar ||
@@ -155,7 +173,34 @@ QmmPlan quant_matmul_plan(const at::Tensor& x1, const at::Tensor& x2, const at::
     }
     std::vector<int64_t> shape(x1.sizes().begin(), x1.sizes().end());
     shape.back() = N;
-    return {M, N, K, out_type, shape};
+    return {M, N, K, nz, out_type, shape};
+}
+
+// The NZ weight (the layout the reference's matmuls read after npu_format_cast, op_plugin/ops/base_ops/aclops/
+// MmKernelNpu.cpp:303-316): x1 rows and the output 16-byte aligned (a misaligned x1 view is copied).
+at::Tensor quant_matmul_nz(const QmmPlan& pl, at::Tensor x1, const at::Tensor& x2_in, const at::Tensor& scale_in,
+                           const std::optional<at::Tensor>& offset, const std::optional<at::Tensor>& pertoken_scale,
+                           const std::optional<at::Tensor>& bias, at::Tensor out) {
+    if (reinterpret_cast<uintptr_t>(x1.data_ptr()) % 16 != 0) x1 = x1.clone();
+    auto x2 = x2_in.contiguous();
+    if (reinterpret_cast<uintptr_t>(x2.data_ptr()) % 16 != 0) x2 = x2.clone();
+    auto scale = scale_in.scalar_type() == at::kFloat ? scale_in.contiguous() : scale_in.to(at::kFloat);
+    at::Tensor off, pt, b;
+    if (offset.has_value()) off = offset->contiguous();
+    if (pertoken_scale.has_value()) pt = pertoken_scale->contiguous();
+    if (bias.has_value()) b = bias->contiguous();
+    size_t ws_bytes = 0;
+    check_rc(qk_quant_matmul_nz_workspace_size(pl.M, pl.N, pl.K, qk_dtype_of(pl.out_type), &ws_bytes),
+             "npu_quant_matmul");
+    at::Tensor ws = ws_bytes ? workspace_for(x1, ws_bytes) : at::Tensor();
+    const int rc = qk_quant_matmul_nz(
+        x1.data_ptr<int8_t>(), pl.K, x2.data_ptr<int8_t>(), pl.M, pl.N, pl.K, scale.data_ptr<float>(), scale.numel(),
+        off.defined() ? off.data_ptr<float>() : nullptr, off.defined() ? off.numel() : 0,
+        pt.defined() ? pt.data_ptr<float>() : nullptr, b.defined() ? b.data_ptr() : nullptr,
+        b.defined() ? qk_dtype_of(b.scalar_type()) : 0, out.data_ptr(), qk_dtype_of(pl.out_type),
+        ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(x1));
+    check_rc(rc, "npu_quant_matmul");
+    return out;
 }
 
 at::Tensor npu_quant_matmul(const at::Tensor& x1_in, const at::Tensor& x2_in, const at::Tensor& scale_in,
@@ -166,6 +211,7 @@ at::Tensor npu_quant_matmul(const at::Tensor& x1_in, const at::Tensor& x2_in, co
     auto out = at::empty(pl.out_shape, x1_in.options().dtype(pl.out_type));
     if (pl.M == 0 || pl.N == 0) return out;
     auto x1 = x1_in.contiguous();
+    if (pl.nz) return quant_matmul_nz(pl, x1, x2_in, scale_in, offset, pertoken_scale, bias, out);
     // Transposed view of an [N,K] weight is read in place, as the reference
     // flags mat2 instead of copying it (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:40-53).
     at::Tensor x2 = x2_in;
@@ -208,19 +254,6 @@ struct WqPlan {
     bool int4, nz;
     std::vector<int64_t> out_shape;
 };
-
-// An int4 weight in the NZ layout written by npu_format_cast(w, 29): int32
-// [N/16, K/128, 64, 4] (the shape carries the format; see qk_weight_format_cast).
-bool is_w4_nz(const at::Tensor& w) {
-    return w.scalar_type() == at::kInt && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 4;
-}
-
-// An int8 weight in the NZ layout: int8 [N/16, K/64, 64, 16].
-bool is_w8_nz(const at::Tensor& w) {
-    return w.scalar_type() == at::kChar && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 16;
-}
-
-bool is_nz(const at::Tensor& w) { return is_w4_nz(w) || is_w8_nz(w); }
 
 WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at::Tensor& antiquant_scale,
                          const std::optional<at::Tensor>& antiquant_offset,

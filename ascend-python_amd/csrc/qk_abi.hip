@@ -80,6 +80,8 @@ bool parse_plan(const char* spec, PlanOverride& o) {
             r.mid_bm = std::atoi(v.c_str());
         } else if (k == "mid_split" && (v == "1" || v == "2")) {
             r.mid_split = std::atoi(v.c_str());
+        } else if (k == "mid_bn" && (v == "64" || v == "128")) {
+            r.mid_bn = std::atoi(v.c_str());
         } else if (k == "w4nz" && v == "off") {
             r.w4nz_off = true;
         } else if (k == "w4nz_wg" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 65536) {
@@ -148,6 +150,58 @@ bool is_float_out(int dt) { return dt == QK_F16 || dt == QK_BF16 || dt == QK_F32
 constexpr int64_t kMaxGrid = (int64_t)1 << 31;  // gridDim.x limit
 constexpr int64_t kMaxExactK = 131071;           // 131071 * 128 * 128 < 2^31
 
+// The size, output-type and epilogue checks both W8A8 entry points share; fills p's sizes and epilogue.
+int quant_matmul_args(const char* op, int64_t M, int64_t N, int64_t K, const float* scale, int64_t scale_len,
+                      const float* offset, int64_t offset_len, const float* pertoken_scale, const void* bias,
+                      int bias_dtype, void* out, int out_dtype, qk::QmmArgs& p) {
+    if (M < 0 || N < 0 || K < 0) return fail(QK_ERR_ARG, "%s: negative size M=%lld N=%lld K=%lld", op, (long long)M, (long long)N, (long long)K);
+    if (!(is_float_out(out_dtype) || out_dtype == QK_I8 || out_dtype == QK_I32))
+        return fail(QK_ERR_ARG, "%s: unsupported output dtype %d", op, out_dtype);
+    if (K > kMaxExactK) return fail(QK_ERR_UNSUPPORTED, "%s: K=%lld exceeds %lld, the int32-exact bound", op, (long long)K, (long long)kMaxExactK);
+    if (M == 0 || N == 0) return QK_OK;
+    if (!out) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    if (out_dtype != QK_I32) {
+        if (!scale) return fail(QK_ERR_ARG, "%s: scale is required for output dtype %d", op, out_dtype);
+        if (scale_len != 1 && scale_len != N)
+            return fail(QK_ERR_ARG, "%s: scale must have 1 or N=%lld elements (got %lld)", op, (long long)N, (long long)scale_len);
+    }
+    if (offset) {
+        if (out_dtype != QK_I8) return fail(QK_ERR_ARG, "%s: offset is only valid with an int8 output", op);
+        if (offset_len != 1 && offset_len != N)
+            return fail(QK_ERR_ARG, "%s: offset must have 1 or N elements (got %lld)", op, (long long)offset_len);
+    }
+    if (pertoken_scale && !is_float_out(out_dtype))
+        return fail(QK_ERR_ARG, "%s: pertoken_scale needs a float16/bfloat16/float32 output", op);
+    if (bias) {
+        if (!(bias_dtype == QK_I32 || is_half(bias_dtype) || bias_dtype == QK_F32))
+            return fail(QK_ERR_ARG, "%s: bias dtype %d unsupported", op, bias_dtype);
+        if (bias_dtype != QK_I32 && !is_float_out(out_dtype))
+            return fail(QK_ERR_ARG, "%s: a float bias needs a float output (int8/int32 outputs take an int32 bias)", op);
+    }
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.epi.scale = scale;
+    p.epi.scale_per_ch = scale_len != 1;
+    p.epi.offset = offset;
+    p.epi.offset_per_ch = offset_len != 1;
+    p.epi.pertoken = pertoken_scale;
+    p.epi.bias = bias;
+    p.epi.bias_dtype = bias ? bias_dtype : 0;
+    p.epi.out = out;
+    p.epi.ldo = N;
+    p.epi.out_dtype = out_dtype;
+    return QK_OK;
+}
+
+int check_workspace(const char* op, size_t need, const void* workspace, size_t workspace_bytes) {
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(QK_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, workspace_bytes);
+    if (need > 0 && (uintptr_t)workspace % 256 != 0)
+        return fail(QK_ERR_WORKSPACE, "%s: the workspace must be 256-byte aligned", op);
+    return QK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -189,60 +243,60 @@ int qk_quant_matmul(const int8_t* x1, int64_t ldx1, const int8_t* x2, int64_t x2
                     int out_dtype, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
     g_last_error.clear();
     const char* op = "npu_quant_matmul";
-    if (M < 0 || N < 0 || K < 0) return fail(QK_ERR_ARG, "%s: negative size M=%lld N=%lld K=%lld", op, (long long)M, (long long)N, (long long)K);
-    if (!(is_float_out(out_dtype) || out_dtype == QK_I8 || out_dtype == QK_I32))
-        return fail(QK_ERR_ARG, "%s: unsupported output dtype %d", op, out_dtype);
-    if (K > kMaxExactK) return fail(QK_ERR_UNSUPPORTED, "%s: K=%lld exceeds %lld, the int32-exact bound", op, (long long)K, (long long)kMaxExactK);
-    if (M == 0 || N == 0) return QK_OK;
-    if (!out || (K > 0 && (!x1 || !x2))) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    qk::QmmArgs p;
+    int rc = quant_matmul_args(op, M, N, K, scale, scale_len, offset, offset_len, pertoken_scale, bias, bias_dtype,
+                               out, out_dtype, p);
+    if (rc != QK_OK || M == 0 || N == 0) return rc;
+    if (K > 0 && (!x1 || !x2)) return fail(QK_ERR_ARG, "%s: null pointer", op);
     if (ldx1 < K) return fail(QK_ERR_ARG, "%s: ldx1=%lld < K=%lld", op, (long long)ldx1, (long long)K);
     if (!(x2_stride_k == 1 || x2_stride_n == 1))
         return fail(QK_ERR_ARG, "%s: x2 must be [K,N]-contiguous or a transposed view of [N,K] (strides %lld,%lld)", op,
                     (long long)x2_stride_k, (long long)x2_stride_n);
-    if (out_dtype != QK_I32) {
-        if (!scale) return fail(QK_ERR_ARG, "%s: scale is required for output dtype %d", op, out_dtype);
-        if (scale_len != 1 && scale_len != N)
-            return fail(QK_ERR_ARG, "%s: scale must have 1 or N=%lld elements (got %lld)", op, (long long)N, (long long)scale_len);
-    }
-    if (offset) {
-        if (out_dtype != QK_I8) return fail(QK_ERR_ARG, "%s: offset is only valid with an int8 output", op);
-        if (offset_len != 1 && offset_len != N)
-            return fail(QK_ERR_ARG, "%s: offset must have 1 or N elements (got %lld)", op, (long long)offset_len);
-    }
-    if (pertoken_scale && !is_float_out(out_dtype))
-        return fail(QK_ERR_ARG, "%s: pertoken_scale needs a float16/bfloat16/float32 output", op);
-    if (bias) {
-        if (!(bias_dtype == QK_I32 || is_half(bias_dtype) || bias_dtype == QK_F32))
-            return fail(QK_ERR_ARG, "%s: bias dtype %d unsupported", op, bias_dtype);
-        if (bias_dtype != QK_I32 && !is_float_out(out_dtype))
-            return fail(QK_ERR_ARG, "%s: a float bias needs a float output (int8/int32 outputs take an int32 bias)", op);
-    }
-    const size_t need = qk::quant_matmul_workspace(M, N, K);
-    if (need > 0 && (!workspace || workspace_bytes < need))
-        return fail(QK_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", op, need, workspace_bytes);
-    if (need > 0 && (uintptr_t)workspace % 256 != 0)
-        return fail(QK_ERR_WORKSPACE, "%s: the workspace must be 256-byte aligned", op);
-
-    qk::QmmArgs p;
+    if ((rc = check_workspace(op, qk::quant_matmul_workspace(M, N, K), workspace, workspace_bytes)) != QK_OK) return rc;
     p.a = x1;
     p.lda = ldx1;
     p.b = x2;
     p.sbk = x2_stride_k;
     p.sbn = x2_stride_n;
-    p.M = M;
-    p.N = N;
-    p.K = K;
-    p.epi.scale = scale;
-    p.epi.scale_per_ch = scale_len != 1;
-    p.epi.offset = offset;
-    p.epi.offset_per_ch = offset_len != 1;
-    p.epi.pertoken = pertoken_scale;
-    p.epi.bias = bias;
-    p.epi.bias_dtype = bias ? bias_dtype : 0;
-    p.epi.out = out;
-    p.epi.ldo = N;
-    p.epi.out_dtype = out_dtype;
     return launched(qk::launch_quant_matmul(p, workspace, workspace_bytes, (hipStream_t)stream), op);
+}
+
+int qk_quant_matmul_nz_workspace_size(int64_t M, int64_t N, int64_t K, int out_dtype, size_t* bytes) {
+    g_last_error.clear();
+    (void)out_dtype;
+    if (!bytes) return fail(QK_ERR_ARG, "npu_quant_matmul: bytes is null");
+    if (M < 0 || N < 0 || K < 0) return fail(QK_ERR_ARG, "npu_quant_matmul: negative size");
+    *bytes = qk::quant_matmul_nz_workspace(M, N, K);
+    return QK_OK;
+}
+
+int qk_quant_matmul_nz(const int8_t* x1, int64_t ldx1, const int8_t* x2_nz, int64_t M, int64_t N, int64_t K,
+                       const float* scale, int64_t scale_len, const float* offset, int64_t offset_len,
+                       const float* pertoken_scale, const void* bias, int bias_dtype, void* out, int out_dtype,
+                       void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_quant_matmul";
+    qk::QmmArgs p;
+    int rc = quant_matmul_args(op, M, N, K, scale, scale_len, offset, offset_len, pertoken_scale, bias, bias_dtype,
+                               out, out_dtype, p);
+    if (rc != QK_OK || M == 0 || N == 0) return rc;
+    if (K % 64 != 0 || N % 16 != 0)
+        return fail(QK_ERR_ARG, "%s: an NZ weight needs K %% 64 == 0 and N %% 16 == 0 (K=%lld, N=%lld)", op,
+                    (long long)K, (long long)N);
+    if (K > 0 && (!x1 || !x2_nz)) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    if (ldx1 < K || ldx1 % 16 != 0 || ldx1 >= ((int64_t)1 << 24))
+        return fail(QK_ERR_ARG, "%s: with an NZ weight ldx1 must be a multiple of 16 in [K, 2^24) (ldx1=%lld, K=%lld)",
+                    op, (long long)ldx1, (long long)K);
+    if ((uintptr_t)x1 % 16 != 0 || (uintptr_t)x2_nz % 16 != 0 || (uintptr_t)out % 16 != 0)
+        return fail(QK_ERR_ARG, "%s: with an NZ weight x1, x2 and out must be 16-byte aligned", op);
+    if ((rc = check_workspace(op, qk::quant_matmul_nz_workspace(M, N, K), workspace, workspace_bytes)) != QK_OK)
+        return rc;
+    p.a = x1;
+    p.lda = ldx1;
+    p.b = x2_nz;
+    p.sbk = 0;
+    p.sbn = 0;
+    return launched(qk::launch_quant_matmul_nz(p, workspace, workspace_bytes, (hipStream_t)stream), op);
 }
 
 int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weight_dtype, int64_t group_size,

@@ -69,9 +69,10 @@ QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, 
 
 ABI_SYMBOLS = (
     "qk_last_error", "qk_abi_version", "qk_debug_set_plan", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",
-    "qk_quant_matmul", "qk_weight_quant_bmm_workspace_size", "qk_weight_quant_bmm", "qk_weight_quant_bmm_noalloc",
-    "qk_int4_pack", "qk_weight_format_cast", "qk_quantize_per_tensor", "qk_quantize_per_channel", "qk_dequantize",
-    "qk_rms_norm", "qk_rms_norm_quant", "qk_swiglu", "qk_swiglu_quant",
+    "qk_quant_matmul", "qk_quant_matmul_nz_workspace_size", "qk_quant_matmul_nz", "qk_weight_quant_bmm_workspace_size",
+    "qk_weight_quant_bmm", "qk_weight_quant_bmm_noalloc", "qk_int4_pack", "qk_weight_format_cast",
+    "qk_quantize_per_tensor", "qk_quantize_per_channel", "qk_dequantize", "qk_rms_norm", "qk_rms_norm_quant",
+    "qk_swiglu", "qk_swiglu_quant",
 )
 
 _abi = None
@@ -90,6 +91,8 @@ def abi() -> ctypes.CDLL:
         L.qk_dynamic_quant.argtypes = [P, I, I64, I64, P, P, P, P]
         L.qk_quant_matmul_workspace_size.argtypes = [I64, I64, I64, I, ctypes.POINTER(SZ)]
         L.qk_quant_matmul.argtypes = [P, I64, P, I64, I64, I64, I64, I64, P, I64, P, I64, P, P, I, P, I, P, SZ, P]
+        L.qk_quant_matmul_nz_workspace_size.argtypes = [I64, I64, I64, I, ctypes.POINTER(SZ)]
+        L.qk_quant_matmul_nz.argtypes = [P, I64, P, I64, I64, I64, P, I64, P, I64, P, P, I, P, I, P, SZ, P]
         L.qk_weight_quant_bmm_workspace_size.argtypes = [I64, I64, I64, I, I64, ctypes.POINTER(SZ)]
         L.qk_weight_quant_bmm.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P, SZ, P]
         L.qk_weight_quant_bmm_noalloc.argtypes = [P, I, P, I, P, P, I, I64, I64, I64, I64, P, I, P, I, P]

@@ -5,9 +5,10 @@ One step = one pass of the path over one batch of synthetic input:
         per-token x per-channel scales, bf16 bias, bf16 out)            (W8A8 prefill)
   cfg3  npu_weight_quant_batchmatmul(x bf16 [16,4096], W int4 [4096,11008], group 128,
         fp16 scale + offset, bf16 out)                                  (W4A16 decode)
-        on the weight in the FRACTAL_NZ (MFMA-tiled) layout, cast once with
-        npu_format_cast(w, 29) when the weights are loaded, as the reference casts
-        matmul weights to FRACTAL_NZ; the row-major (ND) weight is timed beside it
+Both weights are in the FRACTAL_NZ (MFMA-tiled) layout, cast once with
+npu_format_cast(w, 29) when the weights are loaded (not timed), as the reference
+casts matmul weights to FRACTAL_NZ before its matmuls; each kernel on the
+row-major (ND) weight is timed beside it and reported as `nd_weight`.
 Operand sets rotate so the weights streamed per step never sit in the 256 MB
 Infinity Cache.  Per-kernel durations come from HIP events recorded on the
 stream the kernels run on: runs of back-to-back launches of each kernel over the
@@ -301,7 +302,14 @@ def other_configs(q, W, dev, min_launches: int) -> dict:
                                            output_dtype=torch.bfloat16), 32)
     res["cfg1_w8a8_m128_k4096_n4096_nk_view"] = {"avg_us": round(t * 1e6, 2),
                                                  "TOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1)}
+    # and cast once (untimed) to the int8 NZ layout: 1 KB blocks, each the B operand of one int8 MFMA
+    wz = [q.npu_format_cast(w, q.ACL_FORMAT_FRACTAL_NZ) for w in wt]  # the [K,N] view, made contiguous
     del wt
+    t = timed(lambda i: q.npu_quant_matmul(xq, wz[i % 32], sc, pertoken_scale=xs, bias=b,
+                                           output_dtype=torch.bfloat16), 32)
+    res["cfg1_w8a8_m128_k4096_n4096_nz"] = {"avg_us": round(t * 1e6, 2),
+                                            "TOPS": round(2 * c.M * c.N * c.K / t / 1e12, 1)}
+    del wz
 
     # cfg2: decode-shaped W8A8, K=8192, N=28672, M in {1,4,16}; W 235 MB per set, 3 sets
     c0 = W.CFG2[0]
@@ -315,7 +323,18 @@ def other_configs(q, W, dev, min_launches: int) -> dict:
         nb = c.K * c.N + c.M * c.K + 4 * c.M + 4 * c.N + 2 * c.M * c.N
         res[f"cfg2_w8a8_m{c.M}_k8192_n28672"] = {"avg_us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
                                                  "hbm_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4)}
+    # the same weights cast once (untimed) to the int8 NZ layout: the no-split decode stream
+    wz = [q.npu_format_cast(w, q.ACL_FORMAT_FRACTAL_NZ) for w in ws]
     del ws
+    for c in W.CFG2:
+        x = torch.randn((c.M, c.K), generator=g, device=dev).half()
+        xq, xs = q.npu_dynamic_quant(x)
+        t = timed(lambda i: q.npu_quant_matmul(xq, wz[i % 3], sc, pertoken_scale=xs, output_dtype=torch.bfloat16),
+                  12)
+        nb = c.K * c.N + c.M * c.K + 4 * c.M + 4 * c.N + 2 * c.M * c.N
+        res[f"cfg2_w8a8_m{c.M}_k8192_n28672_nz"] = {"avg_us": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1),
+                                                    "hbm_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4)}
+    del wz
 
     # cfg3 M=2048: W4A16 prefill, K=4096, N=11008, group 128, fp16 scale + offset
     c = W.CFG3[1]
@@ -381,6 +400,8 @@ def main():
         ws4.append(torch.randint(-127, 128, (c4.K, c4.N), generator=g, device=dev, dtype=torch.int8))
     scale4 = d4["w_scale"].to(dev)
     bias4 = d4["bias"].to(dev)
+    # weight-load-time format cast (not timed): int8 NZ blocks, each one MFMA B operand
+    wz4 = [q.npu_format_cast(w, q.ACL_FORMAT_FRACTAL_NZ) for w in ws4]
 
     # ---------------- cfg3 M=16 operands
     c3 = W.CFG3[0]
@@ -406,7 +427,7 @@ def main():
         xq, xsc = q.npu_dynamic_quant(xs4[s4])
         if ev is not None:
             ev[1].record()
-        out = q.npu_quant_matmul(xq, ws4[s4], scale4, pertoken_scale=xsc, bias=bias4, output_dtype=torch.bfloat16)
+        out = q.npu_quant_matmul(xq, wz4[s4], scale4, pertoken_scale=xsc, bias=bias4, output_dtype=torch.bfloat16)
         if ev is not None:
             ev[2].record()
         o3 = q.npu_weight_quant_batchmatmul(x3, wz3[s3], sc3[s3], of3[s3], antiquant_group_size=128)
@@ -452,9 +473,13 @@ def main():
                                output_dtype=torch.bfloat16)
 
     xq_sets = [q.npu_dynamic_quant(xs4[s]) for s in range(W8A8_SETS)]
-    gemm_t = launch_runs(lambda i: q.npu_quant_matmul(xq_sets[i % W8A8_SETS][0], ws4[i % W8A8_SETS], scale4,
-                                                      pertoken_scale=xq_sets[i % W8A8_SETS][1], bias=bias4,
-                                                      output_dtype=torch.bfloat16), 8, args.min_launches, prime)
+
+    def gemm(wset):
+        return lambda i: q.npu_quant_matmul(xq_sets[i % W8A8_SETS][0], wset[i % W8A8_SETS], scale4,
+                                            pertoken_scale=xq_sets[i % W8A8_SETS][1], bias=bias4,
+                                            output_dtype=torch.bfloat16)
+    gemm_t = launch_runs(gemm(wz4), 8, args.min_launches, prime)
+    gemm_nd_t = launch_runs(gemm(ws4), 8, args.min_launches, prime)
     del xq_sets
     w4_t = launch_runs(lambda i: q.npu_weight_quant_batchmatmul(x3, wz3[i % W4_SETS], sc3[i % W4_SETS],
                                                                 of3[i % W4_SETS], antiquant_group_size=128),
@@ -485,6 +510,7 @@ def main():
     gemm_step_s = float(np.mean(t_gemm))
     gemm_s = gemm_t["s"]
     tops = ops4 / gemm_s / 1e12
+    gemm_nd_s = gemm_nd_t["s"]
     bytes4 = c4.M * c4.K + c4.K * c4.N + 4 * c4.M + 4 * c4.N + 2 * c4.N + 2 * c4.M * c4.N
     ng = c3.K // c3.group
     bytes3 = c3.M * c3.K * 2 + c3.K * c3.N // 2 + 2 * 2 * ng * c3.N + c3.M * c3.N * 2
@@ -498,7 +524,7 @@ def main():
     traffic = hbm_traffic()
     t_w4 = traffic.get("w4nz_decode")
     w4nd_s = w4nd_t["s"]
-    t_gemm_traffic = traffic.get("qmm_dma", traffic.get("qmm_big"))
+    t_gemm_traffic = traffic.get("qmm_dma_nz")
 
     line = {
         "metric": "W8A8 GEMM TOPS (M=4096) + W4A16 decode GB/s (M=16); % of MI355X roofline",
@@ -514,14 +540,21 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded; see op_plugin_amd/workloads.py)",
         "config": {"workload": "cfg4 W8A8 prefill: dynamic quant fp16 [4096,8192] + quant_matmul int8 "
-                               "[4096,8192]x[8192,8192] bf16 out; cfg3 W4A16 decode M=16 K=4096 N=11008 G=128",
+                               "[4096,8192]x[8192,8192] bf16 out; cfg3 W4A16 decode M=16 K=4096 N=11008 G=128; "
+                               "weights in FRACTAL_NZ (cast once at load)",
                    "w8a8_operand_sets": W8A8_SETS, "w4a16_operand_sets": W4_SETS},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
                      "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": t_gemm_traffic,
                      "kernel": "qmm (W8A8 GEMM)", "avg_us": round(gemm_s * 1e6, 2),
                      "algorithmic": f"2*M*N*K = {ops4:.0f} int8 ops per launch",
                      "timing": timing_note(gemm_t) + ", rotating over the 4 operand sets",
-                     "avg_us_event_pair_in_step": round(gemm_step_s * 1e6, 2)},
+                     "avg_us_event_pair_in_step": round(gemm_step_s * 1e6, 2),
+                     "weight_format": "FRACTAL_NZ (npu_format_cast(w, 29) once at weight load; kernel qmm_dma on "
+                                      "NZ blocks)",
+                     "nd_weight": {"avg_us": round(gemm_nd_s * 1e6, 2), "TOPS": round(ops4 / gemm_nd_s / 1e12, 2),
+                                   "frac": round(ops4 / gemm_nd_s / 1e12 / PEAK_I8_TOPS, 4),
+                                   "traffic": traffic.get("qmm_dma"),
+                                   "kernel": "qmm_dma ([K, N] row-major weight)", "timing": timing_note(gemm_nd_t)}},
         "secondary": {
             "metric": "W4A16 decode GB/s (M=16)", "value": round(gbs3, 1), "unit": "GB/s",
             "roofline": {"bound": "hbm", "achieved": round(gbs3, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",

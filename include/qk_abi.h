@@ -149,6 +149,35 @@ int qk_quant_matmul(const int8_t* x1, int64_t ldx1,
                     void* workspace, size_t workspace_bytes, qk_stream_t stream);
 
 /*
+ * npu_quant_matmul (W8A8) on an int8 weight in the NZ layout, phase 1: the
+ * workspace bytes qk_quant_matmul_nz needs for this shape (0 when none).
+ */
+int qk_quant_matmul_nz_workspace_size(int64_t M, int64_t N, int64_t K, int out_dtype, size_t* bytes);
+
+/*
+ * npu_quant_matmul (W8A8) on an int8 weight in the NZ layout, phase 2 -- the
+ * same op as qk_quant_matmul with x2 already cast to the device-native tiled
+ * format, as the reference casts matmul weights to FRACTAL_NZ before its
+ * matmuls (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:303-316,
+ * op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:103-107) and hands
+ * aclnnQuantMatmul* the NZ tensor behind EXEC_NPU_CMD
+ * (op_plugin/utils/op_api_common.h:552-566).
+ * x2_nz: int8 [N/16][K/64][64][16] as qk_weight_format_cast writes it from
+ * an int8 [K,N] weight (K % 64 == 0, N % 16 == 0).  x1, x2_nz and out must be
+ * 16-byte aligned, ldx1 a multiple of 16 below 2^24.  Every other argument,
+ * the arithmetic and the result are those of qk_quant_matmul (bit-identical
+ * outputs for the same weight in either layout).
+ */
+int qk_quant_matmul_nz(const int8_t* x1, int64_t ldx1, const int8_t* x2_nz,
+                       int64_t M, int64_t N, int64_t K,
+                       const float* scale, int64_t scale_len,
+                       const float* offset, int64_t offset_len,
+                       const float* pertoken_scale,
+                       const void* bias, int bias_dtype,
+                       void* out, int out_dtype,
+                       void* workspace, size_t workspace_bytes, qk_stream_t stream);
+
+/*
  * npu_weight_quant_batchmatmul, phase 1 (see qk_quant_matmul_workspace_size).
  */
 int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weight_dtype,
