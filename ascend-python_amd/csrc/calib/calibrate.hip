@@ -14,10 +14,10 @@
 //  calib_dma_fill    the rate at which one CU fills its LDS by direct
 //                    global->LDS loads (buffer_load_dwordx4 ... lds, as the
 //                    GEMM kernels stage operands): NW waves each keep 16 such
-//                    1 KB loads in flight, from a span that stays in L2 or one
-//                    that streams from HBM, in row pieces of PIECE contiguous
-//                    bytes (the rest of each 1 KB load from rows `rowstride`
-//                    apart, as a [K,N] weight's column block is read).
+//                    1 KB loads in flight, in row pieces of PIECE contiguous
+//                    bytes from rows `rowstride` apart (rowstride == PIECE:
+//                    one contiguous KB), from a span that stays in L2 or one
+//                    read once from HBM.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -133,8 +133,8 @@ int qk_calib_stream_read(const void* buf, int64_t bytes, int grid, uint32_t* out
     return (int)hipGetLastError();
 }
 
-// variant: 0 = 4 waves, 1 = 8 waves, 2 = 16 waves (256-byte pieces); 3 = 8 waves, 128-byte pieces;
-// 4 = 8 waves, 64-byte pieces.  buf holds span + 64 * rowstride bytes; out holds grid words.
+// variant: 0 = 4 waves, 1 = 8 waves, 2 = 16 waves (256-byte pieces).  buf holds span + 64 * rowstride
+// bytes; out holds grid words.
 int qk_calib_dma_fill(int variant, int grid, const void* buf, uint32_t span, uint32_t rowstride, int n_instr,
                       uint32_t stride_wg, int32_t* out, hipStream_t stream) {
     const int8_t* b = static_cast<const int8_t*>(buf);
@@ -142,8 +142,6 @@ int qk_calib_dma_fill(int variant, int grid, const void* buf, uint32_t span, uin
     case 0: calib_dma_fill<4, 256><<<grid, 256, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
     case 1: calib_dma_fill<8, 256><<<grid, 512, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
     case 2: calib_dma_fill<16, 256><<<grid, 1024, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
-    case 3: calib_dma_fill<8, 128><<<grid, 512, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
-    case 4: calib_dma_fill<8, 64><<<grid, 512, 0, stream>>>(b, span, rowstride, n_instr, stride_wg, out); break;
     default: return -1;
     }
     return (int)hipGetLastError();

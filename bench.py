@@ -194,8 +194,9 @@ def timing_note(t: dict) -> str:
 def calibrate(dev, min_launches: int) -> dict:
     """Ceilings of this box for the roofline figures: the int8 MFMA issue rate with register operands (constant
     and pseudo-random bits: the clock is power-limited by the bits the MFMA unit toggles), the read rate of
-    one launch streaming a buffer of the cfg3 decode weight's size, a device copy, and the launch-to-launch
-    floor of an empty kernel.  Kernels: op_plugin_amd/libqk_calib.so (measurement only)."""
+    one launch streaming a buffer of the cfg3 decode weight's size, a device copy, the launch-to-launch
+    floor of an empty kernel, HBM streaming reads that touch each byte once, and the LDS fill rate of
+    direct global->LDS loads.  Kernels: op_plugin_amd/libqk_calib.so (measurement only)."""
     import ctypes
     import torch
     from op_plugin_amd import LIB_PATH
@@ -236,25 +237,35 @@ def calibrate(dev, min_launches: int) -> dict:
     t = launch_runs(lambda i: one.fill_(i), 24, min_launches, prime)
     res["launch_floor_us"] = round(t["s"] * 1e6, 2)
     del bufs, dst
-    # per-CU fill rate of direct global->LDS loads: 256 workgroups, 2 MB each, 16 loads in flight per wave,
-    # from a 2 MB span every XCD keeps in its L2 (contiguous rows) and from a 510 MB span that streams from
-    # HBM (rows 4096 B apart, as a [K,N] weight's column block is read)
+    # HBM streaming ceilings: a 1 GiB buffer (4x the 256 MB Infinity Cache) read once per launch, and reads of
+    # the cfg2 weight's size (235 MB), by plain 16-byte loads; then the rate at which direct global->LDS loads
+    # (buffer_load_dwordx4 ... lds, 1 KB contiguous per load, 16 in flight per wave, 256 workgroups) fill
+    # LDS, from a 2 MB span every XCD keeps in its L2 and from the 1 GiB buffer, each byte read once
     L.qk_calib_dma_fill.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                     ctypes.c_int, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
-    big = torch.empty((511 << 20), dtype=torch.int8, device=dev)
+    gib = 1 << 30
+    big = torch.empty(gib + (1 << 20), dtype=torch.int8, device=dev)
+    big.random_()
+    # (the 235 MB read rotates over three regions of the buffer, the working set of cfg2's three weight sets)
+    for name, nbytes, nreg in (("stream_read_1GiB", gib, 1), ("stream_read_235MB_3_regions", 235 << 20, 3)):
+        g = (nbytes // 16 + 1024 * 8 - 1) // (1024 * 8)
+        bout = torch.empty(g * 1024, dtype=torch.int32, device=dev)
+        t = launch_runs(lambda i: L.qk_calib_stream_read(big.data_ptr() + (i % nreg) * nbytes, nbytes, g,
+                                                         bout.data_ptr(), st), 3, 9, prime)
+        res[name] = {"us": round(t["s"] * 1e6, 1), "TB/s": round(nbytes / t["s"] / 1e12, 2),
+                     "frac_of_8000": round(nbytes / t["s"] / 1e9 / PEAK_HBM_GBS, 4)}
+        del bout
     fout = torch.empty(256, dtype=torch.int32, device=dev)
     fill = {}
-    for where, span, stride_wg, cases in (("l2_2MB", 2 << 20, 8192, ((0, 4, 256), (1, 8, 256), (2, 16, 256))),
-                                         ("hbm_510MB_rowstride4096", 510 << 20, 2 << 20,
-                                          ((1, 8, 256), (3, 8, 128), (4, 8, 64)))):
-        for v, nw, piece in cases:
-            rowstride = piece if where.startswith("l2") else 4096
-            n_instr = 2048 // nw
-            t = launch_runs(lambda i: L.qk_calib_dma_fill(v, 256, big.data_ptr(), span, rowstride, n_instr, stride_wg,
+    for where, span, per_wg in (("l2_2MB", 2 << 20, 2 << 20), ("hbm_1GiB_once", gib, gib // 256)):
+        for v, nw in ((0, 4), (1, 8), (2, 16)):
+            n_instr = per_wg // 1024 // nw
+            stride_wg = 8192 if where.startswith("l2") else per_wg
+            t = launch_runs(lambda i: L.qk_calib_dma_fill(v, 256, big.data_ptr(), span, 256, n_instr, stride_wg,
                                                           fout.data_ptr(), st), 2, 8, prime)
             nb = 256 * nw * n_instr * 1024
-            fill[f"{where}_{nw}waves_{piece}B"] = {"us": round(t["s"] * 1e6, 1), "TB/s": round(nb / t["s"] / 1e12, 2),
-                                                   "GB/s_per_CU": round(nb / t["s"] / 256 / 1e9, 1)}
+            fill[f"{where}_{nw}waves"] = {"us": round(t["s"] * 1e6, 1), "TB/s": round(nb / t["s"] / 1e12, 2),
+                                          "GB/s_per_CU": round(nb / t["s"] / 256 / 1e9, 1)}
     res["dma_fill"] = fill
     return res
 
