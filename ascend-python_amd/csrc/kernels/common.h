@@ -288,6 +288,8 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
 //   w4nz=off                                        NZ int4 weights: unpack to ND and take the row-major kernels
 //   w4nz_wg=<n>                                     NZ decode kernel: workgroups along N
+//   w4nz_nit=<1..8>                                 NZ decode kernel: 128-row superblocks per wave (K/128 must
+//                                                   split evenly into at most 16 waves of them)
 struct PlanOverride {
     int w4_stream_nwave = 0, w4_stream_nkb = 0, w4_stream_pf = 0;  // 0: the planner's choice
     bool w4_stream_off = false;
@@ -298,7 +300,7 @@ struct PlanOverride {
     int mid_bm = 0, mid_split = 0, mid_bn = 0;
     int skinny_splits = 0;
     bool w4nz_off = false;
-    int w4nz_wg = 0;
+    int w4nz_wg = 0, w4nz_nit = 0;
 };
 const PlanOverride& plan_override();
 bool set_plan_override(const char* spec);  // false: spec not understood (override unchanged)

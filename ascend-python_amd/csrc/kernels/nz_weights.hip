@@ -549,8 +549,9 @@ NzPlan nz_plan(const WqbmmArgs& p) {
     const int64_t S = p.K / 128, NBT = p.N / 16;
     // superblocks per wave: the fewest that give at most 16 waves and split K evenly
     int nit = 0;
+    const int want = plan_override().w4nz_nit;  // debug override: superblocks per wave
     for (int t = 1; t <= 8; ++t)
-        if (S % t == 0 && S / t <= kNzMaxWaves) {
+        if (S % t == 0 && S / t <= kNzMaxWaves && (want == 0 || t == want)) {
             nit = t;
             break;
         }

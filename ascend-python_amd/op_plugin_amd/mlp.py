@@ -20,8 +20,9 @@ from . import (npu_dynamic_quant, npu_quant_matmul, npu_rms_norm, npu_rms_norm_d
 def quant_mlp(x: torch.Tensor, gamma: torch.Tensor, w_gate_up: torch.Tensor, s_gate_up: torch.Tensor,
               w_down: torch.Tensor, s_down: torch.Tensor, eps: float = 1e-6, fused: bool = True,
               out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """x [T, H] fp16/bf16, gamma [H], w_gate_up int8 [H, 2I] (or a transposed [2I, H] view),
-    s_gate_up fp32 [2I], w_down int8 [I, H] (or a transposed view), s_down fp32 [H] -> [T, H]."""
+    """x [T, H] fp16/bf16, gamma [H], w_gate_up int8 [H, 2I] (or a transposed [2I, H] view, or the int8 NZ
+    weight npu_format_cast(w, 29) writes), s_gate_up fp32 [2I], w_down int8 [I, H] (likewise), s_down fp32 [H]
+    -> [T, H]."""
     if fused:
         y1, s1, _ = npu_rms_norm_dynamic_quant(x, gamma, eps)
     else:

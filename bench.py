@@ -375,6 +375,11 @@ def other_configs(q, W, dev, min_launches: int) -> dict:
     ops = 2 * T * H * 2 * I + 2 * T * I * H
     res["cfg5_quant_mlp_t512_h4096_i14336"] = {"avg_us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 1),
                                                "mfma_frac": round(ops / t / 1e12 / PEAK_I8_TOPS, 4)}
+    # the same block on its two weights cast once (untimed) to the int8 NZ layout
+    wgu_nz, wd_nz = q.npu_format_cast(wgu, q.ACL_FORMAT_FRACTAL_NZ), q.npu_format_cast(wd, q.ACL_FORMAT_FRACTAL_NZ)
+    t = timed(lambda i: quant_mlp(x, gamma, wgu_nz, sgu, wd_nz, sd, eps=W.CFG5["eps"]), 8)
+    res["cfg5_quant_mlp_t512_h4096_i14336_nz"] = {"avg_us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 1),
+                                                  "mfma_frac": round(ops / t / 1e12 / PEAK_I8_TOPS, 4)}
     return res
 
 

@@ -202,6 +202,21 @@ def test_abi_rms_norm_and_swiglu(ops, oracle):
     close(y, oracle.swiglu(W.bits(h.cpu()), F16), torch.float16)
 
 
+def test_quant_mlp_block_cfg5_nz_weights(ops):
+    """cfg5 with both weights cast once to the int8 NZ layout (npu_format_cast(w, 29)): the block gives the
+    bits of the block on the [K,N] weights (gate_up on 256 x 256 tiles, down with its K split, both on NZ
+    blocks)."""
+    from op_plugin_amd.mlp import quant_mlp
+    c = W.CFG5
+    say(f"quant_mlp cfg5 on NZ weights T={c['tokens']}")
+    d = W.mlp_inputs(c["tokens"], c["hidden"], c["intermediate"], seed=1)
+    dev = {k: v.to(DEV) for k, v in d.items()}
+    wgu_nz, wd_nz = ops.npu_format_cast(dev["w_gu"], 29), ops.npu_format_cast(dev["w_d"], 29)
+    out = quant_mlp(dev["x"], dev["gamma"], wgu_nz, dev["s_gu"], wd_nz, dev["s_d"], eps=c["eps"])
+    ref = quant_mlp(dev["x"], dev["gamma"], dev["w_gu"], dev["s_gu"], dev["w_d"], dev["s_d"], eps=c["eps"])
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 def test_quant_mlp_block_cfg5(ops, oracle):
     """cfg5, all 512 rows, every stage against the oracle on the GPU's own inputs to that stage:
     RMSNorm within one ulp; its fused quantization bit-exact (= qo_dynamic_quant of the GPU's RMSNorm
