@@ -146,6 +146,9 @@ def test_meta_shapes():
     assert w8z.shape == (688, 64, 64, 16) and q.get_npu_format(w8z) == 29
     assert q.npu_weight_quant_batchmatmul(_m((16, 4096), torch.bfloat16), w8z, _m((32, 11008), torch.float16),
                                           antiquant_group_size=128).shape == (16, 11008)
+    out = q.npu_quant_matmul(_m((3, 7, 4096), torch.int8), w8z, _m((11008,), torch.float32),
+                             pertoken_scale=_m((21,), torch.float32), output_dtype=torch.bfloat16)   # W8A8, NZ weight
+    assert out.shape == (3, 7, 11008) and out.dtype == torch.bfloat16
     assert q.quantize_per_tensor(_m((3, 8), torch.float16), 0.1, 2, torch.quint8).dtype == torch.uint8
     qq = q.quantize_per_channel(_m((3, 8), torch.bfloat16), _m((8,), torch.float64), _m((8,), torch.int64), -1,
                                 torch.qint32)
@@ -207,6 +210,10 @@ def test_meta_shapes():
     (lambda: q.npu_format_cast(_m((96, 16), torch.int8), 29), "K % 64"),
     (lambda: q.npu_weight_quant_batchmatmul(_m((2, 256), torch.bfloat16), _m((1, 1, 64, 4), torch.int32),
                                             _m((1, 16), torch.float16), antiquant_group_size=128), "weight's K"),
+    (lambda: q.npu_quant_matmul(_m((4, 128), torch.int8), _m((4, 1, 64, 16), torch.int8), _m((1,), torch.float32)),
+     "weight's K"),
+    (lambda: q.npu_quant_matmul(_m((4, 64), torch.int8), _m((4, 1, 64, 4), torch.int8), _m((1,), torch.float32)),
+     "2-D"),
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((64,), torch.float16)), "dtype of self"),
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((32,), torch.bfloat16)), "trailing dims"),
     (lambda: q.npu_rms_norm_dynamic_quant(_m((4, 8, 8), torch.bfloat16), _m((8, 8), torch.bfloat16)), "1-D gamma"),
