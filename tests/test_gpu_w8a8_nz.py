@@ -120,6 +120,32 @@ def test_quant_matmul_nz(ops, oracle, M, N, K, out_dtype, bias_dtype):
     _check(ops, oracle, M, N, K, out_dtype, bias_dtype, seed=M * 7 + N + 3 * K)
 
 
+def test_quant_matmul_nz_random_shapes(ops):
+    """Seeded random shapes across the NZ dispatch (decode stream, mid-M, 256 x 256 tiles with and without a K
+    split, unpack fallback): every int32 accumulator against the exact product (float64 BLAS is exact here:
+    |sums| < 2^53), and the bf16 output with per-token scale and bias bit for bit against the row-major weight."""
+    rng = np.random.default_rng(20261202)
+    shapes = [(int(m), 16 * int(n), 64 * int(k)) for m, n, k in zip(
+        rng.choice([1, 2, 5, 9, 16, 17, 31, 64, 100, 128, 200, 256, 257, 300, 512, 768], 18),
+        rng.integers(1, 200, 18), rng.integers(1, 40, 18))]
+    shapes += [(512, 1024, 1024), (768, 512, 2048), (256, 4096, 256)]  # whole 256 x 256 tiles
+    for M, N, K in shapes:
+        say(f"quant_matmul NZ random M={M} N={N} K={K}")
+        g = torch.Generator().manual_seed(M * 31 + N * 7 + K)
+        a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+        w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+        ad, wd = a.to(DEV), w.to(DEV)
+        wnz = ops.npu_format_cast(wd, 29)
+        acc = ops.npu_quant_matmul(ad, wnz, torch.ones(1, device=DEV), output_dtype=torch.int32).cpu()
+        assert torch.equal(acc.double(), a.double() @ w.double()), (M, N, K)
+        s = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(DEV)
+        pt = (1e-2 * torch.rand(M, generator=g)).to(DEV)
+        b = torch.randn(N, generator=g).to(torch.bfloat16).to(DEV)
+        out = ops.npu_quant_matmul(ad, wnz, s, pertoken_scale=pt, bias=b, output_dtype=torch.bfloat16)
+        nd = ops.npu_quant_matmul(ad, wd, s, pertoken_scale=pt, bias=b, output_dtype=torch.bfloat16)
+        assert torch.equal(out.view(torch.int16), nd.view(torch.int16)), (M, N, K)
+
+
 @pytest.mark.parametrize("idx", [0, 1, 2])
 def test_quant_matmul_nz_cfg2(ops, oracle, idx):
     """cfg2 decode shapes (M = 1, 4, 16; K=8192, N=28672; activations with 1 % outlier channels, dynamically
