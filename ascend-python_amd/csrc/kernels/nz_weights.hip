@@ -38,80 +38,158 @@ constexpr int kNzThreads = 256;
 constexpr int kNzMaxWaves = 16;
 constexpr int kNzTilePitch = 320; // floats per 16x16 tile in the reduction buffer
 
-// word index and nibble of weight element (k, n) in the NZ layout
-__host__ __device__ __forceinline__ int64_t nz4_index(int64_t k, int64_t n, int64_t S, int* nibble) {
-    const int64_t c = (k & 127) >> 3, i = k & 7;
-    const int64_t lane = (n & 15) + 16 * (c & 3), j = c >> 2;
-    *nibble = (int)((i & 1) ? 4 + (i >> 1) : (i >> 1));
-    return ((((n >> 4) * S + (k >> 7)) * 64 + lane) << 2) + j;
+// The casts move one tile per workgroup through LDS: 16 n-blocks (256 columns; fewer in the last group) by one
+// K block row (128 rows for int4, 64 for int8).  The NZ side is read or written as its whole 1 KB blocks and
+// the ND side as whole row pieces (32 words / 256 bytes per row, one dword per lane), so both are streamed in
+// whole lines; the change of layout is a register transpose of nibbles or bytes between the two.
+constexpr int kCastNB = 16;    // n-blocks per tile
+constexpr int kCastPad = 4;    // dwords of padding per NZ block in LDS (spreads the blocks over the banks)
+
+// nibble of row i (0..7) of an 8-row chunk inside an NZ word: even rows in nibbles 0..3, odd rows in 4..7
+__host__ __device__ __forceinline__ int nz4_nibble(int i) { return (i & 1) ? 4 + (i >> 1) : (i >> 1); }
+
+// NZ -> ND [K, N/8] (int4).  Tile = superblock sb (128 rows) x n-block group nbg.
+__global__ __launch_bounds__(kNzThreads) void w4_nz_unpack_kernel(const int32_t* __restrict__ nz, int64_t K,
+                                                                  int64_t N, int32_t* __restrict__ nd) {
+    __shared__ uint32_t blk[kCastNB][64 * 4 + kCastPad];
+    const int64_t S = K / 128, NBT = N / 16, NW = N / 8;
+    const int64_t sb = blockIdx.x % S, nbg = blockIdx.x / S;
+    const int nb = (int)(NBT - nbg * kCastNB < kCastNB ? NBT - nbg * kCastNB : kCastNB);
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {  // 1024 lane chunks of 16 bytes: chunk q = block q>>6, lane q&63
+        const int q = t + kNzThreads * u, b = q >> 6, l = q & 63;
+        if (b < nb)
+            *reinterpret_cast<u32x4*>(&blk[b][4 * l]) =
+                *reinterpret_cast<const u32x4*>(nz + (((nbg * kCastNB + b) * S + sb) * 64 + l) * 4);
+    }
+    __syncthreads();
+    // thread -> word column wc of the tile (block wc>>1, columns 8*(wc&1)..+7 of it) and 8-row chunks c
+    const int wc = t & 31, b = wc >> 1, h = wc & 1;
+    if (b >= nb) return;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const int c = (t >> 5) + 8 * pass;  // rows 8c..8c+7 of the superblock
+        uint32_t d[8];                      // NZ word c>>2 of the 8 lanes holding columns 8h..8h+7
+#pragma unroll
+        for (int q = 0; q < 8; ++q) d[q] = blk[b][4 * (8 * h + 16 * (c & 3) + q) + (c >> 2)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) w |= ((d[q] >> (4 * nz4_nibble(i))) & 0xfu) << (4 * q);
+            nd[(sb * 128 + 8 * c + i) * NW + nbg * (2 * kCastNB) + wc] = (int32_t)w;
+        }
+    }
 }
 
-// ND [K, N/8] -> NZ: one thread per NZ word, gathering its 8 nibbles.
+// ND [K, N/8] -> NZ (int4): the inverse tile.
 __global__ __launch_bounds__(kNzThreads) void w4_nz_pack_kernel(const int32_t* __restrict__ nd, int64_t K, int64_t N,
                                                                 int32_t* __restrict__ nz) {
-    const int64_t total = K * N / 8, NW = N / 8, S = K / 128;
-    for (int64_t idx = (int64_t)blockIdx.x * kNzThreads + threadIdx.x; idx < total;
-         idx += (int64_t)gridDim.x * kNzThreads) {
-        const int64_t j = idx & 3, lane = (idx >> 2) & 63, sb = idx >> 8;
-        const int64_t s = sb % S, nb = sb / S;
-        const int64_t n = nb * 16 + (lane & 15), c = 4 * j + (lane >> 4), k0 = s * 128 + 8 * c;
-        uint32_t word = 0;
+    __shared__ uint32_t rows[128][2 * kCastNB + 1];
+    const int64_t S = K / 128, NBT = N / 16, NW = N / 8;
+    const int64_t sb = blockIdx.x % S, nbg = blockIdx.x / S;
+    const int nb = (int)(NBT - nbg * kCastNB < kCastNB ? NBT - nbg * kCastNB : kCastNB);
+    const int nw = 2 * nb, t = threadIdx.x;
+    for (int e = t; e < 128 * 2 * kCastNB; e += kNzThreads) {  // one dword per lane: 128-byte row pieces
+        const int r = e >> 5, w = e & 31;
+        if (w < nw) rows[r][w] = (uint32_t)nd[(sb * 128 + r) * NW + nbg * (2 * kCastNB) + w];
+    }
+    __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t v = ((uint32_t)nd[(k0 + i) * NW + (n >> 3)] >> (4 * (n & 7))) & 0xfu;
-            word |= v << (4 * ((i & 1) ? 4 + (i >> 1) : (i >> 1)));
+    for (int u = 0; u < 4; ++u) {  // lane chunk q = (block q>>6, lane q&63): 4 words j, chunk c = 4j + lane/16
+        const int q = t + kNzThreads * u, b = q >> 6, l = q & 63;
+        if (b >= nb) continue;
+        const int n16 = l & 15, wc = 2 * b + (n16 >> 3), sh = 4 * (n16 & 7);
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 4 * j + (l >> 4);
+            uint32_t w = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w |= ((rows[8 * c + i][wc] >> sh) & 0xfu) << (4 * nz4_nibble(i));
+            o[j] = w;
         }
-        nz[idx] = (int32_t)word;
+        *reinterpret_cast<u32x4*>(nz + (((nbg * kCastNB + b) * S + sb) * 64 + l) * 4) = o;
     }
 }
 
-// NZ -> ND [K, N/8]: one thread per ND word.
-__global__ __launch_bounds__(kNzThreads) void w4_nz_unpack_kernel(const int32_t* __restrict__ nz, int64_t K, int64_t N,
-                                                                  int32_t* __restrict__ nd) {
-    const int64_t total = K * N / 8, NW = N / 8, S = K / 128;
-    for (int64_t idx = (int64_t)blockIdx.x * kNzThreads + threadIdx.x; idx < total;
-         idx += (int64_t)gridDim.x * kNzThreads) {
-        const int64_t k = idx / NW, n0 = (idx % NW) * 8;
-        uint32_t word = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int p;
-            const int64_t w = nz4_index(k, n0 + i, S, &p);
-            word |= (((uint32_t)nz[w] >> (4 * p)) & 0xfu) << (4 * i);
-        }
-        nd[idx] = (int32_t)word;
-    }
+// 4 x 4 byte transpose: o[j] byte i = r[i] byte j.
+__device__ __forceinline__ void bytes4x4(const uint32_t r[4], uint32_t o[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(r[1], r[0], 0x05010400u);  // r0b0 r1b0 r0b1 r1b1
+    const uint32_t t1 = __builtin_amdgcn_perm(r[1], r[0], 0x07030602u);  // r0b2 r1b2 r0b3 r1b3
+    const uint32_t t2 = __builtin_amdgcn_perm(r[3], r[2], 0x05010400u);
+    const uint32_t t3 = __builtin_amdgcn_perm(r[3], r[2], 0x07030602u);
+    o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
-// int8 ND [K, N] -> NZ: one thread per 16-byte lane chunk (16 rows of one column).
-__global__ __launch_bounds__(kNzThreads) void w8_nz_pack_kernel(const int8_t* __restrict__ nd, int64_t K, int64_t N,
-                                                                int8_t* __restrict__ nz) {
-    const int64_t total = K * N / 16, S = K / 64;
-    for (int64_t idx = (int64_t)blockIdx.x * kNzThreads + threadIdx.x; idx < total;
-         idx += (int64_t)gridDim.x * kNzThreads) {
-        const int64_t lane = idx & 63, sb = idx >> 6;
-        const int64_t s = sb % S, nb = sb / S;
-        const int64_t n = nb * 16 + (lane & 15), k0 = s * 64 + 16 * (lane >> 4);
-        u32x4 v = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i >> 2] |= (uint32_t)(uint8_t)nd[(k0 + i) * N + n] << (8 * (i & 3));
-        reinterpret_cast<u32x4*>(nz)[idx] = v;
-    }
-}
-
-// int8 NZ -> ND: one thread per 16-byte lane chunk, scattered back to its 16 rows.
+// int8 NZ -> ND [K, N].  Tile = K block kb (64 rows) x n-block group nbg (256 bytes per row).
 __global__ __launch_bounds__(kNzThreads) void w8_nz_unpack_kernel(const int8_t* __restrict__ nz, int64_t K, int64_t N,
                                                                   int8_t* __restrict__ nd) {
-    const int64_t total = K * N / 16, S = K / 64;
-    for (int64_t idx = (int64_t)blockIdx.x * kNzThreads + threadIdx.x; idx < total;
-         idx += (int64_t)gridDim.x * kNzThreads) {
-        const int64_t lane = idx & 63, sb = idx >> 6;
-        const int64_t s = sb % S, nb = sb / S;
-        const int64_t n = nb * 16 + (lane & 15), k0 = s * 64 + 16 * (lane >> 4);
-        const u32x4 v = reinterpret_cast<const u32x4*>(nz)[idx];
+    __shared__ uint32_t blk[kCastNB][64 * 4 + kCastPad];
+    const int64_t KB = K / 64, NBT = N / 16;
+    const int64_t kb = blockIdx.x % KB, nbg = blockIdx.x / KB;
+    const int nb = (int)(NBT - nbg * kCastNB < kCastNB ? NBT - nbg * kCastNB : kCastNB);
+    const int t = threadIdx.x;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) nd[(k0 + i) * N + n] = (int8_t)(v[i >> 2] >> (8 * (i & 3)));
+    for (int u = 0; u < 4; ++u) {
+        const int q = t + kNzThreads * u, b = q >> 6, l = q & 63;
+        if (b < nb)
+            *reinterpret_cast<u32x4*>(&blk[b][4 * l]) =
+                *reinterpret_cast<const u32x4*>(nz + (((nbg * kCastNB + b) * KB + kb) * 64 + l) * 16);
     }
+    __syncthreads();
+    // thread -> 4-column group w (columns 4w..4w+3 of the tile: block w>>2) and 4-row groups rq
+    const int w = t & 63, b = w >> 2;
+    if (b >= nb) return;
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int rq = (t >> 6) + 4 * pass;  // rows 4rq..4rq+3 of the K block
+        uint32_t r[4], o[4];                 // r[e]: rows 4rq..+3 of column 4w+e (dword rq&3 of its lane)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = blk[b][4 * ((4 * w + e) % 16 + 16 * (rq >> 2)) + (rq & 3)];
+        bytes4x4(r, o);                      // o[kk]: columns 4w..4w+3 of row 4rq+kk
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            *reinterpret_cast<uint32_t*>(nd + (kb * 64 + 4 * rq + kk) * N + nbg * (16 * kCastNB) + 4 * w) = o[kk];
+    }
+}
+
+// int8 ND [K, N] -> NZ: the inverse tile.
+__global__ __launch_bounds__(kNzThreads) void w8_nz_pack_kernel(const int8_t* __restrict__ nd, int64_t K, int64_t N,
+                                                                int8_t* __restrict__ nz) {
+    __shared__ uint32_t rows[64][4 * kCastNB + 1];
+    const int64_t KB = K / 64, NBT = N / 16;
+    const int64_t kb = blockIdx.x % KB, nbg = blockIdx.x / KB;
+    const int nb = (int)(NBT - nbg * kCastNB < kCastNB ? NBT - nbg * kCastNB : kCastNB);
+    const int nw = 4 * nb, t = threadIdx.x;
+    for (int e = t; e < 64 * 4 * kCastNB; e += kNzThreads) {  // one dword per lane: 256-byte row pieces
+        const int r = e >> 6, w = e & 63;
+        if (w < nw)
+            rows[r][w] = *reinterpret_cast<const uint32_t*>(nd + (kb * 64 + r) * N + nbg * (16 * kCastNB) + 4 * w);
+    }
+    __syncthreads();
+    // thread -> (block b, 16-row group g, 4-column group cg): the whole 16-byte chunks of lanes 4cg + e + 16g,
+    // e = 0..3 (64 contiguous bytes; the 4 threads of one (b, g) write 256)
+    const int b = t >> 4, g = (t >> 2) & 3, cg = t & 3;
+    if (b >= nb) return;
+    uint32_t o[4][4];  // o[e][dw]: rows 16g + 4dw .. +3 of column 4cg + e
+#pragma unroll
+    for (int dw = 0; dw < 4; ++dw) {
+        uint32_t r[4], c[4];  // r[kk]: columns 4cg..+3 of row 16g + 4dw + kk
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) r[kk] = rows[16 * g + 4 * dw + kk][4 * b + cg];
+        bytes4x4(r, c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e][dw] = c[e];
+    }
+    int8_t* dst = nz + (((nbg * kCastNB + b) * KB + kb) * 64 + 4 * cg + 16 * g) * 16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<u32x4*>(dst + 16 * e) = (u32x4){o[e][0], o[e][1], o[e][2], o[e][3]};
 }
 
 // The B operand held in one NZ word: dword q takes nibbles q (k = 2q, low
@@ -614,10 +692,6 @@ hipError_t launch_nz_dt(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream)
 
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-int64_t grid_for(int64_t total) {
-    int64_t blocks = (total + kNzThreads - 1) / kNzThreads;
-    return blocks > 65536 ? 65536 : (blocks < 1 ? 1 : blocks);
-}
 
 // bytes of the ND form of an NZ weight
 size_t nd_weight_bytes(const WqbmmArgs& p) { return (size_t)(p.w_dtype == QK_I8_NZ ? p.K * p.N : p.K * p.N / 2); }
@@ -645,7 +719,9 @@ NzGemmPlan nzg_plan(const WqbmmArgs& p) {
         return g;
     g.tiles_m = (int)((p.M + nzg::BM - 1) / nzg::BM);
     g.tiles_n = (int)(p.N / nzg::BN);
-    if ((int64_t)g.tiles_m * g.tiles_n < 96) return g;  // too few tiles to fill the CUs
+    // measured at N = 11008: from 86 tiles (M = 129-256) this kernel beats unpacking to ND and the row-major
+    // kernels; with 43 (M = 65-128) the row-major split kernels are faster even after the unpack
+    if ((int64_t)g.tiles_m * g.tiles_n < 64) return g;
     g.ok = true;
     return g;
 }
@@ -673,22 +749,24 @@ hipError_t launch_nzg_dt(const WqbmmArgs& p, const NzGemmPlan& g, float* xsum, h
 }  // namespace
 
 hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t N, int32_t* dst, hipStream_t stream) {
-    const int64_t total = K * N / 8;
-    if (total == 0) return hipSuccess;
+    if (K * N == 0) return hipSuccess;
+    const int64_t tiles = (K / 128) * ((N / 16 + kCastNB - 1) / kCastNB);
+    if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
     if (to_nz)
-        w4_nz_pack_kernel<<<dim3((uint32_t)grid_for(total)), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
+        w4_nz_pack_kernel<<<dim3((uint32_t)tiles), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
     else
-        w4_nz_unpack_kernel<<<dim3((uint32_t)grid_for(total)), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
+        w4_nz_unpack_kernel<<<dim3((uint32_t)tiles), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
     return hipGetLastError();
 }
 
 hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N, int8_t* dst, hipStream_t stream) {
-    const int64_t total = K * N / 16;
-    if (total == 0) return hipSuccess;
+    if (K * N == 0) return hipSuccess;
+    const int64_t tiles = (K / 64) * ((N / 16 + kCastNB - 1) / kCastNB);
+    if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
     if (to_nz)
-        w8_nz_pack_kernel<<<dim3((uint32_t)grid_for(total)), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
+        w8_nz_pack_kernel<<<dim3((uint32_t)tiles), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
     else
-        w8_nz_unpack_kernel<<<dim3((uint32_t)grid_for(total)), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
+        w8_nz_unpack_kernel<<<dim3((uint32_t)tiles), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
     return hipGetLastError();
 }
 

@@ -451,8 +451,8 @@ int qk_weight_format_cast(const void* src, int src_format, void* dst, int dst_fo
     const uintptr_t bytes = (uintptr_t)(weight_dtype == QK_I32 ? K * N / 2 : K * N);
     if ((uintptr_t)src < (uintptr_t)dst + bytes && (uintptr_t)dst < (uintptr_t)src + bytes)
         return fail(QK_ERR_ARG, "%s: src and dst overlap", op);
-    if (weight_dtype == QK_I8 && ((uintptr_t)src | (uintptr_t)dst) % 16 != 0)
-        return fail(QK_ERR_ARG, "%s: int8 weights must be 16-byte aligned", op);
+    if (((uintptr_t)src | (uintptr_t)dst) % 16 != 0)
+        return fail(QK_ERR_ARG, "%s: src and dst must be 16-byte aligned", op);
     const hipError_t e =
         weight_dtype == QK_I32
             ? qk::launch_w4_nz_cast(static_cast<const int32_t*>(src), to_nz, K, N, static_cast<int32_t*>(dst),

@@ -236,7 +236,8 @@ int qk_weight_quant_bmm_noalloc(const void* x, int x_dtype,
  * (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:303-316,
  * op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:103-107), done once when
  * weights are loaded.  src_format -> dst_format is QK_FORMAT_ND ->
- * QK_FORMAT_FRACTAL_NZ or back; N % 16 == 0; src and dst must not overlap.
+ * QK_FORMAT_FRACTAL_NZ or back; N % 16 == 0; src and dst must not overlap and
+ * must be 16-byte aligned.
  * weight_dtype QK_I32 (int4 packed, [K, N/8] in ND; K % 128 == 0): NZ is int32
  * [N/16][K/128][64][4]; element (k, n) is in word
  *   ((n/16 * (K/128) + k/128) * 64 + lane) * 4 + j,
