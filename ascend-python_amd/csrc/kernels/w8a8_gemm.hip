@@ -1284,7 +1284,7 @@ __global__ __launch_bounds__(nzd::NT) void qmm_nzd(QmmArgs p, int nwg) {
     const int b0 = (int)((int64_t)wg * NBT / nwg), nb = (int)((int64_t)(wg + 1) * NBT / nwg) - b0;
     const int m = c < M ? c : M - 1;
 
-    // sizes checked on the host: (M-1)*lda + K and NB * K * 16 fit in 31 bits
+    // 31-bit ranges by the C ABI's limits (M <= 16, ldx1 < 2^24, K <= 131071): (M-1)*lda + K and NB*K*16
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.a, (uint32_t)((M - 1) * p.lda + p.K));
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.b + (int64_t)b0 * p.K * 16, (uint32_t)(nb * p.K * 16));
     const uint32_t x_lane = (uint32_t)m * (uint32_t)p.lda + 16u * (uint32_t)g, w_lane = 16u * (uint32_t)lane;
