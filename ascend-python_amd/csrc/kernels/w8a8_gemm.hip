@@ -303,7 +303,9 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t ro = (m0 + wm * WMR + 16 * i + 4 * g + r) * p.N + n0 + wn * 128 + fr;
+                const int64_t m = m0 + wm * WMR + 16 * i + 4 * g + r;
+                if (m >= p.M) continue;  // the last row tile of a ragged M
+                const int64_t ro = m * p.N + n0 + wn * 128 + fr;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) dst[ro + 16 * j] = acc[i][j][r];
             }
@@ -351,6 +353,7 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
         for (int it = 0; it < BM * CPRO / NT; ++it) {
             const int q = tid + it * NT;
             const int row = q / CPRO, c = q % CPRO;
+            if (m0 + row >= p.M) break;  // rows past a ragged M (q grows with the row)
             const i32x4 v = *reinterpret_cast<const i32x4*>(smem + row * ROWB + 16 * c);
             *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo + n0 + 8 * c) = v;
         }
@@ -607,7 +610,10 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
 
     // buffer views of this tile's operand rows (sizes checked on the host to fit 32 bits)
     const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem;
-    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.a + m0 * p.lda, (uint32_t)(BM * p.lda));
+    // A rows past M (the last row tile of a ragged M) fall outside the range and read as zeros: the row offset
+    // of every A load is in its voff, which the range check covers
+    const int64_t rows_valid = p.M - m0 < BM ? p.M - m0 : BM;
+    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.a + m0 * p.lda, (uint32_t)(rows_valid * p.lda));
     // an NZ column block: BN/16 consecutive n-blocks of K/64 1 KB blocks, BN * K contiguous bytes
     const __amdgpu_buffer_rsrc_t rsB = B_NZ   ? make_rsrc(p.b + n0 * p.K, (uint32_t)(BN * p.K))
                                        : B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
@@ -652,7 +658,7 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int b = 16 * h + 4 * gw + i;
-            dma16(rsA, lds + b * 1024, (i & 1) ? va1 : va0, (uint32_t)(8 * b) * lda + k0);
+            dma16(rsA, lds + b * 1024, ((i & 1) ? va1 : va0) + (uint32_t)(8 * b) * lda, k0);
         }
     };
 
@@ -745,7 +751,7 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
         const QmmEpilogue& e = p.epi;
         const int64_t n = n0 + 4 * lane, m = m0 + 4 * lane;  // 64 lanes x 16 B: 256 columns or rows
         if (wave == 0 && e.scale && e.scale_per_ch) warm = e.scale[n];
-        else if (wave == 1 && e.pertoken) warm = e.pertoken[m];
+        else if (wave == 1 && e.pertoken && m < p.M) warm = e.pertoken[m];
         else if (wave == 2 && e.bias_dtype) {
             const int es = (e.bias_dtype == QK_F32 || e.bias_dtype == QK_I32) ? 4 : 2;
             if (16 * lane < 256 * es) warm = *(const float*)((const char*)e.bias + n0 * es + 16 * lane);
@@ -1424,22 +1430,29 @@ hipError_t launch_by_m(const QmmArgs& p, hipStream_t stream) {
     return launch_tiled<128, 128, B_KN>(p, stream);
 }
 
+// Whole 256-column tiles and K ranges, 32-bit per-lane offsets (the 64-bit bases stay uniform) and 16-byte
+// aligned output rows: what the 256x256 kernels need along N and K.
+bool big_nk_full(const QmmArgs& p, int nsplit) {
+    return p.N % big::BN == 0 && p.K % (big::BK * nsplit) == 0 && p.lda < (1 << 24) && p.sbk < (1 << 24) &&
+           p.sbn < (1 << 24) && (uintptr_t)p.epi.out % 16 == 0 && p.epi.ldo % 8 == 0;
+}
+
+// The direct-to-LDS kernel (any M: a ragged last row tile reads zeros past M and stores only its rows): K
+// ranges of whole 4-stage rings, 16-byte aligned rows, and every operand range of a tile addressable by a
+// 32-bit buffer offset.
+bool big_dma_ok(const QmmArgs& p, bool b_kn, int nsplit) {
+    return plan_override().qmm_dma && big_nk_full(p, nsplit) && (p.K / nsplit) % (dm::BK * dm::NST) == 0 &&
+           p.lda % 16 == 0 && (uintptr_t)p.a % 16 == 0 && (uintptr_t)p.b % 16 == 0 &&
+           (b_kn ? (p.sbk % 16 == 0 && (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32)) : (p.sbn % 16 == 0));
+}
+
 template <int OUT>
 hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, int nsplit, int32_t* partial,
                       hipStream_t stream) {
     const dim3 grid((uint32_t)(tiles_m * tiles_n * nsplit));
-    // full tiles and 32-bit per-lane offsets (the 64-bit bases stay uniform)
-    const bool full = p.M % big::BM == 0 && p.N % big::BN == 0 && p.K % (big::BK * nsplit) == 0 &&
-                      p.lda < (1 << 24) && p.sbk < (1 << 24) && p.sbn < (1 << 24) &&
-                      (uintptr_t)p.epi.out % 16 == 0 && p.epi.ldo % 8 == 0;
-    if (nsplit > 1 && !full) return hipErrorInvalidValue;  // the plan only splits whole tiles
-    // direct-to-LDS kernel: K ranges of whole 4-stage rings, 16-byte aligned rows, and every operand
-    // range of a tile addressable by a 32-bit buffer offset
-    const bool dma_on = plan_override().qmm_dma;  // debug override: off keeps the register-staged kernel
-    const bool dma = dma_on && full && (p.K / nsplit) % (dm::BK * dm::NST) == 0 && p.lda % 16 == 0 &&
-                     (uintptr_t)p.a % 16 == 0 && (uintptr_t)p.b % 16 == 0 &&
-                     (b_kn ? (p.sbk % 16 == 0 && (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32))
-                           : (p.sbn % 16 == 0));
+    const bool full = big_nk_full(p, nsplit) && p.M % big::BM == 0;  // the register-staged kernel's whole tiles
+    const bool dma = big_dma_ok(p, b_kn, nsplit);
+    if (nsplit > 1 && !full && !dma) return hipErrorInvalidValue;  // not planned (launch_quant_matmul unsplits)
     if (dma) {
         if (b_kn) qmm_dma<kLayKN, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
         else qmm_dma<kLayNK, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
@@ -1473,7 +1486,8 @@ BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
         b.ok = true;
         return b;
     }
-    if (M % big::BM != 0 || N % big::BN != 0 || K % big::BK != 0) return b;
+    // a split needs whole tiles along N and K; a ragged M only runs split on the direct-to-LDS kernel
+    if (N % big::BN != 0 || K % big::BK != 0) return b;
     int ns = 1;
     while (tm * tn * ns < 192 && ns < 16 && K % ((int64_t)ns * 2 * big::BK) == 0 && K / (ns * 2) >= 512) ns *= 2;
     if (ns == 1 || tm * tn * ns < 64 || (int64_t)ns * M * N * 4 > ((int64_t)512 << 20)) return b;
@@ -1709,8 +1723,11 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
         if (need && (!workspace || ws_bytes < need)) return hipErrorInvalidValue;
         return b_kn16 ? launch_skinny<true>(p, sp, partial, stream) : launch_skinny<false>(p, sp, partial, stream);
     }
-    const BigPlan bp = big_plan(p.M, p.N, p.K);
+    BigPlan bp = big_plan(p.M, p.N, p.K);
     bool big_ok = bp.ok && a_ok && (b_nk || (b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0));
+    // a split of a ragged M runs only on the direct-to-LDS kernel; otherwise the register-staged kernel runs
+    // the shape unsplit (the planned workspace is then unused)
+    if (big_ok && bp.nsplit > 1 && p.M % big::BM != 0 && !big_dma_ok(p, b_kn, bp.nsplit)) bp.nsplit = 1;
     if (big_ok && bp.nsplit > 1) {
         // splits need whole aligned tiles and the workspace; otherwise the tiled kernels take the shape
         const size_t need = QK_SPLIT_COUNTER_BYTES + (size_t)bp.nsplit * p.M * p.N * sizeof(int32_t);
@@ -1741,7 +1758,7 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
 // ---------------------------------------------------------------------------
 // W8A8 on an int8 NZ weight (p.b: [N/16][K/64][64][16]; p.sbk and p.sbn unused).  By shape: M <= 16 the
 // decode stream qmm_nzd (no workspace); the mid-M plan qmm_mid on NZ blocks (64-column blocks, no split);
-// whole 256 x 256 tiles qmm_dma on NZ blocks (a K split as planned for the row-major weight); any other
+// 256-column tiles (any M) qmm_dma on NZ blocks (a K split as planned for the row-major weight); any other
 // shape unpacks the weight to [K,N] in the workspace and runs the row-major kernels on it:
 // [ND weight, 256-byte rounded][that call's workspace].  The C ABI guarantees 16-byte aligned x1 rows
 // (row stride below 2^24), weight and output.
@@ -1781,10 +1798,10 @@ hipError_t launch_nzd(const QmmArgs& p, const NzdPlan& z, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// qmm_dma on NZ blocks: whole tiles and K ranges of whole four-stage rings
+// qmm_dma on NZ blocks: whole 256-column tiles (any M) and K ranges of whole four-stage rings
 bool nz_dma_ok(const BigPlan& b, int64_t M, int64_t N, int64_t K) {
-    return plan_override().qmm_dma && b.ok && M % dm::BM == 0 && N % dm::BN == 0 &&
-           K % ((int64_t)b.nsplit * dm::BK * dm::NST) == 0;
+    (void)M;
+    return plan_override().qmm_dma && b.ok && N % dm::BN == 0 && K % ((int64_t)b.nsplit * dm::BK * dm::NST) == 0;
 }
 
 template <int OUT>

@@ -404,6 +404,74 @@ def test_quant_matmul_prefill_kernel_epilogues(ops, oracle, K, out_dtype, bias_d
                            f"{got_np[tuple(bad[0])]} vs {ref[tuple(bad[0])]}")
 
 
+@pytest.mark.parametrize("M,N,K,kn,out_dtype,bias_dtype", [
+    (300, 8192, 1024, True, torch.bfloat16, torch.bfloat16),  # 64 tiles, K split 2, last row tile 44 rows
+    (1000, 8192, 4096, True, torch.bfloat16, torch.bfloat16), # 128 tiles, K split 2, last row tile 232 rows
+    (257, 4096, 2048, True, torch.int8, torch.int32),         # 32 tiles, K split 4, one row in the last tile
+    (600, 8192, 2048, False, torch.int32, None),              # [N,K] view, 96 tiles, K split 2
+    (4000, 4096, 1024, False, torch.float16, torch.float32),  # [N,K] view, 256 tiles unsplit, 160-row last tile
+    (3900, 8192, 512, True, torch.float32, torch.int32),      # 512 tiles unsplit (one ring), 60-row last tile
+])
+def test_quant_matmul_prefill_ragged_m(ops, oracle, M, N, K, kn, out_dtype, bias_dtype):
+    """M not a multiple of 256 on the 256 x 256 direct-to-LDS kernel (rows past M load as zeros and are not
+    stored), unsplit and with K splits: every int32 accumulator through exact row and column checksums, and
+    the last row tile's rows (the ragged ones), with first and middle rows, bit-exact against the oracle."""
+    say(f"quant_matmul ragged M={M} N={N} K={K} {'[K,N]' if kn else '[N,K] view'} out={out_dtype} bias={bias_dtype}")
+    g = torch.Generator().manual_seed(M * 5 + N + K)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    ad = a.to(DEV)
+    wd = w.to(DEV) if kn else w.t().contiguous().to(DEV).t()
+    acc = ops.npu_quant_matmul(ad, wd, torch.ones(1, device=DEV), output_dtype=torch.int32)
+    a64, w64, acc64 = a.to(torch.int64), w.to(torch.int64), acc.cpu().to(torch.int64)
+    assert torch.equal(acc64.sum(0), a64.sum(0) @ w64)
+    assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
+    integer_out = out_dtype in (torch.int8, torch.int32)
+    s = (1e-4 + 1e-3 * torch.rand(N, generator=g)) if out_dtype is torch.int8 else 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    pt = 1e-2 * torch.rand(M, generator=g)
+    off = torch.randn(N, generator=g) if out_dtype is torch.int8 else None
+    b = None
+    if bias_dtype is torch.int32:
+        b = torch.randint(-1000, 1000, (N,), generator=g, dtype=torch.int32)
+    elif bias_dtype is not None:
+        b = torch.randn(N, generator=g).to(bias_dtype)
+    kw = dict(bias=None if b is None else b.to(DEV), output_dtype=out_dtype)
+    if out_dtype is torch.int8:
+        kw["offset"] = off.to(DEV)
+    elif not integer_out:
+        kw["pertoken_scale"] = pt.to(DEV)
+    out = ops.npu_quant_matmul(ad, wd, s.to(DEV), **kw).cpu()
+    last = (M - 1) // 256 * 256
+    rows = np.unique(np.r_[0:2, M // 2 - 1:M // 2 + 1, last:min(last + 4, M), max(last, M - 6):M])
+    bias_np = None if b is None else (b.numpy() if b.dtype in (torch.int32, torch.float32) else W.bits(b))
+    ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(),
+                              pertoken=None if integer_out else pt[rows].numpy(),
+                              offset=None if off is None else off.numpy(), bias=bias_np,
+                              bias_dtype=CODE[b.dtype] if b is not None else BF16, out_dtype=CODE[out_dtype])
+    got = out[rows]
+    got_np = got.numpy() if out_dtype in (torch.float32, torch.int32, torch.int8) else W.bits(got)
+    bad = np.argwhere(got_np != ref)
+    assert bad.size == 0, (f"{len(bad)} mismatches, first at (row {rows[bad[0][0]]}, col {bad[0][1]}): "
+                           f"{got_np[tuple(bad[0])]} vs {ref[tuple(bad[0])]}")
+
+
+def test_quant_matmul_prefill_ragged_m_register_staged(ops, plan):
+    """With the direct-to-LDS kernel switched off (debug override qmm_dma=0) a ragged M that the planner splits
+    runs unsplit on the register-staged 256 x 256 kernel: the same bf16 bits as the split direct-to-LDS run."""
+    say("quant_matmul ragged M=300 N=8192 K=1024, qmm_dma on vs off")
+    g = torch.Generator().manual_seed(21)
+    M, N, K = 300, 8192, 1024
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8).to(DEV)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8).to(DEV)
+    s = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(DEV)
+    pt = (1e-2 * torch.rand(M, generator=g)).to(DEV)
+    b = torch.randn(N, generator=g).to(torch.bfloat16).to(DEV)
+    dma = ops.npu_quant_matmul(a, w, s, pertoken_scale=pt, bias=b, output_dtype=torch.bfloat16)
+    plan("qmm_dma=0")
+    reg = ops.npu_quant_matmul(a, w, s, pertoken_scale=pt, bias=b, output_dtype=torch.bfloat16)
+    assert torch.equal(dma.view(torch.int16), reg.view(torch.int16))
+
+
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32, torch.int32])
 @pytest.mark.parametrize("per_tensor", [False, True])

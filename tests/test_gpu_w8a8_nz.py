@@ -111,7 +111,10 @@ def _check(ops, oracle, M, N, K, out_dtype, bias_dtype, seed):
     (4096, 4096, 1024, torch.bfloat16, torch.bfloat16),
     (2048, 2048, 1024, torch.float16, None),
     (1024, 1024, 2048, torch.bfloat16, torch.bfloat16),
-    # unpack-to-[K,N] fallback: ragged M above 256, N % 64 != 0 with K % 256 != 0
+    # the same on a ragged M: 160-row last tile unsplit; 232-row last tile with a K split of 4
+    (4000, 4096, 1024, torch.float16, torch.float32),
+    (1000, 4096, 2048, torch.bfloat16, torch.bfloat16),
+    # unpack-to-[K,N] fallback: K not a multiple of 256 above the mid-M range, N % 64 != 0 with K % 256 != 0
     (300, 1024, 192, torch.bfloat16, torch.bfloat16),
     (40, 4112, 320, torch.int32, None),
 ])
