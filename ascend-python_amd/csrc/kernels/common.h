@@ -139,6 +139,9 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, u
 // Cache-policy operand of the raw buffer loads/stores for device-coherent
 // access (the sc1 bit on gfx950).
 constexpr int kCoherent = 16;
+// Cache-policy operand for a load of data read once (the nt bit: the line is
+// not kept in the L2 against the lines other workgroups read again).
+constexpr int kNonTemporal = 2;
 constexpr int kSplitCountBits = 16;
 __device__ __forceinline__ bool splitk_last(uint64_t* ctr, uint32_t nsplit, uint64_t tag) {
     __shared__ uint32_t splitk_count;

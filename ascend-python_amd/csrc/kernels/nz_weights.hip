@@ -25,7 +25,8 @@
 // over all of K, so no partial sums leave the workgroup.  Its waves split K
 // into equal runs of superblocks; every wave issues the loads of two
 // superblocks ahead (for K = 4096 that is all of its loads, issued before the
-// first MFMA), folds group scale and offset into its accumulators per
+// first MFMA; x by whole-line DMAs into the wave's LDS slots, the weights
+// non-temporal), folds group scale and offset into its accumulators per
 // superblock with the algebra of the row-major kernels,
 //   acc += s * sum_k x*(w + BASE) + s*(offset - BASE) * sum_k x,
 // and the waves' sums are added through LDS in K order (deterministic).
@@ -232,22 +233,55 @@ __device__ __forceinline__ u32x4 nz8_operand(uint32_t lo, uint32_t hi) {
 // NB: n-blocks per workgroup (the last workgroups may own one fewer: their
 // extra block repeats a real one and is not stored).  NIT: superblocks per
 // wave.  The grid is (workgroups along N) x (16-row blocks of M); a
-// workgroup has K / (128 * NIT) waves.  A superblock's scale and offset rows
-// (the workgroup's NB*16 columns of one group) come in with one 16-byte load
-// per fetching lane and reach the other lanes through the wave's own LDS slot.
+// workgroup has K / (128 * NIT) waves.
+// * The x rows of a superblock (16 rows x 256 bytes) come into the wave's own
+//   LDS slot by four direct-to-LDS loads of four whole rows each (whole
+//   128-byte lines; loads into VGPRs in the MFMA's lane order would touch 16
+//   half lines per instruction), and the A operands are read back from there.
+//   Superblock it's DMAs have landed once at most the vector-memory loads
+//   issued after them are outstanding (the wave waits on vmcnt itself; the
+//   compiler does not count these loads).
+// * The packed weights are read once, with the non-temporal hint, so that
+//   they stream past the L2 instead of evicting the x rows every workgroup of
+//   the XCD reads again (measured: 8.5 -> 7.4 us on the cfg3 decode shape,
+//   with either change alone about half of that).
+// * A superblock's scale and offset rows (the workgroup's NB*16 columns of
+//   one group) come in with one 16-byte load per fetching lane and reach the
+//   other lanes through the wave's own LDS slot.
+// * The waves' sums meet in LDS (each wave's in its own x slots, which it no
+//   longer reads) and are added in K order.
 // W8: int8 NZ weights (two 1 KB blocks per 128 rows; the operand of 16-bit MFMA
 // step j is rows 16g + 8*(j&1) .. +8 of block j>>1, and its A operand is
 // x[m, 128s + 64*(j>>1) + 16g + 8*(j&1) ..]).
+constexpr int kNzXSlot = 4096;  // bytes of x per superblock and wave: 16 rows x 256 bytes
+
+// s_waitcnt vmcnt(n) for a value known after unrolling; "memory" keeps the LDS reads after it
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+#define QK_WAIT_CASE(v) \
+    case v: asm volatile("s_waitcnt vmcnt(" #v ")" ::: "memory"); break;
+        QK_WAIT_CASE(0) QK_WAIT_CASE(1) QK_WAIT_CASE(2) QK_WAIT_CASE(3) QK_WAIT_CASE(4) QK_WAIT_CASE(5)
+        QK_WAIT_CASE(6) QK_WAIT_CASE(7) QK_WAIT_CASE(8) QK_WAIT_CASE(9) QK_WAIT_CASE(10) QK_WAIT_CASE(11)
+        QK_WAIT_CASE(12) QK_WAIT_CASE(13) QK_WAIT_CASE(14) QK_WAIT_CASE(15) QK_WAIT_CASE(16) QK_WAIT_CASE(17)
+        QK_WAIT_CASE(18) QK_WAIT_CASE(19) QK_WAIT_CASE(20) QK_WAIT_CASE(21) QK_WAIT_CASE(22) QK_WAIT_CASE(23)
+#undef QK_WAIT_CASE
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+
 template <int DT, int NB, int NIT, bool HAS_OFF, bool W8>
 __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int nwg, int nrb) {
     typedef Mfma<DT> MM;
     constexpr int WL = W8 ? 2 : 1;         // weight loads per block and superblock
     constexpr int PF = NIT < 2 ? NIT : 2;  // superblocks in flight per wave
-    constexpr int SL = PF;                 // register slots
+    constexpr int SL = PF;                 // x slots and scale rows per wave
     constexpr int NT = HAS_OFF ? 2 : 1;    // scale rows per superblock (scale, offset)
     constexpr int RL = 2 * NB;             // 16-byte pieces of one row (NB*16 columns)
+    constexpr int GRP = 5 + NB * WL;       // vector-memory loads per superblock: 4 x DMAs, scale rows, weights
     static_assert(NT * RL <= 64, "one load instruction fetches a superblock's scale rows");
-    __shared__ __attribute__((aligned(16))) float red[kNzMaxWaves][NB][kNzTilePitch];
+    // per wave: its x slots, later its partial sums (NB tiles of kNzTilePitch floats)
+    constexpr int WSLOT = SL * kNzXSlot > NB * kNzTilePitch * 4 ? SL * kNzXSlot : NB * kNzTilePitch * 4;
+    __shared__ __attribute__((aligned(16))) char xbuf[kNzMaxWaves * WSLOT];
     __shared__ __attribute__((aligned(16))) uint16_t srow[kNzMaxWaves][SL][NT][NB * 16];
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -261,11 +295,18 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
     // block range of this workgroup (32-bit: (nwg + 1) * NBT < 2^31, checked by the planner)
     const int b0 = (int)((uint32_t)(wg * NBT) / (uint32_t)nwg), b1 = (int)((uint32_t)((wg + 1) * NBT) / (uint32_t)nwg);
     const int s0 = wave * NIT;
-    // rows past M read row M-1 (each output row depends on its own x row only) and are not stored
-    const int m = rb * 16 + c < M ? rb * 16 + c : M - 1;
 
+    // x DMA q of a superblock: rows 4q .. 4q+3 of the row block, lane -> (row 4q + lane/16, 16-byte piece
+    // lane%16); rows past M read row M-1 (each output row depends on its own x row only) and are not stored
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
-    const uint32_t x_lane = ((uint32_t)m * (uint32_t)K + (W8 ? 16u : 8u) * (uint32_t)g) * 2u;
+    uint32_t x_dma[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int row = rb * 16 + 4 * q + (lane >> 4);
+        x_dma[q] = (uint32_t)(row < M ? row : M - 1) * (uint32_t)K * 2u + 16u * (uint32_t)(lane & 15);
+    }
+    char* const xw = xbuf + wave * WSLOT;
+    const uint32_t xw_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)xbuf + (uint32_t)(wave * WSLOT);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (uint32_t)K * (uint32_t)N / (W8 ? 1u : 2u));
     const uint32_t w_lane = (uint32_t)lane * 16u;
     // lane l < NT*RL fetches 16 bytes of row l / RL (scale, offset) of a superblock's group: columns
@@ -280,24 +321,25 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
 #pragma unroll
     for (int b = 0; b < NB; ++b) blk[b] = b0 + b < b1 ? b0 + b : b1 - 1;
 
-    u32x4 xa[SL][4], wv[SL][NB][WL], sa[SL];
+    u32x4 wv[SL][NB][WL], sa[SL];
+    // one superblock's loads in a fixed order: 4 x DMAs, the scale rows, the weights (non-temporal)
     auto issue = [&](int it) {
+        asm volatile("" ::: "memory");  // the LDS reads of the slot's previous superblock stay before its DMAs
         __builtin_amdgcn_sched_barrier(0);
         const int s = s0 + it, sl = it % SL;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dma16(xr, xw_lds + (uint32_t)(sl * kNzXSlot + q * 1024), x_dma[q], (uint32_t)s * 256u);
         const uint32_t grp = (uint32_t)(s * 128) / (uint32_t)G;
         sa[sl] = *reinterpret_cast<const u32x4*>(sl_base + (size_t)grp * (uint32_t)N);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t xo = W8 ? (uint32_t)(s * 256 + 128 * (j >> 1) + 16 * (j & 1)) : (uint32_t)(s * 256 + 64 * j);
-            xa[sl][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, x_lane, xo, 0));
-        }
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
             for (int h = 0; h < WL; ++h)
                 wv[sl][b][h] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               wr, w_lane, ((uint32_t)blk[b] * (uint32_t)(WL * S) + (uint32_t)(WL * s + h)) * 1024u, 0));
+                               wr, w_lane, ((uint32_t)blk[b] * (uint32_t)(WL * S) + (uint32_t)(WL * s + h)) * 1024u,
+                               kNonTemporal));
         __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
@@ -312,11 +354,17 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int sl = it % SL;
+        // superblock it's x DMAs have landed: after them this wave issued its scale rows and weights and
+        // the whole groups of the superblocks up to it + PF - 1
+        const int later = (it + PF - 1 < NIT - 1 ? PF - 1 : NIT - 1 - it);
+        wait_vmcnt(1 + NB * WL + later * GRP);
         // this superblock's scale rows through the wave's LDS slot
         if (lane < NT * RL) *reinterpret_cast<u32x4*>(&srow[wave][sl][0][0] + 8 * lane) = sa[sl];
         u32x4 xk[4], wk[NB][WL];
+        const char* xrow = xw + sl * kNzXSlot + c * 256;  // x row c of the row block
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xk[j] = xa[sl][j];
+        for (int j = 0; j < 4; ++j)
+            xk[j] = *reinterpret_cast<const u32x4*>(xrow + (W8 ? 128 * (j >> 1) + 32 * g + 16 * (j & 1) : 64 * j + 16 * g));
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -341,20 +389,20 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[b][r] = __builtin_fmaf(sf, ag[r], __builtin_fmaf(sx, xs[r], acc[b][r]));
         }
+        // the x reads of slot sl were consumed by the MFMAs above, so its next DMA may land
         if (it + PF < NIT) issue(it + PF);
     }
 
-    // the K ranges of waves a short K leaves out add as zeros in the reduction below
+    // partial sums of wave w: NB tiles at xbuf + w * WSLOT; lane (c, g) holds rows 4g..4g+3 of column c of
+    // each block, row r of a tile sits at 16*(r + r/4) + column, so the 64 lanes of one store hit 64 banks.
+    // The K ranges of waves a short K leaves out add as zeros.
     for (int w = nwave + wave; w < kNzMaxWaves; w += nwave)
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-            for (int e = lane; e < kNzTilePitch; e += 64) red[w][b][e] = 0.0f;
-    // lane (c, g) holds rows 4g..4g+3 of column c of each block; row r of a
-    // tile sits at 16*(r + r/4) + column, so the 64 lanes of one store hit 64 banks
+        for (int e = lane; e < NB * kNzTilePitch; e += 64) reinterpret_cast<float*>(xbuf + w * WSLOT)[e] = 0.0f;
+    float* const red = reinterpret_cast<float*>(xw);
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][b][16 * (5 * g + r) + c] = acc[b][r];
+        for (int r = 0; r < 4; ++r) red[b * kNzTilePitch + 16 * (5 * g + r) + c] = acc[b][r];
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
 
@@ -362,10 +410,10 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
     const int nb = b1 - b0;
     for (int t = threadIdx.x; t < NB * 256; t += blockDim.x) {
         const int b = t >> 8, row = (t >> 4) & 15, col = t & 15;
-        const int at = 16 * (row + (row >> 2)) + col;
+        const int at = b * kNzTilePitch + 16 * (row + (row >> 2)) + col;
         float part[kNzMaxWaves];
 #pragma unroll
-        for (int w = 0; w < kNzMaxWaves; ++w) part[w] = red[w][b][at];
+        for (int w = 0; w < kNzMaxWaves; ++w) part[w] = reinterpret_cast<const float*>(xbuf + w * WSLOT)[at];
         float v = part[0];
 #pragma unroll
         for (int w = 1; w < kNzMaxWaves; ++w) v += part[w];

@@ -842,14 +842,21 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
 #pragma unroll
         for (int i = 0; i < B_PER_T; ++i) {
             const int q = tid + kThreads * i;
+            // one row tile (M <= 16) reads each weight byte once: non-temporal, so the weight streams past
+            // the L2 instead of evicting the x rows that every workgroup reads again
+            auto wload = [](const int8_t* src) {
+                const i32x4* v = reinterpret_cast<const i32x4*>(src);
+                if constexpr (MT == 1) return __builtin_nontemporal_load(v);
+                else return *v;
+            };
             if (!B_KN) {
                 const int r = q >> 3, c = q & 7;
                 const int64_t n = n0 + r;
-                rb[i] = n < p.N ? *reinterpret_cast<const i32x4*>(p.b + n * p.sbn + k0 + 16 * c) : (i32x4){0, 0, 0, 0};
+                rb[i] = n < p.N ? wload(p.b + n * p.sbn + k0 + 16 * c) : (i32x4){0, 0, 0, 0};
             } else {
                 const int kr = q >> 4, c16 = q & 15;
                 const int64_t n = n0 + 16 * c16;
-                rb[i] = n < p.N ? *reinterpret_cast<const i32x4*>(p.b + (k0 + kr) * p.sbk + n) : (i32x4){0, 0, 0, 0};
+                rb[i] = n < p.N ? wload(p.b + (k0 + kr) * p.sbk + n) : (i32x4){0, 0, 0, 0};
             }
         }
     };
@@ -1308,7 +1315,8 @@ __global__ __launch_bounds__(nzd::NT) void qmm_nzd(QmmArgs p, int nwg) {
 #pragma unroll
         for (int b = 0; b < NB; ++b)
             wv[sl][b] = __builtin_bit_cast(
-                i32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, in ? blk[b] + kb * 1024u + w_lane : kOff, 0, 0));
+                i32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, in ? blk[b] + kb * 1024u + w_lane : kOff, 0,
+                                                             kNonTemporal));
         __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
