@@ -112,7 +112,7 @@ __global__ __launch_bounds__(NT) void rms_norm_vec(const uint16_t* __restrict__ 
     for (int i = 0; i < VPT; ++i) {
         const int idx = threadIdx.x + i * NT;
         if (idx < nv) {
-            unpack8(xr[idx], DT, v[i]);
+            unpack8(__builtin_nontemporal_load(xr + idx), DT, v[i]);  // read once
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[i][e], v[i][e], ss);
         }
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(NT) void rms_norm_vec(const uint16_t* __restrict__ 
                 v[i][e] = load_half_bits(yb[i][e], DT);  // y as a later read of it would see it
                 amax = fmaxf(amax, fabsf(v[i][e]));
             }
-            if (!QUANT) reinterpret_cast<u32x4*>(y + row * D)[idx] = pack16<DT>(yb[i]);
+            if (!QUANT) __builtin_nontemporal_store(pack16<DT>(yb[i]), reinterpret_cast<u32x4*>(y + row * D) + idx);
         }
     }
     if (!QUANT) return;
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(NT) void rms_norm_vec(const uint16_t* __restrict__ 
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = threadIdx.x + i * NT;
-        if (idx < nv) reinterpret_cast<u32x2*>(q + row * D)[idx] = packq(v[i], rq);
+        if (idx < nv) __builtin_nontemporal_store(packq(v[i], rq), reinterpret_cast<u32x2*>(q + row * D) + idx);
     }
 }
 
@@ -256,8 +256,8 @@ __global__ __launch_bounds__(NT) void swiglu_vec(const uint16_t* __restrict__ h,
         const int idx = threadIdx.x + i * NT;
         if (idx < nv) {
             float a[8], b[8];
-            unpack8(ar[idx], DT, a);
-            unpack8(br[idx], DT, b);
+            unpack8(__builtin_nontemporal_load(ar + idx), DT, a);  // read once
+            unpack8(__builtin_nontemporal_load(br + idx), DT, b);
             uint32_t yb[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(NT) void swiglu_vec(const uint16_t* __restrict__ h,
                 v[i][e] = load_half_bits(yb[e], DT);
                 amax = fmaxf(amax, fabsf(v[i][e]));
             }
-            if (!QUANT) reinterpret_cast<u32x4*>(y + row * I)[idx] = pack16<DT>(yb);
+            if (!QUANT) __builtin_nontemporal_store(pack16<DT>(yb), reinterpret_cast<u32x4*>(y + row * I) + idx);
         }
     }
     if (!QUANT) return;
@@ -276,7 +276,7 @@ __global__ __launch_bounds__(NT) void swiglu_vec(const uint16_t* __restrict__ h,
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = threadIdx.x + i * NT;
-        if (idx < nv) reinterpret_cast<u32x2*>(q + row * I)[idx] = packq(v[i], rq);
+        if (idx < nv) __builtin_nontemporal_store(packq(v[i], rq), reinterpret_cast<u32x2*>(q + row * I) + idx);
     }
 }
 

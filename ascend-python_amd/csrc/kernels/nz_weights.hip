@@ -642,7 +642,8 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
         const int row = q / CPRO, c = q % CPRO;
         if (row >= rows) break;
         const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * OROWB + 16 * c);
-        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N + n0 + 8 * c) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N +
+                                                                n0 + 8 * c));  // written once
     }
 }
 

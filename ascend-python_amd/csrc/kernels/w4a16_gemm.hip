@@ -918,7 +918,8 @@ __global__ __launch_bounds__(512) void w4_gemm(WqbmmArgs p, int tiles_m, int til
         for (int q = tid; q < pf::BM * CPRO; q += NT) {
             const int row = q / CPRO, c = q % CPRO;
             const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * OROWB + 16 * c);
-            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N + n0 + 8 * c) = v;
+            __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N +
+                                                                n0 + 8 * c));  // written once
         }
         return;
     }
@@ -1271,7 +1272,8 @@ __global__ __launch_bounds__(pd::NT) void w4_dma(WqbmmArgs p, int tiles_m, int t
     for (int q = tid; q < BM * CPRO; q += NT) {
         const int row = q / CPRO, c = q % CPRO;
         const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * OROWB + 16 * c);
-        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N + n0 + 8 * c) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N +
+                                                                n0 + 8 * c));  // written once
     }
 }
 
