@@ -1386,7 +1386,7 @@ __global__ __launch_bounds__(kThreads) void qmm_reduce(QmmArgs p, int nsplit, co
             const int ns = nsplit < 16 ? nsplit : 16;
 #pragma unroll
             for (int k = 0; k < 16; ++k)
-                if (k < ns) part[k] = src[(int64_t)k * total4 + idx];
+                if (k < ns) part[k] = __builtin_nontemporal_load(src + (int64_t)k * total4 + idx);  // read once
             uint32_t s[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int k = 0; k < 16; ++k)
@@ -1399,6 +1399,30 @@ __global__ __launch_bounds__(kThreads) void qmm_reduce(QmmArgs p, int nsplit, co
                 for (int t = 0; t < 4; ++t) s[t] += (uint32_t)v[t];
             }
             const int64_t o = idx * 4, m = o / p.N, n = o % p.N;
+            const QmmEpilogue& e = p.epi;
+            if (e.out_dtype == QK_BF16 || e.out_dtype == QK_F16) {
+                // qmm_store's operations for 4 columns of one row, one 8-byte store
+                const float pt = e.pertoken ? e.pertoken[m] : 1.0f;
+                uint32_t h[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    int32_t acc = (int32_t)s[t];
+                    float bf = 0.0f;
+                    if (e.bias_dtype == QK_I32) acc = (int32_t)((uint32_t)acc + (uint32_t)((const int32_t*)e.bias)[n + t]);
+                    else if (e.bias_dtype) bf = load_scalar(e.bias, n + t, e.bias_dtype);
+                    float v = (float)acc;
+                    if (e.pertoken) v = v * pt;
+                    v = __builtin_fmaf(v, e.scale[e.scale_per_ch ? n + t : 0], bf);
+                    h[t] = e.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+                }
+                uint16_t* dst = static_cast<uint16_t*>(e.out) + m * e.ldo + n;
+                if (((uintptr_t)dst & 7) == 0)
+                    *reinterpret_cast<u32x2*>(dst) = (u32x2){h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+                else
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) dst[t] = (uint16_t)h[t];
+                continue;
+            }
 #pragma unroll
             for (int t = 0; t < 4; ++t) qmm_store(p.epi, m, n + t, (int32_t)s[t]);
         }
