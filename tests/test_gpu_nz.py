@@ -279,3 +279,49 @@ def test_abi_w8_nz(ops, oracle):
     assert rc == 0, ops.last_error()
     torch.cuda.synchronize()
     _close(out, _w8_ref(oracle, d, 128, torch.bfloat16), torch.bfloat16)
+
+
+# ----------------------------------------------------------------------------- seeded random decode shapes
+
+def _random_decode_shapes(seed, n):
+    """M <= 64 decode shapes the NZ decode kernel plans for: K = 128 * S superblocks (S from 1 to 64, so 1 to 4
+    superblocks per wave and 1 to 16 waves), groups of 128 / 256 / 512 rows or per channel, N any multiple of 16
+    (sized so the C oracle finishes in well under a second)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        S = int(rng.choice([1, 2, 3, 4, 5, 6, 8, 12, 16, 24, 32, 48, 64]))
+        K = 128 * S
+        group = int(rng.choice([g for g in (128, 256, 512) if K % g == 0] + [0]))
+        M = int(rng.integers(1, 65))
+        nmax = max(2, min(400, int(6e7 // (M * K * 16))))
+        N = 16 * int(rng.integers(1, nmax + 1))
+        out.append((M, N, K, group, bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,fp16,bias", _random_decode_shapes(2026, 12))
+def test_w4a16_nz_decode_random_shapes(ops, oracle, M, N, K, group, offset, fp16, bias):
+    """The NZ decode kernel (x rows by direct-to-LDS loads, non-temporal weight stream) on seeded random shapes
+    against the oracle, within rtol / atol 1e-2."""
+    x_dtype = torch.float16 if fp16 else torch.bfloat16
+    say(f"w4a16 NZ decode random M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    d = _inputs(M, N, K, group, offset, x_dtype, seed=M * 7 + N + K)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(N)).to(x_dtype) if bias else None
+    nz = ops.npu_format_cast(d["w_packed"].to(DEV), 29)
+    out = _run(ops, d, group, nz, bias=b)
+    _close(out, _ref(oracle, d, group, bias=b, x_dtype=x_dtype), x_dtype)
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,fp16,bias", _random_decode_shapes(7, 8))
+def test_w8a16_nz_decode_random_shapes(ops, oracle, M, N, K, group, offset, fp16, bias):
+    """The same kernel on int8 NZ weights (two 1 KB blocks per 128 rows) on seeded random shapes."""
+    x_dtype = torch.float16 if fp16 else torch.bfloat16
+    say(f"w8a16 NZ decode random M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    d = _w8(M, N, K, group, offset, x_dtype, seed=M * 5 + N + K)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(N + 1)).to(x_dtype) if bias else None
+    nz = ops.npu_format_cast(d["w"].to(DEV), 29)
+    out = ops.npu_weight_quant_batchmatmul(
+        d["x"].to(DEV), nz, d["scale"].to(DEV), None if d["offset"] is None else d["offset"].to(DEV),
+        bias=None if b is None else b.to(DEV), antiquant_group_size=group)
+    _close(out, _w8_ref(oracle, d, group, x_dtype, bias=b), x_dtype)
