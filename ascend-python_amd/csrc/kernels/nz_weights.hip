@@ -269,7 +269,8 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
     }
 }
 
-template <int DT, int NB, int NIT, bool HAS_OFF, bool W8>
+// SDT: the dtype of the scale and offset rows (QK_F16 or QK_BF16), fixed at compile time.
+template <int DT, int NB, int NIT, bool HAS_OFF, bool W8, int SDT>
 __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int nwg, int nrb) {
     typedef Mfma<DT> MM;
     constexpr int WL = W8 ? 2 : 1;         // weight loads per block and superblock
@@ -383,8 +384,8 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
                 else
                     ag = MM::mma(xk[j], nz_operand<MM::MAGIC>(wk[b][0][j]), ag);
             }
-            const float sf = load_half_bits(srow[wave][sl][0][16 * b + c], p.s_dtype);
-            const float of = HAS_OFF ? load_half_bits(srow[wave][sl][NT - 1][16 * b + c], p.s_dtype) : 0.0f;
+            const float sf = load_half_bits(srow[wave][sl][0][16 * b + c], SDT);
+            const float of = HAS_OFF ? load_half_bits(srow[wave][sl][NT - 1][16 * b + c], SDT) : 0.0f;
             const float sx = sf * (of - BASE);
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[b][r] = __builtin_fmaf(sf, ag[r], __builtin_fmaf(sx, xs[r], acc[b][r]));
@@ -702,7 +703,8 @@ template <int DT, int NB, int NIT, bool OFF, bool W8>
 hipError_t launch_nz_k(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
     if constexpr (NB <= nz_max_blocks(NIT, W8)) {
         const dim3 grid((uint32_t)(z.nwg * z.nrb)), block((uint32_t)(64 * z.nwave));
-        w4nz_decode<DT, NB, NIT, OFF, W8><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
+        if (p.s_dtype == QK_BF16) w4nz_decode<DT, NB, NIT, OFF, W8, QK_BF16><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
+        else w4nz_decode<DT, NB, NIT, OFF, W8, QK_F16><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;  // not planned (nz_plan caps NB by nz_max_blocks)
