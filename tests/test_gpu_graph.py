@@ -1,0 +1,85 @@
+"""The ops under HIP graph capture (torch.cuda.CUDAGraph): captured once, replayed several times with eager
+work and synchronisations between the replays, every replay bit for bit equal to the eager call.
+
+This covers the split-K counters at the head of the workspace, whose per-call tag is baked into the captured
+kernel arguments: the last arrival of each tile clears its counter word, so every replay finds it empty (the
+workspace contract in include/qk_abi.h). No op issues a memset or allocates inside the library, so nothing
+else is captured but kernels.
+"""
+import pytest
+import torch
+
+from op_plugin_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import op_plugin_amd
+    return op_plugin_amd
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _inputs():
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((16, 4096), generator=g).to(torch.float16)
+    w8 = torch.randint(-127, 128, (4096, 4096), generator=g, dtype=torch.int8)      # [K, N]
+    s8 = (1e-3 + 9e-3 * torch.rand(4096, generator=g)).float()
+    bias = (0.1 * torch.randn(4096, generator=g)).to(torch.bfloat16)
+    c = W.W4A16Case(M=16, N=11008, K=4096, group=128, x_dtype=torch.bfloat16, offset=True)
+    d4 = W.w4a16_inputs(c, seed=3)
+    return dict(x=x.to(DEV), w8=w8.to(DEV), s8=s8.to(DEV), bias=bias.to(DEV), x4=d4["x"].to(DEV),
+                w4=d4["w_packed"].to(DEV), sc4=d4["scale"].to(DEV), of4=d4["offset"].to(DEV))
+
+
+def _path(ops, t, w4nz):
+    """dynamic quant -> W8A8 (M = 16 on a [K,N] weight: the split stream + reduce), W4A16 decode on the
+    row-major weight (split-K stream with its counters) and on the NZ weight."""
+    xq, xs = ops.npu_dynamic_quant(t["x"])
+    y8 = ops.npu_quant_matmul(xq, t["w8"], t["s8"], pertoken_scale=xs, bias=t["bias"], output_dtype=torch.bfloat16)
+    y4 = ops.npu_weight_quant_batchmatmul(t["x4"], t["w4"], t["sc4"], t["of4"], antiquant_group_size=128)
+    y4nz = ops.npu_weight_quant_batchmatmul(t["x4"], w4nz, t["sc4"], t["of4"], antiquant_group_size=128)
+    return xq, xs, y8, y4, y4nz
+
+
+def test_graph_replays_match_eager(ops):
+    say("HIP graph: dynamic quant + W8A8 split stream + W4A16 split stream + NZ decode, 5 replays")
+    t = _inputs()
+    w4nz = ops.npu_format_cast(t["w4"], 29)
+    eager = [r.clone() for r in _path(ops, t, w4nz)]
+    torch.cuda.synchronize()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            _path(ops, t, w4nz)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = _path(ops, t, w4nz)
+    torch.cuda.synchronize()
+
+    for r in range(5):
+        for o in captured:
+            o.zero_()  # a fill kernel, not a memset node; the replay must rewrite every output
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, ref in zip(("y", "scale", "w8a8", "w4a16", "w4a16_nz"), captured, eager):
+            assert torch.equal(got, ref), f"replay {r}: {name} differs from the eager call"
+        # eager work between the replays, on the same workspace-holding allocator and stream
+        again = _path(ops, t, w4nz)
+        torch.cuda.synchronize()
+        for name, got, ref in zip(("y", "scale", "w8a8", "w4a16", "w4a16_nz"), again, eager):
+            assert torch.equal(got, ref), f"eager call after replay {r}: {name} differs"
