@@ -222,6 +222,37 @@ __device__ __forceinline__ int32_t quant_row(float v, const RowQuant& q) {
     return quant1(v, q.s);
 }
 
+// Eight values of one row -> eight int8 (element e in byte e % 4 of dword e / 4), each equal to
+// quant1(v[e], s).  On a row whose 1/s is safely normal (q.fast), t = v * r is rounded to an integer by
+// adding 1.5 * 2^23 (the fp32 add rounds to nearest even, as rint does), and the low byte of the sum's bits is
+// the two's-complement int8: |t| <= 127 * (1 + 2^-22) here (s = RN(absmax / 127), r = RN(1 / s), |v| <=
+// absmax), so it rounds into [-127, 127] and needs no clamp.  The fast and the exact rule agree unless t lies
+// within 2^-14 of a half-integer (see quant_row) or is NaN; such a group of eight (about one in a thousand) is
+// redone element by element with quant_row.  No branch per element on the common path.
+__device__ __forceinline__ u32x2 quant8(const float (&v)[8], const RowQuant& q) {
+    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+    uint32_t m[8];
+    bool exact = !q.fast;
+    if (q.fast) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float t = v[e] * q.r;
+            const float mf = t + kMagic;
+            const float d = t - (mf - kMagic);  // t - rint(t), exact
+            exact |= !(fabsf(d) < 0.5f - 0x1p-14f);
+            m[e] = __float_as_uint(mf);
+        }
+    }
+    if (exact) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m[e] = (uint32_t)quant_row(v[e], q);
+    }
+    // byte 0 of each: two v_perm_b32 (bytes of m[2k+1] and m[2k] into the low half) and one shift-or per dword
+    const uint32_t p01 = __builtin_amdgcn_perm(m[1], m[0], 0x0c0c0400u), p23 = __builtin_amdgcn_perm(m[3], m[2], 0x0c0c0400u);
+    const uint32_t p45 = __builtin_amdgcn_perm(m[5], m[4], 0x0c0c0400u), p67 = __builtin_amdgcn_perm(m[7], m[6], 0x0c0c0400u);
+    return (u32x2){p01 | (p23 << 16), p45 | (p67 << 16)};
+}
+
 // ---------------------------------------------------------------- XCD-aware ids
 // The dispatcher hands consecutive workgroup ids to the 8 XCDs round-robin,
 // and each XCD has its own L2.  Renumbering so that the ids one XCD receives

@@ -85,15 +85,7 @@ __device__ __forceinline__ u32x4 pack16(const uint32_t yb[8]) {
     return o;
 }
 
-__device__ __forceinline__ u32x2 packq(const float yf[8], const RowQuant& rq) {
-    u32x2 o = {0u, 0u};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        o[0] |= ((uint32_t)quant_row(yf[e], rq) & 0xffu) << (8 * e);
-        o[1] |= ((uint32_t)quant_row(yf[4 + e], rq) & 0xffu) << (8 * e);
-    }
-    return o;
-}
+__device__ __forceinline__ u32x2 packq(const float (&yf)[8], const RowQuant& rq) { return quant8(yf, rq); }
 
 // ---------------------------------------------------------------- RMSNorm
 // Vector path: D % 8 == 0, 16-byte aligned rows, D <= 8 * NT * VPT.

@@ -256,3 +256,36 @@ def test_fast_quantizer_rule():
         assert np.array_equal(got, ref), trial
         slow += int(np.sum(~fast))
     assert slow >= 8 * 1000  # the tie rows took the division path
+
+
+def test_quant8_magic_rounding_rule():
+    """quant8 (csrc/kernels/common.h) rounds t = RN(v * RN(1/s)) to an integer by adding 1.5 * 2^23 in float32
+    and takes the low byte of the sum's bits as the int8; a group of eight with an element within 2^-14 of a
+    half-integer (or NaN) is redone with the exact rule.  Emulated here in numpy float32 (IEEE, round to nearest
+    even) on rows of widely varying magnitude with planted exact ties, against clamp(rint(RN(v / s)))."""
+    import numpy as np
+
+    rng = np.random.default_rng(5)
+    f32 = np.float32
+    magic = f32(12582912.0)
+    redone = 0
+    for trial in range(24):
+        v = (rng.standard_normal(16384) * 2.0 ** int(rng.integers(-60, 60))).astype(f32)
+        if trial % 3 == 0:
+            s0 = f32(f32(np.max(np.abs(v))) / f32(127))
+            v[:1000] = ((rng.integers(-127, 127, 1000).astype(f32) + f32(0.5)) * s0).astype(f32)
+        if trial % 4 == 1:
+            v[5] = -v[np.argmax(np.abs(v))]  # the absmax element with both signs: t = +-127 exactly
+        s = f32(f32(np.max(np.abs(v))) / f32(127))
+        ref = np.clip(np.rint((v / s).astype(f32)), -128, 127).astype(np.int64)
+        t = (v * f32(f32(1) / s)).astype(f32)
+        mf = (t + magic).astype(f32)
+        d = (t - (mf - magic).astype(f32)).astype(f32)
+        safe = np.abs(d) < f32(0.5 - 2.0 ** -14)
+        byte = (mf.view(np.uint32) & 0xFF).astype(np.int64)
+        fast = np.where(byte > 127, byte - 256, byte)
+        group_safe = safe.reshape(-1, 8).all(axis=1).repeat(8)
+        assert np.all(np.abs(t) <= 127 * (1 + 2.0 ** -22))
+        assert np.array_equal(fast[group_safe], ref[group_safe]), trial
+        redone += int(np.sum(~group_safe))
+    assert redone >= 8 * 1000  # the tie rows' groups took the exact path
