@@ -375,12 +375,19 @@ struct WqbmmArgs {
 hipError_t launch_weight_quant_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 // xsum[g][m] = fp32 sum of x[m][k] over group g (G a multiple of 64), for the prefill kernels' group algebra
 hipError_t launch_w4_xsum(const WqbmmArgs& p, float* xsum, hipStream_t stream);
-size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group);
+// no_cast: the size without the plan that casts a row-major int4 weight to NZ in the workspace (for
+// callers whose scratch cannot hold the cast weight; the launch then runs the row-major kernels)
+size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group, bool no_cast = false);
 
 // NZ weights (nz_weights.hip): the ND <-> NZ casts (int4, int8) and the weight-quant matmul on NZ weights.
 hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t N, int32_t* dst, hipStream_t stream);
 hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N, int8_t* dst, hipStream_t stream);
 size_t w4_nz_workspace(const WqbmmArgs& args);
+// A row-major int4 weight at large M: cast to NZ into the workspace, then the NZ prefill GEMM.  The size is 0
+// when the plan does not apply; the launch returns false (running nothing) when it does not apply to these
+// operands or the workspace cannot hold it, else true with the launch status in *err.
+size_t w4_cast_nz_workspace(const WqbmmArgs& args);
+bool launch_w4_cast_nz(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream, hipError_t* err);
 hipError_t launch_w4_nz_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 
 // Static quantization (static_quant.hip): x [outer][C][inner] (fp32/fp16/bf16) -> q (int8/uint8/int32);

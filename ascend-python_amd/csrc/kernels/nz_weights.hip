@@ -829,7 +829,7 @@ size_t w4_nz_workspace(const WqbmmArgs& p) {
     if (!plan_override().w4nz_off && nzg_plan(p).ok) return nzg_workspace(p);
     const int nd_dtype = p.w_dtype == QK_I8_NZ ? QK_I8 : QK_I32;
     return QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(p)) +
-           weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group);
+           weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group, true);
 }
 
 hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes, hipStream_t stream) {
@@ -845,7 +845,7 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
     const bool w8 = p.w_dtype == QK_I8_NZ;
     const int nd_dtype = w8 ? QK_I8 : QK_I32;
     const size_t nd_bytes = round256(nd_weight_bytes(p));
-    const size_t rest = weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group);
+    const size_t rest = weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group, true);
     if (!workspace || ws_bytes < QK_SPLIT_COUNTER_BYTES + nd_bytes + rest || (uintptr_t)workspace % 256 != 0)
         return hipErrorInvalidValue;
     char* ws = static_cast<char*>(workspace);
@@ -859,6 +859,42 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
     q.w = nd;
     q.w_dtype = nd_dtype;
     return launch_weight_quant_bmm(q, rest ? ws + QK_SPLIT_COUNTER_BYTES + nd_bytes : nullptr, rest, stream);
+}
+
+// Row-major int4 [K, N/8] weights at large M: the call casts the weight into its workspace
+// ([QK_SPLIT_COUNTER_BYTES, unused][NZ weight][x group sums fp32 [K/G][M]]) and runs the NZ prefill GEMM on
+// it.  The cast reads and writes the packed weight once (K * N bytes in all); from M = 1024 the NZ GEMM saves
+// more than that costs (cfg3's 4096 x 11008 weight: cast ~15 us, NZ GEMM ~195 us against ~250 us for the
+// row-major prefill kernel).  The debug overrides that force or disable a prefill kernel switch it off.
+constexpr int64_t kCastNzMinM = 1024;
+
+size_t w4_cast_nz_workspace(const WqbmmArgs& p) {
+    const PlanOverride& ov = plan_override();
+    if (p.w_dtype != QK_I32 || p.M < kCastNzMinM || ov.w4nz_off || ov.w4_gemm != 0) return 0;
+    WqbmmArgs q = p;
+    q.w = reinterpret_cast<const void*>((uintptr_t)256);  // the cast's destination: 256-byte aligned
+    q.w_dtype = QK_I4_NZ;
+    if (!nzg_plan(q).ok) return 0;
+    return round256(QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)) + (nzg_workspace(q) - QK_SPLIT_COUNTER_BYTES));
+}
+
+bool launch_w4_cast_nz(const WqbmmArgs& p, void* workspace, size_t ws_bytes, hipStream_t stream, hipError_t* err) {
+    const size_t need = w4_cast_nz_workspace(p);
+    if (need == 0 || !workspace || ws_bytes < need || (uintptr_t)workspace % 256 != 0) return false;
+    char* ws = static_cast<char*>(workspace);
+    int32_t* nz = reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES);
+    WqbmmArgs q = p;
+    q.w = nz;
+    q.w_dtype = QK_I4_NZ;
+    const NzGemmPlan g = nzg_plan(q);  // with the call's own operands (their alignment)
+    if (!g.ok) return false;
+    hipError_t e = launch_w4_nz_cast(static_cast<const int32_t*>(p.w), true, p.K, p.N, nz, stream);
+    if (e == hipSuccess) {
+        float* xs = reinterpret_cast<float*>(ws + QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)));
+        e = p.x_dtype == QK_BF16 ? launch_nzg_dt<QK_BF16>(q, g, xs, stream) : launch_nzg_dt<QK_F16>(q, g, xs, stream);
+    }
+    *err = e;
+    return true;
 }
 
 }  // namespace qk

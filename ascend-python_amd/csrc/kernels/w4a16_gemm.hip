@@ -1603,7 +1603,7 @@ hipError_t launch_w4_xsum(const WqbmmArgs& p, float* xsum, hipStream_t stream) {
     return hipGetLastError();
 }
 
-size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group) {
+size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group, bool no_cast) {
     WqbmmArgs p{};
     p.M = M;
     p.N = N;
@@ -1615,6 +1615,8 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     p.w = (void*)(uintptr_t)256;
     if (p.group == 0) p.group = p.K;
     if (w_dtype == QK_I4_NZ || w_dtype == QK_I8_NZ) return w4_nz_workspace(p);
+    if (!no_cast)
+        if (const size_t c = w4_cast_nz_workspace(p)) return c;
     // [split-K counters][fp32 partials [nsplit][M][N]]
     const StreamPlan s = stream_plan(p);
     if (s.ok) return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
@@ -1651,6 +1653,8 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
                                       : launch_reduce<QK_F16>(p, sp.nsplit, partial, stream);
     }
     if (!sp.ok) {
+        hipError_t ce = hipSuccess;  // large M on an int4 weight: cast to NZ in the workspace, NZ prefill GEMM
+        if (launch_w4_cast_nz(p, workspace, ws_bytes, stream, &ce)) return ce;
         GemmPlan gp = gemm_plan(p);
         if (gp.ok) {
             // without the workspace the size query asked for, the register-staged kernel runs

@@ -335,7 +335,8 @@ int weight_quant_bmm_run(const char* op, const void* x, int x_dtype, const void*
     if (bias && !(is_half(bias_dtype) || bias_dtype == QK_F32)) return fail(QK_ERR_ARG, "%s: bias dtype %d unsupported", op, bias_dtype);
     if (M == 0 || N == 0) return QK_OK;
     if (!out || (K > 0 && (!x || !weight || !antiquant_scale))) return fail(QK_ERR_ARG, "%s: null pointer", op);
-    const size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size);
+    // the no-allocation scratch is sized without the cast-to-NZ plan (the cast weight may not fit in it)
+    const size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, scratch != nullptr);
     if (scratch && need > 0) {
         int rc = QK_OK;
         workspace = scratch(need, &workspace_bytes, &rc);
