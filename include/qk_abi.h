@@ -29,7 +29,8 @@
  * contents -- uninitialised memory is fine.  A non-empty workspace begins with
  * QK_SPLIT_COUNTER_BYTES of split-K arrival counters, followed by the partial
  * sums (split-K shapes) or by the activations' per-group sums (weight-quant
- * matmul at large M).  Each counter carries the tag of the call that counts
+ * matmul at large M; from M = 1024 on a row-major int4 weight the weight cast
+ * to NZ, K*N/2 bytes rounded to 256, comes first, then the sums).  Each counter carries the tag of the call that counts
  * into it (48 bits drawn per call, never 0 or all ones), so what an earlier
  * call or another user left there is not mistaken for arrivals of this call;
  * the one exception is memory whose counter words happen to hold this call's

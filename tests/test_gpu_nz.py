@@ -181,6 +181,57 @@ def test_w4a16_nz_prefill_kernel(ops, oracle, M, N, K, group, offset, x_dtype, b
     torch.testing.assert_close(out.float(), nd_out.float(), rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,bias", [
+    (1024, 2048, 1024, 128, True, torch.bfloat16, True),     # 8 x 8 tiles, one step per group
+    (1100, 2048, 2048, 256, False, torch.float16, False),    # two steps per group, last row tile of 76 rows
+    (1024, 2560, 1024, 0, True, torch.bfloat16, True),       # per channel
+])
+def test_w4a16_row_major_cast_to_nz(ops, oracle, plan, M, N, K, group, offset, x_dtype, bias):
+    """M >= 1024 on a row-major int4 weight: the call casts the weight to NZ in its workspace (which the size query
+    reports) and runs the NZ prefill kernel on the copy. Every output within rtol/atol 1e-2 of the float64
+    dequant-matmul (pinned against the C oracle on four rows) and of the row-major prefill kernel (the cast
+    switched off by the debug override)."""
+    say(f"w4a16 row-major cast to NZ M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    L = ops.abi()
+    ws = ctypes.c_size_t(0)
+    assert L.qk_weight_quant_bmm_workspace_size(M, N, K, ops.QK_I32, group, ctypes.byref(ws)) == 0
+    assert ws.value >= 4096 + K * N // 2, "the workspace holds the cast weight"
+    d = _inputs(M, N, K, group, offset, x_dtype, seed=M + N + K + 2)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(7)).to(x_dtype) if bias else None
+    wd = d["w_packed"].to(DEV)
+    out = _run(ops, d, group, wd, bias=b)
+    ref64 = exact.wq_dequant_matmul(d["x"], d["w"], d["scale"], d["offset"], group, bias=b)
+    rows = np.r_[0:2, M - 2:M]
+    pin = _ref(oracle, dict(d, x=d["x"][rows]), group, bias=b, x_dtype=x_dtype)
+    pin_diff = (W.from_bits(pin, x_dtype).float() - ref64[rows].float()).abs()
+    assert pin_diff.max().item() <= 2.0**-7 * ref64[rows].abs().max().item() + 1e-3
+    torch.testing.assert_close(out.cpu().float(), ref64.float(), rtol=1e-2, atol=1e-2)
+    plan("w4nz=off")
+    rm = _run(ops, d, group, wd, bias=b)
+    torch.testing.assert_close(out.float(), rm.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_abi_noalloc_row_major_beyond_cast(ops, oracle):
+    """The no-allocation entry point at M = 1024 on cfg3's row-major int4 weight, whose NZ copy (22.5 MB) does not
+    fit its 16 MB scratch: it sizes its scratch without the cast and runs the row-major prefill kernel, within
+    rtol/atol 1e-2 of the op (which casts) and of the float64 dequant-matmul."""
+    M, N, K = 1024, 11008, 4096
+    say(f"ABI qk_weight_quant_bmm_noalloc row-major int4 M={M} N={N} K={K}")
+    L = ops.abi()
+    d = _inputs(M, N, K, 128, True, torch.bfloat16, seed=21)
+    x, w, sc, off = d["x"].to(DEV), d["w_packed"].to(DEV), d["scale"].to(DEV), d["offset"].to(DEV)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    rc = L.qk_weight_quant_bmm_noalloc(x.data_ptr(), BF16, w.data_ptr(), ops.QK_I32, sc.data_ptr(), off.data_ptr(),
+                                       F16, M, N, K, 128, None, 0, out.data_ptr(), BF16,
+                                       torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ops.last_error()
+    op_out = _run(ops, d, 128, w)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.float(), op_out.float(), rtol=1e-2, atol=1e-2)
+    ref64 = exact.wq_dequant_matmul(d["x"], d["w"], d["scale"], d["offset"], 128)
+    torch.testing.assert_close(out.cpu().float(), ref64.float(), rtol=1e-2, atol=1e-2)
+
+
 def test_abi_nz_and_noalloc(ops, oracle):
     """qk_weight_quant_bmm with QK_I4_NZ through the C ABI (no workspace needed), and the no-allocation entry
     point on the same NZ weight, against the oracle."""
