@@ -125,16 +125,32 @@ static inline float load_any(const void* p, int64_t i, int dt) {
     }
 }
 
+/*
+ * Saturating conversion of an integral float to int8 with C99 fmaxf / fminf
+ * (IEEE 754 maxNum / minNum): t is clamped to [-128, 127] before the integer
+ * conversion, so the conversion is always defined, and a NaN t gives -128
+ * (fmaxf(NaN, -128) = -128).  These are the clamp operations the kernels use
+ * (fmaxf / fminf on gfx950, which return the non-NaN operand).
+ */
+static int8_t qo_sat_i8(float t) {
+    t = fminf(fmaxf(t, -128.0f), 127.0f);
+    return (int8_t)(int)t;
+}
+
 /* ------------------------------------------------------------------ */
 /* npu_dynamic_quant: per-row symmetric int8, scale = absmax / 127.    */
 /* ------------------------------------------------------------------ */
 /*
  * For each row r of x viewed as [rows, K]:
  *   xf[k]  = float(x[r,k]) (* smooth[k] when given, one float32 multiply)
- *   a      = max_k |xf[k]|
+ *   a      = max_k |xf[k]|                     (fmaxf from 0: NaN elements do not enter)
  *   s      = a / 127.0f                        (IEEE float32 division)
- *   y[r,k] = clamp(rint(xf[k] / s), -128, 127) (rint: ties to even)
+ *   y[r,k] = qo_sat_i8(rint(xf[k] / s))        (rint: ties to even; clamp to [-128, 127])
  * A row of zeros gives s = 0 and y = 0.
+ * Non-finite inputs follow the same formula: a row holding +-Inf gets
+ * s = +Inf, its finite elements 0 (x / Inf = +-0) and its +-Inf elements
+ * -128 (Inf / Inf = NaN); a NaN element of a row with s > 0 gives -128; a row
+ * whose nonzero values are all NaN has a = 0, so s = 0 and y = 0.
  * Dtype map int8 output as QInt8 -> kChar
  * (op_plugin/ops/base_ops/aclops/QuantizePerChannelKernelNpu.cpp:81-84).
  */
@@ -146,8 +162,7 @@ void qo_dynamic_quant(const uint16_t* x, int x_dtype, int64_t rows, int64_t K,
         for (int64_t k = 0; k < K; ++k) {
             float v = load_half(xr, k, x_dtype);
             if (smooth) v = v * smooth[k];
-            float a = fabsf(v);
-            if (a > amax) amax = a;
+            amax = fmaxf(amax, fabsf(v));
         }
         float s = amax / 127.0f;
         scale[r] = s;
@@ -156,10 +171,7 @@ void qo_dynamic_quant(const uint16_t* x, int x_dtype, int64_t rows, int64_t K,
             if (s != 0.0f) {
                 float v = load_half(xr, k, x_dtype);
                 if (smooth) v = v * smooth[k];
-                float t = rintf(v / s);
-                if (t > 127.0f) t = 127.0f;
-                if (t < -128.0f) t = -128.0f;
-                q = (int8_t)(int)t;
+                q = qo_sat_i8(rintf(v / s));
             }
             y[r * K + k] = q;
         }
@@ -234,10 +246,7 @@ void qo_quant_matmul_epilogue(const int32_t* acc, int64_t M, int64_t N,
             float v = (float)a;
             if (out_dtype == QO_I8) {
                 float off = offset ? offset[offset_len == 1 ? 0 : n] : 0.0f;
-                float t = rintf(fmaf(v, s, off));
-                if (t > 127.0f) t = 127.0f;
-                if (t < -128.0f) t = -128.0f;
-                ((int8_t*)out)[o] = (int8_t)(int)t;
+                ((int8_t*)out)[o] = qo_sat_i8(rintf(fmaf(v, s, off)));
                 continue;
             }
             if (pertoken) v = v * pertoken[m];

@@ -217,8 +217,10 @@ def test_quant_mlp_block_cfg5_nz_weights(ops):
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
-def test_quant_mlp_block_cfg5(ops, oracle):
-    """cfg5, all 512 rows, every stage against the oracle on the GPU's own inputs to that stage:
+@pytest.mark.parametrize("nz", [False, True])
+def test_quant_mlp_block_cfg5(ops, oracle, nz):
+    """cfg5, all 512 rows, every stage against the oracle on the GPU's own inputs to that stage, with the
+    [K,N] weights and (nz) with both weights cast once to the int8 NZ layout, as bench.py times the block:
     RMSNorm within one ulp; its fused quantization bit-exact (= qo_dynamic_quant of the GPU's RMSNorm
     output); the gate_up W8A8 bit-exact (exact float64 accumulator, pinned to qo_w8a8_acc, plus
     qo_quant_matmul_epilogue); SwiGLU within one ulp and its fused quantization bit-exact; the down W8A8
@@ -230,21 +232,23 @@ def test_quant_mlp_block_cfg5(ops, oracle):
     from op_plugin_amd.mlp import quant_mlp
     c = W.CFG5
     T = c["tokens"]
-    say(f"quant_mlp cfg5 T={T} H={c['hidden']} I={c['intermediate']} (all rows, every stage)")
+    say(f"quant_mlp cfg5 T={T} H={c['hidden']} I={c['intermediate']} (all rows, every stage) nz={nz}")
     d = W.mlp_inputs(T, c["hidden"], c["intermediate"], seed=0)
     dev = {k: v.to(DEV) for k, v in d.items()}
-    out = quant_mlp(dev["x"], dev["gamma"], dev["w_gu"], dev["s_gu"], dev["w_d"], dev["s_d"], eps=c["eps"])
-    out_u = quant_mlp(dev["x"], dev["gamma"], dev["w_gu"], dev["s_gu"], dev["w_d"], dev["s_d"], eps=c["eps"],
-                      fused=False)
+    w_gu, w_d = dev["w_gu"], dev["w_d"]
+    if nz:
+        w_gu, w_d = ops.npu_format_cast(w_gu, 29), ops.npu_format_cast(w_d, 29)
+    out = quant_mlp(dev["x"], dev["gamma"], w_gu, dev["s_gu"], w_d, dev["s_d"], eps=c["eps"])
+    out_u = quant_mlp(dev["x"], dev["gamma"], w_gu, dev["s_gu"], w_d, dev["s_d"], eps=c["eps"], fused=False)
     assert out.shape == (T, c["hidden"]) and out.dtype == torch.bfloat16
     assert torch.equal(out, out_u)
     # the block's stages, op by op
     y = ops.npu_rms_norm(dev["x"], dev["gamma"], c["eps"])[0]
     q1, s1, _ = ops.npu_rms_norm_dynamic_quant(dev["x"], dev["gamma"], c["eps"])
-    h = ops.npu_quant_matmul(q1, dev["w_gu"], dev["s_gu"], pertoken_scale=s1, output_dtype=torch.bfloat16)
+    h = ops.npu_quant_matmul(q1, w_gu, dev["s_gu"], pertoken_scale=s1, output_dtype=torch.bfloat16)
     sw = ops.npu_swiglu(h)
     q2, s2 = ops.npu_swiglu_dynamic_quant(h)
-    o = ops.npu_quant_matmul(q2, dev["w_d"], dev["s_d"], pertoken_scale=s2, output_dtype=torch.bfloat16)
+    o = ops.npu_quant_matmul(q2, w_d, dev["s_d"], pertoken_scale=s2, output_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     assert torch.equal(o, out)
     pin = np.r_[0, T - 1]

@@ -103,6 +103,38 @@ def test_dynamic_quant_edge_cases(ops, oracle, dtype, K):
     assert np.array_equal(y.cpu().numpy(), ry)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K", [8, 1000, 1001, 8192])
+def test_dynamic_quant_non_finite_and_half_max(ops, oracle, dtype, K):
+    """Rows at +-65504 (NPU_HALF_MAX, op_plugin/utils/OpConstants.h:25), rows holding NaN or +-Inf, an all-NaN row,
+    and for bf16 rows at the bf16 limit: bit-exact against the oracle's stated non-finite contract (NaN elements
+    do not enter the absmax; a NaN quotient gives -128; a row with an infinity has s = +Inf).  K = 1001 takes the
+    generic kernel, the others the vector kernel."""
+    say(f"dynamic_quant non-finite / half-max {dtype} K={K}")
+    g = torch.Generator().manual_seed(K + 1)
+    x = torch.randn((9, K), generator=g)
+    nan, inf = float("nan"), float("inf")
+    x[0, 0], x[0, K // 2] = 65504.0, -65504.0                  # fp16 limits with ordinary values
+    x[1] = 0.0
+    x[1, K - 1] = -65504.0                                      # a lone -65504
+    x[2, 1 % K] = nan                                           # one NaN in an ordinary row
+    x[3, ::3] = nan                                             # many NaNs
+    x[4, K - 1] = inf                                           # +Inf: s = +Inf
+    x[5, 0] = -inf
+    x[5, K // 2] = inf
+    x[5, K // 3] = nan
+    x[6] = nan                                                  # all NaN: s = 0, y = 0
+    x[7, 3 % K] = 3.3895e38 if dtype == torch.bfloat16 else 65504.0   # the dtype's largest finite value
+    x[8, :8] = torch.tensor([127.0, nan, 126.5, -0.5, 1.5, -inf if K > 8 else 2.0, 0.0, -2.5])
+    x = x.to(dtype)
+    y, s = ops.npu_dynamic_quant(x.to(DEV))
+    ry, rs = oracle.dynamic_quant(W.bits(x), CODE[dtype])
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert ry[6].tolist() == [0] * K and rs[6] == 0.0
+    assert ry[2, 1 % K] == -128 and rs[4] == np.inf
+
+
 def test_dynamic_quant_smooth_and_batch_dims(ops, oracle):
     say("dynamic_quant smooth scales, 3-D input")
     g = torch.Generator().manual_seed(11)
@@ -140,14 +172,20 @@ def test_quant_matmul_int32_exact(ops, oracle, M, N, K, transposed):
     assert np.array_equal(out.cpu().numpy(), ref)
 
 
-def _w8a8_full_path(ops, oracle, case, seed=0):
+def _w8a8_full_path(ops, oracle, case, seed=0, nz=False):
     """dynamic quant -> W8A8 -> bf16 on a whole config, every output element bit-exact against the oracle:
     the quantized rows and scales from qo_dynamic_quant, the accumulator from a float64 GEMM (exact; pinned
-    against qo_w8a8_acc on its first and last rows here), the epilogue from qo_quant_matmul_epilogue."""
+    against qo_w8a8_acc on its first and last rows here), the epilogue from qo_quant_matmul_epilogue.
+    nz: the weight is cast once to the int8 NZ layout (npu_format_cast(w, 29)) and the op reads that.
+    Returns the quantized activations (device), the weight the op read (device) and the exact accumulator."""
     d = W.w8a8_inputs(case, seed)
     x, w, ws, b = d["x"], d["w"], d["w_scale"], d["bias"]
     xq, xs = ops.npu_dynamic_quant(x.to(DEV))
-    out = ops.npu_quant_matmul(xq, w.to(DEV), ws.to(DEV), pertoken_scale=xs,
+    wd = w.to(DEV)
+    if nz:
+        wd = ops.npu_format_cast(wd, 29)
+        assert ops.get_npu_format(wd) == 29
+    out = ops.npu_quant_matmul(xq, wd, ws.to(DEV), pertoken_scale=xs,
                                bias=None if b is None else b.to(DEV), output_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     rq, rs = oracle.dynamic_quant(W.bits(x), CODE[x.dtype])
@@ -162,12 +200,13 @@ def _w8a8_full_path(ops, oracle, case, seed=0):
     bf16_close(got, ref)
     bad = np.argwhere(got != ref)
     assert bad.size == 0, f"{len(bad)} bf16 outputs differ in bits, first at {tuple(bad[0])}"
-    return xq, w
+    return xq, wd, acc
 
 
-def test_quant_matmul_cfg1(ops, oracle):
-    say("quant_matmul cfg1 full path 128x4096x4096")
-    _w8a8_full_path(ops, oracle, W.CFG1)
+@pytest.mark.parametrize("nz", [False, True])
+def test_quant_matmul_cfg1(ops, oracle, nz):
+    say(f"quant_matmul cfg1 full path 128x4096x4096 nz={nz}")
+    _w8a8_full_path(ops, oracle, W.CFG1, nz=nz)
 
 
 @pytest.mark.parametrize("idx", [0, 1, 2])
@@ -177,14 +216,16 @@ def test_quant_matmul_cfg2_decode(ops, oracle, idx):
     _w8a8_full_path(ops, oracle, c)
 
 
-def test_quant_matmul_cfg4_prefill(ops, oracle):
-    """Full 4096x8192x8192: every quantized activation, scale and bf16 output bit-exact against the oracle,
-    and the int32 output (the raw accumulators) equal to the exact accumulator element for element."""
+@pytest.mark.parametrize("nz", [False, True])
+def test_quant_matmul_cfg4_prefill(ops, oracle, nz):
+    """Full 4096x8192x8192 on the [K,N] weight and on its int8 NZ cast (the weight bench.py's headline line
+    times): every quantized activation, scale and bf16 output bit-exact against the oracle, and the int32
+    output (the raw accumulators) equal to the exact accumulator element for element."""
     c = W.CFG4
-    say("quant_matmul cfg4 prefill 4096x8192x8192 (whole output)")
-    xq, w = _w8a8_full_path(ops, oracle, c)
-    acc = ops.npu_quant_matmul(xq, w.to(DEV), torch.ones(1, device=DEV), output_dtype=torch.int32)
-    assert np.array_equal(acc.cpu().numpy(), exact.w8a8_acc(xq.cpu().numpy(), w.numpy()))
+    say(f"quant_matmul cfg4 prefill 4096x8192x8192 (whole output) nz={nz}")
+    xq, wd, acc_ref = _w8a8_full_path(ops, oracle, c, nz=nz)
+    acc = ops.npu_quant_matmul(xq, wd, torch.ones(1, device=DEV), output_dtype=torch.int32)
+    assert np.array_equal(acc.cpu().numpy(), acc_ref)
 
 
 @pytest.mark.parametrize("M,N,K,kn", [

@@ -75,6 +75,35 @@ def test_dynamic_quant_known_answers(oracle, code):
 
 
 @pytest.mark.parametrize("code", [F16, BF16])
+def test_dynamic_quant_non_finite_known_answers(oracle, code):
+    """The contract for non-finite rows, by hand: NaN elements do not enter the absmax (fmaxf from 0), the
+    clamp is fmaxf / fminf, so a NaN quotient gives -128; a row holding an infinity has s = +Inf, its finite
+    elements give 0 and its infinite ones Inf / Inf = NaN, so -128; an all-NaN row has s = 0 and y = 0."""
+    nan, inf = float("nan"), float("inf")
+    rows = [
+        [nan, 127.0, -3.5, 0.5, 2.5, nan],       # s = 1: NaN -> -128, ties to even
+        [inf, 5.0, -inf, 0.0, -1.0, 3.0],        # s = +Inf
+        [nan, nan, 0.0, 0.0, -0.0, nan],         # NaN only: s = 0, y = 0
+        [-inf, 0.0, 0.0, 0.0, 0.0, 0.0],         # a lone -Inf
+    ]
+    y, s = oracle.dynamic_quant(_half_bits(rows, code), code)
+    assert s[0] == 1.0 and s[1] == np.inf and s[2] == 0.0 and s[3] == np.inf
+    assert y.tolist() == [[-128, 127, -4, 0, 2, -128], [-128, 0, -128, 0, 0, 0], [0] * 6, [-128, 0, 0, 0, 0, 0]]
+
+
+def test_dynamic_quant_half_max_rows(oracle):
+    """Rows at the fp16 limit +-65504 (NPU_HALF_MAX, op_plugin/utils/OpConstants.h:25): s = RN(65504 / 127) and
+    the limits map to +-127; the float64 quotient of every other element is within half a step of y."""
+    row = [65504.0, -65504.0, 1.0, 257.0, -32752.0, 0.0, 515.0, -516.0]
+    x = _half_bits([row, [-65504.0] + [0.0] * 7], F16)
+    y, s = oracle.dynamic_quant(x, F16)
+    assert s[0] == np.float32(65504.0) / np.float32(127.0) and s[1] == s[0]
+    assert y[0, 0] == 127 and y[0, 1] == -127 and y[1, 0] == -127 and (y[1, 1:] == 0).all()
+    q = np.array(row) / np.float64(s[0])
+    assert np.all(np.abs(y[0] - q) <= 0.5 + 1e-5)
+
+
+@pytest.mark.parametrize("code", [F16, BF16])
 @pytest.mark.parametrize("K", [1, 7, 64, 4096])
 def test_dynamic_quant_invariants(oracle, code, K):
     g = torch.Generator().manual_seed(K)
