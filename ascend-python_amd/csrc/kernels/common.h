@@ -136,6 +136,12 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, u
 // this call's tag.  The last arrival sets the word to zero (every other
 // arrival has happened by then), so a captured graph that replays one tag
 // also finds an empty counter each time.
+// The first compare-and-swap guesses that every other split has already
+// arrived (expected value: this tag with nsplit - 1 arrivals) and clears the
+// word in the same operation; it fails with the word's actual value
+// otherwise, and the count goes on from there.  So the last arrival -- the
+// one the tile waits for -- finishes in a single atomic round trip, where an
+// atomic load followed by a compare-and-swap took two.
 // Cache-policy operand of the raw buffer loads/stores for device-coherent
 // access (the sc1 bit on gfx950).
 constexpr int kCoherent = 16;
@@ -148,14 +154,19 @@ __device__ __forceinline__ bool splitk_last(uint64_t* ctr, uint32_t nsplit, uint
     __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint64_t old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint64_t nw;
-        do {
-            nw = (old >> kSplitCountBits) == tag ? old + 1 : (tag << kSplitCountBits) | 1u;
-        } while (!__hip_atomic_compare_exchange_weak(ctr, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT));
-        const uint32_t n = (uint32_t)(nw & ((1u << kSplitCountBits) - 1));
-        if (n == nsplit) __hip_atomic_store(ctr, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t base = tag << kSplitCountBits;
+        uint64_t old = base | (nsplit - 1u);
+        uint32_t n = nsplit;
+        if (!__hip_atomic_compare_exchange_strong(ctr, &old, (uint64_t)0, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)) {
+            uint64_t nw;
+            do {
+                nw = (old >> kSplitCountBits) == tag ? old + 1 : base | 1u;
+            } while (!__hip_atomic_compare_exchange_weak(ctr, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT));
+            n = (uint32_t)(nw & ((1u << kSplitCountBits) - 1));
+            if (n == nsplit) __hip_atomic_store(ctr, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         splitk_count = n;
     }
     __syncthreads();
