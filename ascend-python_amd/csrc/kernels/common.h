@@ -373,7 +373,7 @@ struct WqbmmArgs {
     const void* x;
     int x_dtype;
     const void* w;
-    int w_dtype;          // QK_I32 (int4 packed), QK_I8, QK_I4_NZ or QK_I8_NZ
+    int w_dtype;          // QK_I32 (int4 packed), QK_I8, QK_I4_NZ, QK_I8_NZ or QK_I8_NK
     const void* scale;
     const void* offset;
     int s_dtype;
@@ -393,6 +393,8 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
 // NZ weights (nz_weights.hip): the ND <-> NZ casts (int4, int8) and the weight-quant matmul on NZ weights.
 hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t N, int32_t* dst, hipStream_t stream);
 hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N, int8_t* dst, hipStream_t stream);
+// int8 [N, K] -> [K, N]
+hipError_t launch_w8_nk_transpose(const int8_t* src, int64_t K, int64_t N, int8_t* dst, hipStream_t stream);
 size_t w4_nz_workspace(const WqbmmArgs& args);
 // A row-major int4 weight at large M: cast to NZ into the workspace, then the NZ prefill GEMM.  The size is 0
 // when the plan does not apply; the launch returns false (running nothing) when it does not apply to these

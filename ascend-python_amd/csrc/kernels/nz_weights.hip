@@ -193,6 +193,44 @@ __global__ __launch_bounds__(kNzThreads) void w8_nz_pack_kernel(const int8_t* __
         *reinterpret_cast<u32x4*>(dst + 16 * e) = (u32x4){o[e][0], o[e][1], o[e][2], o[e][3]};
 }
 
+// int8 [N, K] -> [K, N] (the row-major weight the prefill kernels read), for the shapes the decode kernel's
+// in-place read of an [N, K] weight does not take.  A 64 x 64 tile per workgroup through LDS: each thread moves
+// 16 bytes of a source row in (one 16-byte load where the row piece is whole and aligned) and 16 bytes of a
+// destination row out; the ragged edges go byte by byte.
+constexpr int kTrT = 64;
+__global__ __launch_bounds__(kNzThreads) void w8_nk_transpose_kernel(const int8_t* __restrict__ src, int64_t K,
+                                                                     int64_t N, int8_t* __restrict__ dst) {
+    __shared__ int8_t tile[kTrT][kTrT + 4];
+    const int64_t k0 = (int64_t)blockIdx.x * kTrT, n0 = (int64_t)blockIdx.y * kTrT;
+    const int t = threadIdx.x, r = t >> 2, q = 16 * (t & 3);
+    {   // source row n0 + r, bytes k0 + q .. +15
+        const int64_t n = n0 + r, k = k0 + q;
+        const int8_t* sp = src + n * K + k;
+        if (n < N && k + 16 <= K && ((uintptr_t)sp & 15) == 0) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(sp);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) tile[r][q + e] = (int8_t)(v[e >> 2] >> (8 * (e & 3)));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) tile[r][q + e] = (n < N && k + e < K) ? sp[e] : (int8_t)0;
+        }
+    }
+    __syncthreads();
+    {   // destination row k0 + r, bytes n0 + q .. +15: column r of the tile, rows q .. q+15
+        const int64_t k = k0 + r, n = n0 + q;
+        int8_t* dp = dst + k * N + n;
+        if (k >= K) return;
+        if (n + 16 <= N && ((uintptr_t)dp & 15) == 0) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e >> 2] |= (uint32_t)(uint8_t)tile[q + e][r] << (8 * (e & 3));
+            *reinterpret_cast<u32x4*>(dp) = v;
+        } else {
+            for (int e = 0; e < 16 && n + e < N; ++e) dp[e] = tile[q + e][r];
+        }
+    }
+}
+
 // The B operand held in one NZ word: dword q takes nibbles q (k = 2q, low
 // half) and 4 + q (k = 2q + 1, high half) as magic values 128 + (w + 8)
 // (bf16) or 1024 + (w + 8) (fp16): one shift and one and-xor each.
@@ -270,7 +308,12 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
 }
 
 // SDT: the dtype of the scale and offset rows (QK_F16 or QK_BF16), fixed at compile time.
-template <int DT, int NB, int NIT, bool HAS_OFF, bool W8, int SDT>
+// NK (int8 only): the weight is stored [N, K] (row n holds column n's K bytes, the nn.Linear layout) instead
+// of in NZ blocks.  The 16 bytes lane (c, g) takes from an NZ block -- rows 16g..16g+15 of column c -- are
+// contiguous in such a row, so the same loads read it in place: per lane c*K + 16g, per 64-row block
+// 16*K*(n-block) + 64*(K block).  The two 64-row blocks of a superblock are the two halves of each
+// column's 128-byte line, loaded back to back.
+template <int DT, int NB, int NIT, bool HAS_OFF, bool W8, int SDT, bool NK = false>
 __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int nwg, int nrb) {
     typedef Mfma<DT> MM;
     constexpr int WL = W8 ? 2 : 1;         // weight loads per block and superblock
@@ -308,8 +351,9 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
     }
     char* const xw = xbuf + wave * WSLOT;
     const uint32_t xw_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)xbuf + (uint32_t)(wave * WSLOT);
+    static_assert(!NK || W8, "the [N, K] layout is an int8 weight's");
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (uint32_t)K * (uint32_t)N / (W8 ? 1u : 2u));
-    const uint32_t w_lane = (uint32_t)lane * 16u;
+    const uint32_t w_lane = NK ? (uint32_t)c * (uint32_t)K + 16u * (uint32_t)g : (uint32_t)lane * 16u;
     // lane l < NT*RL fetches 16 bytes of row l / RL (scale, offset) of a superblock's group: columns
     // 16*b0 + 8*(l % RL) .. +8, clamped into the row (the clamped columns belong to no block of this
     // workgroup and are never used); the other lanes repeat lane 0's address
@@ -339,7 +383,9 @@ __global__ __launch_bounds__(64 * kNzMaxWaves) void w4nz_decode(WqbmmArgs p, int
             for (int h = 0; h < WL; ++h)
                 wv[sl][b][h] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               wr, w_lane, ((uint32_t)blk[b] * (uint32_t)(WL * S) + (uint32_t)(WL * s + h)) * 1024u,
+                               wr, w_lane,
+                               NK ? (uint32_t)blk[b] * 16u * (uint32_t)K + (uint32_t)(128 * s + 64 * h)
+                                  : ((uint32_t)blk[b] * (uint32_t)(WL * S) + (uint32_t)(WL * s + h)) * 1024u,
                                kNonTemporal));
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -664,7 +710,7 @@ struct NzPlan {
 NzPlan nz_plan(const WqbmmArgs& p) {
     NzPlan z{false, 0, 0, 0, 0, 0};
     const int64_t G = p.group == 0 ? p.K : p.group;
-    const bool w8 = p.w_dtype == QK_I8_NZ;
+    const bool w8 = p.w_dtype == QK_I8_NZ || p.w_dtype == QK_I8_NK;
     if (!(p.w_dtype == QK_I4_NZ || w8) || p.M <= 0 || p.M > 64 || p.N <= 0 || p.K <= 0) return z;
     if (p.N % 16 != 0 || p.K % 128 != 0 || G <= 0 || G % 128 != 0 || p.K % G != 0) return z;
     // 32-bit buffer offsets
@@ -699,43 +745,48 @@ NzPlan nz_plan(const WqbmmArgs& p) {
     return z;
 }
 
-template <int DT, int NB, int NIT, bool OFF, bool W8>
+template <int DT, int NB, int NIT, bool OFF, bool W8, bool NK>
 hipError_t launch_nz_k(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
     if constexpr (NB <= nz_max_blocks(NIT, W8)) {
         const dim3 grid((uint32_t)(z.nwg * z.nrb)), block((uint32_t)(64 * z.nwave));
-        if (p.s_dtype == QK_BF16) w4nz_decode<DT, NB, NIT, OFF, W8, QK_BF16><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
-        else w4nz_decode<DT, NB, NIT, OFF, W8, QK_F16><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
+        if (p.s_dtype == QK_BF16)
+            w4nz_decode<DT, NB, NIT, OFF, W8, QK_BF16, NK><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
+        else
+            w4nz_decode<DT, NB, NIT, OFF, W8, QK_F16, NK><<<grid, block, 0, stream>>>(p, z.nwg, z.nrb);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;  // not planned (nz_plan caps NB by nz_max_blocks)
 }
 
-template <int DT, int NB, bool OFF, bool W8>
+template <int DT, int NB, bool OFF, bool W8, bool NK>
 hipError_t launch_nz_nit(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
     switch (z.nit) {
-    case 1: return launch_nz_k<DT, NB, 1, OFF, W8>(p, z, stream);
-    case 2: return launch_nz_k<DT, NB, 2, OFF, W8>(p, z, stream);
-    case 3: return launch_nz_k<DT, NB, 3, OFF, W8>(p, z, stream);
-    case 4: return launch_nz_k<DT, NB, 4, OFF, W8>(p, z, stream);
-    case 5: return launch_nz_k<DT, NB, 5, OFF, W8>(p, z, stream);
-    case 6: return launch_nz_k<DT, NB, 6, OFF, W8>(p, z, stream);
-    case 7: return launch_nz_k<DT, NB, 7, OFF, W8>(p, z, stream);
-    default: return launch_nz_k<DT, NB, 8, OFF, W8>(p, z, stream);
+    case 1: return launch_nz_k<DT, NB, 1, OFF, W8, NK>(p, z, stream);
+    case 2: return launch_nz_k<DT, NB, 2, OFF, W8, NK>(p, z, stream);
+    case 3: return launch_nz_k<DT, NB, 3, OFF, W8, NK>(p, z, stream);
+    case 4: return launch_nz_k<DT, NB, 4, OFF, W8, NK>(p, z, stream);
+    case 5: return launch_nz_k<DT, NB, 5, OFF, W8, NK>(p, z, stream);
+    case 6: return launch_nz_k<DT, NB, 6, OFF, W8, NK>(p, z, stream);
+    case 7: return launch_nz_k<DT, NB, 7, OFF, W8, NK>(p, z, stream);
+    default: return launch_nz_k<DT, NB, 8, OFF, W8, NK>(p, z, stream);
     }
 }
 
-template <int DT, bool OFF, bool W8>
+template <int DT, bool OFF, bool W8, bool NK = false>
 hipError_t launch_nz_nb(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
     switch (z.nb) {
-    case 1: return launch_nz_nit<DT, 1, OFF, W8>(p, z, stream);
-    case 2: return launch_nz_nit<DT, 2, OFF, W8>(p, z, stream);
-    case 3: return launch_nz_nit<DT, 3, OFF, W8>(p, z, stream);
-    default: return launch_nz_nit<DT, 4, OFF, W8>(p, z, stream);
+    case 1: return launch_nz_nit<DT, 1, OFF, W8, NK>(p, z, stream);
+    case 2: return launch_nz_nit<DT, 2, OFF, W8, NK>(p, z, stream);
+    case 3: return launch_nz_nit<DT, 3, OFF, W8, NK>(p, z, stream);
+    default: return launch_nz_nit<DT, 4, OFF, W8, NK>(p, z, stream);
     }
 }
 
 template <int DT>
 hipError_t launch_nz_dt(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream) {
+    if (p.w_dtype == QK_I8_NK)
+        return p.offset ? launch_nz_nb<DT, true, true, true>(p, z, stream)
+                        : launch_nz_nb<DT, false, true, true>(p, z, stream);
     if (p.w_dtype == QK_I8_NZ)
         return p.offset ? launch_nz_nb<DT, true, true>(p, z, stream) : launch_nz_nb<DT, false, true>(p, z, stream);
     return p.offset ? launch_nz_nb<DT, true, false>(p, z, stream) : launch_nz_nb<DT, false, false>(p, z, stream);
@@ -744,8 +795,10 @@ hipError_t launch_nz_dt(const WqbmmArgs& p, const NzPlan& z, hipStream_t stream)
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 
-// bytes of the ND form of an NZ weight
-size_t nd_weight_bytes(const WqbmmArgs& p) { return (size_t)(p.w_dtype == QK_I8_NZ ? p.K * p.N : p.K * p.N / 2); }
+// bytes of the ND form of an NZ (or [N, K]) weight
+size_t nd_weight_bytes(const WqbmmArgs& p) {
+    return (size_t)(p.w_dtype == QK_I8_NZ || p.w_dtype == QK_I8_NK ? p.K * p.N : p.K * p.N / 2);
+}
 
 // Prefill plan on an int4 NZ weight: M > 64 with at least 96 tiles of 128 x 256, N % 256 == 0, groups of
 // whole 128-row NZ blocks, 16-byte aligned operands and 32-bit buffer offsets.  The workspace holds the x
@@ -810,6 +863,14 @@ hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t 
     return hipGetLastError();
 }
 
+hipError_t launch_w8_nk_transpose(const int8_t* src, int64_t K, int64_t N, int8_t* dst, hipStream_t stream) {
+    if (K * N == 0) return hipSuccess;
+    const int64_t gk = (K + kTrT - 1) / kTrT, gn = (N + kTrT - 1) / kTrT;
+    if (gk >= ((int64_t)1 << 31) || gn > 65535) return hipErrorInvalidValue;
+    w8_nk_transpose_kernel<<<dim3((uint32_t)gk, (uint32_t)gn), dim3(kNzThreads), 0, stream>>>(src, K, N, dst);
+    return hipGetLastError();
+}
+
 hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N, int8_t* dst, hipStream_t stream) {
     if (K * N == 0) return hipSuccess;
     const int64_t tiles = (K / 64) * ((N / 16 + kCastNB - 1) / kCastNB);
@@ -824,10 +885,12 @@ hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N
 // NZ weights (int4 QK_I4_NZ, int8 QK_I8_NZ): the decode kernel where it applies (no workspace);
 // otherwise the weight is unpacked into the workspace and the row-major kernels run on it:
 // [QK_SPLIT_COUNTER_BYTES, unused][ND weight][row-major call's workspace].
+// An int8 [N, K] weight (QK_I8_NK) takes the same decode kernel (reading it in place) or is transposed into the
+// workspace for the row-major kernels: [QK_SPLIT_COUNTER_BYTES, unused][[K, N] weight][row-major call's workspace].
 size_t w4_nz_workspace(const WqbmmArgs& p) {
     if (!plan_override().w4nz_off && nz_plan(p).ok) return 0;
     if (!plan_override().w4nz_off && nzg_plan(p).ok) return nzg_workspace(p);
-    const int nd_dtype = p.w_dtype == QK_I8_NZ ? QK_I8 : QK_I32;
+    const int nd_dtype = p.w_dtype == QK_I4_NZ ? QK_I32 : QK_I8;
     return QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(p)) +
            weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group, true);
 }
@@ -842,7 +905,7 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
         float* xs = reinterpret_cast<float*>(static_cast<char*>(workspace) + QK_SPLIT_COUNTER_BYTES);
         return p.x_dtype == QK_BF16 ? launch_nzg_dt<QK_BF16>(p, g, xs, stream) : launch_nzg_dt<QK_F16>(p, g, xs, stream);
     }
-    const bool w8 = p.w_dtype == QK_I8_NZ;
+    const bool w8 = p.w_dtype != QK_I4_NZ;
     const int nd_dtype = w8 ? QK_I8 : QK_I32;
     const size_t nd_bytes = round256(nd_weight_bytes(p));
     const size_t rest = weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group, true);
@@ -850,10 +913,13 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
         return hipErrorInvalidValue;
     char* ws = static_cast<char*>(workspace);
     void* nd = ws + QK_SPLIT_COUNTER_BYTES;
-    hipError_t e = w8 ? launch_w8_nz_cast(static_cast<const int8_t*>(p.w), false, p.K, p.N, static_cast<int8_t*>(nd),
-                                          stream)
-                      : launch_w4_nz_cast(static_cast<const int32_t*>(p.w), false, p.K, p.N, static_cast<int32_t*>(nd),
-                                          stream);
+    hipError_t e;
+    if (p.w_dtype == QK_I8_NK)
+        e = launch_w8_nk_transpose(static_cast<const int8_t*>(p.w), p.K, p.N, static_cast<int8_t*>(nd), stream);
+    else if (w8)
+        e = launch_w8_nz_cast(static_cast<const int8_t*>(p.w), false, p.K, p.N, static_cast<int8_t*>(nd), stream);
+    else
+        e = launch_w4_nz_cast(static_cast<const int32_t*>(p.w), false, p.K, p.N, static_cast<int32_t*>(nd), stream);
     if (e != hipSuccess) return e;
     WqbmmArgs q = p;
     q.w = nd;

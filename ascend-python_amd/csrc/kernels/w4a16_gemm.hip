@@ -1614,7 +1614,7 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     p.x = p.scale = p.offset = p.out = (void*)(uintptr_t)256;
     p.w = (void*)(uintptr_t)256;
     if (p.group == 0) p.group = p.K;
-    if (w_dtype == QK_I4_NZ || w_dtype == QK_I8_NZ) return w4_nz_workspace(p);
+    if (w_dtype == QK_I4_NZ || w_dtype == QK_I8_NZ || w_dtype == QK_I8_NK) return w4_nz_workspace(p);
     if (!no_cast)
         if (const size_t c = w4_cast_nz_workspace(p)) return c;
     // [split-K counters][fp32 partials [nsplit][M][N]]
@@ -1631,7 +1631,8 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
     if (a.M == 0 || a.N == 0) return hipSuccess;
     WqbmmArgs p = a;
     if (p.group == 0) p.group = p.K;  // per channel == one group spanning K
-    if (p.w_dtype == QK_I4_NZ || p.w_dtype == QK_I8_NZ) return launch_w4_nz_bmm(p, workspace, ws_bytes, stream);
+    if (p.w_dtype == QK_I4_NZ || p.w_dtype == QK_I8_NZ || p.w_dtype == QK_I8_NK)
+        return launch_w4_nz_bmm(p, workspace, ws_bytes, stream);
     // a split workspace is [counters][partials]: the stream kernel finishes each strip in its last
     // split's workgroup (one counter per strip); the decode kernel uses the reduce kernel
     char* ws = static_cast<char*>(workspace);

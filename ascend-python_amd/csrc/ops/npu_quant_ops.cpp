@@ -19,11 +19,14 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <ATen/ExpandUtils.h>
+
 #include <cmath>
 #include <map>
 #include <mutex>
 #include <optional>
 #include <tuple>
+#include <unordered_map>
 #include <vector>
 
 #include "../../../include/qk_abi.h"
@@ -103,27 +106,132 @@ std::tuple<at::Tensor, at::Tensor> npu_dynamic_quant_meta(const at::Tensor& inpu
     return dynamic_quant_shapes(input, smooth_scales);
 }
 
-// ---------------------------------------------------------------- npu_quant_matmul
+// ---------------------------------------------------------------- storage format
 
-// An int4 weight in the NZ layout written by npu_format_cast(w, 29): int32
-// [N/16, K/128, 64, 4] (the shape carries the format; see qk_weight_format_cast).
+// The reference keeps a tensor's storage format (ND, FRACTAL_NZ, ...) in the
+// NPU descriptor of its storage and reads it from there
+// (npu_preparation::get_tensor_npu_format, op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:81;
+// get_npu_desc, op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:57-66).  A
+// PyTorch-ROCm storage has no such descriptor, so the format is kept here,
+// keyed by the storage: npu_format_cast and npu_convert_weight_to_int4pack
+// (inner_k_tiles=4) record the storage of every FRACTAL_NZ weight they return,
+// with its sizes and dtype.  A tensor is FRACTAL_NZ when its storage is
+// recorded and still alive and the tensor views all of it as recorded (offset
+// 0, the recorded sizes and dtype, contiguous); every other tensor is ND,
+// whatever its shape.  A weak reference per record tells the recorded storage
+// from a new one allocated at the same address.  (As with a device-local
+// descriptor, copies -- clone, .to(), a load from disk -- are ND until cast.)
+struct NzRecord {
+    c10::weak_intrusive_ptr<c10::StorageImpl> storage;
+    std::vector<int64_t> sizes;
+    at::ScalarType dtype;
+};
+std::mutex g_nz_mu;
+std::unordered_map<const c10::StorageImpl*, NzRecord> g_nz;
+
+void record_nz(const at::Tensor& t) {
+    std::lock_guard<std::mutex> lock(g_nz_mu);
+    for (auto it = g_nz.begin(); it != g_nz.end();) it = it->second.storage.expired() ? g_nz.erase(it) : std::next(it);
+    g_nz.insert_or_assign(t.storage().unsafeGetStorageImpl(),
+                          NzRecord{t.storage().getWeakStorageImpl(), t.sizes().vec(), t.scalar_type()});
+}
+
+bool recorded_nz(const at::Tensor& t) {
+    if (!t.has_storage() || t.storage_offset() != 0 || !t.is_contiguous()) return false;
+    const c10::StorageImpl* key = t.storage().unsafeGetStorageImpl();
+    std::lock_guard<std::mutex> lock(g_nz_mu);
+    auto it = g_nz.find(key);
+    if (it == g_nz.end()) return false;
+    const auto live = it->second.storage.lock();
+    if (!live || live.get() != key) {  // a new storage at the address of a freed one
+        g_nz.erase(it);
+        return false;
+    }
+    return t.sizes().equals(it->second.sizes) && t.scalar_type() == it->second.dtype;
+}
+
+// An int4 weight in the NZ layout written by npu_format_cast(w, 29): int32 [N/16, K/128, 64, 4].
 bool is_w4_nz(const at::Tensor& w) {
-    return w.scalar_type() == at::kInt && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 4;
+    return w.scalar_type() == at::kInt && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 4 && recorded_nz(w);
 }
 
 // An int8 weight in the NZ layout: int8 [N/16, K/64, 64, 16].
 bool is_w8_nz(const at::Tensor& w) {
-    return w.scalar_type() == at::kChar && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 16;
+    return w.scalar_type() == at::kChar && w.dim() == 4 && w.size(2) == 64 && w.size(3) == 16 && recorded_nz(w);
 }
 
 bool is_nz(const at::Tensor& w) { return is_w4_nz(w) || is_w8_nz(w); }
+
+// torch_npu.get_npu_format for the formats of this path: FRACTAL_NZ (29) or ND (2).
+int64_t get_npu_format(const at::Tensor& self) { return is_nz(self) ? QK_FORMAT_FRACTAL_NZ : QK_FORMAT_ND; }
+
+// ---------------------------------------------------------------- batched weights
+
+// A weight with batch dims (>= 3-D): the output batch is the broadcast of x's
+// batch dims (those before [M, K]; a 2-D x has none) and the weight's (those
+// before [K, N]), as the reference's matmul output rule
+// (op_plugin/ops/base_ops/opapi/MatmulKernelNpuOpApi.cpp:45-73) and bmm
+// (op_plugin/ops/base_ops/opapi/BmmKernelNpuOpApi.cpp:24-52).  Each element of
+// the broadcast batch is one [M, K] x [K, N] call; `xb` / `wb` give the batch
+// element of x / of the weight it reads (0 along a broadcast dim).
+struct Batch {
+    std::vector<int64_t> shape;  // broadcast batch dims
+    std::vector<int64_t> xb, wb; // per element: linear batch index into x and into the weight
+};
+
+Batch batch_of(at::IntArrayRef x_batch, at::IntArrayRef w_batch, const char* op) {
+    Batch b;
+    try {
+        b.shape = at::infer_size(x_batch, w_batch);
+    } catch (const c10::Error&) {
+        TORCH_CHECK(false, op, ": batch dims of x ", x_batch, " and of the weight ", w_batch, " do not broadcast");
+    }
+    int64_t n = 1;
+    for (int64_t d : b.shape) n *= d;
+    b.xb.resize(n);
+    b.wb.resize(n);
+    const int64_t nd = (int64_t)b.shape.size();
+    for (int64_t e = 0; e < n; ++e) {
+        int64_t rem = e, xi = 0, wi = 0, xs = 1, ws = 1;
+        for (int64_t d = nd - 1; d >= 0; --d) {
+            const int64_t idx = rem % b.shape[d];
+            rem /= b.shape[d];
+            const int64_t dx = d - (nd - (int64_t)x_batch.size()), dw = d - (nd - (int64_t)w_batch.size());
+            if (dx >= 0) {
+                xi += (x_batch[dx] == 1 ? 0 : idx) * xs;
+                xs *= x_batch[dx];
+            }
+            if (dw >= 0) {
+                wi += (w_batch[dw] == 1 ? 0 : idx) * ws;
+                ws *= w_batch[dw];
+            }
+        }
+        b.xb[e] = xi;
+        b.wb[e] = wi;
+    }
+    return b;
+}
+
+// ---------------------------------------------------------------- npu_quant_matmul
 
 struct QmmPlan {
     int64_t M, N, K;
     bool nz;  // x2 is an int8 NZ weight
     at::ScalarType out_type;
     std::vector<int64_t> out_shape;
+    bool batched;  // x2 has batch dims: M is x1's second-to-last dim, one call per element of `batch`
+    Batch batch;
 };
+
+// Element offset of batch element `lin` (row-major over the first nb dims) of t, by t's strides.
+int64_t batch_offset(const at::Tensor& t, int64_t nb, int64_t lin) {
+    int64_t off = 0;
+    for (int64_t d = nb - 1; d >= 0; --d) {
+        off += (lin % t.size(d)) * t.stride(d);
+        lin /= t.size(d);
+    }
+    return off;
+}
 
 QmmPlan quant_matmul_plan(const at::Tensor& x1, const at::Tensor& x2, const at::Tensor& scale,
                           const std::optional<at::Tensor>& offset, const std::optional<at::Tensor>& pertoken_scale,
@@ -132,15 +240,17 @@ QmmPlan quant_matmul_plan(const at::Tensor& x1, const at::Tensor& x2, const at::
     TORCH_CHECK(x1.scalar_type() == at::kChar && x2.scalar_type() == at::kChar, op,
                 ": x1 and x2 must be int8, got ", x1.scalar_type(), " and ", x2.scalar_type());
     TORCH_CHECK(x1.dim() >= 2 && x1.dim() <= 6, op, ": x1 must have 2 to 6 dimensions, got ", x1.dim());
-    // x2 is [K, N] (or the transposed view of [N, K]), or the int8 NZ weight npu_format_cast(x2, 29) writes
+    // x2 is [K, N] (or the transposed view of [N, K]), the int8 NZ weight npu_format_cast(x2, 29) writes, or
+    // a batch of [K, N] weights [..., K, N] (2 to 6 dims in all)
     const bool nz = is_w8_nz(x2);
-    TORCH_CHECK(x2.dim() == 2 || nz, op, ": x2 must be 2-D [K, N] or an int8 NZ weight [N/16, K/64, 64, 16], got ",
-                x2.sizes());
+    TORCH_CHECK((x2.dim() >= 2 && x2.dim() <= 6) || nz, op,
+                ": x2 must be [K, N], a batch [..., K, N] or an int8 NZ weight [N/16, K/64, 64, 16], got ", x2.sizes());
+    const bool batched = !nz && x2.dim() >= 3;
     const int64_t K = x1.size(-1);
-    const int64_t x2_k = nz ? x2.size(1) * 64 : x2.size(0);
+    const int64_t x2_k = nz ? x2.size(1) * 64 : x2.size(-2);
     TORCH_CHECK(x2_k == K, op, ": x1 last dim (", K, ") must equal the weight's K (", x2_k, ")");
-    const int64_t N = nz ? x2.size(0) * 16 : x2.size(1);
-    const int64_t M = leading_rows(x1);
+    const int64_t N = nz ? x2.size(0) * 16 : x2.size(-1);
+    const int64_t M = batched ? x1.size(-2) : leading_rows(x1);
     const at::ScalarType out_type = output_dtype.value_or(at::kChar);
     TORCH_CHECK(out_type == at::kBFloat16 || out_type == at::kHalf || out_type == at::kChar ||
                     out_type == at::kInt || out_type == at::kFloat,
@@ -159,8 +269,8 @@ QmmPlan quant_matmul_plan(const at::Tensor& x1, const at::Tensor& x2, const at::
         TORCH_CHECK(out_type == at::kBFloat16 || out_type == at::kHalf || out_type == at::kFloat, op,
                     ": pertoken_scale needs output_dtype bfloat16, float16 or float32");
         TORCH_CHECK(pertoken_scale->scalar_type() == at::kFloat, op, ": pertoken_scale must be float32");
-        TORCH_CHECK(pertoken_scale->numel() == M, op, ": pertoken_scale must have M=", M, " elements, got ",
-                    pertoken_scale->numel());
+        TORCH_CHECK(pertoken_scale->numel() == leading_rows(x1), op, ": pertoken_scale must have one element per row"
+                    " of x1 (", leading_rows(x1), "), got ", pertoken_scale->numel());
     }
     if (bias.has_value()) {
         const auto bt = bias->scalar_type();
@@ -173,7 +283,14 @@ QmmPlan quant_matmul_plan(const at::Tensor& x1, const at::Tensor& x2, const at::
     }
     std::vector<int64_t> shape(x1.sizes().begin(), x1.sizes().end());
     shape.back() = N;
-    return {M, N, K, nz, out_type, shape};
+    Batch b;
+    if (batched) {
+        b = batch_of(x1.sizes().slice(0, x1.dim() - 2), x2.sizes().slice(0, x2.dim() - 2), op);
+        shape = b.shape;
+        shape.push_back(M);
+        shape.push_back(N);
+    }
+    return {M, N, K, nz, out_type, shape, batched, b};
 }
 
 // The NZ weight (the layout the reference's matmuls read after npu_format_cast, op_plugin/ops/base_ops/aclops/
@@ -209,17 +326,19 @@ at::Tensor npu_quant_matmul(const at::Tensor& x1_in, const at::Tensor& x2_in, co
     QmmPlan pl = quant_matmul_plan(x1_in, x2_in, scale_in, offset, pertoken_scale, bias, output_dtype);
     const c10::DeviceGuard guard(x1_in.device());
     auto out = at::empty(pl.out_shape, x1_in.options().dtype(pl.out_type));
-    if (pl.M == 0 || pl.N == 0) return out;
+    if (out.numel() == 0) return out;
     auto x1 = x1_in.contiguous();
     if (pl.nz) return quant_matmul_nz(pl, x1, x2_in, scale_in, offset, pertoken_scale, bias, out);
     // Transposed view of an [N,K] weight is read in place, as the reference
     // flags mat2 instead of copying it (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:40-53).
+    // For a batch of weights the same holds for the last two dims of every slice.
     at::Tensor x2 = x2_in;
-    const bool kn = x2.stride(1) == 1 && x2.stride(0) >= std::max<int64_t>(1, pl.N);
-    const bool nk = x2.stride(0) == 1 && x2.stride(1) >= std::max<int64_t>(1, pl.K);
+    const int64_t d = x2.dim();
+    const bool kn = x2.stride(d - 1) == 1 && x2.stride(d - 2) >= std::max<int64_t>(1, pl.N);
+    const bool nk = x2.stride(d - 2) == 1 && x2.stride(d - 1) >= std::max<int64_t>(1, pl.K);
     if (!kn && !nk) x2 = x2.contiguous();
-    const int64_t sbk = kn || (!nk) ? x2.stride(0) : 1;
-    const int64_t sbn = kn || (!nk) ? 1 : x2.stride(1);
+    const int64_t sbk = kn || (!nk) ? x2.stride(d - 2) : 1;
+    const int64_t sbn = kn || (!nk) ? 1 : x2.stride(d - 1);
     auto scale = scale_in.scalar_type() == at::kFloat ? scale_in.contiguous() : scale_in.to(at::kFloat);
     at::Tensor off, pt, b;
     if (offset.has_value()) off = offset->contiguous();
@@ -229,13 +348,21 @@ at::Tensor npu_quant_matmul(const at::Tensor& x1_in, const at::Tensor& x2_in, co
     check_rc(qk_quant_matmul_workspace_size(pl.M, pl.N, pl.K, qk_dtype_of(pl.out_type), &ws_bytes),
              "npu_quant_matmul");
     at::Tensor ws = ws_bytes ? workspace_for(x1, ws_bytes) : at::Tensor();
-    const int rc = qk_quant_matmul(
-        x1.data_ptr<int8_t>(), pl.K, x2.data_ptr<int8_t>(), sbk, sbn, pl.M, pl.N, pl.K, scale.data_ptr<float>(),
-        scale.numel(), off.defined() ? off.data_ptr<float>() : nullptr, off.defined() ? off.numel() : 0,
-        pt.defined() ? pt.data_ptr<float>() : nullptr, b.defined() ? b.data_ptr() : nullptr,
-        b.defined() ? qk_dtype_of(b.scalar_type()) : 0, out.data_ptr(), qk_dtype_of(pl.out_type),
-        ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(x1));
-    check_rc(rc, "npu_quant_matmul");
+    // one call per batch element (a single call with no batch); the calls share the workspace, in stream order
+    const int64_t nb = pl.batched ? (int64_t)pl.batch.xb.size() : 1;
+    const size_t osz = out.element_size();
+    for (int64_t e = 0; e < nb; ++e) {
+        const int64_t xb = pl.batched ? pl.batch.xb[e] : 0;
+        const int64_t woff = pl.batched ? batch_offset(x2, d - 2, pl.batch.wb[e]) : 0;
+        const int rc = qk_quant_matmul(
+            x1.data_ptr<int8_t>() + xb * pl.M * pl.K, pl.K, x2.data_ptr<int8_t>() + woff, sbk, sbn, pl.M, pl.N, pl.K,
+            scale.data_ptr<float>(), scale.numel(), off.defined() ? off.data_ptr<float>() : nullptr,
+            off.defined() ? off.numel() : 0, pt.defined() ? pt.data_ptr<float>() + xb * pl.M : nullptr,
+            b.defined() ? b.data_ptr() : nullptr, b.defined() ? qk_dtype_of(b.scalar_type()) : 0,
+            static_cast<char*>(out.data_ptr()) + (size_t)(e * pl.M * pl.N) * osz, qk_dtype_of(pl.out_type),
+            ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(x1));
+        check_rc(rc, "npu_quant_matmul");
+    }
     return out;
 }
 
@@ -253,6 +380,9 @@ struct WqPlan {
     int64_t M, N, K, group;
     bool int4, nz;
     std::vector<int64_t> out_shape;
+    bool batched;      // the weight has batch dims: one call per element of `batch`
+    Batch batch;
+    bool scale_batched;  // antiquant_scale / antiquant_offset carry the weight's batch dims
 };
 
 WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at::Tensor& antiquant_scale,
@@ -264,30 +394,37 @@ WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at
                 ": x must be float16 or bfloat16, got ", x.scalar_type());
     TORCH_CHECK(x.dim() >= 2, op, ": x must be at least 2-D, got ", x.dim());
     const bool nz = is_nz(weight);
-    TORCH_CHECK(weight.dim() == 2 || nz, op,
-                ": weight must be 2-D (ND) or an NZ weight (int4 [N/16, K/128, 64, 4], int8 [N/16, K/64, 64, 16]), got ",
-                weight.sizes());
+    TORCH_CHECK((weight.dim() >= 2 && weight.dim() <= 6) || nz, op,
+                ": weight must be [K, N] (ND), a batch [..., K, N] or an NZ weight (int4 [N/16, K/128, 64, 4], int8 "
+                "[N/16, K/64, 64, 16]), got ", weight.sizes());
     TORCH_CHECK(weight.scalar_type() == at::kInt || weight.scalar_type() == at::kChar, op,
                 ": weight must be int32 (int4 packed 8 per element) or int8, got ", weight.scalar_type());
     TORCH_CHECK(!quant_scale.has_value() && !quant_offset.has_value(), op,
                 ": quant_scale/quant_offset (int8 output) are not supported by this build");
     const bool int4 = weight.scalar_type() == at::kInt;
+    const bool batched = !nz && weight.dim() >= 3;
     const int64_t K = x.size(-1);
-    const int64_t wk = nz ? weight.size(1) * (int4 ? 128 : 64) : weight.size(0);
+    const int64_t wk = nz ? weight.size(1) * (int4 ? 128 : 64) : weight.size(-2);
     TORCH_CHECK(wk == K, op, ": x last dim (", K, ") must equal the weight's K (", wk, ")");
-    const int64_t N = nz ? weight.size(0) * 16 : (int4 ? weight.size(1) * 8 : weight.size(1));
+    const int64_t N = nz ? weight.size(0) * 16 : (int4 ? weight.size(-1) * 8 : weight.size(-1));
     TORCH_CHECK(group >= 0, op, ": antiquant_group_size must be >= 0");
     TORCH_CHECK(group == 0 || K % group == 0, op, ": K=", K, " must be a multiple of antiquant_group_size=", group);
     const auto st = antiquant_scale.scalar_type();
     TORCH_CHECK(st == at::kHalf || st == at::kBFloat16, op, ": antiquant_scale must be float16 or bfloat16");
     const int64_t ng = group > 0 ? K / group : 1;
-    const bool per_ch_ok = group == 0 && antiquant_scale.numel() == N &&
-                           (antiquant_scale.dim() == 1 || (antiquant_scale.dim() == 2 && antiquant_scale.size(0) == 1));
-    const bool grouped_ok = group > 0 && antiquant_scale.dim() == 2 && antiquant_scale.size(0) == ng &&
-                            antiquant_scale.size(1) == N;
+    // with a batch of weights the scales may carry the weight's batch dims in front ([..., K/group, N] or [..., N])
+    const at::IntArrayRef wbatch = batched ? weight.sizes().slice(0, weight.dim() - 2) : at::IntArrayRef();
+    const int64_t snb = (int64_t)wbatch.size();
+    const bool scale_batched = batched && antiquant_scale.dim() > (group > 0 ? 2 : 1) &&
+                               antiquant_scale.dim() >= snb && antiquant_scale.sizes().slice(0, snb).equals(wbatch);
+    const at::IntArrayRef ss = scale_batched ? antiquant_scale.sizes().slice(snb) : antiquant_scale.sizes();
+    int64_t ss_numel = 1;
+    for (int64_t v : ss) ss_numel *= v;
+    const bool per_ch_ok = group == 0 && ss_numel == N && (ss.size() == 1 || (ss.size() == 2 && ss[0] == 1));
+    const bool grouped_ok = group > 0 && ss.size() == 2 && ss[0] == ng && ss[1] == N;
     TORCH_CHECK(per_ch_ok || grouped_ok, op, ": antiquant_scale must be ", group > 0 ? "[K/group, N] = [" : "[N] = [",
                 group > 0 ? ng : N, group > 0 ? ", " : "", group > 0 ? std::to_string(N) : std::string(""),
-                "], got ", antiquant_scale.sizes());
+                "]", batched ? " (optionally after the weight's batch dims)" : "", ", got ", antiquant_scale.sizes());
     if (antiquant_offset.has_value()) {
         TORCH_CHECK(antiquant_offset->scalar_type() == st, op, ": antiquant_offset must match antiquant_scale's dtype");
         TORCH_CHECK(antiquant_offset->sizes() == antiquant_scale.sizes(), op,
@@ -300,8 +437,23 @@ WqPlan weight_quant_plan(const at::Tensor& x, const at::Tensor& weight, const at
     }
     std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
     shape.back() = N;
-    const int64_t M = leading_rows(x);
-    return {M, N, K, group, int4, nz, shape};
+    const int64_t M = batched ? x.size(-2) : leading_rows(x);
+    Batch b;
+    if (batched) {
+        b = batch_of(x.sizes().slice(0, x.dim() - 2), wbatch, op);
+        shape = b.shape;
+        shape.push_back(M);
+        shape.push_back(N);
+    }
+    return {M, N, K, group, int4, nz, shape, batched, b, scale_batched};
+}
+
+// An int8 ND weight passed as the transposed view of an [N, K] tensor (the nn.Linear layout): read in place
+// as QK_I8_NK, as the reference flags a transposed mat2 instead of copying it
+// (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:40-53, op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:39-40).
+bool int8_nk_view(const at::Tensor& w, int64_t K, int64_t N) {
+    const int64_t d = w.dim();
+    return w.scalar_type() == at::kChar && K > 1 && N > 1 && w.stride(d - 2) == 1 && w.stride(d - 1) == K;
 }
 
 at::Tensor npu_weight_quant_batchmatmul(const at::Tensor& x_in, const at::Tensor& weight_in,
@@ -314,25 +466,42 @@ at::Tensor npu_weight_quant_batchmatmul(const at::Tensor& x_in, const at::Tensor
                                   antiquant_group_size);
     const c10::DeviceGuard guard(x_in.device());
     auto out = at::empty(pl.out_shape, x_in.options());
-    if (pl.M == 0 || pl.N == 0) return out;
+    if (out.numel() == 0) return out;
     auto x = x_in.contiguous();
-    auto w = weight_in.contiguous();
+    // the weight is read where it lies: NZ blocks, [K, N] rows, or an int8 [N, K] tensor seen transposed; any
+    // other strides are made contiguous (per slice of a batch, the last two dims decide)
+    const bool nk = !pl.nz && int8_nk_view(weight_in, pl.K, pl.N);
+    const int64_t d = weight_in.dim();
+    const bool rows = !pl.nz && weight_in.stride(d - 1) == 1 && weight_in.stride(d - 2) == weight_in.size(d - 1);
+    auto w = (pl.nz || nk || rows) ? weight_in : weight_in.contiguous();
     auto sc = antiquant_scale.contiguous();
     at::Tensor off, b;
     if (antiquant_offset.has_value()) off = antiquant_offset->contiguous();
     if (bias.has_value()) b = bias->contiguous();
-    const int wdt = pl.nz ? (pl.int4 ? QK_I4_NZ : QK_I8_NZ) : (pl.int4 ? QK_I32 : QK_I8);
+    const int wdt = pl.nz ? (pl.int4 ? QK_I4_NZ : QK_I8_NZ) : (pl.int4 ? QK_I32 : (nk ? QK_I8_NK : QK_I8));
     size_t ws_bytes = 0;
     check_rc(qk_weight_quant_bmm_workspace_size(pl.M, pl.N, pl.K, wdt, pl.group, &ws_bytes),
              "npu_weight_quant_batchmatmul");
     at::Tensor ws = ws_bytes ? workspace_for(x, ws_bytes) : at::Tensor();
-    const int rc = qk_weight_quant_bmm(x.data_ptr(), qk_dtype_of(x.scalar_type()), w.data_ptr(), wdt, sc.data_ptr(),
-                                       off.defined() ? off.data_ptr() : nullptr, qk_dtype_of(sc.scalar_type()), pl.M,
-                                       pl.N, pl.K, pl.group, b.defined() ? b.data_ptr() : nullptr,
-                                       b.defined() ? qk_dtype_of(b.scalar_type()) : 0, out.data_ptr(),
-                                       qk_dtype_of(out.scalar_type()), ws.defined() ? ws.data_ptr() : nullptr,
-                                       ws_bytes, current_stream(x));
-    check_rc(rc, "npu_weight_quant_batchmatmul");
+    // one call per batch element (a single call with no batch); the calls share the workspace, in stream order
+    const int64_t nb = pl.batched ? (int64_t)pl.batch.xb.size() : 1;
+    const size_t xsz = x.element_size(), wsz = w.element_size(), ssz = sc.element_size(), osz = out.element_size();
+    const int64_t s_slice = pl.group > 0 ? (pl.K / pl.group) * pl.N : pl.N;  // scale elements per weight
+    for (int64_t e = 0; e < nb; ++e) {
+        const int64_t xb = pl.batched ? pl.batch.xb[e] : 0, wb = pl.batched ? pl.batch.wb[e] : 0;
+        const int64_t woff = pl.batched ? batch_offset(w, d - 2, wb) : 0;
+        const int64_t soff = pl.scale_batched ? wb * s_slice : 0;
+        const int rc = qk_weight_quant_bmm(
+            static_cast<const char*>(x.data_ptr()) + (size_t)(xb * pl.M * pl.K) * xsz, qk_dtype_of(x.scalar_type()),
+            static_cast<const char*>(w.data_ptr()) + (size_t)woff * wsz, wdt,
+            static_cast<const char*>(sc.data_ptr()) + (size_t)soff * ssz,
+            off.defined() ? static_cast<const char*>(off.data_ptr()) + (size_t)soff * ssz : nullptr,
+            qk_dtype_of(sc.scalar_type()), pl.M, pl.N, pl.K, pl.group, b.defined() ? b.data_ptr() : nullptr,
+            b.defined() ? qk_dtype_of(b.scalar_type()) : 0,
+            static_cast<char*>(out.data_ptr()) + (size_t)(e * pl.M * pl.N) * osz, qk_dtype_of(out.scalar_type()),
+            ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(x));
+        check_rc(rc, "npu_weight_quant_batchmatmul");
+    }
     return out;
 }
 
@@ -386,14 +555,17 @@ at::Tensor npu_convert_weight_to_int4pack(const at::Tensor& weight, int64_t inne
     check_rc(qk_weight_format_cast(out.data_ptr(), QK_FORMAT_ND, nz.data_ptr(), QK_FORMAT_FRACTAL_NZ, QK_I32,
                                    w.size(0), w.size(1), current_stream(w)),
              "npu_convert_weight_to_int4pack");
+    record_nz(nz);
     return nz;
 }
 
 at::Tensor npu_convert_weight_to_int4pack_meta(const at::Tensor& weight, int64_t inner_k_tiles) {
     auto shape = int4pack_shape(weight);
     int4pack_check_tiles(weight, inner_k_tiles);
-    if (inner_k_tiles == 4) shape = nz_shape(weight.size(0), weight.size(1));
-    return at::empty(shape, weight.options().dtype(at::kInt));
+    if (inner_k_tiles == 0) return at::empty(shape, weight.options().dtype(at::kInt));
+    auto nz = at::empty(nz_shape(weight.size(0), weight.size(1)), weight.options().dtype(at::kInt));
+    record_nz(nz);
+    return nz;
 }
 
 // ---------------------------------------------------------------- npu_format_cast
@@ -450,13 +622,16 @@ at::Tensor npu_format_cast(const at::Tensor& self, int64_t acl_format) {
                                    c.to_nz ? QK_FORMAT_FRACTAL_NZ : QK_FORMAT_ND, c.int4 ? QK_I32 : QK_I8, c.K, c.N,
                                    current_stream(src)),
              "npu_format_cast");
+    if (c.to_nz) record_nz(out);
     return out;
 }
 
 at::Tensor npu_format_cast_meta(const at::Tensor& self, int64_t acl_format) {
     const CastPlan c = format_cast_plan(self, acl_format);
     if (c.identity) return self;
-    return at::empty(c.shape, self.options());
+    auto out = at::empty(c.shape, self.options());
+    if (c.to_nz) record_nz(out);
+    return out;
 }
 
 // ---------------------------------------------------------------- quantize_per_tensor / _per_channel / dequantize
@@ -710,6 +885,8 @@ TORCH_LIBRARY(npu, m) {
         "Tensor? quant_scale=None, Tensor? quant_offset=None, Tensor? bias=None, int antiquant_group_size=0) -> Tensor");
     m.def("npu_convert_weight_to_int4pack(Tensor weight, int inner_k_tiles=0) -> Tensor");
     m.def("npu_format_cast(Tensor self, int acl_format) -> Tensor");
+    // torch_npu.get_npu_format: the storage format the storage of self is recorded in (ND 2, FRACTAL_NZ 29)
+    m.def("get_npu_format(Tensor self) -> int");
     // static quantization: op_plugin/config/v2r2/op_plugin_functions.yaml:1231, 1233 and
     // op_plugin/config/v1r11/op_plugin_functions.yaml:127
     m.def("quantize_per_channel(Tensor self, Tensor scales, Tensor zero_points, int axis, ScalarType dtype) -> Tensor");
@@ -737,6 +914,8 @@ TORCH_LIBRARY_IMPL(npu, CUDA, m) {
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant);
     m.impl("npu_swiglu_dynamic_quant", &npu_swiglu_dynamic_quant);
 }
+
+TORCH_LIBRARY_IMPL(npu, CompositeExplicitAutograd, m) { m.impl("get_npu_format", &get_npu_format); }
 
 TORCH_LIBRARY_IMPL(npu, Meta, m) {
     m.impl("npu_dynamic_quant", &npu_dynamic_quant_meta);

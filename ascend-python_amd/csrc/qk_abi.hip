@@ -210,7 +210,7 @@ extern "C" {
 
 const char* qk_last_error(void) { return g_last_error.c_str(); }
 
-int qk_abi_version(void) { return 4; }
+int qk_abi_version(void) { return 5; }
 
 int qk_debug_set_plan(const char* spec) {
     g_last_error.clear();
@@ -321,14 +321,18 @@ int weight_quant_bmm_run(const char* op, const void* x, int x_dtype, const void*
                          int out_dtype, void* (*scratch)(size_t need, size_t* bytes, int* rc), void* workspace,
                          size_t workspace_bytes, qk_stream_t stream) {
     if (!is_half(x_dtype)) return fail(QK_ERR_ARG, "%s: x must be float16 or bfloat16", op);
-    if (weight_dtype != QK_I32 && weight_dtype != QK_I8 && weight_dtype != QK_I4_NZ && weight_dtype != QK_I8_NZ)
-        return fail(QK_ERR_ARG, "%s: weight must be int32 (packed int4), int8, or NZ int4 / int8", op);
+    if (weight_dtype != QK_I32 && weight_dtype != QK_I8 && weight_dtype != QK_I4_NZ && weight_dtype != QK_I8_NZ &&
+        weight_dtype != QK_I8_NK)
+        return fail(QK_ERR_ARG, "%s: weight must be int32 (packed int4), int8 ([K, N] or [N, K]), or NZ int4 / int8", op);
     if (!is_half(scale_dtype)) return fail(QK_ERR_ARG, "%s: antiquant_scale must be float16 or bfloat16", op);
     if (!is_half(out_dtype)) return fail(QK_ERR_ARG, "%s: output must be float16 or bfloat16", op);
     if (M < 0 || N < 0 || K < 0 || group_size < 0) return fail(QK_ERR_ARG, "%s: negative size", op);
     if (weight_dtype == QK_I32 && N % 8 != 0) return fail(QK_ERR_ARG, "%s: int4 packing needs N %% 8 == 0 (N=%lld)", op, (long long)N);
-    if ((weight_dtype == QK_I4_NZ || weight_dtype == QK_I8_NZ) && (N % 16 != 0 || K % 128 != 0))
-        return fail(QK_ERR_ARG, "%s: an NZ weight needs N %% 16 == 0 and K %% 128 == 0 (N=%lld K=%lld)", op,
+    if (weight_dtype == QK_I4_NZ && (N % 16 != 0 || K % 128 != 0))
+        return fail(QK_ERR_ARG, "%s: an int4 NZ weight needs N %% 16 == 0 and K %% 128 == 0 (N=%lld K=%lld)", op,
+                    (long long)N, (long long)K);
+    if (weight_dtype == QK_I8_NZ && (N % 16 != 0 || K % 64 != 0))
+        return fail(QK_ERR_ARG, "%s: an int8 NZ weight needs N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)", op,
                     (long long)N, (long long)K);
     if (group_size > 0 && K % group_size != 0)
         return fail(QK_ERR_ARG, "%s: K=%lld is not a multiple of antiquant_group_size=%lld", op, (long long)K, (long long)group_size);

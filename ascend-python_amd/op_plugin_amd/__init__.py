@@ -63,7 +63,7 @@ npu_rms_norm_dynamic_quant = torch.ops.npu.npu_rms_norm_dynamic_quant
 npu_swiglu_dynamic_quant = torch.ops.npu.npu_swiglu_dynamic_quant
 
 # qk_abi.h constants
-QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_U8, QK_I4_NZ, QK_I8_NZ = 1, 2, 3, 4, 5, 6, 16, 17
+QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_U8, QK_I4_NZ, QK_I8_NZ, QK_I8_NK = 1, 2, 3, 4, 5, 6, 16, 17, 18
 ACL_FORMAT_ND, ACL_FORMAT_FRACTAL_NZ = 2, 29
 QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, -2, -3, -4
 
@@ -113,12 +113,10 @@ def abi() -> ctypes.CDLL:
 
 
 def get_npu_format(t: torch.Tensor) -> int:
-    """Storage format of a matmul weight, as torch_npu.get_npu_format reports it:
-    FRACTAL_NZ (29) for an NZ weight (int4 int32 [N/16, K/128, 64, 4], int8 [N/16, K/64, 64, 16]), ND (2)
-    otherwise."""
-    nz = t.dim() == 4 and t.shape[2] == 64 and ((t.dtype == torch.int32 and t.shape[3] == 4) or
-                                                 (t.dtype == torch.int8 and t.shape[3] == 16))
-    return ACL_FORMAT_FRACTAL_NZ if nz else ACL_FORMAT_ND
+    """Storage format of a tensor, as torch_npu.get_npu_format reports it: FRACTAL_NZ (29) for a weight that
+    npu_format_cast(w, 29) or npu_convert_weight_to_int4pack(w, inner_k_tiles=4) returned (the format is recorded
+    with its storage, not inferred from the shape), ND (2) for every other tensor."""
+    return int(torch.ops.npu.get_npu_format(t))
 
 
 def last_error() -> str:

@@ -64,7 +64,14 @@ typedef enum {
      * layouts that qk_weight_format_cast writes: int4, int32 [N/16][K/128][64][4];
      * int8, int8 [N/16][K/64][64][16] */
     QK_I4_NZ = 16,
-    QK_I8_NZ = 17
+    QK_I8_NZ = 17,
+    /* weight code of qk_weight_quant_bmm for an int8 weight stored [N, K] (row n
+     * holds column n's K values: the nn.Linear layout, which the op receives as
+     * the transposed view [K, N] of that tensor); read in place, as the reference
+     * flags a transposed mat2 instead of copying it
+     * (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:40-53,
+     * op_plugin/ops/base_ops/aclops/LinearKernelNpu.cpp:39-40) */
+    QK_I8_NK = 18
 } qk_dtype;
 
 /* Weight storage formats: the reference's aclFormat numbers for ND and
@@ -87,7 +94,8 @@ const char* qk_last_error(void);
 /* ABI revision; bumped on any incompatible signature or contract change
  * (2: the split-K counters at the head of a workspace; 3: the counters are
  * tagged per call, so a workspace needs no initialisation; 4: NZ weights,
- * qk_weight_format_cast, static quantization). */
+ * qk_weight_format_cast, static quantization; 5: the [N, K] int8 weight code
+ * QK_I8_NK, int8 NZ weights with K % 64 == 0 in qk_weight_quant_bmm). */
 int qk_abi_version(void);
 
 /* Debug and test hook, no counterpart in the reference: forces kernel choices
@@ -190,8 +198,9 @@ int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weig
  * is bmm (op_plugin/ops/base_ops/opapi/BmmKernelNpuOpApi.cpp:24-52).
  * x: [M,K] fp16/bf16 row-major.  weight: QK_I32 -> int4 packed [K, N/8]
  * (nibble i of word j is column 8j+i, two's complement); QK_I8 -> int8 [K,N];
- * QK_I4_NZ / QK_I8_NZ -> int4 / int8 in the NZ layouts of qk_weight_format_cast
- * (N % 16 == 0, K % 128 == 0).
+ * QK_I8_NK -> int8 stored [N,K] (element (k, n) at weight[n*K + k]); QK_I4_NZ /
+ * QK_I8_NZ -> int4 / int8 in the NZ layouts of qk_weight_format_cast
+ * (N % 16 == 0; K % 128 == 0 for int4, K % 64 == 0 for int8).
  * antiquant_scale / antiquant_offset: [K/group, N] (group_size > 0) or [N]
  * (group_size == 0, per channel), of scale_dtype (fp16/bf16); offset may be NULL.
  * bias: [N] or NULL.  out: [M,N] of out_dtype (fp16/bf16).

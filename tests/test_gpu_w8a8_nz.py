@@ -196,7 +196,8 @@ def test_quant_matmul_nz_k0(ops):
     say("quant_matmul NZ K=0")
     N = 64
     a = torch.empty((5, 0), dtype=torch.int8, device=DEV)
-    wnz = torch.empty((N // 16, 0, 64, 16), dtype=torch.int8, device=DEV)
+    wnz = ops.npu_format_cast(torch.empty((0, N), dtype=torch.int8, device=DEV), 29)
+    assert wnz.shape == (N // 16, 0, 64, 16) and ops.get_npu_format(wnz) == 29
     b = torch.randn(N, device=DEV).to(torch.bfloat16)
     out = ops.npu_quant_matmul(a, wnz, torch.ones(N, device=DEV), bias=b, output_dtype=torch.bfloat16)
     assert torch.equal(out, b.float().expand(5, N).to(torch.bfloat16))

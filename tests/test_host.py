@@ -28,7 +28,7 @@ def test_abi_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), f"{n} declared in qk_abi.h but not exported"
     assert set(names) == set(q.ABI_SYMBOLS)
-    assert q.abi().qk_abi_version() == 4
+    assert q.abi().qk_abi_version() == 5
 
 
 def test_debug_plan_override_parsing():
@@ -171,6 +171,44 @@ def test_meta_shapes():
     assert qq.shape == (2, 5, 32) and qq.dtype == torch.int8 and sc.shape == (2, 5)
 
 
+def test_storage_format_is_recorded_not_inferred():
+    """get_npu_format reads the format recorded with a tensor's storage by npu_format_cast /
+    npu_convert_weight_to_int4pack(inner_k_tiles=4), as the reference reads its storage descriptor
+    (op_plugin/ops/base_ops/aclops/MmKernelNpu.cpp:57-66): a tensor of the same shape made any other way is ND,
+    and a view that does not cover the storage as cast is ND."""
+    nz = q.npu_format_cast(_m((256, 64), torch.int8), 29)
+    assert nz.shape == (4, 4, 64, 16) and q.get_npu_format(nz) == 29
+    assert q.get_npu_format(nz.view(4, 4, 64, 16)) == 29          # the same storage, viewed whole
+    assert q.get_npu_format(_m((4, 4, 64, 16), torch.int8)) == 2  # the shape alone is not the format
+    assert q.get_npu_format(nz[1:]) == 2                          # part of the storage
+    assert q.get_npu_format(nz.reshape(16, 64, 16)) == 2          # other sizes
+    w4 = q.npu_convert_weight_to_int4pack(_m((256, 32), torch.int32), inner_k_tiles=4)
+    assert q.get_npu_format(w4) == 29 and q.get_npu_format(q.npu_format_cast(w4, 2)) == 2
+    assert q.get_npu_format(torch.zeros(2, 2)) == 2               # any device
+    # a raw 4-D int8 tensor of the NZ shape is a batch of [64, 16] weights, not an NZ weight
+    out = q.npu_quant_matmul(_m((5, 64), torch.int8), _m((4, 1, 64, 16), torch.int8), _m((1,), torch.float32),
+                             output_dtype=torch.int32)
+    assert out.shape == (4, 1, 5, 16)
+
+
+def test_meta_batched_weights():
+    """Weights with batch dims follow the reference's matmul output rule
+    (op_plugin/ops/base_ops/opapi/MatmulKernelNpuOpApi.cpp:45-73): a 2-D x is broadcast over the weight's batch,
+    and the batch dims of x and weight broadcast against each other."""
+    f32, i8, i32, bf16, f16 = torch.float32, torch.int8, torch.int32, torch.bfloat16, torch.float16
+    assert q.npu_quant_matmul(_m((5, 64), i8), _m((3, 64, 48), i8), _m((48,), f32),
+                              pertoken_scale=_m((5,), f32), output_dtype=bf16).shape == (3, 5, 48)
+    assert q.npu_quant_matmul(_m((2, 5, 64), i8), _m((3, 1, 64, 48), i8), _m((1,), f32),
+                              output_dtype=i32).shape == (3, 2, 5, 48)
+    assert q.npu_quant_matmul(_m((2, 5, 64), i8), _m((2, 48, 64), i8).transpose(-1, -2), _m((48,), f32),
+                              pertoken_scale=_m((10,), f32), output_dtype=f16).shape == (2, 5, 48)
+    out = q.npu_weight_quant_batchmatmul(_m((2, 16, 4096), bf16), _m((2, 4096, 1376), i32), _m((2, 32, 11008), f16),
+                                         _m((2, 32, 11008), f16), antiquant_group_size=128)
+    assert out.shape == (2, 16, 11008) and out.dtype == bf16
+    assert q.npu_weight_quant_batchmatmul(_m((16, 256), f16), _m((4, 256, 64), i8), _m((64,), f16)).shape \
+        == (4, 16, 64)
+
+
 @pytest.mark.parametrize("call,msg", [
     (lambda: q.npu_dynamic_quant(_m((4, 8), torch.float32)), "float16 or bfloat16"),
     (lambda: q.npu_dynamic_quant(_m((4, 8), torch.float16), smooth_scales=_m((7,), torch.float32)), "smooth_scales"),
@@ -208,12 +246,20 @@ def test_meta_shapes():
     (lambda: q.npu_format_cast(_m((128, 2), torch.int32), 3), "only ND"),
     (lambda: q.npu_format_cast(_m((128, 16), torch.float16), 29), "int4-packed"),
     (lambda: q.npu_format_cast(_m((96, 16), torch.int8), 29), "K % 64"),
-    (lambda: q.npu_weight_quant_batchmatmul(_m((2, 256), torch.bfloat16), _m((1, 1, 64, 4), torch.int32),
+    (lambda: q.npu_weight_quant_batchmatmul(_m((2, 256), torch.bfloat16),
+                                            q.npu_format_cast(_m((128, 2), torch.int32), 29),
                                             _m((1, 16), torch.float16), antiquant_group_size=128), "weight's K"),
-    (lambda: q.npu_quant_matmul(_m((4, 128), torch.int8), _m((4, 1, 64, 16), torch.int8), _m((1,), torch.float32)),
-     "weight's K"),
-    (lambda: q.npu_quant_matmul(_m((4, 64), torch.int8), _m((4, 1, 64, 4), torch.int8), _m((1,), torch.float32)),
-     "2-D"),
+    (lambda: q.npu_quant_matmul(_m((4, 128), torch.int8), q.npu_format_cast(_m((64, 64), torch.int8), 29),
+                                _m((1,), torch.float32)), "weight's K"),
+    (lambda: q.npu_quant_matmul(_m((4, 64), torch.int8), _m((1, 1, 1, 1, 1, 64, 4), torch.int8),
+                                _m((1,), torch.float32)), "x2 must be"),
+    (lambda: q.npu_quant_matmul(_m((2, 4, 64), torch.int8), _m((3, 64, 8), torch.int8), _m((1,), torch.float32)),
+     "do not broadcast"),
+    (lambda: q.npu_weight_quant_batchmatmul(_m((2, 4, 128), torch.bfloat16), _m((3, 128, 2), torch.int32),
+                                            _m((1, 16), torch.float16), antiquant_group_size=128), "do not broadcast"),
+    (lambda: q.npu_weight_quant_batchmatmul(_m((2, 4, 128), torch.bfloat16), _m((2, 128, 2), torch.int32),
+                                            _m((3, 1, 16), torch.float16), antiquant_group_size=128),
+     "antiquant_scale must be"),
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((64,), torch.float16)), "dtype of self"),
     (lambda: q.npu_rms_norm(_m((4, 64), torch.bfloat16), _m((32,), torch.bfloat16)), "trailing dims"),
     (lambda: q.npu_rms_norm_dynamic_quant(_m((4, 8, 8), torch.bfloat16), _m((8, 8), torch.bfloat16)), "1-D gamma"),
