@@ -339,8 +339,12 @@ int weight_quant_bmm_run(const char* op, const void* x, int x_dtype, const void*
     if (bias && !(is_half(bias_dtype) || bias_dtype == QK_F32)) return fail(QK_ERR_ARG, "%s: bias dtype %d unsupported", op, bias_dtype);
     if (M == 0 || N == 0) return QK_OK;
     if (!out || (K > 0 && (!x || !weight || !antiquant_scale))) return fail(QK_ERR_ARG, "%s: null pointer", op);
-    // the no-allocation scratch is sized without the cast-to-NZ plan (the cast weight may not fit in it)
-    const size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, scratch != nullptr);
+    // The no-allocation scratch runs the op's own plan (so the same kernels, the same bits) wherever that
+    // plan's workspace fits in it; otherwise the plan without the cast to NZ of a row-major int4 weight, whose
+    // cast weight is what does not fit.
+    size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, false);
+    if (scratch && need > QK_NOALLOC_SCRATCH_BYTES)
+        need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, true);
     if (scratch && need > 0) {
         int rc = QK_OK;
         workspace = scratch(need, &workspace_bytes, &rc);

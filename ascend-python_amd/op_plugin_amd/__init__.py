@@ -66,6 +66,7 @@ npu_swiglu_dynamic_quant = torch.ops.npu.npu_swiglu_dynamic_quant
 QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_U8, QK_I4_NZ, QK_I8_NZ, QK_I8_NK = 1, 2, 3, 4, 5, 6, 16, 17, 18
 ACL_FORMAT_ND, ACL_FORMAT_FRACTAL_NZ = 2, 29
 QK_OK, QK_ERR_ARG, QK_ERR_UNSUPPORTED, QK_ERR_WORKSPACE, QK_ERR_LAUNCH = 0, -1, -2, -3, -4
+QK_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 ABI_SYMBOLS = (
     "qk_last_error", "qk_abi_version", "qk_debug_set_plan", "qk_dynamic_quant", "qk_quant_matmul_workspace_size",

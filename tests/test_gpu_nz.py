@@ -232,6 +232,69 @@ def test_abi_noalloc_row_major_beyond_cast(ops, oracle):
     torch.testing.assert_close(out.cpu().float(), ref64.float(), rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("M", [1024, 2048])
+def test_w4a16_cfg3_cast_path_runs_and_matches_row_major_bits(ops, oracle, plan, M):
+    """cfg3's shape (N=11008, K=4096, 128-row groups, offset, bf16, no bias) at M >= 1024 on the row-major int4
+    weight, through the C ABI with a 0xA5-filled workspace: after the call the workspace holds the weight cast to
+    NZ (bit for bit what npu_format_cast writes), which shows the cast and the NZ prefill kernel ran; its output
+    equals bit for bit the row-major prefill kernel's (the cast switched off), whose 256 x 128 tiles add each
+    group's raw sums in the same k order and fold them alike; and it is within rtol / atol 1e-2 of the float64
+    dequant-matmul."""
+    N, K = 11008, 4096
+    say(f"w4a16 cfg3 M={M}: per-call cast to NZ ran, bits equal to the row-major kernel")
+    L = ops.abi()
+    d = _inputs(M, N, K, 128, True, torch.bfloat16, seed=M + 3)
+    x, w, sc, off = d["x"].to(DEV), d["w_packed"].to(DEV), d["scale"].to(DEV), d["offset"].to(DEV)
+    need = ctypes.c_size_t(0)
+    assert L.qk_weight_quant_bmm_workspace_size(M, N, K, ops.QK_I32, 128, ctypes.byref(need)) == 0
+    ws = torch.full((need.value,), 0xA5, dtype=torch.uint8, device=DEV)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    rc = L.qk_weight_quant_bmm(x.data_ptr(), BF16, w.data_ptr(), ops.QK_I32, sc.data_ptr(), off.data_ptr(), F16,
+                               M, N, K, 128, None, 0, out.data_ptr(), BF16, ws.data_ptr(), need.value,
+                               torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ops.last_error()
+    nz = ops.npu_format_cast(w, 29)
+    torch.cuda.synchronize()
+    cast_region = ws[4096:4096 + K * N // 2]
+    assert torch.equal(cast_region, nz.view(torch.uint8).reshape(-1)), "the workspace does not hold the NZ cast"
+    plan("w4nz=off")
+    rm = _run(ops, d, 128, w)
+    plan("")
+    assert torch.equal(out.view(torch.int16), rm.view(torch.int16))
+    ref64 = exact.wq_dequant_matmul(d["x"], d["w"], d["scale"], d["offset"], 128)
+    torch.testing.assert_close(out.cpu().float(), ref64.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_abi_noalloc_row_major_cast_fits_scratch(ops, oracle):
+    """The no-allocation entry point at M = 1024 on a row-major int4 weight whose NZ copy (1 MB) fits its 16 MB
+    scratch: the cast and the NZ prefill kernel run inside the library's array. Two calls in a row (the second on
+    other inputs, so stale scratch would show), each equal bit for bit to qk_weight_quant_bmm on an allocated
+    workspace and within rtol / atol 1e-2 of the float64 dequant-matmul."""
+    M, N, K = 1024, 2048, 1024
+    L = ops.abi()
+    s = torch.cuda.current_stream().cuda_stream
+    for seed in (31, 32):
+        say(f"ABI qk_weight_quant_bmm_noalloc row-major int4 M={M} N={N} K={K} seed={seed}")
+        d = _inputs(M, N, K, 128, True, torch.bfloat16, seed=seed)
+        x, w, sc, off = d["x"].to(DEV), d["w_packed"].to(DEV), d["scale"].to(DEV), d["offset"].to(DEV)
+        need = ctypes.c_size_t(0)
+        assert L.qk_weight_quant_bmm_workspace_size(M, N, K, ops.QK_I32, 128, ctypes.byref(need)) == 0
+        assert 4096 + K * N // 2 <= need.value <= ops.QK_NOALLOC_SCRATCH_BYTES
+        ws = torch.empty(need.value, dtype=torch.uint8, device=DEV)
+        ref = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+        assert L.qk_weight_quant_bmm(x.data_ptr(), BF16, w.data_ptr(), ops.QK_I32, sc.data_ptr(), off.data_ptr(),
+                                     F16, M, N, K, 128, None, 0, ref.data_ptr(), BF16, ws.data_ptr(), need.value,
+                                     s) == 0, ops.last_error()
+        assert L.qk_weight_quant_bmm_noalloc(x.data_ptr(), BF16, w.data_ptr(), ops.QK_I32, sc.data_ptr(),
+                                             off.data_ptr(), F16, M, N, K, 128, None, 0, out.data_ptr(), BF16,
+                                             s) == 0, ops.last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        ref64 = exact.wq_dequant_matmul(d["x"], d["w"], d["scale"], d["offset"], 128)
+        torch.testing.assert_close(out.cpu().float(), ref64.float(), rtol=1e-2, atol=1e-2)
+
+
 def test_abi_nz_and_noalloc(ops, oracle):
     """qk_weight_quant_bmm with QK_I4_NZ through the C ABI (no workspace needed), and the no-allocation entry
     point on the same NZ weight, against the oracle."""
