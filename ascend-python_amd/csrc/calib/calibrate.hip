@@ -11,6 +11,13 @@
 //  calib_stream_read the HBM read ceiling of one launch: every thread issues
 //                    its 16-byte loads of a buffer up front and folds them
 //                    into one word (so the loads are not removed).
+//  calib_stream_wave the same read in the load form of the decode kernels:
+//                    each wave instruction is one contiguous KB (64 lanes x
+//                    16 bytes, buffer loads with the non-temporal hint or the
+//                    default policy), U per lane issued up front, W waves per
+//                    workgroup, as many workgroups as cover the buffer; a
+//                    sweep over (W, U) gives the best one launch of that size
+//                    reaches.
 //  calib_dma_fill    the rate at which one CU fills its LDS by direct
 //                    global->LDS loads (buffer_load_dwordx4 ... lds, as the
 //                    GEMM kernels stage operands): NW waves each keep 16 such
@@ -81,6 +88,28 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// An empty kernel: what a launch of a given grid costs inside its own duration (dispatch, wave launch, end of
+// kernel), with no work at all.
+__global__ __launch_bounds__(1024) void calib_empty(uint32_t* out) {
+    if (threadIdx.x == 1023 && blockIdx.x == 0x7fffffff) out[0] = 1u;  // never true
+}
+
+// Wave w of workgroup b reads KB chunks (b*W + w)*U .. +U-1 of the buffer (loads past its end return zeros).
+template <int W, int U, int POL>
+__global__ __launch_bounds__(64 * W) void calib_stream_wave(const void* buf, uint32_t bytes, uint32_t* out) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(buf, bytes);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t c0 = (uint32_t)(blockIdx.x * W + wave) * U;
+    u32x4 v[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i)
+        v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16u * lane, (c0 + i) * 1024u, POL));
+    u32x4 a = v[0];
+#pragma unroll
+    for (int i = 1; i < U; ++i) a ^= v[i];
+    if (a[0] == 0x9e3779b9u && a[1] == 0x7f4a7c15u) out[blockIdx.x] = a[2];  // never true: keeps the loads
+}
+
 // 16 bytes per lane into LDS bytes [lds + 16*lane, +16); the kernel counts vmcnt itself
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff, uint32_t soff) {
     asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds));
@@ -131,6 +160,50 @@ int qk_calib_stream_read(const void* buf, int64_t bytes, int grid, uint32_t* out
     if ((int64_t)grid * 1024 * 8 < n16) return -1;
     calib_stream_read<8><<<dim3((uint32_t)grid), dim3(1024), 0, stream>>>(static_cast<const u32x4*>(buf), n16, out);
     return (int)hipGetLastError();
+}
+
+// The read of calib_stream_wave: shape s of {W, U, policy} below (-1: past the last shape); grid from the size.
+// out holds at least (bytes / 1024 + 1) words.
+int qk_calib_stream_wave(int shape, const void* buf, int64_t bytes, uint32_t* out, hipStream_t stream) {
+    struct Shape { int w, u, nt; };
+    static const Shape shapes[] = {{16, 6, 1}, {16, 6, 0}, {16, 3, 1}, {16, 2, 1}, {8, 4, 1},
+                                   {8, 2, 1}, {4, 8, 1}, {4, 4, 1}, {4, 2, 1}, {4, 1, 1}};
+    if (shape < 0 || shape >= (int)(sizeof(shapes) / sizeof(shapes[0])) || bytes <= 0 || bytes >= (1ll << 31)) return -1;
+    const Shape& sh = shapes[shape];
+    const int64_t chunks = (bytes + 1023) / 1024;
+    const uint32_t grid = (uint32_t)((chunks + sh.w * sh.u - 1) / (sh.w * sh.u));
+    const uint32_t b = (uint32_t)bytes;
+    switch (shape) {
+    case 0: calib_stream_wave<16, 6, 2><<<grid, 1024, 0, stream>>>(buf, b, out); break;
+    case 1: calib_stream_wave<16, 6, 0><<<grid, 1024, 0, stream>>>(buf, b, out); break;
+    case 2: calib_stream_wave<16, 3, 2><<<grid, 1024, 0, stream>>>(buf, b, out); break;
+    case 3: calib_stream_wave<16, 2, 2><<<grid, 1024, 0, stream>>>(buf, b, out); break;
+    case 4: calib_stream_wave<8, 4, 2><<<grid, 512, 0, stream>>>(buf, b, out); break;
+    case 5: calib_stream_wave<8, 2, 2><<<grid, 512, 0, stream>>>(buf, b, out); break;
+    case 6: calib_stream_wave<4, 8, 2><<<grid, 256, 0, stream>>>(buf, b, out); break;
+    case 7: calib_stream_wave<4, 4, 2><<<grid, 256, 0, stream>>>(buf, b, out); break;
+    case 8: calib_stream_wave<4, 2, 2><<<grid, 256, 0, stream>>>(buf, b, out); break;
+    default: calib_stream_wave<4, 1, 2><<<grid, 256, 0, stream>>>(buf, b, out); break;
+    }
+    return (int)hipGetLastError();
+}
+
+// grid x threads empty workgroups (threads <= 1024).
+int qk_calib_empty(int grid, int threads, uint32_t* out, hipStream_t stream) {
+    if (grid <= 0 || threads <= 0 || threads > 1024) return -1;
+    calib_empty<<<dim3((uint32_t)grid), dim3((uint32_t)threads), 0, stream>>>(out);
+    return (int)hipGetLastError();
+}
+
+// The (W, U, non-temporal) of shape s, for the report.
+int qk_calib_stream_wave_shape(int shape, int* w, int* u, int* nt) {
+    static const int t[][3] = {{16, 6, 1}, {16, 6, 0}, {16, 3, 1}, {16, 2, 1}, {8, 4, 1},
+                               {8, 2, 1}, {4, 8, 1}, {4, 4, 1}, {4, 2, 1}, {4, 1, 1}};
+    if (shape < 0 || shape >= 10) return -1;
+    *w = t[shape][0];
+    *u = t[shape][1];
+    *nt = t[shape][2];
+    return 0;
 }
 
 // variant: 0 = 4 waves, 1 = 8 waves, 2 = 16 waves (256-byte pieces).  buf holds span + 64 * rowstride

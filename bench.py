@@ -227,9 +227,33 @@ def calibrate(dev, min_launches: int) -> dict:
     sout = torch.empty(sgrid * 1024, dtype=torch.int32, device=dev)
     t = launch_runs(lambda i: L.qk_calib_stream_read(bufs[i % 24].data_ptr(), nbytes, sgrid, sout.data_ptr(), st),
                     24, min_launches, prime)
-    res["stream_read_24MB"] = {"us": round(t["s"] * 1e6, 2), "GB/s": round(nbytes / t["s"] / 1e9, 1),
-                               "frac_of_8000": round(nbytes / t["s"] / 1e9 / PEAK_HBM_GBS, 4),
-                               "grid": f"{sgrid} x 1024 threads, 8 x 16-byte loads each in flight"}
+    res["stream_read_24MB_thread_loads"] = {
+        "us": round(t["s"] * 1e6, 2), "GB/s": round(nbytes / t["s"] / 1e9, 1),
+        "frac_of_8000": round(nbytes / t["s"] / 1e9 / PEAK_HBM_GBS, 4),
+        "grid": f"{sgrid} x 1024 threads, 8 x 16-byte loads each in flight, consecutive threads on consecutive 16 B"}
+    # the decode kernels' load form: 1 KB per wave instruction, U per lane up front, over launch shapes; the
+    # cfg3 decode weight's 22,544,384 bytes exactly
+    L.qk_calib_stream_wave.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    L.qk_calib_stream_wave_shape.argtypes = [ctypes.c_int] + [ctypes.POINTER(ctypes.c_int)] * 3
+    wbytes = 4096 * 11008 // 2
+    wout = torch.empty(wbytes // 1024 + 1, dtype=torch.int32, device=dev)
+    sweep = {}
+    for shp in range(10):
+        w_, u_, nt_ = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        L.qk_calib_stream_wave_shape(shp, ctypes.byref(w_), ctypes.byref(u_), ctypes.byref(nt_))
+        t = launch_runs(lambda i: L.qk_calib_stream_wave(shp, bufs[i % 24].data_ptr(), wbytes, wout.data_ptr(), st),
+                        24, min_launches, prime)
+        grid_w = -(-(wbytes // 1024) // (w_.value * u_.value))
+        sweep[f"{grid_w}wg_x_{w_.value}waves_x_{u_.value}KB{'_nt' if nt_.value else ''}"] = round(t["s"] * 1e6, 2)
+    L.qk_calib_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    t = launch_runs(lambda i: L.qk_calib_empty(230, 1024, wout.data_ptr(), st), 24, min_launches, prime)
+    res["empty_kernel_230x1024_us"] = round(t["s"] * 1e6, 2)  # the decode kernel's grid, back-to-back
+    best = min(sweep, key=sweep.get)
+    res["stream_read_22.5MB_wave_loads"] = {
+        "best_us": sweep[best], "best_shape": best, "GB/s": round(wbytes / sweep[best] / 1e3, 1),
+        "frac_of_8000": round(wbytes / sweep[best] / 1e3 / PEAK_HBM_GBS, 4), "sweep_us": sweep,
+        "what": "one launch reading the 22,544,384 B of the cfg3 int4 weight once, 1 KB per wave load, all loads "
+                "of a lane issued before the first use; back-to-back launches over 24 rotating buffers"}
     dst = [torch.empty_like(bufs[0]) for _ in range(2)]
     t = launch_runs(lambda i: dst[i % 2].copy_(bufs[i % 24]), 24, min_launches, prime)
     res["device_copy_24MB"] = {"us": round(t["s"] * 1e6, 2), "GB/s_read_plus_write": round(2 * nbytes / t["s"] / 1e9, 1)}
