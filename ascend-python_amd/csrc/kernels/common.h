@@ -327,6 +327,7 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   w4_gemm=force | nodma | off                     prefill kernels on few tiles / register-staged only / never
 //   w4_splits=<n>                                   K splits of the 32-row-block decode kernel
 //   qmm_dma=0                                       W8A8 prefill: register-staged kernel instead of the DMA one
+//   qmm_bm128=0                                     W8A8 K splits: 256-row tiles only (no 128-row split tiles)
 //   qmm_mid=0                                       W8A8 M <= 256: split stream / tiled kernels instead of qmm_mid
 //   mid_bm=<16|32|64>, mid_split=<1|2>              qmm_mid: row block and K split (where the shape allows them)
 //   mid_bn=<64|128>                                 qmm_mid: column block (128 only for a [K,N] weight)
@@ -341,6 +342,7 @@ struct PlanOverride {
     int w4_gemm = 0;  // 0 planner, 1 force, 2 nodma, 3 off
     int w4_splits = 0;
     bool qmm_dma = true;
+    bool qmm_bm128 = true;
     bool qmm_mid = true;
     int mid_bm = 0, mid_split = 0, mid_bn = 0;
     int skinny_splits = 0;

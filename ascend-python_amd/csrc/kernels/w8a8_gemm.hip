@@ -581,12 +581,22 @@ constexpr int SMEM = RING > OUT_BYTES ? RING : OUT_BYTES;
 
 }  // namespace dm
 
-template <int BL, int OUT>
+// BMX = 128 (K splits only): 128-row tiles, so a shape with few 256-row tiles needs half the K splits (and half
+// the int32 partials) to fill the CUs.  Waves then own 32 x 128 (two row tiles), an A slot is 16 KB, and each
+// split stores its exact sums in the MFMA output layout, one whole KB per store instruction:
+// partial[split][tile][wave][TM*8 fragments][64 lanes] x 16 bytes (qmm_reduce_tiled reads it back).
+template <int BL, int OUT, int BMX = 256>
 __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int tiles_n, int nsplit,
                                                   int32_t* __restrict__ partial) {
     using namespace dm;
     constexpr bool B_KN = BL == kLayKN, B_NZ = BL == kLayNZ;
-    __shared__ __attribute__((aligned(1024))) int8_t smem[SMEM];
+    static_assert(BMX == 256 || (BMX == 128 && OUT == QK_I32), "128-row tiles run as K splits only");
+    constexpr int BM = BMX;          // tile rows
+    constexpr int TM = BM / 64;      // MFMA row tiles per wave (the wave tile is BM/4 x 128)
+    constexpr int A_SL = BM * A_KB;  // one A slot
+    constexpr int NA = BM / 64;      // A DMAs per wave per half range
+    constexpr int RING = NST * B_ST + NSA * A_SL;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[BM == 256 ? SMEM : RING];
 
     const int tiles = tiles_m * tiles_n;
     const int bid_all = xcd_swizzle(blockIdx.x, tiles * nsplit);
@@ -658,16 +668,16 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
         const uint32_t lds = sbase + A_BASE + (uint32_t)(r % NSA) * A_SL;
         const uint32_t k0 = k_base + (uint32_t)rs * A_KB;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int b = 16 * h + 4 * gw + i;
+        for (int i = 0; i < NA; ++i) {
+            const int b = 4 * NA * h + NA * gw + i;  // rows 8b .. 8b+7 (b & 1 == i & 1)
             dma16(rsA, lds + b * 1024, ((i & 1) ? va1 : va0) + (uint32_t)(8 * b) * lda, k0);
         }
     };
 
     // fragment read offsets: A for the low / high 64 K-bytes of a slot (slot s adds s * 32 KB); the
     // weight for stage 0 (stage st adds st * 16 KB)
-    const int a_rd0 = A_BASE + (wm * 64 + fr) * A_KB + 16 * (g ^ ((fr >> 1) & 7));
-    const int a_rd1 = A_BASE + (wm * 64 + fr) * A_KB + 16 * ((4 + g) ^ ((fr >> 1) & 7));
+    const int a_rd0 = A_BASE + (wm * (BM / 4) + fr) * A_KB + 16 * (g ^ ((fr >> 1) & 7));
+    const int a_rd1 = A_BASE + (wm * (BM / 4) + fr) * A_KB + 16 * ((4 + g) ^ ((fr >> 1) & 7));
     const int b_rd = (wn * 128 + fr) * 64 + 16 * (g ^ ((fr >> 1) & 3));
     // transpose reads: lanes 2b / 2b+1 of each 16-lane group address k row 16g + b (and +8), columns
     // 0..7 / 8..15 of the 16-column tile, whose chunk index is XOR-ed by h(k)
@@ -731,7 +741,7 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
         issue_a(1, 0);
         issue_a(1, 1);
         issue_a(2, 0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(12));  // range 0 (stages 0 and 1)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * NA));  // range 0 (stages 0 and 1)
     } else {        // loop indices -3..-1: weight stages 0..2
         issue_b(0, 0);
         issue_b(1, 1);
@@ -766,7 +776,7 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
             for (int u = 0; u < NST; ++u) {
                 const int t = t0 + u;
                 mma();
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NA));
                 bar();
                 if (t + 1 < nk) frags(t + 1, (u + 1) & 3);
                 issue_a((t + 5) >> 1, (t + 1) & 1);
@@ -792,9 +802,17 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     // the trailing DMAs (past the last stage) land before the LDS is reused or released
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     asm volatile("" ::"v"(warm));
-    EpiOps<TM> ops;
-    if (nsplit == 1) load_epi_ops<TM>(p, ops, m0, n0, wm, wn, lane);
-    big_epilogue<OUT, TM, NT, true>(p, acc, ops, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
+    if constexpr (BM == 128) {  // the split's exact sums in the MFMA layout, one KB per store, read once
+        i32x4* dst = reinterpret_cast<i32x4*>(partial) + (((int64_t)split * tiles + bid) * 8 + wave) * (TM * 8 * 64) + lane;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) __builtin_nontemporal_store(acc[i][j], dst + (i * 8 + j) * 64);
+    } else {
+        EpiOps<TM> ops;
+        if (nsplit == 1) load_epi_ops<TM>(p, ops, m0, n0, wm, wn, lane);
+        big_epilogue<OUT, TM, NT, true>(p, acc, ops, smem, m0, n0, wm, wn, lane, tid, split, nsplit, partial);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1436,6 +1454,79 @@ __global__ __launch_bounds__(kThreads) void qmm_reduce(QmmArgs p, int nsplit, co
     }
 }
 
+// The splits of qmm_dma<.., 128> (partial[split][tile][wave][16 fragments][64 lanes] x int32x4): one thread per
+// 16-byte piece of a tile -- rows 4g..4g+3 of one column of one 16 x 16 fragment -- adds the NS splits' pieces in
+// split order and applies qmm_store's operations to its four outputs.  All of a thread's loads (the column's
+// scale and bias bits, the four rows' per-token scales, every split's piece) go out before the first use, in
+// straight-line code: with qmm_store's per-element loads and a run-time split count, the compiler waited on
+// each load in turn and the kernel took 33 us for 36 MB.  Rows past M (a ragged last row tile) are not stored.
+template <int NS>
+__global__ __launch_bounds__(kThreads) void qmm_reduce_tiled(QmmArgs p, int tiles_m, int tiles_n,
+                                                             const i32x4* __restrict__ partial) {
+    constexpr int BM = 128, TM = 2, PIECES = 8 * TM * 8 * 64;  // pieces per tile
+    const int64_t per_split = (int64_t)tiles_m * tiles_n * PIECES;
+    constexpr int GM = 8;
+    const int per_group = GM * tiles_n;
+    const QmmEpilogue& e = p.epi;
+    const bool half = e.out_dtype == QK_BF16 || e.out_dtype == QK_F16;
+    for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < per_split;
+         idx += (int64_t)gridDim.x * kThreads) {
+        const int lane = (int)(idx & 63), f = (int)((idx >> 6) % (TM * 8)), wave = (int)((idx / (64 * TM * 8)) & 7);
+        const int bid = (int)(idx / PIECES);
+        const int grp = bid / per_group, first_m = grp * GM;
+        const int gm = min(tiles_m - first_m, GM);
+        const int tm = first_m + (bid % per_group) % gm, tn = (bid % per_group) / gm;
+        const int64_t m = (int64_t)tm * BM + (wave >> 1) * (BM / 4) + 16 * (f >> 3) + 4 * (lane >> 4);
+        const int64_t n = (int64_t)tn * 256 + (wave & 1) * 128 + 16 * (f & 7) + (lane & 15);
+        if (!half) {
+            uint32_t s[4] = {0u, 0u, 0u, 0u};
+            for (int k = 0; k < NS; ++k) {
+                const i32x4 v = partial[(int64_t)k * per_split + idx];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] += (uint32_t)v[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (m + r < p.M) qmm_store(e, m + r, n, (int32_t)s[r]);
+            continue;
+        }
+        // branch-free loads (a branch between two loads made the compiler wait on the first): an absent bias
+        // or per-token scale reads the scale array's first word instead, and the value is not used
+        const float sc = e.scale[e.scale_per_ch ? n : 0];
+        const bool b4 = e.bias_dtype == QK_I32 || e.bias_dtype == QK_F32;
+        const uint16_t* bp = e.bias_dtype ? reinterpret_cast<const uint16_t*>(e.bias) + (b4 ? 2 * n : n)
+                                          : reinterpret_cast<const uint16_t*>(e.scale);
+        const uint32_t blo = bp[0], bhi = bp[b4 ? 1 : 0];
+        const float* ptp = e.pertoken ? e.pertoken : e.scale;
+        float pt[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pt[r] = ptp[e.pertoken ? (m + r < p.M ? m + r : p.M - 1) : 0];
+        i32x4 part[NS];
+#pragma unroll
+        for (int k = 0; k < NS; ++k) part[k] = __builtin_nontemporal_load(partial + (int64_t)k * per_split + idx);
+        uint32_t s[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] += (uint32_t)part[k][r];
+        const uint32_t braw = b4 ? (blo | (bhi << 16)) : blo;
+        const uint32_t bi = e.bias_dtype == QK_I32 ? braw : 0u;
+        const float bf = e.bias_dtype == QK_F32    ? __uint_as_float(braw)
+                         : e.bias_dtype == QK_F16  ? f16_bits_to_f32((uint16_t)braw)
+                         : e.bias_dtype == QK_BF16 ? bf16_bits_to_f32((uint16_t)braw)
+                                                   : 0.0f;
+        uint16_t* dst = static_cast<uint16_t*>(e.out) + m * e.ldo + n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {  // qmm_store's operations, in its order
+            float v = (float)(int32_t)(s[r] + bi);
+            if (e.pertoken) v = v * pt[r];
+            v = __builtin_fmaf(v, sc, bf);
+            const uint32_t h = e.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+            if (m + r < p.M) dst[r * e.ldo] = (uint16_t)h;
+        }
+    }
+}
+
 // Any shape / stride / alignment: one thread per output element.
 __global__ __launch_bounds__(kThreads) void qmm_generic(QmmArgs p) {
     const int64_t total = p.M * p.N;
@@ -1505,12 +1596,24 @@ hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, int
 // of 128 and at least 512) until about 192 workgroups run, when the int32
 // partials stay within 512 MB.  From sizes only, so the workspace query and
 // the launch agree.
+// bm = 128: the split runs on 128-row tiles of the direct-to-LDS kernel (qmm_dma<.., 128>, tiled partials and
+// qmm_reduce_tiled), chosen where it needs fewer splits than 256-row tiles: half the partial bytes written and
+// read again (cfg5's down projection, 512 x 4096 x 14336: 4 splits of 64 tiles instead of 8 of 32; measured
+// 34.3 + ~8 us against 36.7 + 15.5 us).
 struct BigPlan {
     bool ok = false;
     int tiles_m = 0, tiles_n = 0, nsplit = 1;
+    int bm = 256;
 };
 
-BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
+// the power-of-two K split that brings `tiles` to about 192 workgroups (each split at least 512 deep)
+int big_splits(int64_t tiles, int64_t K) {
+    int ns = 1;
+    while (tiles * ns < 192 && ns < 16 && K % ((int64_t)ns * 2 * big::BK) == 0 && K / (ns * 2) >= 512) ns *= 2;
+    return ns;
+}
+
+BigPlan big_plan(int64_t M, int64_t N, int64_t K, bool allow128 = true) {
     BigPlan b;
     const int64_t tm = (M + big::BM - 1) / big::BM, tn = (N + big::BN - 1) / big::BN;
     if (K <= 0 || tm * tn >= (1 << 30)) return b;
@@ -1522,12 +1625,44 @@ BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
     }
     // a split needs whole tiles along N and K; a ragged M only runs split on the direct-to-LDS kernel
     if (N % big::BN != 0 || K % big::BK != 0) return b;
-    int ns = 1;
-    while (tm * tn * ns < 192 && ns < 16 && K % ((int64_t)ns * 2 * big::BK) == 0 && K / (ns * 2) >= 512) ns *= 2;
+    const int ns = big_splits(tm * tn, K);
     if (ns == 1 || tm * tn * ns < 64 || (int64_t)ns * M * N * 4 > ((int64_t)512 << 20)) return b;
     b.nsplit = ns;
     b.ok = true;
+    const int64_t tm2 = (M + 127) / 128;
+    const int ns2 = big_splits(tm2 * tn, K);
+    if (allow128 && plan_override().qmm_bm128 && ns2 < ns && tm2 * tn * ns2 >= 64 &&
+        K % ((int64_t)ns2 * dm::BK * dm::NST) == 0) {
+        b.bm = 128;
+        b.tiles_m = (int)tm2;
+        b.nsplit = ns2;
+    }
     return b;
+}
+
+// [split-K counters][partials]: int32 [nsplit][M][N], or for 128-row tiles [nsplit][tiles][128 x 256]
+size_t big_split_workspace(const BigPlan& b, int64_t M, int64_t N) {
+    const size_t rows = b.bm == 128 ? (size_t)b.tiles_m * 128 : (size_t)M;
+    return QK_SPLIT_COUNTER_BYTES + (size_t)b.nsplit * rows * (size_t)N * sizeof(int32_t);
+}
+
+template <int BL>
+hipError_t launch_split128(const QmmArgs& p, const BigPlan& b, int32_t* partial, hipStream_t stream) {
+    qmm_dma<BL, QK_I32, 128><<<dim3((uint32_t)(b.tiles_m * b.tiles_n * b.nsplit)), dim3(dm::NT), 0, stream>>>(
+        p, b.tiles_m, b.tiles_n, b.nsplit, partial);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    int64_t blocks = ((int64_t)b.tiles_m * b.tiles_n * 8 * 16 * 64 + kThreads - 1) / kThreads;
+    if (blocks > 65536) blocks = 65536;
+    const dim3 grid((uint32_t)blocks), block(kThreads);
+    const i32x4* part = reinterpret_cast<const i32x4*>(partial);
+    switch (b.nsplit) {  // big_plan's 128-row splits: 2, 4 or 8
+    case 2: qmm_reduce_tiled<2><<<grid, block, 0, stream>>>(p, b.tiles_m, b.tiles_n, part); break;
+    case 4: qmm_reduce_tiled<4><<<grid, block, 0, stream>>>(p, b.tiles_m, b.tiles_n, part); break;
+    case 8: qmm_reduce_tiled<8><<<grid, block, 0, stream>>>(p, b.tiles_m, b.tiles_n, part); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -1723,8 +1858,14 @@ size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K) {
     if (s.mt != 0)
         return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
     const BigPlan b = big_plan(M, N, K);
-    if (b.ok && b.nsplit > 1) return QK_SPLIT_COUNTER_BYTES + (size_t)b.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
-    return 0;
+    if (!b.ok || b.nsplit == 1) return 0;
+    // a 128-row split plan falls back to the 256-row one where its kernel does not apply: room for either
+    const size_t need = big_split_workspace(b, M, N);
+    if (b.bm == 128) {
+        const size_t alt = big_split_workspace(big_plan(M, N, K, false), M, N);
+        return need > alt ? need : alt;
+    }
+    return need;
 }
 
 hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_bytes, hipStream_t stream) {
@@ -1759,6 +1900,13 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
     }
     BigPlan bp = big_plan(p.M, p.N, p.K);
     bool big_ok = bp.ok && a_ok && (b_nk || (b_kn && p.N % 16 == 0 && p.sbk % 16 == 0 && (uintptr_t)p.b % 16 == 0));
+    if (big_ok && bp.bm == 128) {
+        // the 128-row split needs the direct-to-LDS kernel and its workspace; otherwise the shape runs unsplit
+        const size_t need = big_split_workspace(bp, p.M, p.N);
+        if (big_dma_ok(p, b_kn, bp.nsplit) && partial && ws_bytes >= need && (uintptr_t)partial % 16 == 0)
+            return b_kn ? launch_split128<kLayKN>(p, bp, partial, stream) : launch_split128<kLayNK>(p, bp, partial, stream);
+        bp = big_plan(p.M, p.N, p.K, false);
+    }
     // a split of a ragged M runs only on the direct-to-LDS kernel; otherwise the register-staged kernel runs
     // the shape unsplit (the planned workspace is then unused)
     if (big_ok && bp.nsplit > 1 && p.M % big::BM != 0 && !big_dma_ok(p, b_kn, bp.nsplit)) bp.nsplit = 1;
@@ -1854,8 +2002,7 @@ size_t quant_matmul_nz_workspace(int64_t M, int64_t N, int64_t K) {
     if (nzd_plan(M, N, K).nb) return 0;
     if (mid_plan(M, N, K, false).bm) return 0;
     const BigPlan b = big_plan(M, N, K);
-    if (nz_dma_ok(b, M, N, K))
-        return b.nsplit > 1 ? QK_SPLIT_COUNTER_BYTES + (size_t)b.nsplit * (size_t)M * (size_t)N * sizeof(int32_t) : 0;
+    if (nz_dma_ok(b, M, N, K)) return b.nsplit > 1 ? big_split_workspace(b, M, N) : 0;
     return round_up256((size_t)K * (size_t)N) + quant_matmul_workspace(M, N, K);
 }
 
@@ -1878,9 +2025,10 @@ hipError_t launch_quant_matmul_nz(const QmmArgs& p, void* workspace, size_t ws_b
             default: return launch_dma_nz<QK_I32>(p, b, nullptr, stream);
             }
         }
-        const size_t need = QK_SPLIT_COUNTER_BYTES + (size_t)b.nsplit * (size_t)p.M * (size_t)p.N * sizeof(int32_t);
+        const size_t need = big_split_workspace(b, p.M, p.N);
         if (!ws || ws_bytes < need || (uintptr_t)ws % 16 != 0) return hipErrorInvalidValue;
         int32_t* partial = reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES);
+        if (b.bm == 128) return launch_split128<kLayNZ>(p, b, partial, stream);
         const hipError_t e = launch_dma_nz<QK_I32>(p, b, partial, stream);
         if (e != hipSuccess) return e;
         int64_t blocks = (p.M * p.N / 4 + kThreads - 1) / kThreads;

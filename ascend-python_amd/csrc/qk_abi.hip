@@ -74,6 +74,8 @@ bool parse_plan(const char* spec, PlanOverride& o) {
             r.w4_splits = a;
         } else if (k == "qmm_dma" && (v == "0" || v == "1")) {
             r.qmm_dma = v == "1";
+        } else if (k == "qmm_bm128" && (v == "0" || v == "1")) {
+            r.qmm_bm128 = v == "1";
         } else if (k == "qmm_mid" && (v == "0" || v == "1")) {
             r.qmm_mid = v == "1";
         } else if (k == "mid_bm" && (v == "16" || v == "32" || v == "64")) {

@@ -35,14 +35,40 @@ def test_debug_plan_override_parsing():
     """The planners' one debug override: accepted specs, and refusal (with the override unchanged) of
     specs it does not understand.  Nothing is launched."""
     for spec in ("", "w4_stream=16:4:4", "w4_stream=off", "w4_gemm=force,skinny_splits=4", "qmm_dma=0", "qmm_mid=0",
-                 "mid_bm=32,mid_split=2", "mid_bn=64",
+                 "mid_bm=32,mid_split=2", "mid_bn=64", "qmm_bm128=0",
                  "w4_splits=8,w4_gemm=nodma", "w4nz=off", "w4nz_wg=172", "w4nz_nit=4"):
         q.debug_set_plan(spec)
     for bad in ("w4_stream=12:4:2", "w4_gemm=maybe", "skinny_splits=3", "nonsense", "qmm_dma=2", "w4nz=on",
-                "w4nz_wg=0"):
+                "w4nz_wg=0", "qmm_bm128=2"):
         with pytest.raises(ValueError, match="not understood"):
             q.debug_set_plan(bad)
     q.debug_set_plan("")
+
+
+def test_w8a8_split_plan_workspace_sizes():
+    """The K-split plans' workspaces (host arithmetic only).  cfg5's down projection (512 x 4096 x 14336) has 32
+    tiles of 256 x 256, split 8 ways to fill the CUs; on 128-row tiles it has 64, split 4 ways: half the int32
+    partials.  The NZ weight always runs the 128-row split; a row-major weight may fall back to the 256-row one
+    (another kernel) and asks room for either."""
+    L = q.abi()
+    ws = ctypes.c_size_t(0)
+    M, N, K = 512, 4096, 14336
+    ctr = 4096  # QK_SPLIT_COUNTER_BYTES
+    try:
+        assert L.qk_quant_matmul_nz_workspace_size(M, N, K, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == ctr + 4 * M * N * 4
+        assert L.qk_quant_matmul_workspace_size(M, N, K, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == ctr + 8 * M * N * 4
+        # a ragged M pads the 128-row tiles' partials to whole tiles: 300 rows -> 3 tiles, 4 splits
+        assert L.qk_quant_matmul_nz_workspace_size(300, 4096, 8192, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == ctr + 4 * 384 * 4096 * 4
+        q.debug_set_plan("qmm_bm128=0")
+        assert L.qk_quant_matmul_nz_workspace_size(M, N, K, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == ctr + 8 * M * N * 4
+        assert L.qk_quant_matmul_nz_workspace_size(300, 4096, 8192, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == ctr + 8 * 300 * 4096 * 4
+    finally:
+        q.debug_set_plan("")
 
 
 def test_abi_refuses_bad_arguments_without_launch():
