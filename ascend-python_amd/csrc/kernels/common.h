@@ -127,21 +127,22 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, u
 // writeback or invalidate is needed.  Call from every thread of the workgroup
 // (it contains barriers).
 //
-// A counter is one 64-bit word: bits 63..16 hold the tag of the call that
-// counted into it, bits 15..0 that call's arrivals.  Every call draws its own
-// tag (48 bits, never 0 and never all ones), and an arrival that finds a
-// different tag starts the count at one.  So the word needs no
-// initialisation: leftovers of any earlier call, a zero fill, a 0xFF fill or
-// other data all count as "no arrivals yet" unless their upper 48 bits equal
-// this call's tag.  The last arrival sets the word to zero (every other
-// arrival has happened by then), so a captured graph that replays one tag
-// also finds an empty counter each time.
-// The first compare-and-swap guesses that every other split has already
-// arrived (expected value: this tag with nsplit - 1 arrivals) and clears the
-// word in the same operation; it fails with the word's actual value
-// otherwise, and the count goes on from there.  So the last arrival -- the
-// one the tile waits for -- finishes in a single atomic round trip, where an
-// atomic load followed by a compare-and-swap took two.
+// A counter is one 64-bit word.  Every call draws a tag T (48 bits, never 0
+// and never all ones), and each arrival adds D = T * 2^16 + 1 with one
+// fetch-and-add, so after j arrivals of this call on an empty word the word
+// is j * D (mod 2^64), whose low 16 bits are j.  An arrival that reads such a
+// value (j < nsplit, the word equal to j * D) is arrival j + 1: one atomic
+// round trip, the same as a plain counter.  Zero is j = 0, and the last
+// arrival sets the word back to zero (every other arrival has happened by
+// then), so a workspace the library used before, or a zero fill, counts from
+// zero; a captured graph that replays one tag likewise finds zero each time.
+// Any other value is a stale word (a 0xFF fill, other data: a multiple of D
+// below nsplit * D by chance only, odds about 2^-48 per word): that arrival's
+// add is void and it registers with a compare-and-swap loop instead, which
+// replaces a stale word by D (arrival 1) and adds D to a valid one.  Adds that
+// land on a stale word are wiped by that replacement, and their arrivals
+// register by compare-and-swap themselves; adds that land on a valid word
+// count.  So each arrival is counted exactly once.
 // Cache-policy operand of the raw buffer loads/stores for device-coherent
 // access (the sc1 bit on gfx950).
 constexpr int kCoherent = 16;
@@ -154,19 +155,23 @@ __device__ __forceinline__ bool splitk_last(uint64_t* ctr, uint32_t nsplit, uint
     __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint64_t base = tag << kSplitCountBits;
-        uint64_t old = base | (nsplit - 1u);
-        uint32_t n = nsplit;
-        if (!__hip_atomic_compare_exchange_strong(ctr, &old, (uint64_t)0, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT)) {
+        const uint64_t d = (tag << kSplitCountBits) | 1u;
+        constexpr uint64_t kCount = ((uint64_t)1 << kSplitCountBits) - 1;
+        auto valid = [&](uint64_t w) { return (w & kCount) < nsplit && w == (w & kCount) * d; };
+        uint64_t old = __hip_atomic_fetch_add(ctr, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t n;
+        if (valid(old)) {
+            n = (uint32_t)(old & kCount) + 1u;
+        } else {
+            old += d;  // the word as this add left it; a failed compare-and-swap returns the actual value
             uint64_t nw;
             do {
-                nw = (old >> kSplitCountBits) == tag ? old + 1 : base | 1u;
+                nw = valid(old) ? old + d : d;
             } while (!__hip_atomic_compare_exchange_weak(ctr, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT));
-            n = (uint32_t)(nw & ((1u << kSplitCountBits) - 1));
-            if (n == nsplit) __hip_atomic_store(ctr, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            n = (uint32_t)(nw & kCount);
         }
+        if (n == nsplit) __hip_atomic_store(ctr, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         splitk_count = n;
     }
     __syncthreads();

@@ -30,12 +30,14 @@
  * QK_SPLIT_COUNTER_BYTES of split-K arrival counters, followed by the partial
  * sums (split-K shapes) or by the activations' per-group sums (weight-quant
  * matmul at large M; from M = 1024 on a row-major int4 weight the weight cast
- * to NZ, K*N/2 bytes rounded to 256, comes first, then the sums).  Each counter carries the tag of the call that counts
- * into it (48 bits drawn per call, never 0 or all ones), so what an earlier
- * call or another user left there is not mistaken for arrivals of this call;
- * the one exception is memory whose counter words happen to hold this call's
- * random 48-bit tag (odds 2^-48 per counter word for random contents, zero for
- * zero- or 0xFF-filled memory).  The workgroup that completes a tile's splits
+ * to NZ, K*N/2 bytes rounded to 256, comes first, then the sums).  Each arrival adds D = tag * 2^16 + 1 to its
+ * counter (a 48-bit tag drawn per call, never 0 or all ones), so a counter of
+ * this call holds j * D after j arrivals; a zero word is empty (the last
+ * arrival leaves zero behind), and any other word that is not such a multiple
+ * -- what another user left there, a 0xFF fill -- is recognised as stale and
+ * replaced.  The one exception is memory whose counter words happen to hold a
+ * small multiple of this call's D (odds below 2^-48 per counter word for
+ * random contents, zero for zero- or 0xFF-filled memory).  The workgroup that completes a tile's splits
  * adds them up itself, so no second kernel runs.  Calls that may be in flight
  * at the same time need distinct workspaces.
  */

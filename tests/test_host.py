@@ -361,3 +361,54 @@ def test_quant8_magic_rounding_rule():
         assert np.array_equal(fast[group_safe], ref[group_safe]), trial
         redone += int(np.sum(~group_safe))
     assert redone >= 8 * 1000  # the tie rows' groups took the exact path
+
+
+def test_split_counter_protocol_model():
+    """The split-K arrival counter of splitk_last (csrc/kernels/common.h), stepped on the CPU: nsplit arrivals,
+    each a fetch-and-add of D = tag * 2^16 + 1 and, on a stale word, a compare-and-swap loop, interleaved at
+    random on initial words that a workspace may hold (zero, 0xFF fill, small integers, random bits, stale
+    multiples of D).  Every interleaving must count the arrivals 1..nsplit exactly once and leave the word zero."""
+    import random
+    MASK = (1 << 64) - 1
+    KC = (1 << 16) - 1
+    rng = random.Random(7)
+    for trial in range(3000):
+        nsplit = rng.choice([2, 3, 4, 8, 16])
+        tag = rng.randrange(1, (1 << 48) - 1)
+        d = ((tag << 16) | 1) & MASK
+
+        def valid(w):
+            return (w & KC) < nsplit and w == ((w & KC) * d) & MASK
+
+        word = rng.choice([0, MASK, rng.randrange(0, 1 << 20), rng.getrandbits(64), (-rng.randrange(1, 40) * d) & MASK,
+                           ((nsplit + rng.randrange(0, 5)) * d) & MASK, (tag << 16) & MASK])
+        # per arrival: stage 0 = fetch-and-add pending, 1 = CAS pending (expected value held), 2 = done
+        stage = [0] * nsplit
+        expect = [0] * nsplit
+        counts = []
+        last = []
+        while any(s != 2 for s in stage):
+            a = rng.choice([i for i in range(nsplit) if stage[i] != 2])
+            if stage[a] == 0:
+                old = word
+                word = (word + d) & MASK
+                if valid(old):
+                    n = (old & KC) + 1
+                else:
+                    expect[a] = (old + d) & MASK
+                    stage[a] = 1
+                    continue
+            else:
+                nw = ((expect[a] + d) & MASK) if valid(expect[a]) else d
+                if word != expect[a]:
+                    expect[a] = word  # failed compare-and-swap: retry with the actual value
+                    continue
+                word = nw
+                n = nw & KC
+            stage[a] = 2
+            counts.append(n)
+            if n == nsplit:
+                word = 0
+                last.append(a)
+        assert sorted(counts) == list(range(1, nsplit + 1)), (trial, counts)
+        assert len(last) == 1 and word == 0
