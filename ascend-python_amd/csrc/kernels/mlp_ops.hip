@@ -99,7 +99,15 @@ __global__ __launch_bounds__(NT) void rms_norm_vec(const uint16_t* __restrict__ 
     const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
     const int nv = (int)(D >> 3);
     float v[VPT][8];
+    u32x4 graw[VPT];
     float ss = 0.0f;
+    // gamma's loads go out with the row's (they are L2 hits after the first rows), so the output pass does
+    // not wait for a second round trip after the row reduction
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        if (idx < nv) graw[i] = gr[idx];
+    }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = threadIdx.x + i * NT;
@@ -111,7 +119,8 @@ __global__ __launch_bounds__(NT) void rms_norm_vec(const uint16_t* __restrict__ 
     }
     ss = block_sum<NT / 64>(ss);
     const float rs = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
-    if (threadIdx.x == 0 && rstd) rstd[row] = rs;
+    // rstd is stored after the last barrier: a store ahead of a barrier makes its wave wait for the store's
+    // completion there, and every other wave with it
     float amax = 0.0f;
     uint32_t yb[VPT][8];
 #pragma unroll
@@ -119,7 +128,7 @@ __global__ __launch_bounds__(NT) void rms_norm_vec(const uint16_t* __restrict__ 
         const int idx = threadIdx.x + i * NT;
         if (idx < nv) {
             float g[8];
-            unpack8(gr[idx], DT, g);
+            unpack8(graw[i], DT, g);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 yb[i][e] = to16<DT>((v[i][e] * rs) * g[e]);
@@ -129,10 +138,16 @@ __global__ __launch_bounds__(NT) void rms_norm_vec(const uint16_t* __restrict__ 
             if (!QUANT) __builtin_nontemporal_store(pack16<DT>(yb[i]), reinterpret_cast<u32x4*>(y + row * D) + idx);
         }
     }
-    if (!QUANT) return;
+    if (!QUANT) {
+        if (threadIdx.x == 0 && rstd) rstd[row] = rs;
+        return;
+    }
     amax = block_absmax_w<NT / 64>(amax);
     const float s = amax / 127.0f;
-    if (threadIdx.x == 0) scale[row] = s;
+    if (threadIdx.x == 0) {
+        scale[row] = s;
+        if (rstd) rstd[row] = rs;
+    }
     const RowQuant rq = row_quant(s);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
