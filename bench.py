@@ -529,20 +529,32 @@ def main():
                          W4_SETS, args.min_launches, prime)
     dq_t = launch_runs(lambda i: q.npu_dynamic_quant(xs4[i % W8A8_SETS]), 12, args.min_launches, prime)
 
-    # ---------------- parity spot check of set 0 against the oracle (rows 0..7)
+    # ---------------- parity check of set 0 against the oracle: the whole dynamic-quant output; 24 rows of the
+    # bf16 GEMM output (the first, middle and last 8) bit for bit; the whole int32 product of the same kernel
+    # through exact row and column checksums (sum over m of acc[m, n] = (sum over m of a[m, :]) . w[:, n], and
+    # likewise over n, in int64); the W4A16 decode within 1e-2
     parity = None
     try:
         from oracle import oracle
         out, o3 = step(0)
+        xq0, xs0 = q.npu_dynamic_quant(xs4[0])
+        acc0 = q.npu_quant_matmul(xq0, wz4[0], torch.ones(1, device=dev), output_dtype=torch.int32)
         torch.cuda.synchronize()
-        rq, rs = oracle.dynamic_quant(W.bits(d4["x"][:8]), oracle.F16)
-        ref = oracle.quant_matmul(rq, d4["w"].numpy(), d4["w_scale"].numpy(), pertoken=rs, bias=W.bits(d4["bias"]),
-                                  bias_dtype=oracle.BF16, out_dtype=oracle.BF16)
-        ok4 = bool(np.array_equal(W.bits(out[:8].cpu()), ref))
+        rq, rs = oracle.dynamic_quant(W.bits(d4["x"]), oracle.F16)
+        ok_q = bool(np.array_equal(xq0.cpu().numpy(), rq) and np.array_equal(xs0.cpu().numpy(), rs))
+        rows = np.r_[0:8, c4.M // 2:c4.M // 2 + 8, c4.M - 8:c4.M]
+        ref = oracle.quant_matmul(rq[rows], d4["w"].numpy(), d4["w_scale"].numpy(), pertoken=rs[rows],
+                                  bias=W.bits(d4["bias"]), bias_dtype=oracle.BF16, out_dtype=oracle.BF16)
+        ok4 = bool(np.array_equal(W.bits(out.cpu())[rows], ref))
+        a64, w64n = rq.astype(np.int64), d4["w"].numpy().astype(np.int64)
+        g_acc = acc0.cpu().numpy().astype(np.int64)
+        ok_sums = bool(np.array_equal(g_acc.sum(axis=0), a64.sum(axis=0) @ w64n) and
+                       np.array_equal(g_acc.sum(axis=1), a64 @ w64n.sum(axis=1)))
         r3 = oracle.weight_quant_bmm(W.bits(d3["x"]), oracle.BF16, d3["w_packed"].numpy(), W.bits(d3["scale"]),
                                      W.bits(d3["offset"]), oracle.F16, 128)
         ok3 = bool(torch.allclose(o3.cpu().float(), W.from_bits(r3, torch.bfloat16).float(), rtol=1e-2, atol=1e-2))
-        parity = {"w8a8_rows0_7_bit_exact": ok4, "w4a16_within_1e-2": ok3}
+        parity = {"dynamic_quant_whole_bit_exact": ok_q, "w8a8_bf16_24_rows_bit_exact": ok4,
+                  "w8a8_int32_row_and_column_sums_exact": ok_sums, "w4a16_within_1e-2": ok3}
     except Exception as e:  # the bench still reports its timing
         parity = {"error": repr(e)[:200]}
 
