@@ -257,6 +257,8 @@ def test_w4a16_cfg3_cast_path_runs_and_matches_row_major_bits(ops, oracle, plan,
     torch.cuda.synchronize()
     cast_region = ws[4096:4096 + K * N // 2]
     assert torch.equal(cast_region, nz.view(torch.uint8).reshape(-1)), "the workspace does not hold the NZ cast"
+    on_nz = _run(ops, d, 128, nz)  # the same kernel on the weight cast once
+    assert torch.equal(out.view(torch.int16), on_nz.view(torch.int16))
     plan("w4nz=off")
     rm = _run(ops, d, 128, w)
     plan("")
