@@ -80,6 +80,14 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
+// SwiGLU of one gate / up pair, a * sigmoid(a) * b, evaluated as (a * rcp(1 + exp2(-a * log2(e)))) * b on the
+// hardware exp2 and reciprocal (exp(-a) is +inf below a = -88.7).  Shared by the SwiGLU kernels and the
+// gate-up GEMM's fused epilogue, so both round the same fp32 value.
+__device__ __forceinline__ float silu_mul(float a, float b) {
+    const float e = __builtin_amdgcn_exp2f(-a * 1.44269504088896341f);
+    return (a * __builtin_amdgcn_rcpf(1.0f + e)) * b;
+}
+
 __device__ __forceinline__ float load_half_bits(uint32_t bits, int dtype) {
     return dtype == QK_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
 }
@@ -375,6 +383,10 @@ size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K);
 // the same op on an int8 NZ weight (args.b: [N/16][K/64][64][16]; args.sbk / args.sbn unused)
 hipError_t launch_quant_matmul_nz(const QmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t quant_matmul_nz_workspace(int64_t M, int64_t N, int64_t K);
+// The quantized MLP block's gate-up GEMM with SwiGLU fused: args.N = 2I weight columns (gate, then up), the
+// output h [M, I] (bf16 / fp16, args.epi.ldo = I); the weight as NZ blocks (nz) or [K, 2I] rows.
+// hipErrorInvalidValue where the shape or operands do not fit the kernel.
+hipError_t launch_quant_matmul_swiglu(const QmmArgs& args, bool nz, hipStream_t stream);
 
 struct WqbmmArgs {
     const void* x;

@@ -242,11 +242,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_f32_generic(const float* __
     for (int64_t d = threadIdx.x; d < D; d += kThreads) y[row * D + d] = (xr[d] * rs) * gamma[d];
 }
 
-// ---------------------------------------------------------------- SwiGLU
-__device__ __forceinline__ float silu_mul(float a, float b) {
-    const float e = __builtin_amdgcn_exp2f(-a * 1.44269504088896341f);  // exp(-a); +inf below a = -88.7
-    return (a * __builtin_amdgcn_rcpf(1.0f + e)) * b;
-}
+// ---------------------------------------------------------------- SwiGLU (silu_mul: common.h)
 
 template <int DT, int NT, int VPT, bool QUANT>
 __global__ __launch_bounds__(NT) void swiglu_vec(const uint16_t* __restrict__ h, int64_t I,

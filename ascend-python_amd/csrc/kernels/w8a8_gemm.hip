@@ -25,6 +25,7 @@ constexpr int LDS_ROW = 80;   // padded row stride (bytes) of the LDS tiles
 // the int8 NZ layout [N/16][K/64][64][16] (1 KB blocks of 16 columns x 64 rows, lane l of a block holding
 // rows 16(l/16)..+15 of column l%16: one v_mfma_i32_16x16x64_i8 B operand per block).
 constexpr int kLayNK = 0, kLayKN = 1, kLayNZ = 2;
+constexpr int kOutSwiGLU = 64;  // qmm_dma's OUT for the fused gate-up + SwiGLU form (+ the output dtype)
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
     return __builtin_amdgcn_perm(hi, lo, sel);
@@ -261,14 +262,16 @@ struct EpiOps {
     float pt[TM][4];
 };
 
-template <int TM>
+// SWI (the gate-up GEMM with SwiGLU fused): wave column half wn = 0 holds the gate columns n0 .., wn = 1 the up
+// columns n_up .., of the same outputs.
+template <int TM, bool SWI = false>
 __device__ __forceinline__ void load_epi_ops(const QmmArgs& p, EpiOps<TM>& o, int64_t m0, int64_t n0, int wm,
-                                             int wn, int lane) {
+                                             int wn, int lane, int64_t n_up = 0) {
     const QmmEpilogue& e = p.epi;
     const int fr = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int64_t n = n0 + wn * 128 + 16 * j + fr;
+        const int64_t n = (SWI ? (wn == 0 ? n0 : n_up) : n0 + wn * 128) + 16 * j + fr;
         const bool ok = n < p.N;
         o.sc[j] = (ok && e.scale) ? e.scale[e.scale_per_ch ? n : 0] : 0.0f;
         o.of[j] = (ok && e.offset) ? e.offset[e.offset_per_ch ? n : 0] : 0.0f;
@@ -377,6 +380,58 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
                 if (ok) big::store_elem<OUT>(e.out, ro + 16 * j, acc[i][j][r], sc[j], bf[j], bi[j], pt, of[j]);
             }
         }
+    }
+}
+
+// The gate-up GEMM's fused SwiGLU epilogue (256 x 256 tiles whose column halves are the gate and the up columns of
+// 128 outputs): each half is rounded to the output type exactly as big_epilogue rounds it and staged through
+// LDS; then each thread takes 8 outputs of one row (16 bytes of gate, 16 of up) and stores
+// h = silu(gate) * up rounded to the same type -- the values the SwiGLU kernel computes from the gate-up
+// output in HBM.  h has ldo = N / 2 columns; rows past M are not stored.
+template <int ODT, int TM, int NT>
+__device__ __forceinline__ void swiglu_epilogue(const QmmArgs& p, const i32x4 (&acc)[TM][8], const EpiOps<TM>& ops,
+                                                int8_t* smem, int64_t m0, int64_t n0, int wm, int wn, int lane,
+                                                int tid) {
+    using namespace big;
+    constexpr int WMR = 16 * TM;
+    constexpr int ROWB = 2 * BN + 16;  // padded LDS row (bytes): gate columns, then up columns
+    const int fr = lane & 15, g = lane >> 4;
+    const QmmEpilogue& e = p.epi;
+    auto to16 = [](float v) { return ODT == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v); };
+    __syncthreads();
+    uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = wm * WMR + 16 * i + 4 * g + r;
+            const float pt = ops.pt[i][r];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = __builtin_fmaf((float)acc[i][j][r] * pt, ops.sc[j], 0.0f);  // no bias: + 0
+                ot[row * (ROWB / 2) + wn * 128 + 16 * j + fr] = (uint16_t)to16(v);
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int CH = BN / 16;  // 16-byte chunks of an h row (128 outputs)
+    static_assert(BM * CH % NT == 0, "whole chunks per thread");
+#pragma unroll
+    for (int it = 0; it < BM * CH / NT; ++it) {
+        const int q = tid + it * NT;
+        const int row = q / CH, c = q % CH;
+        if (m0 + row >= p.M) break;  // rows past a ragged M (q grows with the row)
+        const u32x4 gv = *reinterpret_cast<const u32x4*>(smem + row * ROWB + 16 * c);
+        const u32x4 uv = *reinterpret_cast<const u32x4*>(smem + row * ROWB + BN + 16 * c);
+        u32x4 hv;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t lo = to16(silu_mul(load_half_bits(gv[w] & 0xffffu, ODT), load_half_bits(uv[w] & 0xffffu, ODT)));
+            const uint32_t hi = to16(silu_mul(load_half_bits(gv[w] >> 16, ODT), load_half_bits(uv[w] >> 16, ODT)));
+            hv[w] = lo | (hi << 16);
+        }
+        __builtin_nontemporal_store(hv, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo +
+                                                                 n0 + 8 * c));  // written once
     }
 }
 
@@ -585,12 +640,18 @@ constexpr int SMEM = RING > OUT_BYTES ? RING : OUT_BYTES;
 // the int32 partials) to fill the CUs.  Waves then own 32 x 128 (two row tiles), an A slot is 16 KB, and each
 // split stores its exact sums in the MFMA output layout, one whole KB per store instruction:
 // partial[split][tile][wave][TM*8 fragments][64 lanes] x 16 bytes (qmm_reduce_tiled reads it back).
+// OUT = kOutSwiGLU + QK_BF16 / QK_F16: the gate-up GEMM with SwiGLU fused (swiglu_epilogue).  The weight has
+// N = 2I columns, gate then up; tile tn covers outputs 128 tn .. +127, its B columns the gate columns
+// 128 tn .. and the up columns I + 128 tn .. (NZ blocks or [K,N] column chunks addressed apart); no split.
 template <int BL, int OUT, int BMX = 256>
 __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int tiles_n, int nsplit,
                                                   int32_t* __restrict__ partial) {
     using namespace dm;
     constexpr bool B_KN = BL == kLayKN, B_NZ = BL == kLayNZ;
+    constexpr bool SWI = OUT >= kOutSwiGLU;
+    constexpr int ODT = SWI ? OUT - kOutSwiGLU : OUT;
     static_assert(BMX == 256 || (BMX == 128 && OUT == QK_I32), "128-row tiles run as K splits only");
+    static_assert(!SWI || (BMX == 256 && BL != kLayNK && (ODT == QK_BF16 || ODT == QK_F16)), "fused SwiGLU form");
     constexpr int BM = BMX;          // tile rows
     constexpr int TM = BM / 64;      // MFMA row tiles per wave (the wave tile is BM/4 x 128)
     constexpr int A_SL = BM * A_KB;  // one A slot
@@ -609,7 +670,8 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     const int gm = min(tiles_m - first_m, GM);
     const int tm = first_m + (bid % per_group) % gm;
     const int tn = (bid % per_group) / gm;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (SWI ? BN / 2 : BN);
+    const int64_t n_up = SWI ? p.N / 2 + n0 : 0;  // SWI: the tile's first up column
     const int64_t k_len = p.K / nsplit;
     const uint32_t k_base = (uint32_t)(split * k_len);
 
@@ -627,8 +689,11 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     const int64_t rows_valid = p.M - m0 < BM ? p.M - m0 : BM;
     const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.a + m0 * p.lda, (uint32_t)(rows_valid * p.lda));
     // an NZ column block: BN/16 consecutive n-blocks of K/64 1 KB blocks, BN * K contiguous bytes
-    const __amdgpu_buffer_rsrc_t rsB = B_NZ   ? make_rsrc(p.b + n0 * p.K, (uint32_t)(BN * p.K))
-                                       : B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + BN))
+    // SWI: the whole NZ weight (blocks addressed per wave), or the [K,N] rows from the gate columns on, whose
+    // chunks 8..15 are moved to the up columns (I - 128 bytes further)
+    const __amdgpu_buffer_rsrc_t rsB = B_NZ   ? (SWI ? make_rsrc(p.b, (uint32_t)(p.N * p.K))
+                                                     : make_rsrc(p.b + n0 * p.K, (uint32_t)(BN * p.K)))
+                                       : B_KN ? make_rsrc(p.b + n0, (uint32_t)((p.K - 1) * p.sbk + (SWI ? p.N / 2 + BN / 2 : BN)))
                                               : make_rsrc(p.b + n0 * p.sbn, (uint32_t)(BN * p.sbn));
     const uint32_t kblocks = (uint32_t)(p.K >> 6);
     const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)(B_KN ? p.sbk : p.sbn);
@@ -641,8 +706,11 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     // [k][256 B]: one instruction = 4 rows 4b..4b+3 (b = 4*gw + i); lane l -> row l>>4, LDS chunk l&15, and
     // h = 4*(b&1) + (l>>4) + 8*((b>>2)&1), (b>>2)&1 = gw&1
     const int hb = 8 * (gw & 1);
-    const uint32_t vkn0 = (uint32_t)(lane >> 4) * ldb + 16u * (uint32_t)((lane & 15) ^ ((lane >> 4) + hb));
-    const uint32_t vkn1 = (uint32_t)(lane >> 4) * ldb + 16u * (uint32_t)((lane & 15) ^ (4 + (lane >> 4) + hb));
+    auto kn_col = [&](int cc) {  // byte column of chunk cc (SWI: chunks 8..15 are up columns)
+        return 16u * (uint32_t)cc + (SWI && cc >= 8 ? (uint32_t)(p.N / 2 - BN / 2) : 0u);
+    };
+    const uint32_t vkn0 = (uint32_t)(lane >> 4) * ldb + kn_col((lane & 15) ^ ((lane >> 4) + hb));
+    const uint32_t vkn1 = (uint32_t)(lane >> 4) * ldb + kn_col((lane & 15) ^ (4 + (lane >> 4) + hb));
 
     const int nk = (int)(k_len / dm::BK);  // a multiple of NST (checked on the host)
     const int nr = nk / 2;                 // A slots' worth of K
@@ -653,8 +721,10 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int b = 4 * gw + i;
-            if constexpr (B_NZ)  // n-block b of the column block, K block k0/64: one contiguous 1 KB block
-                dma16(rsB, sbase + st * B_ST + b * 1024, ((uint32_t)b * kblocks + (k0 >> 6)) * 1024u + 16u * lane, 0u);
+            if constexpr (B_NZ) {  // n-block b of the column block, K block k0/64: one contiguous 1 KB block
+                const uint32_t nb = SWI ? (uint32_t)(b < 8 ? n0 / 16 + b : n_up / 16 + (b - 8)) : (uint32_t)b;
+                dma16(rsB, sbase + st * B_ST + b * 1024, (nb * kblocks + (k0 >> 6)) * 1024u + 16u * lane, 0u);
+            }
             else if constexpr (B_KN)
                 dma16(rsB, sbase + st * B_ST + b * 1024, (i & 1) ? vkn1 : vkn0, (k0 + 4u * b) * ldb);
             else
@@ -808,6 +878,10 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < 8; ++j) __builtin_nontemporal_store(acc[i][j], dst + (i * 8 + j) * 64);
+    } else if constexpr (SWI) {
+        EpiOps<TM> ops;
+        load_epi_ops<TM, true>(p, ops, m0, n0, wm, wn, lane, n_up);
+        swiglu_epilogue<ODT, TM, NT>(p, acc, ops, smem, m0, n0, wm, wn, lane, tid);
     } else {
         EpiOps<TM> ops;
         if (nsplit == 1) load_epi_ops<TM>(p, ops, m0, n0, wm, wn, lane);
@@ -2046,6 +2120,32 @@ hipError_t launch_quant_matmul_nz(const QmmArgs& p, void* workspace, size_t ws_b
     q.sbk = p.N;
     q.sbn = 1;
     return launch_quant_matmul(q, rest ? ws + nd : nullptr, rest, stream);
+}
+
+hipError_t launch_quant_matmul_swiglu(const QmmArgs& p, bool nz, hipStream_t stream) {
+    const int64_t I = p.N / 2;
+    const QmmEpilogue& e = p.epi;
+    const bool ok =
+        p.M > 0 && I > 0 && p.N == 2 * I && I % 128 == 0 && p.K > 0 && p.K % (dm::BK * dm::NST) == 0 &&
+        p.lda % 16 == 0 && p.lda < (1 << 24) && (uintptr_t)p.a % 16 == 0 && (uintptr_t)p.b % 16 == 0 &&
+        (uintptr_t)e.out % 16 == 0 && e.ldo % 8 == 0 && e.bias_dtype == 0 && e.offset == nullptr && e.scale &&
+        (e.out_dtype == QK_BF16 || e.out_dtype == QK_F16) &&
+        (nz ? (uint64_t)p.N * (uint64_t)p.K < (1ull << 32)
+            : (p.sbn == 1 && p.sbk % 16 == 0 && p.sbk >= p.N && p.sbk < (1 << 24) &&
+               (uint64_t)(p.K - 1) * (uint64_t)p.sbk + (uint64_t)I + 128 < (1ull << 32)));
+    const int64_t tiles_m = (p.M + dm::BM - 1) / dm::BM, tiles_n = I / 128;
+    if (!ok || tiles_m * tiles_n >= ((int64_t)1 << 30)) return hipErrorInvalidValue;
+    const dim3 grid((uint32_t)(tiles_m * tiles_n)), block(dm::NT);
+    const int tm = (int)tiles_m, tn = (int)tiles_n;
+    constexpr int S = kOutSwiGLU;
+    if (nz) {
+        if (e.out_dtype == QK_BF16) qmm_dma<kLayNZ, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, nullptr);
+        else qmm_dma<kLayNZ, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, nullptr);
+    } else {
+        if (e.out_dtype == QK_BF16) qmm_dma<kLayKN, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, nullptr);
+        else qmm_dma<kLayKN, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, nullptr);
+    }
+    return hipGetLastError();
 }
 
 }  // namespace qk

@@ -873,6 +873,74 @@ std::tuple<at::Tensor, at::Tensor> npu_swiglu_dynamic_quant_meta(const at::Tenso
             at::empty(self.sizes().slice(0, self.dim() - 1), self.options().dtype(at::kFloat))};
 }
 
+// ---------------------------------------------------------------- fused gate-up + SwiGLU (quantized MLP block)
+// h = npu_swiglu(npu_quant_matmul(x1, x2, scale, pertoken_scale=..., output_dtype=...)) with x2 [K, 2I] (row-major
+// or the int8 NZ weight) in one GEMM whose epilogue applies the SwiGLU: bit-identical to that chain, which it
+// runs instead where the fused kernel does not take the shape (qk_quant_matmul_swiglu: QK_ERR_UNSUPPORTED).
+std::vector<int64_t> swiglu_matmul_check(const at::Tensor& x1, const at::Tensor& x2, const at::Tensor& scale,
+                                         const std::optional<at::Tensor>& pertoken_scale, at::ScalarType out_type,
+                                         int64_t& K, int64_t& I) {
+    const char* op = "npu_quant_matmul_swiglu";
+    TORCH_CHECK(x1.scalar_type() == at::kChar && x2.scalar_type() == at::kChar, op, ": x1 and x2 must be int8");
+    TORCH_CHECK(x1.dim() >= 2, op, ": x1 must have at least 2 dimensions");
+    const bool nz = is_w8_nz(x2);
+    TORCH_CHECK(nz || x2.dim() == 2, op, ": x2 must be [K, 2I] or an int8 NZ weight, got ", x2.sizes());
+    K = x1.size(-1);
+    const int64_t x2_k = nz ? x2.size(1) * 64 : x2.size(0);
+    TORCH_CHECK(x2_k == K, op, ": x1 last dim (", K, ") must equal the weight's K (", x2_k, ")");
+    const int64_t N = nz ? x2.size(0) * 16 : x2.size(1);
+    TORCH_CHECK(N % 2 == 0, op, ": the weight's column count (", N, ") must be even (gate and up halves)");
+    I = N / 2;
+    TORCH_CHECK(out_type == at::kBFloat16 || out_type == at::kHalf, op, ": output_dtype must be bfloat16 or float16");
+    TORCH_CHECK(scale.dim() == 1 && (scale.size(0) == 1 || scale.size(0) == N), op, ": scale must be [1] or [", N, "]");
+    TORCH_CHECK(scale.scalar_type() == at::kFloat || scale.scalar_type() == at::kBFloat16, op,
+                ": scale must be float32 or bfloat16");
+    if (pertoken_scale.has_value())
+        TORCH_CHECK(pertoken_scale->scalar_type() == at::kFloat && pertoken_scale->numel() == leading_rows(x1), op,
+                    ": pertoken_scale must be float32 with one element per row of x1");
+    std::vector<int64_t> shape(x1.sizes().begin(), x1.sizes().end());
+    shape.back() = I;
+    return shape;
+}
+
+at::Tensor npu_quant_matmul_swiglu(const at::Tensor& x1_in, const at::Tensor& x2_in, const at::Tensor& scale_in,
+                                   const std::optional<at::Tensor>& pertoken_scale,
+                                   std::optional<at::ScalarType> output_dtype) {
+    const at::ScalarType out_type = output_dtype.value_or(at::kBFloat16);
+    int64_t K = 0, I = 0;
+    const auto shape = swiglu_matmul_check(x1_in, x2_in, scale_in, pertoken_scale, out_type, K, I);
+    const c10::DeviceGuard guard(x1_in.device());
+    auto out = at::empty(shape, x1_in.options().dtype(out_type));
+    if (out.numel() == 0) return out;
+    const bool nz = is_w8_nz(x2_in);
+    auto x1 = x1_in.contiguous();
+    const bool kn = !nz && x2_in.stride(1) == 1 && x2_in.stride(0) >= 2 * I;
+    if (nz || kn) {
+        auto scale = scale_in.scalar_type() == at::kFloat ? scale_in.contiguous() : scale_in.to(at::kFloat);
+        at::Tensor pt;
+        if (pertoken_scale.has_value()) pt = pertoken_scale->contiguous();
+        const int rc = qk_quant_matmul_swiglu(
+            x1.data_ptr<int8_t>(), K, x2_in.data_ptr<int8_t>(), nz ? QK_FORMAT_FRACTAL_NZ : QK_FORMAT_ND,
+            nz ? 0 : x2_in.stride(0), leading_rows(x1), I, K, scale.data_ptr<float>(), scale.numel(),
+            pt.defined() ? pt.data_ptr<float>() : nullptr, out.data_ptr(), qk_dtype_of(out_type), current_stream(x1));
+        if (rc != QK_ERR_UNSUPPORTED) {
+            check_rc(rc, "npu_quant_matmul_swiglu");
+            return out;
+        }
+    }
+    // the shapes and layouts the fused kernel does not take: the unfused chain
+    auto h2 = npu_quant_matmul(x1_in, x2_in, scale_in, std::nullopt, pertoken_scale, std::nullopt, out_type);
+    return npu_swiglu(h2, -1);
+}
+
+at::Tensor npu_quant_matmul_swiglu_meta(const at::Tensor& x1, const at::Tensor& x2, const at::Tensor& scale,
+                                        const std::optional<at::Tensor>& pertoken_scale,
+                                        std::optional<at::ScalarType> output_dtype) {
+    const at::ScalarType out_type = output_dtype.value_or(at::kBFloat16);
+    int64_t K = 0, I = 0;
+    return at::empty(swiglu_matmul_check(x1, x2, scale, pertoken_scale, out_type, K, I), x1.options().dtype(out_type));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(npu, m) {
@@ -898,6 +966,8 @@ TORCH_LIBRARY(npu, m) {
     // fusions of this build for the quantized MLP block (no reference op): (q, scale, rstd) and (q, scale)
     m.def("npu_rms_norm_dynamic_quant(Tensor self, Tensor gamma, float epsilon=1e-06) -> (Tensor, Tensor, Tensor)");
     m.def("npu_swiglu_dynamic_quant(Tensor self, int dim=-1) -> (Tensor, Tensor)");
+    m.def("npu_quant_matmul_swiglu(Tensor x1, Tensor x2, Tensor scale, *, Tensor? pertoken_scale=None, "
+          "ScalarType? output_dtype=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(npu, CUDA, m) {
@@ -913,6 +983,7 @@ TORCH_LIBRARY_IMPL(npu, CUDA, m) {
     m.impl("npu_swiglu", &npu_swiglu);
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant);
     m.impl("npu_swiglu_dynamic_quant", &npu_swiglu_dynamic_quant);
+    m.impl("npu_quant_matmul_swiglu", &npu_quant_matmul_swiglu);
 }
 
 TORCH_LIBRARY_IMPL(npu, CompositeExplicitAutograd, m) { m.impl("get_npu_format", &get_npu_format); }
@@ -930,4 +1001,5 @@ TORCH_LIBRARY_IMPL(npu, Meta, m) {
     m.impl("npu_swiglu", &npu_swiglu_meta);
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant_meta);
     m.impl("npu_swiglu_dynamic_quant", &npu_swiglu_dynamic_quant_meta);
+    m.impl("npu_quant_matmul_swiglu", &npu_quant_matmul_swiglu_meta);
 }

@@ -212,7 +212,7 @@ extern "C" {
 
 const char* qk_last_error(void) { return g_last_error.c_str(); }
 
-int qk_abi_version(void) { return 5; }
+int qk_abi_version(void) { return 6; }
 
 int qk_debug_set_plan(const char* spec) {
     g_last_error.clear();
@@ -301,6 +301,36 @@ int qk_quant_matmul_nz(const int8_t* x1, int64_t ldx1, const int8_t* x2_nz, int6
     p.sbk = 0;
     p.sbn = 0;
     return launched(qk::launch_quant_matmul_nz(p, workspace, workspace_bytes, (hipStream_t)stream), op);
+}
+
+int qk_quant_matmul_swiglu(const int8_t* x1, int64_t ldx1, const int8_t* x2, int x2_format, int64_t x2_stride_k,
+                           int64_t M, int64_t I, int64_t K, const float* scale, int64_t scale_len,
+                           const float* pertoken_scale, void* out, int out_dtype, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_quant_matmul_swiglu";
+    if (I < 0 || I > ((int64_t)1 << 40)) return fail(QK_ERR_ARG, "%s: bad I=%lld", op, (long long)I);
+    if (!is_half(out_dtype)) return fail(QK_ERR_ARG, "%s: the output must be float16 or bfloat16 (got %d)", op, out_dtype);
+    if (x2_format != QK_FORMAT_ND && x2_format != QK_FORMAT_FRACTAL_NZ)
+        return fail(QK_ERR_ARG, "%s: x2_format must be QK_FORMAT_ND or QK_FORMAT_FRACTAL_NZ (got %d)", op, x2_format);
+    qk::QmmArgs p;
+    int rc = quant_matmul_args(op, M, 2 * I, K, scale, scale_len, nullptr, 0, pertoken_scale, nullptr, 0, out,
+                               out_dtype, p);
+    if (rc != QK_OK || M == 0 || I == 0) return rc;
+    if (K > 0 && (!x1 || !x2)) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    if (ldx1 < K) return fail(QK_ERR_ARG, "%s: ldx1=%lld < K=%lld", op, (long long)ldx1, (long long)K);
+    if (x2_format == QK_FORMAT_ND && x2_stride_k < 2 * I)
+        return fail(QK_ERR_ARG, "%s: x2_stride_k=%lld < 2I=%lld", op, (long long)x2_stride_k, (long long)(2 * I));
+    p.a = x1;
+    p.lda = ldx1;
+    p.b = x2;
+    p.sbk = x2_format == QK_FORMAT_ND ? x2_stride_k : 0;
+    p.sbn = x2_format == QK_FORMAT_ND ? 1 : 0;
+    p.epi.ldo = I;
+    const hipError_t e = qk::launch_quant_matmul_swiglu(p, x2_format == QK_FORMAT_FRACTAL_NZ, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue)
+        return fail(QK_ERR_UNSUPPORTED, "%s: the fused kernel does not take M=%lld I=%lld K=%lld with these operands "
+                    "(I %% 128, K %% 256, 16-byte aligned rows and pointers)", op, (long long)M, (long long)I, (long long)K);
+    return launched(e, op);
 }
 
 int qk_weight_quant_bmm_workspace_size(int64_t M, int64_t N, int64_t K, int weight_dtype, int64_t group_size,

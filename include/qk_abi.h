@@ -97,7 +97,7 @@ const char* qk_last_error(void);
  * (2: the split-K counters at the head of a workspace; 3: the counters are
  * tagged per call, so a workspace needs no initialisation; 4: NZ weights,
  * qk_weight_format_cast, static quantization; 5: the [N, K] int8 weight code
- * QK_I8_NK, int8 NZ weights with K % 64 == 0 in qk_weight_quant_bmm). */
+ * QK_I8_NK, int8 NZ weights with K % 64 == 0 in qk_weight_quant_bmm; 6: qk_quant_matmul_swiglu). */
 int qk_abi_version(void);
 
 /* Debug and test hook, no counterpart in the reference: forces kernel choices
@@ -346,6 +346,26 @@ int qk_swiglu(const void* h, int dtype, int64_t rows, int64_t I, void* y, qk_str
  */
 int qk_swiglu_quant(const void* h, int dtype, int64_t rows, int64_t I, int8_t* q, float* scale,
                     qk_stream_t stream);
+
+/*
+ * The quantized MLP block's gate-up projection with the SwiGLU fused into the
+ * GEMM's epilogue.  No single reference op: the unfused chain is
+ * qk_quant_matmul (x1 [M,K] int8 x x2 [K,2I] int8, per-channel or per-tensor
+ * scale of 2I or 1 elements, optional pertoken_scale [M], no bias, 16-bit
+ * output) then qk_swiglu, and h [M, I] (out_dtype QK_BF16 or QK_F16, rows of
+ * I elements) is bit-identical to it: the gate and up outputs are rounded to
+ * out_dtype as the GEMM rounds them, and silu(gate) * up as qk_swiglu rounds
+ * it.  Quantizing h with qk_dynamic_quant gives qk_swiglu_quant's q and scale.
+ * x2: x2_format QK_FORMAT_FRACTAL_NZ (the NZ blocks npu_format_cast writes) or
+ * QK_FORMAT_ND ([K, 2I] rows of x2_stride_k >= 2I bytes).  Runs where
+ * I % 128 == 0, K % 256 == 0, ldx1 % 16 == 0 (< 2^24), x1 / x2 / out 16-byte
+ * aligned and every offset fits 32 bits; other requests return
+ * QK_ERR_UNSUPPORTED (the caller composes the two calls instead).  No
+ * workspace.
+ */
+int qk_quant_matmul_swiglu(const int8_t* x1, int64_t ldx1, const int8_t* x2, int x2_format, int64_t x2_stride_k,
+                           int64_t M, int64_t I, int64_t K, const float* scale, int64_t scale_len,
+                           const float* pertoken_scale, void* out, int out_dtype, qk_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -249,8 +249,12 @@ def test_quant_mlp_block_cfg5(ops, oracle, nz):
     sw = ops.npu_swiglu(h)
     q2, s2 = ops.npu_swiglu_dynamic_quant(h)
     o = ops.npu_quant_matmul(q2, w_d, dev["s_d"], pertoken_scale=s2, output_dtype=torch.bfloat16)
+    hf = ops.npu_quant_matmul_swiglu(q1, w_gu, dev["s_gu"], pertoken_scale=s1)  # the block's fused gate-up
+    q2f, s2f = ops.npu_dynamic_quant(hf)
     torch.cuda.synchronize()
     assert torch.equal(o, out)
+    assert torch.equal(hf.view(torch.int16), sw.view(torch.int16))
+    assert torch.equal(q2f, q2) and torch.equal(s2f, s2)
     pin = np.r_[0, T - 1]
     # RMSNorm (one ulp) and its quantization (bit-exact on the GPU's y)
     y_ref, _ = oracle.rms_norm(W.bits(d["x"]), BF16, W.bits(d["gamma"]), c["eps"])
@@ -286,3 +290,49 @@ def test_quant_mlp_block_cfg5(ops, oracle, nz):
     rows = torch.as_tensor(np.flatnonzero(same))
     torch.testing.assert_close(out.cpu().float()[rows], W.from_bits(iref, torch.bfloat16).float()[rows],
                                rtol=1e-2, atol=1e-2)
+
+
+SWIGLU_MM_CASES = [
+    # M, I, K, weight layout, output dtype, per-tensor scale, per-token scale
+    (300, 2048, 1024, "kn", torch.float16, True, False),   # ragged M: the last 256-row tile holds 44 rows
+    (300, 2048, 1024, "nz", torch.bfloat16, False, True),
+    (100, 256, 512, "nz", torch.float16, False, True),     # one row tile, partly filled
+    (513, 1024, 256, "kn", torch.bfloat16, False, True),   # one K ring, three row tiles
+    (64, 96, 256, "kn", torch.bfloat16, False, True),      # I % 128 != 0: the unfused chain
+    (64, 256, 256, "nk", torch.bfloat16, False, True),     # a transposed [2I, K] weight view: the unfused chain
+]
+
+
+@pytest.mark.parametrize("M,I,K,layout,out_dtype,per_tensor,pertoken", SWIGLU_MM_CASES)
+def test_quant_matmul_swiglu(ops, M, I, K, layout, out_dtype, per_tensor, pertoken):
+    """npu_quant_matmul_swiglu (the gate-up GEMM with the SwiGLU in its epilogue) equals
+    npu_swiglu(npu_quant_matmul(...)) bit for bit; through the C ABI the fused kernel takes the shapes it
+    supports and refuses the others with QK_ERR_UNSUPPORTED, for which the op runs the unfused chain."""
+    say(f"quant_matmul_swiglu M={M} I={I} K={K} {layout} {out_dtype} per_tensor={per_tensor} pertoken={pertoken}")
+    g = torch.Generator().manual_seed(M + I + K)
+    x1 = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8).to(DEV)
+    w = torch.randint(-128, 128, (K, 2 * I), generator=g, dtype=torch.int8).to(DEV)
+    s = (1e-4 + 1e-3 * torch.rand(1 if per_tensor else 2 * I, generator=g)).to(DEV)
+    pt = (1e-2 * torch.rand(M, generator=g)).to(DEV) if pertoken else None
+    wd = {"kn": w, "nz": ops.npu_format_cast(w, 29) if layout == "nz" else None,
+          "nk": w.t().contiguous().t()}[layout]
+    h = ops.npu_quant_matmul_swiglu(x1, wd, s, pertoken_scale=pt, output_dtype=out_dtype)
+    ref = ops.npu_swiglu(ops.npu_quant_matmul(x1, wd, s, pertoken_scale=pt, output_dtype=out_dtype))
+    torch.cuda.synchronize()
+    assert h.shape == (M, I) and h.dtype == out_dtype
+    assert torch.equal(h.view(torch.int16), ref.view(torch.int16))
+    if layout == "nk":
+        return
+    L = ops.abi()
+    out = torch.empty((M, I), dtype=out_dtype, device=DEV)
+    rc = L.qk_quant_matmul_swiglu(x1.data_ptr(), K, wd.data_ptr(), 29 if layout == "nz" else 2,
+                                  0 if layout == "nz" else 2 * I, M, I, K, s.data_ptr(), s.numel(),
+                                  None if pt is None else pt.data_ptr(), out.data_ptr(),
+                                  BF16 if out_dtype == torch.bfloat16 else F16,
+                                  torch.cuda.current_stream().cuda_stream)
+    if I % 128 != 0:
+        assert rc == ops.QK_ERR_UNSUPPORTED and "does not take" in ops.last_error()
+        return
+    assert rc == 0, ops.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))

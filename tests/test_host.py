@@ -28,7 +28,7 @@ def test_abi_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), f"{n} declared in qk_abi.h but not exported"
     assert set(names) == set(q.ABI_SYMBOLS)
-    assert q.abi().qk_abi_version() == 5
+    assert q.abi().qk_abi_version() == 6
 
 
 def test_debug_plan_override_parsing():
@@ -144,7 +144,7 @@ def test_schemas_registered():
     for name in ("npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
                  "npu_convert_weight_to_int4pack", "npu_format_cast", "quantize_per_tensor", "quantize_per_channel",
                  "dequantize", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
-                 "npu_swiglu_dynamic_quant"):
+                 "npu_swiglu_dynamic_quant", "npu_quant_matmul_swiglu"):
         assert hasattr(torch.ops.npu, name)
     s = str(torch.ops.npu.npu_quant_matmul.default._schema)
     assert "pertoken_scale" in s and "ScalarType? output_dtype" in s
@@ -195,6 +195,13 @@ def test_meta_shapes():
     assert q.npu_swiglu(_m((512, 28672), torch.bfloat16)).shape == (512, 14336)
     qq, sc = q.npu_swiglu_dynamic_quant(_m((2, 5, 64), torch.float16), dim=2)
     assert qq.shape == (2, 5, 32) and qq.dtype == torch.int8 and sc.shape == (2, 5)
+    h = q.npu_quant_matmul_swiglu(_m((2, 256, 4096), torch.int8), _m((4096, 28672), torch.int8),
+                                  _m((28672,), torch.float32), pertoken_scale=_m((512,), torch.float32))
+    assert h.shape == (2, 256, 14336) and h.dtype == torch.bfloat16
+    w8gu = q.npu_format_cast(_m((4096, 28672), torch.int8), 29)
+    h = q.npu_quant_matmul_swiglu(_m((512, 4096), torch.int8), w8gu, _m((1,), torch.float32),
+                                  output_dtype=torch.float16)
+    assert h.shape == (512, 14336) and h.dtype == torch.float16
 
 
 def test_storage_format_is_recorded_not_inferred():
@@ -237,6 +244,12 @@ def test_meta_batched_weights():
 
 @pytest.mark.parametrize("call,msg", [
     (lambda: q.npu_dynamic_quant(_m((4, 8), torch.float32)), "float16 or bfloat16"),
+    (lambda: q.npu_quant_matmul_swiglu(_m((4, 64), torch.int8), _m((64, 9), torch.int8), _m((9,), torch.float32)),
+     "even"),
+    (lambda: q.npu_quant_matmul_swiglu(_m((4, 64), torch.int8), _m((32, 8), torch.int8), _m((8,), torch.float32)),
+     "must equal"),
+    (lambda: q.npu_quant_matmul_swiglu(_m((4, 64), torch.int8), _m((64, 8), torch.int8), _m((8,), torch.float32),
+                                       output_dtype=torch.float32), "bfloat16 or float16"),
     (lambda: q.npu_dynamic_quant(_m((4, 8), torch.float16), smooth_scales=_m((7,), torch.float32)), "smooth_scales"),
     (lambda: q.npu_quant_matmul(_m((4, 64), torch.int8), _m((32, 8), torch.int8), _m((8,), torch.float32)),
      "must equal"),
