@@ -88,6 +88,25 @@ __device__ __forceinline__ float silu_mul(float a, float b) {
     return (a * __builtin_amdgcn_rcpf(1.0f + e)) * b;
 }
 
+// Largest value over each row of 16 lanes, at every lane of the row: DPP row rotations by 8, 4, 2 and 1 lanes
+// (row_ror, dpp_ctrl 0x120 + n), one VALU max each, no LDS round trip.  Every lane of the row must be active.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xf, 0xf, false)));
+    return v;
+}
+// Largest value over the wave (all 64 lanes active), uniform: row16_max, then the four rows' lanes 0, 16, 32, 48.
+__device__ __forceinline__ float wave_max(float v) {
+    v = row16_max(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
 __device__ __forceinline__ float load_half_bits(uint32_t bits, int dtype) {
     return dtype == QK_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
 }
@@ -369,6 +388,11 @@ bool set_plan_override(const char* spec);  // false: spec not understood (overri
 // Host-side entry points of each kernel file (validated arguments only).
 hipError_t launch_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t K,
                                 const float* smooth, int8_t* y, float* scale, hipStream_t stream);
+// npu_dynamic_quant of x [rows, K] (16-byte aligned rows, K % 8 == 0) whose row absmax is the largest of
+// amax_part[row * parts + j], j < parts (partial absmax of column slices of the row, written by the kernel that
+// produced x): the same y and scale as launch_dynamic_quant, in one elementwise pass with no row reduction.
+hipError_t launch_dynamic_quant_premax(const void* x, int x_dtype, int64_t rows, int64_t K, const float* amax_part,
+                                       int parts, int8_t* y, float* scale, hipStream_t stream);
 
 struct QmmArgs {
     const int8_t* a;
@@ -384,9 +408,10 @@ size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K);
 hipError_t launch_quant_matmul_nz(const QmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t quant_matmul_nz_workspace(int64_t M, int64_t N, int64_t K);
 // The quantized MLP block's gate-up GEMM with SwiGLU fused: args.N = 2I weight columns (gate, then up), the
-// output h [M, I] (bf16 / fp16, args.epi.ldo = I); the weight as NZ blocks (nz) or [K, 2I] rows.
+// output h [M, I] (bf16 / fp16, args.epi.ldo = I); the weight as NZ blocks (nz) or [K, 2I] rows.  amax_part (or
+// null): fp32 [M][I / 128], each 128-column slice's largest |h| per row.
 // hipErrorInvalidValue where the shape or operands do not fit the kernel.
-hipError_t launch_quant_matmul_swiglu(const QmmArgs& args, bool nz, hipStream_t stream);
+hipError_t launch_quant_matmul_swiglu(const QmmArgs& args, bool nz, float* amax_part, hipStream_t stream);
 
 struct WqbmmArgs {
     const void* x;

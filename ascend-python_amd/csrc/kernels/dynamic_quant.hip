@@ -125,6 +125,46 @@ __global__ __launch_bounds__(kThreads) void dyn_quant_generic(const uint16_t* __
     }
 }
 
+// The quantizer for a row whose absmax arrives as `parts` partial maxima (amax_part[row * parts + j], each the
+// largest |x| of one column slice, taken with fmaxf from +0 as above): each wave takes the largest of the
+// row's partials itself (one or two loads per lane and a DPP / readlane reduction: no LDS, no barrier) and
+// quantizes its vectors.  The same s and y as dyn_quant_vec, whose absmax is the same maximum.  Workgroup
+// bid: row bid / chunks, vectors (bid % chunks) * 256 * VPT + ...; the workgroup of chunk 0 stores the scale.
+template <int DT, int VPT>
+__global__ __launch_bounds__(kThreads) void dyn_quant_premax(const uint16_t* __restrict__ x, int64_t K, int chunks,
+                                                             const float* __restrict__ amax_part, int parts,
+                                                             int8_t* __restrict__ y, float* __restrict__ scale) {
+    const int64_t row = blockIdx.x / chunks;
+    const int chunk = blockIdx.x % chunks;
+    const int nv = (int)(K >> 3);
+    const int base = chunk * (kThreads * VPT) + threadIdx.x;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * K);
+    u32x4 raw[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+        if (base + i * kThreads < nv) raw[i] = __builtin_nontemporal_load(xr + base + i * kThreads);  // read once
+    const int lane = threadIdx.x & 63;
+    float amax = 0.0f;
+    for (int j = lane; j < parts; j += 64) amax = fmaxf(amax, amax_part[row * parts + j]);
+    const float s = wave_max(amax) / 127.0f;
+    if (chunk == 0 && threadIdx.x == 0) scale[row] = s;
+    const RowQuant rq = row_quant(s);
+    u32x2* yr = reinterpret_cast<u32x2*>(y + row * K);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = base + i * kThreads;
+        if (idx < nv) {
+            float vf[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t d = raw[i][e >> 1];
+                vf[e] = load_half_bits((e & 1) ? (d >> 16) : (d & 0xffffu), DT);
+            }
+            __builtin_nontemporal_store(quant8(vf, rq), yr + idx);  // written once
+        }
+    }
+}
+
 template <int DT, int VPT, int RPW>
 hipError_t launch_rows(const uint16_t* x, int64_t rows, int64_t K, const float* smooth, int8_t* y, float* scale,
                        hipStream_t stream) {
@@ -162,7 +202,33 @@ hipError_t dispatch(const uint16_t* x, int64_t rows, int64_t K, const float* smo
     return hipGetLastError();
 }
 
+template <int DT>
+hipError_t dispatch_premax(const uint16_t* x, int64_t rows, int64_t K, const float* amax_part, int parts, int8_t* y,
+                           float* scale, hipStream_t stream) {
+    const int64_t nv = K / 8;
+    const int vpt = nv % (2 * kThreads) == 0 ? 2 : 1;  // whole chunks of two vectors per thread where they fit
+    const int64_t chunks = (nv + (int64_t)kThreads * vpt - 1) / ((int64_t)kThreads * vpt);
+    if (chunks * rows >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    const dim3 grid((uint32_t)(chunks * rows)), block(kThreads);
+    if (vpt == 2)
+        dyn_quant_premax<DT, 2><<<grid, block, 0, stream>>>(x, K, (int)chunks, amax_part, parts, y, scale);
+    else
+        dyn_quant_premax<DT, 1><<<grid, block, 0, stream>>>(x, K, (int)chunks, amax_part, parts, y, scale);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_dynamic_quant_premax(const void* x, int x_dtype, int64_t rows, int64_t K, const float* amax_part,
+                                       int parts, int8_t* y, float* scale, hipStream_t stream) {
+    if (rows == 0) return hipSuccess;
+    if (K <= 0 || K % 8 != 0 || K >= ((int64_t)1 << 31) || parts <= 0 || (uintptr_t)x % 16 != 0 ||
+        (uintptr_t)y % 8 != 0 || !amax_part)
+        return hipErrorInvalidValue;
+    const uint16_t* xh = static_cast<const uint16_t*>(x);
+    if (x_dtype == QK_BF16) return dispatch_premax<QK_BF16>(xh, rows, K, amax_part, parts, y, scale, stream);
+    return dispatch_premax<QK_F16>(xh, rows, K, amax_part, parts, y, scale, stream);
+}
 
 hipError_t launch_dynamic_quant(const void* x, int x_dtype, int64_t rows, int64_t K, const float* smooth,
                                 int8_t* y, float* scale, hipStream_t stream) {

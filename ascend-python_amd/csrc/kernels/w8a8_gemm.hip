@@ -351,9 +351,10 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
         }
         __syncthreads();
         constexpr int CPRO = 2 * BN / 16;  // 16-byte chunks per output row
-        static_assert(BM * CPRO % NT == 0, "whole chunks per thread");
+        constexpr int TR = 4 * WMR;        // tile rows (four wave rows)
+        static_assert(TR * CPRO % NT == 0, "whole chunks per thread");
 #pragma unroll
-        for (int it = 0; it < BM * CPRO / NT; ++it) {
+        for (int it = 0; it < TR * CPRO / NT; ++it) {
             const int q = tid + it * NT;
             const int row = q / CPRO, c = q % CPRO;
             if (m0 + row >= p.M) break;  // rows past a ragged M (q grows with the row)
@@ -387,11 +388,14 @@ __device__ __forceinline__ void big_epilogue(const QmmArgs& p, const i32x4 (&acc
 // 128 outputs): each half is rounded to the output type exactly as big_epilogue rounds it and staged through
 // LDS; then each thread takes 8 outputs of one row (16 bytes of gate, 16 of up) and stores
 // h = silu(gate) * up rounded to the same type -- the values the SwiGLU kernel computes from the gate-up
-// output in HBM.  h has ldo = N / 2 columns; rows past M are not stored.
+// output in HBM.  h has ldo = N / 2 columns; rows past M are not stored.  With amax (not null) the tile also
+// stores, per row, the largest |h| of its 128 outputs (fmaxf from +0, so NaN outputs are passed over, as the
+// dynamic quantizer's absmax passes them over) at amax[row * (I / 128) + tn]: the column tiles' partial absmax,
+// from which the row scale of npu_dynamic_quant(h) follows without a reduction over h.
 template <int ODT, int TM, int NT>
 __device__ __forceinline__ void swiglu_epilogue(const QmmArgs& p, const i32x4 (&acc)[TM][8], const EpiOps<TM>& ops,
                                                 int8_t* smem, int64_t m0, int64_t n0, int wm, int wn, int lane,
-                                                int tid) {
+                                                int tid, float* __restrict__ amax, int tn) {
     using namespace big;
     constexpr int WMR = 16 * TM;
     constexpr int ROWB = 2 * BN + 16;  // padded LDS row (bytes): gate columns, then up columns
@@ -414,24 +418,31 @@ __device__ __forceinline__ void swiglu_epilogue(const QmmArgs& p, const i32x4 (&
         }
     }
     __syncthreads();
-    constexpr int CH = BN / 16;  // 16-byte chunks of an h row (128 outputs)
-    static_assert(BM * CH % NT == 0, "whole chunks per thread");
+    constexpr int CH = BN / 16;  // 16-byte chunks of an h row (128 outputs): lanes 16k .. 16k+15 hold one row
+    static_assert(BM * CH % NT == 0 && NT % CH == 0 && CH == 16, "whole rows per 16-lane group");
 #pragma unroll
     for (int it = 0; it < BM * CH / NT; ++it) {
         const int q = tid + it * NT;
         const int row = q / CH, c = q % CH;
-        if (m0 + row >= p.M) break;  // rows past a ragged M (q grows with the row)
+        const bool in = m0 + row < p.M;  // rows past a ragged M are computed, not stored
         const u32x4 gv = *reinterpret_cast<const u32x4*>(smem + row * ROWB + 16 * c);
         const u32x4 uv = *reinterpret_cast<const u32x4*>(smem + row * ROWB + BN + 16 * c);
         u32x4 hv;
+        float mx = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const uint32_t lo = to16(silu_mul(load_half_bits(gv[w] & 0xffffu, ODT), load_half_bits(uv[w] & 0xffffu, ODT)));
             const uint32_t hi = to16(silu_mul(load_half_bits(gv[w] >> 16, ODT), load_half_bits(uv[w] >> 16, ODT)));
             hv[w] = lo | (hi << 16);
+            mx = fmaxf(mx, fmaxf(load_half_bits(lo & 0x7fffu, ODT), load_half_bits(hi & 0x7fffu, ODT)));
         }
-        __builtin_nontemporal_store(hv, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo +
-                                                                 n0 + 8 * c));  // written once
+        if (in)
+            __builtin_nontemporal_store(hv, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(e.out) + (m0 + row) * e.ldo +
+                                                                     n0 + 8 * c));  // written once
+        if (amax) {  // the row's 16 lanes (a DPP row; every lane active here): max over the 128 outputs
+            mx = row16_max(mx);
+            if (in && c == 0) amax[(m0 + row) * (p.N / BN) + tn] = mx;
+        }
     }
 }
 
@@ -643,6 +654,7 @@ constexpr int SMEM = RING > OUT_BYTES ? RING : OUT_BYTES;
 // OUT = kOutSwiGLU + QK_BF16 / QK_F16: the gate-up GEMM with SwiGLU fused (swiglu_epilogue).  The weight has
 // N = 2I columns, gate then up; tile tn covers outputs 128 tn .. +127, its B columns the gate columns
 // 128 tn .. and the up columns I + 128 tn .. (NZ blocks or [K,N] column chunks addressed apart); no split.
+// There `partial`, when not null, receives the tiles' per-row partial absmax of h (fp32 [M][I / 128]).
 template <int BL, int OUT, int BMX = 256>
 __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int tiles_n, int nsplit,
                                                   int32_t* __restrict__ partial) {
@@ -881,7 +893,8 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     } else if constexpr (SWI) {
         EpiOps<TM> ops;
         load_epi_ops<TM, true>(p, ops, m0, n0, wm, wn, lane, n_up);
-        swiglu_epilogue<ODT, TM, NT>(p, acc, ops, smem, m0, n0, wm, wn, lane, tid);
+        swiglu_epilogue<ODT, TM, NT>(p, acc, ops, smem, m0, n0, wm, wn, lane, tid, reinterpret_cast<float*>(partial),
+                                     tn);
     } else {
         EpiOps<TM> ops;
         if (nsplit == 1) load_epi_ops<TM>(p, ops, m0, n0, wm, wn, lane);
@@ -1722,8 +1735,8 @@ size_t big_split_workspace(const BigPlan& b, int64_t M, int64_t N) {
 
 template <int BL>
 hipError_t launch_split128(const QmmArgs& p, const BigPlan& b, int32_t* partial, hipStream_t stream) {
-    qmm_dma<BL, QK_I32, 128><<<dim3((uint32_t)(b.tiles_m * b.tiles_n * b.nsplit)), dim3(dm::NT), 0, stream>>>(
-        p, b.tiles_m, b.tiles_n, b.nsplit, partial);
+    const dim3 sgrid((uint32_t)((int64_t)b.tiles_m * b.tiles_n * b.nsplit)), sblock(dm::NT);
+    qmm_dma<BL, QK_I32, 128><<<sgrid, sblock, 0, stream>>>(p, b.tiles_m, b.tiles_n, b.nsplit, partial);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     int64_t blocks = ((int64_t)b.tiles_m * b.tiles_n * 8 * 16 * 64 + kThreads - 1) / kThreads;
@@ -2122,7 +2135,7 @@ hipError_t launch_quant_matmul_nz(const QmmArgs& p, void* workspace, size_t ws_b
     return launch_quant_matmul(q, rest ? ws + nd : nullptr, rest, stream);
 }
 
-hipError_t launch_quant_matmul_swiglu(const QmmArgs& p, bool nz, hipStream_t stream) {
+hipError_t launch_quant_matmul_swiglu(const QmmArgs& p, bool nz, float* amax_part, hipStream_t stream) {
     const int64_t I = p.N / 2;
     const QmmEpilogue& e = p.epi;
     const bool ok =
@@ -2138,12 +2151,13 @@ hipError_t launch_quant_matmul_swiglu(const QmmArgs& p, bool nz, hipStream_t str
     const dim3 grid((uint32_t)(tiles_m * tiles_n)), block(dm::NT);
     const int tm = (int)tiles_m, tn = (int)tiles_n;
     constexpr int S = kOutSwiGLU;
+    int32_t* ap = reinterpret_cast<int32_t*>(amax_part);
     if (nz) {
-        if (e.out_dtype == QK_BF16) qmm_dma<kLayNZ, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, nullptr);
-        else qmm_dma<kLayNZ, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, nullptr);
+        if (e.out_dtype == QK_BF16) qmm_dma<kLayNZ, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap);
+        else qmm_dma<kLayNZ, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap);
     } else {
-        if (e.out_dtype == QK_BF16) qmm_dma<kLayKN, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, nullptr);
-        else qmm_dma<kLayKN, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, nullptr);
+        if (e.out_dtype == QK_BF16) qmm_dma<kLayKN, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap);
+        else qmm_dma<kLayKN, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap);
     }
     return hipGetLastError();
 }

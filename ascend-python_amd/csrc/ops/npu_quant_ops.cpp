@@ -933,6 +933,55 @@ at::Tensor npu_quant_matmul_swiglu(const at::Tensor& x1_in, const at::Tensor& x2
     return npu_swiglu(h2, -1);
 }
 
+// (q, q_scale) = npu_dynamic_quant(npu_quant_matmul_swiglu(...)) bit for bit: h and the GEMM's per-row partial
+// absmax in a workspace, then one elementwise quantizing pass (qk_quant_matmul_swiglu_quant); the chain where
+// the fused kernels do not take the shape.
+std::tuple<at::Tensor, at::Tensor> npu_quant_matmul_swiglu_quant(const at::Tensor& x1_in, const at::Tensor& x2_in,
+                                                                 const at::Tensor& scale_in,
+                                                                 const std::optional<at::Tensor>& pertoken_scale,
+                                                                 std::optional<at::ScalarType> output_dtype) {
+    const at::ScalarType h_type = output_dtype.value_or(at::kBFloat16);
+    int64_t K = 0, I = 0;
+    const auto shape = swiglu_matmul_check(x1_in, x2_in, scale_in, pertoken_scale, h_type, K, I);
+    const c10::DeviceGuard guard(x1_in.device());
+    auto q = at::empty(shape, x1_in.options().dtype(at::kChar));
+    auto qs = at::empty(at::IntArrayRef(shape).slice(0, shape.size() - 1), x1_in.options().dtype(at::kFloat));
+    if (q.numel() == 0) return {q, qs};
+    const bool nz = is_w8_nz(x2_in);
+    auto x1 = x1_in.contiguous();
+    const bool kn = !nz && x2_in.stride(1) == 1 && x2_in.stride(0) >= 2 * I;
+    if (nz || kn) {
+        auto scale = scale_in.scalar_type() == at::kFloat ? scale_in.contiguous() : scale_in.to(at::kFloat);
+        at::Tensor pt;
+        if (pertoken_scale.has_value()) pt = pertoken_scale->contiguous();
+        const int64_t M = leading_rows(x1);
+        size_t ws_bytes = 0;
+        check_rc(qk_quant_matmul_swiglu_quant_workspace_size(M, I, &ws_bytes), "npu_quant_matmul_swiglu_quant");
+        at::Tensor ws = workspace_for(x1, ws_bytes);
+        const int rc = qk_quant_matmul_swiglu_quant(
+            x1.data_ptr<int8_t>(), K, x2_in.data_ptr<int8_t>(), nz ? QK_FORMAT_FRACTAL_NZ : QK_FORMAT_ND,
+            nz ? 0 : x2_in.stride(0), M, I, K, scale.data_ptr<float>(), scale.numel(),
+            pt.defined() ? pt.data_ptr<float>() : nullptr, qk_dtype_of(h_type), q.data_ptr<int8_t>(),
+            qs.data_ptr<float>(), ws.data_ptr(), ws_bytes, current_stream(x1));
+        if (rc != QK_ERR_UNSUPPORTED) {
+            check_rc(rc, "npu_quant_matmul_swiglu_quant");
+            return {q, qs};
+        }
+    }
+    return npu_dynamic_quant(npu_quant_matmul_swiglu(x1_in, x2_in, scale_in, pertoken_scale, h_type), std::nullopt);
+}
+
+std::tuple<at::Tensor, at::Tensor> npu_quant_matmul_swiglu_quant_meta(const at::Tensor& x1, const at::Tensor& x2,
+                                                                      const at::Tensor& scale,
+                                                                      const std::optional<at::Tensor>& pertoken_scale,
+                                                                      std::optional<at::ScalarType> output_dtype) {
+    const at::ScalarType h_type = output_dtype.value_or(at::kBFloat16);
+    int64_t K = 0, I = 0;
+    const auto shape = swiglu_matmul_check(x1, x2, scale, pertoken_scale, h_type, K, I);
+    return {at::empty(shape, x1.options().dtype(at::kChar)),
+            at::empty(at::IntArrayRef(shape).slice(0, shape.size() - 1), x1.options().dtype(at::kFloat))};
+}
+
 at::Tensor npu_quant_matmul_swiglu_meta(const at::Tensor& x1, const at::Tensor& x2, const at::Tensor& scale,
                                         const std::optional<at::Tensor>& pertoken_scale,
                                         std::optional<at::ScalarType> output_dtype) {
@@ -968,6 +1017,8 @@ TORCH_LIBRARY(npu, m) {
     m.def("npu_swiglu_dynamic_quant(Tensor self, int dim=-1) -> (Tensor, Tensor)");
     m.def("npu_quant_matmul_swiglu(Tensor x1, Tensor x2, Tensor scale, *, Tensor? pertoken_scale=None, "
           "ScalarType? output_dtype=None) -> Tensor");
+    m.def("npu_quant_matmul_swiglu_quant(Tensor x1, Tensor x2, Tensor scale, *, Tensor? pertoken_scale=None, "
+          "ScalarType? output_dtype=None) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(npu, CUDA, m) {
@@ -984,6 +1035,7 @@ TORCH_LIBRARY_IMPL(npu, CUDA, m) {
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant);
     m.impl("npu_swiglu_dynamic_quant", &npu_swiglu_dynamic_quant);
     m.impl("npu_quant_matmul_swiglu", &npu_quant_matmul_swiglu);
+    m.impl("npu_quant_matmul_swiglu_quant", &npu_quant_matmul_swiglu_quant);
 }
 
 TORCH_LIBRARY_IMPL(npu, CompositeExplicitAutograd, m) { m.impl("get_npu_format", &get_npu_format); }
@@ -1002,4 +1054,5 @@ TORCH_LIBRARY_IMPL(npu, Meta, m) {
     m.impl("npu_rms_norm_dynamic_quant", &npu_rms_norm_dynamic_quant_meta);
     m.impl("npu_swiglu_dynamic_quant", &npu_swiglu_dynamic_quant_meta);
     m.impl("npu_quant_matmul_swiglu", &npu_quant_matmul_swiglu_meta);
+    m.impl("npu_quant_matmul_swiglu_quant", &npu_quant_matmul_swiglu_quant_meta);
 }

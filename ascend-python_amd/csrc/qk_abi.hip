@@ -326,10 +326,66 @@ int qk_quant_matmul_swiglu(const int8_t* x1, int64_t ldx1, const int8_t* x2, int
     p.sbk = x2_format == QK_FORMAT_ND ? x2_stride_k : 0;
     p.sbn = x2_format == QK_FORMAT_ND ? 1 : 0;
     p.epi.ldo = I;
-    const hipError_t e = qk::launch_quant_matmul_swiglu(p, x2_format == QK_FORMAT_FRACTAL_NZ, (hipStream_t)stream);
+    const hipError_t e =
+        qk::launch_quant_matmul_swiglu(p, x2_format == QK_FORMAT_FRACTAL_NZ, nullptr, (hipStream_t)stream);
     if (e == hipErrorInvalidValue)
         return fail(QK_ERR_UNSUPPORTED, "%s: the fused kernel does not take M=%lld I=%lld K=%lld with these operands "
                     "(I %% 128, K %% 256, 16-byte aligned rows and pointers)", op, (long long)M, (long long)I, (long long)K);
+    return launched(e, op);
+}
+
+// h [M, I] (16-bit) at the head of the workspace, then the partial absmax fp32 [M][I / 128], 256-byte aligned
+static size_t swiglu_quant_h_bytes(int64_t M, int64_t I) { return ((size_t)M * (size_t)I * 2 + 255) & ~(size_t)255; }
+
+int qk_quant_matmul_swiglu_quant_workspace_size(int64_t M, int64_t I, size_t* bytes) {
+    g_last_error.clear();
+    if (!bytes) return fail(QK_ERR_ARG, "npu_quant_matmul_swiglu_quant: bytes is null");
+    if (M < 0 || I < 0 || M > ((int64_t)1 << 40) || I > ((int64_t)1 << 40))
+        return fail(QK_ERR_ARG, "npu_quant_matmul_swiglu_quant: bad M=%lld I=%lld", (long long)M, (long long)I);
+    *bytes = swiglu_quant_h_bytes(M, I) + (size_t)M * (size_t)((I + 127) / 128) * 4;
+    return QK_OK;
+}
+
+int qk_quant_matmul_swiglu_quant(const int8_t* x1, int64_t ldx1, const int8_t* x2, int x2_format,
+                                 int64_t x2_stride_k, int64_t M, int64_t I, int64_t K, const float* scale,
+                                 int64_t scale_len, const float* pertoken_scale, int h_dtype, int8_t* q,
+                                 float* q_scale, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+    g_last_error.clear();
+    const char* op = "npu_quant_matmul_swiglu_quant";
+    size_t need = 0;
+    int rc = qk_quant_matmul_swiglu_quant_workspace_size(M, I, &need);
+    if (rc != QK_OK) return rc;
+    if (M == 0 || I == 0) return QK_OK;
+    if (!q || !q_scale) return fail(QK_ERR_ARG, "%s: null output", op);
+    if ((rc = check_workspace(op, need, workspace, workspace_bytes)) != QK_OK) return rc;
+    if (!is_half(h_dtype)) return fail(QK_ERR_ARG, "%s: h must be float16 or bfloat16 (got %d)", op, h_dtype);
+    if (I % 128 != 0 || (uintptr_t)q % 8 != 0)
+        return fail(QK_ERR_UNSUPPORTED, "%s: the fused kernels take I %% 128 == 0 and an 8-byte aligned q (I=%lld)", op,
+                    (long long)I);
+    void* h = workspace;
+    float* amax = reinterpret_cast<float*>(static_cast<char*>(workspace) + swiglu_quant_h_bytes(M, I));
+    if (x2_format != QK_FORMAT_ND && x2_format != QK_FORMAT_FRACTAL_NZ)
+        return fail(QK_ERR_ARG, "%s: x2_format must be QK_FORMAT_ND or QK_FORMAT_FRACTAL_NZ (got %d)", op, x2_format);
+    qk::QmmArgs p;
+    if ((rc = quant_matmul_args(op, M, 2 * I, K, scale, scale_len, nullptr, 0, pertoken_scale, nullptr, 0, h, h_dtype,
+                                p)) != QK_OK)
+        return rc;
+    if (K > 0 && (!x1 || !x2)) return fail(QK_ERR_ARG, "%s: null pointer", op);
+    if (ldx1 < K) return fail(QK_ERR_ARG, "%s: ldx1=%lld < K=%lld", op, (long long)ldx1, (long long)K);
+    if (x2_format == QK_FORMAT_ND && x2_stride_k < 2 * I)
+        return fail(QK_ERR_ARG, "%s: x2_stride_k=%lld < 2I=%lld", op, (long long)x2_stride_k, (long long)(2 * I));
+    p.a = x1;
+    p.lda = ldx1;
+    p.b = x2;
+    p.sbk = x2_format == QK_FORMAT_ND ? x2_stride_k : 0;
+    p.sbn = x2_format == QK_FORMAT_ND ? 1 : 0;
+    p.epi.ldo = I;
+    hipError_t e = qk::launch_quant_matmul_swiglu(p, x2_format == QK_FORMAT_FRACTAL_NZ, amax, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue)
+        return fail(QK_ERR_UNSUPPORTED, "%s: the fused kernel does not take M=%lld I=%lld K=%lld with these operands "
+                    "(I %% 128, K %% 256, 16-byte aligned rows and pointers)", op, (long long)M, (long long)I, (long long)K);
+    if (e != hipSuccess) return launched(e, op);
+    e = qk::launch_dynamic_quant_premax(h, h_dtype, M, I, amax, (int)(I / 128), q, q_scale, (hipStream_t)stream);
     return launched(e, op);
 }
 

@@ -25,6 +25,9 @@ Importing this package loads ``_npu_ops.so``, which registers
   quantized MLP block's gate-up projection with the SwiGLU in the GEMM's epilogue, h =
   npu_swiglu(npu_quant_matmul(x1, x2, scale, pertoken_scale=..., output_dtype=...)) bit for bit (x2 [K, 2I] or
   its int8 NZ cast; no bias)
+* ``torch.ops.npu.npu_quant_matmul_swiglu_quant(x1, x2, scale, *, pertoken_scale=None, output_dtype=None) -> (q,
+  scale)``: the same followed by npu_dynamic_quant of h, bit for bit; the GEMM's epilogue stores each row's
+  partial absmax, so the quantizer reads h once with no row reduction
 
 and exposes the same callables here, so code written as
 ``torch_npu.npu_quant_matmul(...)`` runs as ``op_plugin_amd.npu_quant_matmul(...)``
@@ -66,6 +69,7 @@ npu_swiglu = torch.ops.npu.npu_swiglu
 npu_rms_norm_dynamic_quant = torch.ops.npu.npu_rms_norm_dynamic_quant
 npu_swiglu_dynamic_quant = torch.ops.npu.npu_swiglu_dynamic_quant
 npu_quant_matmul_swiglu = torch.ops.npu.npu_quant_matmul_swiglu
+npu_quant_matmul_swiglu_quant = torch.ops.npu.npu_quant_matmul_swiglu_quant
 
 # qk_abi.h constants
 QK_F16, QK_BF16, QK_F32, QK_I8, QK_I32, QK_U8, QK_I4_NZ, QK_I8_NZ, QK_I8_NK = 1, 2, 3, 4, 5, 6, 16, 17, 18
@@ -78,7 +82,8 @@ ABI_SYMBOLS = (
     "qk_quant_matmul", "qk_quant_matmul_nz_workspace_size", "qk_quant_matmul_nz", "qk_weight_quant_bmm_workspace_size",
     "qk_weight_quant_bmm", "qk_weight_quant_bmm_noalloc", "qk_int4_pack", "qk_weight_format_cast",
     "qk_quantize_per_tensor", "qk_quantize_per_channel", "qk_dequantize", "qk_rms_norm", "qk_rms_norm_quant",
-    "qk_swiglu", "qk_swiglu_quant", "qk_quant_matmul_swiglu",
+    "qk_swiglu", "qk_swiglu_quant", "qk_quant_matmul_swiglu", "qk_quant_matmul_swiglu_quant_workspace_size",
+    "qk_quant_matmul_swiglu_quant",
 )
 
 _abi = None
@@ -113,6 +118,8 @@ def abi() -> ctypes.CDLL:
         L.qk_swiglu.argtypes = [P, I, I64, I64, P, P]
         L.qk_swiglu_quant.argtypes = [P, I, I64, I64, P, P, P]
         L.qk_quant_matmul_swiglu.argtypes = [P, I64, P, I, I64, I64, I64, I64, P, I64, P, P, I, P]
+        L.qk_quant_matmul_swiglu_quant_workspace_size.argtypes = [I64, I64, P]
+        L.qk_quant_matmul_swiglu_quant.argtypes = [P, I64, P, I, I64, I64, I64, I64, P, I64, P, I, P, P, P, SZ, P]
         for name in ABI_SYMBOLS:
             getattr(L, name).restype = I if name != "qk_last_error" else ctypes.c_char_p
         _abi = L
@@ -144,5 +151,5 @@ __all__ = [
     "npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
     "npu_convert_weight_to_int4pack", "npu_format_cast", "get_npu_format", "quantize_per_tensor",
     "quantize_per_channel", "dequantize", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
-    "npu_swiglu_dynamic_quant", "npu_quant_matmul_swiglu", "abi", "last_error", "debug_set_plan", "LIB_PATH", "OPS_PATH",
+    "npu_swiglu_dynamic_quant", "npu_quant_matmul_swiglu", "npu_quant_matmul_swiglu_quant", "abi", "last_error", "debug_set_plan", "LIB_PATH", "OPS_PATH",
 ]

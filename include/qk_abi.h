@@ -97,7 +97,8 @@ const char* qk_last_error(void);
  * (2: the split-K counters at the head of a workspace; 3: the counters are
  * tagged per call, so a workspace needs no initialisation; 4: NZ weights,
  * qk_weight_format_cast, static quantization; 5: the [N, K] int8 weight code
- * QK_I8_NK, int8 NZ weights with K % 64 == 0 in qk_weight_quant_bmm; 6: qk_quant_matmul_swiglu). */
+ * QK_I8_NK, int8 NZ weights with K % 64 == 0 in qk_weight_quant_bmm; 6: qk_quant_matmul_swiglu,
+ * qk_quant_matmul_swiglu_quant). */
 int qk_abi_version(void);
 
 /* Debug and test hook, no counterpart in the reference: forces kernel choices
@@ -366,6 +367,26 @@ int qk_swiglu_quant(const void* h, int dtype, int64_t rows, int64_t I, int8_t* q
 int qk_quant_matmul_swiglu(const int8_t* x1, int64_t ldx1, const int8_t* x2, int x2_format, int64_t x2_stride_k,
                            int64_t M, int64_t I, int64_t K, const float* scale, int64_t scale_len,
                            const float* pertoken_scale, void* out, int out_dtype, qk_stream_t stream);
+
+/*
+ * The same projection followed by qk_dynamic_quant of h, as the quantized MLP
+ * block uses it: q [M, I] int8 (rows of I bytes, 8-byte aligned) and q_scale
+ * [M] fp32 equal qk_dynamic_quant(h) bit for bit, h [M, I] being
+ * qk_quant_matmul_swiglu's output rounded to h_dtype (QK_BF16 / QK_F16).  h
+ * lives in the workspace, and the GEMM's epilogue also stores each row's
+ * largest |h| per 128-column slice there, so the quantizer needs no row
+ * reduction.  No single reference op: the chain npu_quant_matmul ->
+ * npu_swiglu -> npu_dynamic_quant.  Workspace: the bytes
+ * qk_quant_matmul_swiglu_quant_workspace_size gives (h plus M * I / 128
+ * floats), 256-byte aligned, any contents.  The shapes
+ * qk_quant_matmul_swiglu takes (I % 128 == 0, K % 256 == 0, ...); others
+ * return QK_ERR_UNSUPPORTED (the caller composes the calls).
+ */
+int qk_quant_matmul_swiglu_quant_workspace_size(int64_t M, int64_t I, size_t* bytes);
+int qk_quant_matmul_swiglu_quant(const int8_t* x1, int64_t ldx1, const int8_t* x2, int x2_format,
+                                 int64_t x2_stride_k, int64_t M, int64_t I, int64_t K, const float* scale,
+                                 int64_t scale_len, const float* pertoken_scale, int h_dtype, int8_t* q,
+                                 float* q_scale, void* workspace, size_t workspace_bytes, qk_stream_t stream);
 
 #ifdef __cplusplus
 }

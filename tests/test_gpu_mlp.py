@@ -303,16 +303,27 @@ SWIGLU_MM_CASES = [
 ]
 
 
-@pytest.mark.parametrize("M,I,K,layout,out_dtype,per_tensor,pertoken", SWIGLU_MM_CASES)
-def test_quant_matmul_swiglu(ops, M, I, K, layout, out_dtype, per_tensor, pertoken):
+SWIGLU_MM_CASES += [
+    # scales so large that fp16 gate / up outputs overflow: rows holding +-inf and NaN (silu(-inf) * inf)
+    (96, 256, 256, "nz", torch.float16, True, False, 40.0),
+    (96, 256, 256, "kn", torch.float16, False, True, 4000.0),
+]
+
+
+@pytest.mark.parametrize("case", SWIGLU_MM_CASES)
+def test_quant_matmul_swiglu(ops, case):
     """npu_quant_matmul_swiglu (the gate-up GEMM with the SwiGLU in its epilogue) equals
-    npu_swiglu(npu_quant_matmul(...)) bit for bit; through the C ABI the fused kernel takes the shapes it
-    supports and refuses the others with QK_ERR_UNSUPPORTED, for which the op runs the unfused chain."""
-    say(f"quant_matmul_swiglu M={M} I={I} K={K} {layout} {out_dtype} per_tensor={per_tensor} pertoken={pertoken}")
+    npu_swiglu(npu_quant_matmul(...)) bit for bit, and npu_quant_matmul_swiglu_quant (h quantized from the
+    epilogue's partial row absmax) equals npu_dynamic_quant of that; through the C ABI the fused kernels take
+    the shapes they support and refuse the others with QK_ERR_UNSUPPORTED, for which the ops run the chain."""
+    M, I, K, layout, out_dtype, per_tensor, pertoken = case[:7]
+    big = case[7] if len(case) > 7 else 1.0
+    say(f"quant_matmul_swiglu M={M} I={I} K={K} {layout} {out_dtype} per_tensor={per_tensor} pertoken={pertoken} "
+        f"scale x{big}")
     g = torch.Generator().manual_seed(M + I + K)
     x1 = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8).to(DEV)
     w = torch.randint(-128, 128, (K, 2 * I), generator=g, dtype=torch.int8).to(DEV)
-    s = (1e-4 + 1e-3 * torch.rand(1 if per_tensor else 2 * I, generator=g)).to(DEV)
+    s = (big * (1e-4 + 1e-3 * torch.rand(1 if per_tensor else 2 * I, generator=g))).to(DEV)
     pt = (1e-2 * torch.rand(M, generator=g)).to(DEV) if pertoken else None
     wd = {"kn": w, "nz": ops.npu_format_cast(w, 29) if layout == "nz" else None,
           "nk": w.t().contiguous().t()}[layout]
@@ -321,6 +332,14 @@ def test_quant_matmul_swiglu(ops, M, I, K, layout, out_dtype, per_tensor, pertok
     torch.cuda.synchronize()
     assert h.shape == (M, I) and h.dtype == out_dtype
     assert torch.equal(h.view(torch.int16), ref.view(torch.int16))
+    q, qs = ops.npu_quant_matmul_swiglu_quant(x1, wd, s, pertoken_scale=pt, output_dtype=out_dtype)
+    rq, rs = ops.npu_dynamic_quant(ref)
+    torch.cuda.synchronize()
+    if big > 1.0:  # the overflow cases do hold non-finite rows
+        assert not torch.isfinite(ref).all()
+    assert q.shape == (M, I) and qs.shape == (M,)
+    assert torch.equal(q, rq)
+    assert torch.equal(qs.view(torch.int32), rs.view(torch.int32))
     if layout == "nk":
         return
     L = ops.abi()
@@ -336,3 +355,23 @@ def test_quant_matmul_swiglu(ops, M, I, K, layout, out_dtype, per_tensor, pertok
     assert rc == 0, ops.last_error()
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    # the fused quantizing form through the C ABI, on a workspace of arbitrary contents
+    ws_bytes = ctypes.c_size_t()
+    assert L.qk_quant_matmul_swiglu_quant_workspace_size(M, I, ctypes.byref(ws_bytes)) == 0
+    assert ws_bytes.value >= M * I * 2 + M * (I // 128) * 4
+    ws = torch.full((ws_bytes.value,), 0x7f, dtype=torch.uint8, device=DEV)
+    q3 = torch.empty((M, I), dtype=torch.int8, device=DEV)
+    qs3 = torch.empty((M,), dtype=torch.float32, device=DEV)
+    rc = L.qk_quant_matmul_swiglu_quant(x1.data_ptr(), K, wd.data_ptr(), 29 if layout == "nz" else 2,
+                                        0 if layout == "nz" else 2 * I, M, I, K, s.data_ptr(), s.numel(),
+                                        None if pt is None else pt.data_ptr(),
+                                        BF16 if out_dtype == torch.bfloat16 else F16, q3.data_ptr(), qs3.data_ptr(),
+                                        ws.data_ptr(), ws_bytes.value, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ops.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(q3, rq) and torch.equal(qs3.view(torch.int32), rs.view(torch.int32))
+    assert torch.equal(ws[:M * I * 2].view(out_dtype).view(M, I).view(torch.int16), ref.view(torch.int16))
+    assert L.qk_quant_matmul_swiglu_quant(x1.data_ptr(), K, wd.data_ptr(), 29 if layout == "nz" else 2,
+                                          0 if layout == "nz" else 2 * I, M, I, K, s.data_ptr(), s.numel(), None,
+                                          BF16, q3.data_ptr(), qs3.data_ptr(), ws.data_ptr(), ws_bytes.value - 4,
+                                          None) == ops.QK_ERR_WORKSPACE

@@ -144,7 +144,7 @@ def test_schemas_registered():
     for name in ("npu_dynamic_quant", "npu_quant_matmul", "npu_weight_quant_batchmatmul",
                  "npu_convert_weight_to_int4pack", "npu_format_cast", "quantize_per_tensor", "quantize_per_channel",
                  "dequantize", "npu_rms_norm", "npu_swiglu", "npu_rms_norm_dynamic_quant",
-                 "npu_swiglu_dynamic_quant", "npu_quant_matmul_swiglu"):
+                 "npu_swiglu_dynamic_quant", "npu_quant_matmul_swiglu", "npu_quant_matmul_swiglu_quant"):
         assert hasattr(torch.ops.npu, name)
     s = str(torch.ops.npu.npu_quant_matmul.default._schema)
     assert "pertoken_scale" in s and "ScalarType? output_dtype" in s
@@ -202,6 +202,8 @@ def test_meta_shapes():
     h = q.npu_quant_matmul_swiglu(_m((512, 4096), torch.int8), w8gu, _m((1,), torch.float32),
                                   output_dtype=torch.float16)
     assert h.shape == (512, 14336) and h.dtype == torch.float16
+    qq, qs = q.npu_quant_matmul_swiglu_quant(_m((2, 256, 4096), torch.int8), w8gu, _m((28672,), torch.float32))
+    assert qq.shape == (2, 256, 14336) and qq.dtype == torch.int8 and qs.shape == (2, 256) and qs.dtype == torch.float32
 
 
 def test_storage_format_is_recorded_not_inferred():
