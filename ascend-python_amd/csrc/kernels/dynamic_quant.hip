@@ -1,8 +1,8 @@
 // npu_dynamic_quant for gfx950: per-row symmetric int8 quantization.
 //
-// One 256-thread workgroup (4 wave64) per row.  The row is read once with
+// One 256- or 512-thread workgroup per row.  The row is read once with
 // 128-bit loads (8 halves per lane per load) and kept in registers; the
-// absmax is reduced across the wave with xor-shuffles and across the four
+// absmax is reduced across each wave with DPP and lane reads and across the
 // waves through LDS; the quantized row is written with 64-bit stores.  The
 // arithmetic is exactly the op contract: s = amax / 127 (IEEE division),
 // y = clamp(rint(x / s)) with ties to even, a zero row giving s = 0, y = 0.
@@ -16,36 +16,32 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Vector path: K % 8 == 0, 16-byte aligned rows, K <= 8 * 256 * VPT.  A
-// workgroup quantizes RPW consecutive rows at once: every load of its rows is
-// issued before the first reduction.  The rows stay packed in registers and
-// each value is widened where it is used (in the absmax and again in the
-// quantizer), which keeps the register count, and so the number of rows in
-// flight per CU, high.
-template <int DT, int VPT, int RPW, bool SMOOTH>
-__global__ __launch_bounds__(kThreads) void dyn_quant_vec(const uint16_t* __restrict__ x, int64_t rows, int64_t K,
-                                                          const float* __restrict__ smooth,
-                                                          int8_t* __restrict__ y, float* __restrict__ scale) {
-    __shared__ float red[RPW][4];
+// Vector path: K % 8 == 0, 16-byte aligned rows, K <= 8 * NT * VPT.  One NT-thread workgroup per row: the
+// row is read once with 16-byte loads, all issued before the first reduction, and stays packed in registers
+// (each value is widened where it is used, in the absmax and again in the quantizer, which keeps the register
+// count, and so the number of rows in flight per CU, high).  The absmax is reduced across each wave with DPP
+// row rotations and lane reads and across the waves through LDS.
+template <int DT, int NT, int VPT, bool SMOOTH>
+__global__ __launch_bounds__(NT) void dyn_quant_vec(const uint16_t* __restrict__ x, int64_t K,
+                                                    const float* __restrict__ smooth, int8_t* __restrict__ y,
+                                                    float* __restrict__ scale) {
+    constexpr int NW = NT / 64;
+    __shared__ float red[NW];
     const int nv = (int)(K >> 3);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t row0 = (int64_t)blockIdx.x * RPW;
-    u32x4 raw[RPW][VPT];
+    const int64_t row = blockIdx.x;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * K);
+    u32x4 raw[VPT];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;  // a ragged last group re-reads a valid row
-        const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * K);
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int idx = threadIdx.x + i * kThreads;
-            if (idx < nv) raw[r][i] = __builtin_nontemporal_load(xr + idx);  // read once
-        }
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        if (idx < nv) raw[i] = __builtin_nontemporal_load(xr + idx);  // read once
     }
     float sm[SMOOTH ? VPT : 1][8];
     if constexpr (SMOOTH) {
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
-            const int idx = threadIdx.x + i * kThreads;
+            const int idx = threadIdx.x + i * NT;
             if (idx < nv) {
                 const f32x4* sp = reinterpret_cast<const f32x4*>(smooth + (int64_t)idx * 8);
                 const f32x4 s0 = sp[0], s1 = sp[1];
@@ -57,46 +53,39 @@ __global__ __launch_bounds__(kThreads) void dyn_quant_vec(const uint16_t* __rest
             }
         }
     }
-    auto value = [&](int r, int i, int e) {
-        const uint32_t d = raw[r][i][e >> 1];
+    auto value = [&](int i, int e) {
+        const uint32_t d = raw[i][e >> 1];
         float v = load_half_bits((e & 1) ? (d >> 16) : (d & 0xffffu), DT);
         if constexpr (SMOOTH) v = v * sm[i][e];
         return v;
     };
-    float amax[RPW];
+    float amax = 0.0f;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        amax[r] = 0.0f;
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        if (idx < nv) {
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int idx = threadIdx.x + i * kThreads;
-            if (idx < nv) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) amax[r] = fmaxf(amax[r], fabsf(value(r, i, e)));
-            }
+            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(value(i, e)));
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) amax[r] = fmaxf(amax[r], __shfl_xor(amax[r], off));
-        if (lane == 0) red[r][wave] = amax[r];
     }
+    amax = wave_max(amax);
+    if (lane == 0) red[wave] = amax;
     __syncthreads();
+    float m = red[0];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const int64_t row = row0 + r;
-        if (row >= rows) break;
-        const float s = fmaxf(fmaxf(red[r][0], red[r][1]), fmaxf(red[r][2], red[r][3])) / 127.0f;
-        if (threadIdx.x == 0) scale[row] = s;
-        const RowQuant rq = row_quant(s);
-        u32x2* yr = reinterpret_cast<u32x2*>(y + row * K);
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w]);
+    const float s = m / 127.0f;
+    if (threadIdx.x == 0) scale[row] = s;
+    const RowQuant rq = row_quant(s);
+    u32x2* yr = reinterpret_cast<u32x2*>(y + row * K);
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int idx = threadIdx.x + i * kThreads;
-            if (idx < nv) {
-                float vf[8];
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        if (idx < nv) {
+            float vf[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vf[e] = value(r, i, e);
-                __builtin_nontemporal_store(quant8(vf, rq), yr + idx);  // written once (measured 24.5 -> 23.1 us at cfg4)
-            }
+            for (int e = 0; e < 8; ++e) vf[e] = value(i, e);
+            __builtin_nontemporal_store(quant8(vf, rq), yr + idx);  // written once (measured 24.5 -> 23.1 us at cfg4)
         }
     }
 }
@@ -165,24 +154,17 @@ __global__ __launch_bounds__(kThreads) void dyn_quant_premax(const uint16_t* __r
     }
 }
 
-template <int DT, int VPT, int RPW>
-hipError_t launch_rows(const uint16_t* x, int64_t rows, int64_t K, const float* smooth, int8_t* y, float* scale,
-                       hipStream_t stream) {
-    const dim3 grid((uint32_t)((rows + RPW - 1) / RPW));
-    if (smooth)
-        dyn_quant_vec<DT, VPT, RPW, true><<<grid, dim3(kThreads), 0, stream>>>(x, rows, K, smooth, y, scale);
-    else
-        dyn_quant_vec<DT, VPT, RPW, false><<<grid, dim3(kThreads), 0, stream>>>(x, rows, K, smooth, y, scale);
-    return hipGetLastError();
-}
-
-// One row per workgroup: with the row kept packed (VPT * 4 VGPRs) the kernel
-// needs about 30 VGPRs at VPT = 4, so 16 workgroups share a CU and their loads
-// overlap the other rows' reductions.  (Two rows per workgroup measured slower.)
-template <int DT, int VPT>
+// One row per workgroup.  512 threads where a row has at least 1024 vectors (cfg4, K = 8192: 20.5-20.8 us against
+// 21.2-21.5 with 256 threads and 26.8 with 1024, one box); 256 below that.
+template <int DT, int NT, int VPT>
 hipError_t launch_vec(const uint16_t* x, int64_t rows, int64_t K, const float* smooth, int8_t* y, float* scale,
                       hipStream_t stream) {
-    return launch_rows<DT, VPT, 1>(x, rows, K, smooth, y, scale, stream);
+    const dim3 grid((uint32_t)rows), block(NT);
+    if (smooth)
+        dyn_quant_vec<DT, NT, VPT, true><<<grid, block, 0, stream>>>(x, K, smooth, y, scale);
+    else
+        dyn_quant_vec<DT, NT, VPT, false><<<grid, block, 0, stream>>>(x, K, smooth, y, scale);
+    return hipGetLastError();
 }
 
 template <int DT>
@@ -190,13 +172,17 @@ hipError_t dispatch(const uint16_t* x, int64_t rows, int64_t K, const float* smo
                     hipStream_t stream) {
     const bool aligned = (K % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 8 == 0) &&
                          (!smooth || (uintptr_t)smooth % 16 == 0);
-    const int64_t per_thread = (K / 8 + kThreads - 1) / kThreads;
-    if (aligned && K > 0 && per_thread <= 16) {
-        if (per_thread <= 1) return launch_vec<DT, 1>(x, rows, K, smooth, y, scale, stream);
-        if (per_thread <= 2) return launch_vec<DT, 2>(x, rows, K, smooth, y, scale, stream);
-        if (per_thread <= 4) return launch_vec<DT, 4>(x, rows, K, smooth, y, scale, stream);
-        if (per_thread <= 8) return launch_vec<DT, 8>(x, rows, K, smooth, y, scale, stream);
-        return launch_vec<DT, 16>(x, rows, K, smooth, y, scale, stream);
+    const int64_t nv = K / 8;
+    if (aligned && K > 0 && rows < ((int64_t)1 << 31) && nv <= 512 * 16) {
+        if (nv < 1024) {
+            if (nv <= 256) return launch_vec<DT, 256, 1>(x, rows, K, smooth, y, scale, stream);
+            if (nv <= 512) return launch_vec<DT, 256, 2>(x, rows, K, smooth, y, scale, stream);
+            return launch_vec<DT, 256, 4>(x, rows, K, smooth, y, scale, stream);
+        }
+        if (nv <= 1024) return launch_vec<DT, 512, 2>(x, rows, K, smooth, y, scale, stream);
+        if (nv <= 2048) return launch_vec<DT, 512, 4>(x, rows, K, smooth, y, scale, stream);
+        if (nv <= 4096) return launch_vec<DT, 512, 8>(x, rows, K, smooth, y, scale, stream);
+        return launch_vec<DT, 512, 16>(x, rows, K, smooth, y, scale, stream);
     }
     dyn_quant_generic<DT><<<dim3((uint32_t)rows), dim3(kThreads), 0, stream>>>(x, K, smooth, y, scale);
     return hipGetLastError();
