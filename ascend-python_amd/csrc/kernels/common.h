@@ -97,6 +97,24 @@ __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xf, 0xf, false)));
     return v;
 }
+// Sum over each row of 16 lanes, at every lane of the row, by the same rotations: lane i adds the value of lane
+// i +- 8, then of i +- 4, 2, 1, and as addition is commutative every lane of the row ends with the same bits.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xf, 0xf, false));
+    return v;
+}
+// Sum over the wave (all 64 lanes active), uniform: row16_sum, then (row 0 + row 1) + (row 2 + row 3).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (a + b) + (c + d);
+}
 // Largest value over the wave (all 64 lanes active), uniform: row16_max, then the four rows' lanes 0, 16, 32, 48.
 __device__ __forceinline__ float wave_max(float v) {
     v = row16_max(v);
@@ -209,12 +227,11 @@ __device__ __forceinline__ bool splitk_last(uint64_t* ctr, uint32_t nsplit, uint
 uint64_t next_split_tag();
 
 // ---------------------------------------------------------------- per-row quantization
-// Row reductions for 256-thread workgroups (4 wave64): xor-shuffles inside a
-// wave, LDS across the four waves.  Every thread gets the result.
+// Row reductions for 256-thread workgroups (4 wave64): DPP and lane reads inside
+// a wave, LDS across the four waves.  Every thread gets the result.
 __device__ __forceinline__ float block_absmax(float amax) {
     __shared__ float red_absmax[4];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    amax = wave_max(amax);
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red_absmax[wave] = amax;
     __syncthreads();

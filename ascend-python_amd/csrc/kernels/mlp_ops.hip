@@ -32,12 +32,11 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Row reductions over the NW waves of a workgroup (wave sums added in wave order).
+// Row reductions over the NW waves of a workgroup (DPP inside a wave; wave sums added in wave order).
 template <int NW>
 __device__ __forceinline__ float block_sum(float v) {
     __shared__ float red_sum[NW];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    v = wave_sum(v);
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red_sum[wave] = v;
     __syncthreads();
@@ -51,8 +50,7 @@ __device__ __forceinline__ float block_sum(float v) {
 template <int NW>
 __device__ __forceinline__ float block_absmax_w(float amax) {
     __shared__ float red_amax[NW];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    amax = wave_max(amax);
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red_amax[wave] = amax;
     __syncthreads();
