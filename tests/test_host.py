@@ -134,6 +134,30 @@ def test_abi_refuses_bad_arguments_without_launch():
     assert L.qk_swiglu(fake, F16, -1, 8, fake, None) == q.QK_ERR_ARG
     assert L.qk_swiglu(None, F16, 3, 8, None, None) == q.QK_ERR_ARG and "null pointer" in q.last_error()
     assert L.qk_swiglu_quant(fake, BF16, 3, 0, fake, fake, None) == q.QK_ERR_ARG and "empty" in q.last_error()
+    # the gate-up GEMM with the SwiGLU fused (x2 [K, 2I] rows: format ND, stride 2I)
+    nd = q.ACL_FORMAT_ND
+    assert L.qk_quant_matmul_swiglu(fake, 256, fake, nd, 512, 4, 256, 256, fake, 512, None, fake, F32,
+                                    None) == q.QK_ERR_ARG and "float16 or bfloat16" in q.last_error()
+    assert L.qk_quant_matmul_swiglu(fake, 256, fake, 5, 512, 4, 256, 256, fake, 512, None, fake, BF16,
+                                    None) == q.QK_ERR_ARG and "x2_format" in q.last_error()
+    assert L.qk_quant_matmul_swiglu(fake, 256, fake, nd, 300, 4, 256, 256, fake, 512, None, fake, BF16,
+                                    None) == q.QK_ERR_ARG and "x2_stride_k" in q.last_error()
+    assert L.qk_quant_matmul_swiglu(fake, 256, fake, nd, 512, 4, 256, 256, fake, 7, None, fake, BF16,
+                                    None) == q.QK_ERR_ARG and "scale" in q.last_error()
+    assert L.qk_quant_matmul_swiglu(None, 256, None, nd, 512, 0, 256, 256, None, 512, None, None, BF16,
+                                    None) == q.QK_OK
+    assert L.qk_quant_matmul_swiglu_quant_workspace_size(512, 14336, ctypes.byref(ws)) == q.QK_OK
+    assert ws.value == 512 * 14336 * 2 + 512 * 112 * 4   # h, then the per-tile row absmax
+    need = ws.value
+    args = (fake, 4096, fake, nd, 28672, 512, 14336, 4096, fake, 28672, fake, BF16, fake, fake)
+    assert L.qk_quant_matmul_swiglu_quant(*args, fake, need - 256, None) == q.QK_ERR_WORKSPACE
+    assert L.qk_quant_matmul_swiglu_quant(*args, None, need, None) == q.QK_ERR_WORKSPACE
+    assert L.qk_quant_matmul_swiglu_quant(*args[:11], F32, *args[12:], ctypes.c_void_p(4096), need,
+                                          None) == q.QK_ERR_ARG and "float16 or bfloat16" in q.last_error()
+    assert L.qk_quant_matmul_swiglu_quant(*args[:12], None, fake, ctypes.c_void_p(4096), need,
+                                          None) == q.QK_ERR_ARG and "null output" in q.last_error()
+    assert L.qk_quant_matmul_swiglu_quant(None, 4096, None, nd, 28672, 0, 14336, 4096, None, 28672, None, BF16, None,
+                                          None, None, 0, None) == q.QK_OK
 
 
 def _m(shape, dtype):
