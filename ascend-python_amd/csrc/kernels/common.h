@@ -457,7 +457,7 @@ hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N
 // int8 [N, K] -> [K, N]
 hipError_t launch_w8_nk_transpose(const int8_t* src, int64_t K, int64_t N, int8_t* dst, hipStream_t stream);
 size_t w4_nz_workspace(const WqbmmArgs& args);
-// A row-major int4 weight at large M: cast to NZ into the workspace, then the NZ prefill GEMM.  The size is 0
+// A row-major int4 or int8 weight at large M: cast to NZ into the workspace, then the NZ prefill GEMM.  The size is 0
 // when the plan does not apply; the launch returns false (running nothing) when it does not apply to these
 // operands or the workspace cannot hold it, else true with the launch status in *err.
 size_t w4_cast_nz_workspace(const WqbmmArgs& args);

@@ -92,9 +92,20 @@ __global__ __launch_bounds__(kNzThreads) void w4_nz_pack_kernel(const int32_t* _
     const int64_t sb = blockIdx.x % S, nbg = blockIdx.x / S;
     const int nb = (int)(NBT - nbg * kCastNB < kCastNB ? NBT - nbg * kCastNB : kCastNB);
     const int nw = 2 * nb, t = threadIdx.x;
-    for (int e = t; e < 128 * 2 * kCastNB; e += kNzThreads) {  // one dword per lane: 128-byte row pieces
-        const int r = e >> 5, w = e & 31;
-        if (w < nw) rows[r][w] = (uint32_t)nd[(sb * 128 + r) * NW + nbg * (2 * kCastNB) + w];
+    if (nb == kCastNB && NW % 4 == 0 && (uintptr_t)nd % 16 == 0) {
+        // whole 128-byte row pieces on 16-byte aligned rows: one 16-byte load per lane (4 per thread)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = t + kNzThreads * u, r = e >> 3, v = e & 7;
+            const u32x4 d = *reinterpret_cast<const u32x4*>(nd + (sb * 128 + r) * NW + nbg * (2 * kCastNB) + 4 * v);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rows[r][4 * v + i] = d[i];
+        }
+    } else {
+        for (int e = t; e < 128 * 2 * kCastNB; e += kNzThreads) {  // one dword per lane: 128-byte row pieces
+            const int r = e >> 5, w = e & 31;
+            if (w < nw) rows[r][w] = (uint32_t)nd[(sb * 128 + r) * NW + nbg * (2 * kCastNB) + w];
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -167,10 +178,24 @@ __global__ __launch_bounds__(kNzThreads) void w8_nz_pack_kernel(const int8_t* __
     const int64_t kb = blockIdx.x % KB, nbg = blockIdx.x / KB;
     const int nb = (int)(NBT - nbg * kCastNB < kCastNB ? NBT - nbg * kCastNB : kCastNB);
     const int nw = 4 * nb, t = threadIdx.x;
-    for (int e = t; e < 64 * 4 * kCastNB; e += kNzThreads) {  // one dword per lane: 256-byte row pieces
-        const int r = e >> 6, w = e & 63;
-        if (w < nw)
-            rows[r][w] = *reinterpret_cast<const uint32_t*>(nd + (kb * 64 + r) * N + nbg * (16 * kCastNB) + 4 * w);
+    if ((uintptr_t)nd % 16 == 0) {
+        // 16-byte loads (N % 16 == 0, so every row and every 16-column block starts on 16 bytes): 4 per thread
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = t + kNzThreads * u, r = e >> 4, v = e & 15;
+            if (4 * v < nw) {
+                const u32x4 d =
+                    *reinterpret_cast<const u32x4*>(nd + (kb * 64 + r) * N + nbg * (16 * kCastNB) + 16 * v);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rows[r][4 * v + i] = d[i];
+            }
+        }
+    } else {
+        for (int e = t; e < 64 * 4 * kCastNB; e += kNzThreads) {  // one dword per lane: 256-byte row pieces
+            const int r = e >> 6, w = e & 63;
+            if (w < nw)
+                rows[r][w] = *reinterpret_cast<const uint32_t*>(nd + (kb * 64 + r) * N + nbg * (16 * kCastNB) + 4 * w);
+        }
     }
     __syncthreads();
     // thread -> (block b, 16-row group g, 4-column group cg): the whole 16-byte chunks of lanes 4cg + e + 16g,
@@ -496,18 +521,36 @@ constexpr int RING = NSTG * STAGE;            // 153 KB
 constexpr int OROWB = 2 * BN + 16;            // padded output staging row (bytes)
 constexpr int SMEM = RING > BM * OROWB ? RING : BM * OROWB;
 static_assert(SMEM <= 160 * 1024, "LDS");
+// int8 NZ weights (W8A16): 64-row steps, so a step's weight is again one 1 KB NZ block per 16 columns and its
+// activation rows are 128 bytes
+constexpr int KS8 = 64;
+constexpr int X8_BYTES = BM * KS8 * 2;        // 16 KB
+constexpr int STAGE8 = X8_BYTES + W_BYTES + SC_BYTES;
+constexpr int RING8 = NSTG * STAGE8;          // 105 KB
+constexpr int SMEM8 = RING8 > BM * OROWB ? RING8 : BM * OROWB;
 }  // namespace nzg
 
-// G1: the group is one step (G == 128), so every step starts a group: its first MFMAs take a zero
+// G1: the group is one step (G == the step's K), so every step starts a group: its first MFMAs take a zero
 // accumulator and each row tile is folded right after its last MFMAs, between the later tiles' MFMAs.
-template <int DT, bool HAS_OFF, bool G1>
+// W8: an int8 NZ weight ([N/16][K/64][64][16]).  A step is 64 rows: one 1 KB block per 16 columns (the int4
+// step's DMA pattern), 128-byte activation rows (chunk c of row r at r*128 + 16*(c ^ (r & 7))), two MFMA k-steps.
+// The B operand of k-step t is rows 16g + 8t .. +8 of the lane's block column (lane c + 16g holds rows 16g ..
+// 16g+15), converted to offset-binary 16-bit values w + 128 (exact); the A operand is the matching 16 bytes of x,
+// k = 16g + 8t .. +8, so both operands run over the step's 64 k in the same permuted order.  The fold's base is
+// 128 instead of the int4 magic base.
+template <int DT, bool HAS_OFF, bool G1, bool W8 = false>
 __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, int tiles_n,
                                                      const float* __restrict__ xsum) {
     typedef Mfma<DT> MM;
     using namespace nzg;
     constexpr int TM = 8, TN = 2;
     constexpr int NSC = HAS_OFF ? 3 : 2;  // group-row DMAs per step: waves 0 .. NSC-1 issue one each
-    __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+    constexpr int KSW = W8 ? KS8 : KS;           // K rows per step
+    constexpr int XB = W8 ? X8_BYTES : X_BYTES;  // activation bytes per stage
+    constexpr int STG = XB + W_BYTES + SC_BYTES;
+    constexpr int NKT = KSW / 32;                // MFMA k-steps per step
+    constexpr float BASE = W8 ? 128.0f : MM::BASE;
+    __shared__ __attribute__((aligned(1024))) char smem[W8 ? SMEM8 : SMEM];
 
     const int bid = xcd_swizzle(blockIdx.x, tiles_m * tiles_n);
     constexpr int GM = 8;
@@ -520,7 +563,7 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
     const int M = (int)p.M, N = (int)p.N, K = (int)p.K, G = (int)p.group;
     const int m0 = tm * BM, n0 = tn * BN;
     const int rows = M - m0 < BM ? M - m0 : BM;
-    const int nk = K / KS, kb_n = K / KS;  // steps; NZ blocks along K per column block
+    const int nk = K / KSW, kb_n = K / KSW;  // steps; NZ blocks along K per column block
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -531,10 +574,16 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
     const uint32_t ldx = (uint32_t)K * 2u;
     const __amdgpu_buffer_rsrc_t rx =
         make_rsrc(static_cast<const char*>(p.x) + (size_t)m0 * ldx, (uint32_t)(rows - 1) * ldx + ldx);
-    // an instruction covers rows 4q..4q+3: lane l -> row 4q + (l>>4), LDS chunk l&15, k chunk (l&15) ^ (row&15)
+    // int4: an instruction covers rows 4q..4q+3: lane l -> row 4q + (l>>4), LDS chunk l&15, k chunk
+    // (l&15) ^ (row&15); W8: rows 8q..8q+7: lane l -> row 8q + (l>>3), LDS chunk l&7, k chunk (l&7) ^ (row&7)
     auto vx = [&](int q) {
-        const int row = 4 * q + (lane >> 4);
-        return (uint32_t)row * ldx + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+        if constexpr (W8) {
+            const int row = 8 * q + (lane >> 3);
+            return (uint32_t)row * ldx + 16u * (uint32_t)((lane & 7) ^ (row & 7));
+        } else {
+            const int row = 4 * q + (lane >> 4);
+            return (uint32_t)row * ldx + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+        }
     };
     // the 16 NZ blocks of the column block: block i of step s at ((n0/16 + i) * kb_n + s) KB
     const __amdgpu_buffer_rsrc_t rw =
@@ -547,20 +596,20 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
     const uint32_t l32 = 16u * (uint32_t)(lane & 31);
 
     auto issue = [&](int s) {
-        const uint32_t base = sbase + (uint32_t)(s % NSTG) * STAGE;
+        const uint32_t base = sbase + (uint32_t)(s % NSTG) * STG;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < XB / 8192; ++u) {  // the stage's activation rows, 1 KB per DMA
             const int q = wave + 8 * u;
-            dma16(rx, base + (uint32_t)q * 1024u, vx(q), (uint32_t)s * (uint32_t)(KS * 2));
+            dma16(rx, base + (uint32_t)q * 1024u, vx(q), (uint32_t)s * (uint32_t)(KSW * 2));
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int i = wave + 8 * u;
-            dma16(rw, base + X_BYTES + (uint32_t)i * 1024u, (uint32_t)i * (uint32_t)kb_n * 1024u + 16u * lane,
+            dma16(rw, base + XB + (uint32_t)i * 1024u, (uint32_t)i * (uint32_t)kb_n * 1024u + 16u * lane,
                   (uint32_t)s * 1024u);
         }
-        const uint32_t g = (uint32_t)(s * KS / G);
-        const uint32_t sdst = base + X_BYTES + W_BYTES;
+        const uint32_t g = (uint32_t)(s * KSW / G);
+        const uint32_t sdst = base + XB + W_BYTES;
         if (wave == 0) dma16(rs, sdst, (g * (uint32_t)N + (uint32_t)n0) * 2u + l32, 0);
         if (HAS_OFF && wave == 1) dma16(ro, sdst + 1024u, (g * (uint32_t)N + (uint32_t)n0) * 2u + l32, 0);
         if (wave == NSC - 1) dma16(rxs, sdst + 2048u, (g * (uint32_t)M + (uint32_t)m0) * 4u + l32, 0);
@@ -577,9 +626,10 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
     for (int s = 0; s < 2 && s < nk; ++s) issue(s);
     for (int s = 0; s < nk; ++s) {
         // stage s has landed once at most stage s+1's DMAs are outstanding
-        if (s + 1 < nk) {
-            if (more) __builtin_amdgcn_s_waitcnt(vmcnt_imm(7));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(6));
+        if (s + 1 < nk) {  // one step's DMAs: XB / 8 KB activation, 2 weight (+1 group row for waves < NSC)
+            constexpr int PER = XB / 8192 + 2;
+            if (more) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER + 1));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         }
@@ -587,12 +637,12 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
         __syncthreads();  // stage s visible to every wave; every wave is done with stage s-1
         __builtin_amdgcn_sched_barrier(0);
         if (s + 2 < nk) issue(s + 2);  // into the buffer of stage s-1
-        const char* As = smem + (s % NSTG) * STAGE;
-        const char* Bs = As + X_BYTES;
+        const char* As = smem + (s % NSTG) * STG;
+        const char* Bs = As + XB;
         u32x4 bw[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const u32x4*>(Bs + (2 * wave + j) * 1024 + 16 * lane);
-        const char* sc = As + X_BYTES + W_BYTES;
+        const char* sc = As + XB + W_BYTES;
         // the group's per-column factors s and s * (offset - BASE) of this wave's columns
         auto col_factors = [&](float (&sf)[TN], float (&sx)[TN]) {
 #pragma unroll
@@ -601,7 +651,7 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
                 sf[j] = load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 2 * col), p.s_dtype);
                 const float of =
                     HAS_OFF ? load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 1024 + 2 * col), p.s_dtype) : 0.0f;
-                sx[j] = sf[j] * (of - MM::BASE);
+                sx[j] = sf[j] * (of - BASE);
             }
         };
         auto fold_row = [&](int i, const float (&sf)[TN], const float (&sx)[TN]) {
@@ -612,24 +662,31 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
                 for (int r = 0; r < 4; ++r)
                     acc[i][j][r] = __builtin_fmaf(sf[j], ag[i][j][r], __builtin_fmaf(sx[j], xs[r], acc[i][j][r]));
         };
+        // k-step t's operands: the activation fragments of the wave's 8 row tiles, the weight of its 2 blocks
+        auto a_frag = [&](int i, int t) {
+            const int r = 16 * i + fr;
+            if constexpr (W8) return *reinterpret_cast<const u32x4*>(As + r * 128 + 16 * ((2 * g4 + t) ^ (r & 7)));
+            else return *reinterpret_cast<const u32x4*>(As + r * 256 + 16 * ((4 * t + g4) ^ (r & 15)));
+        };
+        auto b_op = [&](int j, int t) {
+            if constexpr (W8) return nz8_operand<DT>(bw[j][2 * t], bw[j][2 * t + 1]);
+            else return nz_operand<MM::MAGIC>(bw[j][t]);
+        };
         if constexpr (G1) {
             float sf[TN], sx[TN];
             col_factors(sf, sx);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+            for (int t = 0; t < NKT; ++t) {
                 u32x4 af[TM], b[TN];
 #pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const int r = 16 * i + fr;
-                    af[i] = *reinterpret_cast<const u32x4*>(As + r * 256 + 16 * ((4 * t + g4) ^ (r & 15)));
-                }
+                for (int i = 0; i < TM; ++i) af[i] = a_frag(i, t);
 #pragma unroll
-                for (int j = 0; j < TN; ++j) b[j] = nz_operand<MM::MAGIC>(bw[j][t]);
+                for (int j = 0; j < TN; ++j) b[j] = b_op(j, t);
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
 #pragma unroll
                     for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], b[j], t == 0 ? zero4 : ag[i][j]);
-                    if (t == 3 && i >= 2) fold_row(i - 2, sf, sx);  // two row tiles behind the MFMAs
+                    if (t == NKT - 1 && i >= 2) fold_row(i - 2, sf, sx);  // two row tiles behind the MFMAs
                 }
             }
             fold_row(TM - 2, sf, sx);
@@ -637,21 +694,18 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
             continue;
         }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < NKT; ++t) {
             u32x4 af[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int r = 16 * i + fr;
-                af[i] = *reinterpret_cast<const u32x4*>(As + r * 256 + 16 * ((4 * t + g4) ^ (r & 15)));
-            }
+            for (int i = 0; i < TM; ++i) af[i] = a_frag(i, t);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = nz_operand<MM::MAGIC>(bw[j][t]);
+            for (int j = 0; j < TN; ++j) b[j] = b_op(j, t);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], b[j], ag[i][j]);
         }
-        if (((s + 1) * KS) % G == 0) {  // the group ends with this step: fold it into acc
+        if (((s + 1) * KSW) % G == 0) {  // the group ends with this step: fold it into acc
             float sf[TN], sx[TN];
             col_factors(sf, sx);
 #pragma unroll
@@ -811,10 +865,12 @@ struct NzGemmPlan {
 NzGemmPlan nzg_plan(const WqbmmArgs& p) {
     NzGemmPlan g{false, 0, 0};
     const int64_t G = p.group == 0 ? p.K : p.group;
-    if (p.w_dtype != QK_I4_NZ || p.M <= 64 || p.N <= 0 || p.N % nzg::BN != 0 || p.K <= 0 || p.K % nzg::KS != 0)
+    const bool w8 = p.w_dtype == QK_I8_NZ;
+    const int64_t ks = w8 ? nzg::KS8 : nzg::KS;  // K rows per step
+    if (!(p.w_dtype == QK_I4_NZ || w8) || p.M <= 64 || p.N <= 0 || p.N % nzg::BN != 0 || p.K <= 0 || p.K % ks != 0)
         return g;
-    if (G <= 0 || G % nzg::KS != 0 || p.K % G != 0) return g;
-    if (p.M * p.K * 2 >= ((int64_t)1 << 31) || p.K * p.N / 2 >= ((int64_t)1 << 31) ||
+    if (G <= 0 || G % ks != 0 || p.K % G != 0) return g;
+    if (p.M * p.K * 2 >= ((int64_t)1 << 31) || p.K * p.N / (w8 ? 1 : 2) >= ((int64_t)1 << 31) ||
         (p.K / G) * p.N * 2 >= ((int64_t)1 << 31) || (p.K / G) * p.M * 4 >= ((int64_t)1 << 31) ||
         p.M * p.N >= ((int64_t)1 << 31))
         return g;
@@ -835,18 +891,24 @@ size_t nzg_workspace(const WqbmmArgs& p) {
     return QK_SPLIT_COUNTER_BYTES + (size_t)(p.K / G) * (size_t)p.M * sizeof(float);
 }
 
+template <int DT, bool W8>
+void launch_nzg_k(const WqbmmArgs& p, const NzGemmPlan& g, const float* xsum, hipStream_t stream) {
+    const dim3 grid((uint32_t)(g.tiles_m * g.tiles_n)), block(nzg::NT);
+    if (p.group == (W8 ? nzg::KS8 : nzg::KS)) {
+        if (p.offset) w4nz_gemm<DT, true, true, W8><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+        else w4nz_gemm<DT, false, true, W8><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+    } else {
+        if (p.offset) w4nz_gemm<DT, true, false, W8><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+        else w4nz_gemm<DT, false, false, W8><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+    }
+}
+
 template <int DT>
 hipError_t launch_nzg_dt(const WqbmmArgs& p, const NzGemmPlan& g, float* xsum, hipStream_t stream) {
     hipError_t e = launch_w4_xsum(p, xsum, stream);
     if (e != hipSuccess) return e;
-    const dim3 grid((uint32_t)(g.tiles_m * g.tiles_n)), block(nzg::NT);
-    if (p.group == nzg::KS) {
-        if (p.offset) w4nz_gemm<DT, true, true><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
-        else w4nz_gemm<DT, false, true><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
-    } else {
-        if (p.offset) w4nz_gemm<DT, true, false><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
-        else w4nz_gemm<DT, false, false><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
-    }
+    if (p.w_dtype == QK_I8_NZ) launch_nzg_k<DT, true>(p, g, xsum, stream);
+    else launch_nzg_k<DT, false>(p, g, xsum, stream);
     return hipGetLastError();
 }
 
@@ -927,19 +989,20 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
     return launch_weight_quant_bmm(q, rest ? ws + QK_SPLIT_COUNTER_BYTES + nd_bytes : nullptr, rest, stream);
 }
 
-// Row-major int4 [K, N/8] weights at large M: the call casts the weight into its workspace
+// Row-major int4 [K, N/8] and int8 [K, N] weights at large M: the call casts the weight into its workspace
 // ([QK_SPLIT_COUNTER_BYTES, unused][NZ weight][x group sums fp32 [K/G][M]]) and runs the NZ prefill GEMM on
-// it.  The cast reads and writes the packed weight once (K * N bytes in all); from M = 1024 the NZ GEMM saves
-// more than that costs (cfg3's 4096 x 11008 weight: cast ~15 us, NZ GEMM ~195 us against ~250 us for the
-// row-major prefill kernel).  The debug overrides that force or disable a prefill kernel switch it off.
+// it.  The cast reads and writes the weight once; from M = 1024 the NZ GEMM saves more than that costs (cfg3's
+// 4096 x 11008 weight: int4 cast ~15 us, NZ GEMM ~195 us against ~250 us for the row-major prefill kernel).
+// The debug overrides that force or disable a prefill kernel switch it off.
 constexpr int64_t kCastNzMinM = 1024;
 
 size_t w4_cast_nz_workspace(const WqbmmArgs& p) {
     const PlanOverride& ov = plan_override();
-    if (p.w_dtype != QK_I32 || p.M < kCastNzMinM || ov.w4nz_off || ov.w4_gemm != 0) return 0;
+    if (!(p.w_dtype == QK_I32 || p.w_dtype == QK_I8) || p.M < kCastNzMinM || ov.w4nz_off || ov.w4_gemm != 0)
+        return 0;
     WqbmmArgs q = p;
     q.w = reinterpret_cast<const void*>((uintptr_t)256);  // the cast's destination: 256-byte aligned
-    q.w_dtype = QK_I4_NZ;
+    q.w_dtype = p.w_dtype == QK_I8 ? QK_I8_NZ : QK_I4_NZ;
     if (!nzg_plan(q).ok) return 0;
     return round256(QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)) + (nzg_workspace(q) - QK_SPLIT_COUNTER_BYTES));
 }
@@ -948,13 +1011,17 @@ bool launch_w4_cast_nz(const WqbmmArgs& p, void* workspace, size_t ws_bytes, hip
     const size_t need = w4_cast_nz_workspace(p);
     if (need == 0 || !workspace || ws_bytes < need || (uintptr_t)workspace % 256 != 0) return false;
     char* ws = static_cast<char*>(workspace);
-    int32_t* nz = reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES);
+    void* nz = ws + QK_SPLIT_COUNTER_BYTES;
+    const bool w8 = p.w_dtype == QK_I8;
     WqbmmArgs q = p;
     q.w = nz;
-    q.w_dtype = QK_I4_NZ;
+    q.w_dtype = w8 ? QK_I8_NZ : QK_I4_NZ;
     const NzGemmPlan g = nzg_plan(q);  // with the call's own operands (their alignment)
     if (!g.ok) return false;
-    hipError_t e = launch_w4_nz_cast(static_cast<const int32_t*>(p.w), true, p.K, p.N, nz, stream);
+    hipError_t e = w8 ? launch_w8_nz_cast(static_cast<const int8_t*>(p.w), true, p.K, p.N, static_cast<int8_t*>(nz),
+                                          stream)
+                      : launch_w4_nz_cast(static_cast<const int32_t*>(p.w), true, p.K, p.N, static_cast<int32_t*>(nz),
+                                          stream);
     if (e == hipSuccess) {
         float* xs = reinterpret_cast<float*>(ws + QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)));
         e = p.x_dtype == QK_BF16 ? launch_nzg_dt<QK_BF16>(q, g, xs, stream) : launch_nzg_dt<QK_F16>(q, g, xs, stream);

@@ -428,8 +428,8 @@ int weight_quant_bmm_run(const char* op, const void* x, int x_dtype, const void*
     if (M == 0 || N == 0) return QK_OK;
     if (!out || (K > 0 && (!x || !weight || !antiquant_scale))) return fail(QK_ERR_ARG, "%s: null pointer", op);
     // The no-allocation scratch runs the op's own plan (so the same kernels, the same bits) wherever that
-    // plan's workspace fits in it; otherwise the plan without the cast to NZ of a row-major int4 weight, whose
-    // cast weight is what does not fit.
+    // plan's workspace fits in it; otherwise the plan without the cast to NZ of a row-major int4 / int8 weight,
+    // whose cast weight is what does not fit.
     size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, false);
     if (scratch && need > QK_NOALLOC_SCRATCH_BYTES)
         need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, true);

@@ -231,10 +231,10 @@ int qk_weight_quant_bmm(const void* x, int x_dtype,
  * array of QK_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, and
  * the call allocates nothing.  Where the workspace qk_weight_quant_bmm_workspace_size
  * reports fits in that array, the call runs exactly the kernels qk_weight_quant_bmm
- * runs (the same bits).  Otherwise, for a row-major int4 weight at M >= 1024
- * whose cast to NZ is what does not fit, it runs the row-major prefill kernel
- * without the cast (within the same 1e-2 bar; on cfg3's shape, N = 11008,
- * K = 4096, 128-row groups, the same bits); a shape whose scratch exceeds
+ * runs (the same bits).  Otherwise, for a row-major int4 or int8 weight at
+ * M >= 1024 whose cast to NZ is what does not fit, it runs the row-major
+ * prefill kernel without the cast (within the same 1e-2 bar; for int4 on
+ * cfg3's shape, N = 11008, K = 4096, 128-row groups, the same bits); a shape whose scratch exceeds
  * QK_NOALLOC_SCRATCH_BYTES even so is refused with QK_ERR_UNSUPPORTED.  The call uses the array of the current device, so
  * `stream` must belong to it.  All calls on one GPU share that array: calls
  * that may run at the same time on one GPU (several streams or threads) race

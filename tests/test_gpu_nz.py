@@ -5,8 +5,9 @@
 * npu_weight_quant_batchmatmul on NZ weights: within rtol 1e-2 / atol 1e-2
   of the float64 oracle on the same seeded inputs (the bar of the row-major
   path), through the NZ decode kernel (M <= 64), the NZ prefill kernel (M > 64
-  with enough 128 x 256 tiles) and through the unpack-to-ND fallback (short
-  groups, K with no even wave split, few prefill tiles, forced off).
+  with enough 128 x 256 tiles; int4 and int8 weights) and through the
+  unpack-to-ND fallback (short groups, K with no even wave split, few prefill
+  tiles, forced off).
 """
 import ctypes
 
@@ -377,6 +378,55 @@ def test_w8a16_nz_shapes(ops, oracle, M, N, K, group, offset, x_dtype, bias):
         d["x"].to(DEV), nz, d["scale"].to(DEV), None if d["offset"] is None else d["offset"].to(DEV),
         bias=None if b is None else b.to(DEV), antiquant_group_size=group)
     _close(out, _w8_ref(oracle, d, group, x_dtype, bias=b), x_dtype)
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,bias", [
+    (2048, 11008, 4096, 128, True, torch.bfloat16, False),   # the cfg3 prefill shape with int8 weights
+    (320, 8192, 1024, 64, False, torch.float16, True),       # 64-row groups: one step per group; ragged rows
+    (512, 6144, 768, 0, True, torch.bfloat16, False),        # per channel: one group of 768 rows
+    (1000, 4096, 2048, 256, True, torch.bfloat16, True),     # four steps per group, last row tile of 104 rows
+])
+def test_w8a16_nz_prefill_kernel(ops, oracle, M, N, K, group, offset, x_dtype, bias):
+    """The NZ prefill kernel on int8 NZ weights (64-row steps, one 1 KB block per 16 columns per step): every
+    output element within rtol/atol 1e-2 of the float64 dequant-matmul, which is pinned against the C oracle on
+    four rows; and against the row-major int8 path on the same weight."""
+    say(f"w8a16 NZ prefill M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    d = _w8(M, N, K, group, offset, x_dtype, seed=M + N + K + 3)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(8)).to(x_dtype) if bias else None
+    nz = ops.npu_format_cast(d["w"].to(DEV), 29)
+    out = ops.npu_weight_quant_batchmatmul(
+        d["x"].to(DEV), nz, d["scale"].to(DEV), None if d["offset"] is None else d["offset"].to(DEV),
+        bias=None if b is None else b.to(DEV), antiquant_group_size=group)
+    ref64 = exact.wq_dequant_matmul(d["x"], d["w"], d["scale"], d["offset"], group, bias=b)
+    rows = np.r_[0:2, M - 2:M]
+    pin = _w8_ref(oracle, dict(d, x=d["x"][rows]), group, x_dtype, bias=b)
+    pin_diff = (W.from_bits(pin, x_dtype).float() - ref64[rows].float()).abs()
+    assert pin_diff.max().item() <= 2.0**-7 * ref64[rows].abs().max().item() + 1e-3
+    torch.testing.assert_close(out.cpu().float(), ref64.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,bias", [
+    (1024, 2048, 1024, 128, True, torch.bfloat16, True),     # 8 x 8 tiles, two steps per group
+    (1100, 2048, 2048, 64, False, torch.float16, False),     # one step per group, last row tile of 76 rows
+])
+def test_w8a16_row_major_cast_to_nz(ops, oracle, plan, M, N, K, group, offset, x_dtype, bias):
+    """M >= 1024 on a row-major int8 [K, N] weight: the call casts the weight to NZ in its workspace (which the
+    size query reports) and runs the NZ prefill kernel on the copy; within rtol/atol 1e-2 of the float64
+    dequant-matmul and of the row-major prefill kernel (the cast switched off by the debug override)."""
+    say(f"w8a16 row-major cast to NZ M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    L = ops.abi()
+    ws = ctypes.c_size_t(0)
+    assert L.qk_weight_quant_bmm_workspace_size(M, N, K, ops.QK_I8, group, ctypes.byref(ws)) == 0
+    assert ws.value >= 4096 + K * N, "the workspace holds the cast weight"
+    d = _w8(M, N, K, group, offset, x_dtype, seed=M + N + K + 4)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(9)).to(x_dtype) if bias else None
+    args = (d["x"].to(DEV), d["w"].to(DEV), d["scale"].to(DEV), None if d["offset"] is None else d["offset"].to(DEV))
+    out = ops.npu_weight_quant_batchmatmul(*args, bias=None if b is None else b.to(DEV), antiquant_group_size=group)
+    ref64 = exact.wq_dequant_matmul(d["x"], d["w"], d["scale"], d["offset"], group, bias=b)
+    torch.testing.assert_close(out.cpu().float(), ref64.float(), rtol=1e-2, atol=1e-2)
+    plan("w4nz=off")
+    rm = ops.npu_weight_quant_batchmatmul(*args, bias=None if b is None else b.to(DEV), antiquant_group_size=group)
+    torch.testing.assert_close(out.float(), rm.float(), rtol=1e-2, atol=1e-2)
 
 
 def test_abi_w8_nz(ops, oracle):
