@@ -83,3 +83,45 @@ def test_graph_replays_match_eager(ops):
         torch.cuda.synchronize()
         for name, got, ref in zip(("y", "scale", "w8a8", "w4a16", "w4a16_nz"), again, eager):
             assert torch.equal(got, ref), f"eager call after replay {r}: {name} differs"
+
+
+def test_graph_replays_mlp_block(ops):
+    """The cfg5 quantized MLP block on NZ weights under capture: RMSNorm + quant, the gate-up GEMM with the SwiGLU
+    and the row absmax in its epilogue (h and the partials in a workspace the op takes from the allocator), the
+    premax quantizer, and the down projection's 128-row K split (tagged counters, int32 partials, reduce)."""
+    from op_plugin_amd.mlp import quant_mlp
+    say("HIP graph: cfg5 MLP block (512 x 4096 x 14336) on NZ weights, 3 replays")
+    g = torch.Generator(device=DEV).manual_seed(5)
+    T, H, I = 512, 4096, 14336
+    x = torch.randn((T, H), generator=g, device=DEV).to(torch.bfloat16)
+    gamma = (1 + 0.02 * torch.randn(H, generator=g, device=DEV)).to(torch.bfloat16)
+    wgu = ops.npu_format_cast(torch.randint(-127, 128, (H, 2 * I), generator=g, device=DEV, dtype=torch.int8), 29)
+    sgu = 1e-3 + 9e-3 * torch.rand(2 * I, generator=g, device=DEV)
+    wd = ops.npu_format_cast(torch.randint(-127, 128, (I, H), generator=g, device=DEV, dtype=torch.int8), 29)
+    sd = 1e-3 + 9e-3 * torch.rand(H, generator=g, device=DEV)
+
+    def run():
+        return quant_mlp(x, gamma, wgu, sgu, wd, sd)
+
+    eager = run().clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = run()
+    torch.cuda.synchronize()
+    for r in range(3):
+        captured.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {r}: the block's output differs from the eager call"
+        again = run()
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager), f"eager call after replay {r} differs"
