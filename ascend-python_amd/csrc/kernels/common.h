@@ -382,6 +382,11 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   mid_bn=<64|128>                                 qmm_mid: column block (128 only for a [K,N] weight)
 //   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
 //   w4nz=off                                        NZ int4 weights: unpack to ND and take the row-major kernels
+//   nzg_sk=<0|1|tailfirst>                          NZ prefill GEMM: 0 whole tiles per workgroup (no stream-K);
+//                                                   tailfirst: stream-K with each workgroup's tail segment run
+//                                                   first, so it arrives before the head it would continue
+//                                                   from and runs the whole tile itself (the fallback path)
+//   nzg_sk_dp=<n>                                   NZ prefill stream-K: n whole-tile rounds first
 //   w4nz_wg=<n>                                     NZ decode kernel: workgroups along N
 //   w4nz_nit=<1..8>                                 NZ decode kernel: 128-row superblocks per wave (K/128 must
 //                                                   split evenly into at most 16 waves of them)
@@ -396,6 +401,8 @@ struct PlanOverride {
     int mid_bm = 0, mid_split = 0, mid_bn = 0;
     int skinny_splits = 0;
     bool w4nz_off = false;
+    int nzg_sk = 1;
+    int nzg_sk_dp = -1;  // whole-tile rounds before the stream-K share (-1: the planner's choice)
     int w4nz_wg = 0, w4nz_nit = 0;
 };
 const PlanOverride& plan_override();
@@ -447,20 +454,24 @@ struct WqbmmArgs {
 hipError_t launch_weight_quant_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 // xsum[g][m] = fp32 sum of x[m][k] over group g (G a multiple of 64), for the prefill kernels' group algebra
 hipError_t launch_w4_xsum(const WqbmmArgs& p, float* xsum, hipStream_t stream);
-// no_cast: the size without the plan that casts a row-major int4 weight to NZ in the workspace (for
-// callers whose scratch cannot hold the cast weight; the launch then runs the row-major kernels)
-size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group, bool no_cast = false);
+// Workspace sizes of one call, largest first.  kWsFull: the plan as planned.  kWsNoStreamK: without the NZ
+// prefill kernel's stream-K partials (the same kernels and the same bits, tiles whole per workgroup).
+// kWsNoCast: also without the plan that casts a row-major int4 / int8 weight to NZ in the workspace (the launch
+// then runs the row-major kernels).  For callers whose scratch is bounded; a launch takes the largest plan
+// its workspace holds.
+constexpr int kWsFull = 0, kWsNoStreamK = 1, kWsNoCast = 2;
+size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group, int level = kWsFull);
 
 // NZ weights (nz_weights.hip): the ND <-> NZ casts (int4, int8) and the weight-quant matmul on NZ weights.
 hipError_t launch_w4_nz_cast(const int32_t* src, bool to_nz, int64_t K, int64_t N, int32_t* dst, hipStream_t stream);
 hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N, int8_t* dst, hipStream_t stream);
 // int8 [N, K] -> [K, N]
 hipError_t launch_w8_nk_transpose(const int8_t* src, int64_t K, int64_t N, int8_t* dst, hipStream_t stream);
-size_t w4_nz_workspace(const WqbmmArgs& args);
+size_t w4_nz_workspace(const WqbmmArgs& args, bool stream_k = true);
 // A row-major int4 or int8 weight at large M: cast to NZ into the workspace, then the NZ prefill GEMM.  The size is 0
 // when the plan does not apply; the launch returns false (running nothing) when it does not apply to these
 // operands or the workspace cannot hold it, else true with the launch status in *err.
-size_t w4_cast_nz_workspace(const WqbmmArgs& args);
+size_t w4_cast_nz_workspace(const WqbmmArgs& args, bool stream_k = true);
 bool launch_w4_cast_nz(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream, hipError_t* err);
 hipError_t launch_w4_nz_bmm(const WqbmmArgs& args, void* workspace, size_t ws_bytes, hipStream_t stream);
 

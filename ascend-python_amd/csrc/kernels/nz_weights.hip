@@ -30,6 +30,8 @@
 // superblock with the algebra of the row-major kernels,
 //   acc += s * sum_k x*(w + BASE) + s*(offset - BASE) * sum_k x,
 // and the waves' sums are added through LDS in K order (deterministic).
+#include <atomic>
+
 #include "common.h"
 
 namespace qk {
@@ -538,9 +540,11 @@ constexpr int SMEM8 = RING8 > BM * OROWB ? RING8 : BM * OROWB;
 // 16g+15), converted to offset-binary 16-bit values w + 128 (exact); the A operand is the matching 16 bytes of x,
 // k = 16g + 8t .. +8, so both operands run over the step's 64 k in the same permuted order.  The fold's base is
 // 128 instead of the int4 magic base.
-template <int DT, bool HAS_OFF, bool G1, bool W8 = false>
+template <int DT, bool HAS_OFF, bool G1, bool W8 = false, bool SK = false>
 __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, int tiles_n,
-                                                     const float* __restrict__ xsum) {
+                                                     const float* __restrict__ xsum, uint64_t* __restrict__ ctr,
+                                                     float* __restrict__ part, uint64_t tag, int tail_first,
+                                                     int dp_rounds) {
     typedef Mfma<DT> MM;
     using namespace nzg;
     constexpr int TM = 8, TN = 2;
@@ -552,28 +556,50 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
     constexpr float BASE = W8 ? 128.0f : MM::BASE;
     __shared__ __attribute__((aligned(1024))) char smem[W8 ? SMEM8 : SMEM];
 
-    const int bid = xcd_swizzle(blockIdx.x, tiles_m * tiles_n);
+    const int M = (int)p.M, N = (int)p.N, K = (int)p.K, G = (int)p.group;
+    const int kb_n = K / KSW;                 // NZ blocks along K per column block
+    const int gsteps = G / KSW, nu = K / G;   // steps per group; groups per tile
+    const int ntiles = tiles_m * tiles_n;
+    // tile t -> (tm, tn): groups of 8 row tiles, row tile fastest, so neighbouring tiles share a column block
     constexpr int GM = 8;
     const int per_group = GM * tiles_n;
-    const int grp = bid / per_group;
-    const int first_m = grp * GM;
-    const int gm = min(tiles_m - first_m, GM);
-    const int tm = first_m + (bid % per_group) % gm;
-    const int tn = (bid % per_group) / gm;
-    const int M = (int)p.M, N = (int)p.N, K = (int)p.K, G = (int)p.group;
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int rows = M - m0 < BM ? M - m0 : BM;
-    const int nk = K / KSW, kb_n = K / KSW;  // steps; NZ blocks along K per column block
+    auto tile_mn = [&](int t, int& tm, int& tn) {
+        const int first_m = (t / per_group) * GM;
+        const int gm = min(tiles_m - first_m, GM);
+        tm = first_m + (t % per_group) % gm;
+        tn = (t % per_group) / gm;
+    };
+
+    // The workgroup's segments, in the order it runs them.  Whole tiles: one, the workgroup's own.  Stream-K
+    // (one workgroup per CU): range r of the ntiles * nu groups, tile-major, is r * U / P .. (r+1) * U / P; it
+    // runs first the head of the tile its range ends in (groups 0 .. ub of tile tb, handed on to range r + 1
+    // through partial slot r), then its whole tiles, then the tail of the tile its range starts in (groups
+    // ua .. nu of tile ta), which continues from range r - 1's head.  Each tile has at most two segments (a
+    // range holds at least one tile's groups).
+    int r = 0, ta = 0, ua = 0, tb = 0, ub = 0, nseg = 1;
+    bool has_head = false, has_tail = false;
+    const int P = (int)gridDim.x;
+    if constexpr (SK) {
+        r = xcd_swizzle(blockIdx.x, P);
+        const int D = dp_rounds * P;  // tiles run whole first, one per workgroup per round (lockstep)
+        const int64_t U = (int64_t)(ntiles - D) * nu;
+        const int64_t a = (int64_t)r * U / P, b = (int64_t)(r + 1) * U / P;
+        ta = D + (int)(a / nu);
+        ua = (int)(a % nu);
+        tb = D + (int)((b - 1) / nu);
+        ub = (int)(b - (int64_t)(tb - D) * nu);
+        has_head = ub < nu;
+        has_tail = ua != 0;
+        nseg = dp_rounds + (int)has_head + (tb - (int)has_head) - (ta + (int)has_tail) + 1 + (int)has_tail;
+    } else {
+        ta = xcd_swizzle(blockIdx.x, ntiles);
+    }
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fr = lane & 15, g4 = lane >> 4;
     const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
-
-    // activations: rows past M read as zeros (range-checked offsets), K*2 bytes per row
     const uint32_t ldx = (uint32_t)K * 2u;
-    const __amdgpu_buffer_rsrc_t rx =
-        make_rsrc(static_cast<const char*>(p.x) + (size_t)m0 * ldx, (uint32_t)(rows - 1) * ldx + ldx);
     // int4: an instruction covers rows 4q..4q+3: lane l -> row 4q + (l>>4), LDS chunk l&15, k chunk
     // (l&15) ^ (row&15); W8: rows 8q..8q+7: lane l -> row 8q + (l>>3), LDS chunk l&7, k chunk (l&7) ^ (row&7)
     auto vx = [&](int q) {
@@ -585,166 +611,244 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
             return (uint32_t)row * ldx + 16u * (uint32_t)((lane & 15) ^ (row & 15));
         }
     };
-    // the 16 NZ blocks of the column block: block i of step s at ((n0/16 + i) * kb_n + s) KB
-    const __amdgpu_buffer_rsrc_t rw =
-        make_rsrc(static_cast<const char*>(p.w) + (size_t)(n0 / 16) * kb_n * 1024, (uint32_t)(16 * kb_n * 1024));
     // group rows: 512 bytes each (lanes 32..63 repeat 0..31 into the unused upper half of the KB)
     const uint32_t nsb = (uint32_t)(K / G) * (uint32_t)N * 2u;
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scale, nsb);
     const __amdgpu_buffer_rsrc_t ro = make_rsrc(HAS_OFF ? p.offset : p.scale, nsb);
     const __amdgpu_buffer_rsrc_t rxs = make_rsrc(xsum, (uint32_t)(K / G) * (uint32_t)M * 4u);
     const uint32_t l32 = 16u * (uint32_t)(lane & 31);
-
-    auto issue = [&](int s) {
-        const uint32_t base = sbase + (uint32_t)(s % NSTG) * STG;
-#pragma unroll
-        for (int u = 0; u < XB / 8192; ++u) {  // the stage's activation rows, 1 KB per DMA
-            const int q = wave + 8 * u;
-            dma16(rx, base + (uint32_t)q * 1024u, vx(q), (uint32_t)s * (uint32_t)(KSW * 2));
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int i = wave + 8 * u;
-            dma16(rw, base + XB + (uint32_t)i * 1024u, (uint32_t)i * (uint32_t)kb_n * 1024u + 16u * lane,
-                  (uint32_t)s * 1024u);
-        }
-        const uint32_t g = (uint32_t)(s * KSW / G);
-        const uint32_t sdst = base + XB + W_BYTES;
-        if (wave == 0) dma16(rs, sdst, (g * (uint32_t)N + (uint32_t)n0) * 2u + l32, 0);
-        if (HAS_OFF && wave == 1) dma16(ro, sdst + 1024u, (g * (uint32_t)N + (uint32_t)n0) * 2u + l32, 0);
-        if (wave == NSC - 1) dma16(rxs, sdst + 2048u, (g * (uint32_t)M + (uint32_t)m0) * 4u + l32, 0);
+    // stream-K partial slots: slot [wave][row tile][column tile][lane] x 16 B, whole KB per store instruction
+    constexpr uint32_t SLOT = BM * BN * 4;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, SK ? (uint32_t)(gridDim.x - 1) * SLOT : 0u);
+    auto part_off = [&](int slot, int i, int j) {
+        return (uint32_t)slot * SLOT + (uint32_t)((wave * TM * TN + i * TN + j) * 1024 + 16 * lane);
     };
 
-    f32x4 acc[TM][TN], ag[TM][TN];
-    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = ag[i][j] = zero4;
-
-    const bool more = wave < NSC;  // this wave issues one more DMA per step
-    for (int s = 0; s < 2 && s < nk; ++s) issue(s);
-    for (int s = 0; s < nk; ++s) {
-        // stage s has landed once at most stage s+1's DMAs are outstanding
-        if (s + 1 < nk) {  // one step's DMAs: XB / 8 KB activation, 2 weight (+1 group row for waves < NSC)
-            constexpr int PER = XB / 8192 + 2;
-            if (more) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER + 1));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
-        } else {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();  // stage s visible to every wave; every wave is done with stage s-1
-        __builtin_amdgcn_sched_barrier(0);
-        if (s + 2 < nk) issue(s + 2);  // into the buffer of stage s-1
-        const char* As = smem + (s % NSTG) * STG;
-        const char* Bs = As + XB;
-        u32x4 bw[TN];
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const u32x4*>(Bs + (2 * wave + j) * 1024 + 16 * lane);
-        const char* sc = As + XB + W_BYTES;
-        // the group's per-column factors s and s * (offset - BASE) of this wave's columns
-        auto col_factors = [&](float (&sf)[TN], float (&sx)[TN]) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int col = 32 * wave + 16 * j + fr;
-                sf[j] = load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 2 * col), p.s_dtype);
-                const float of =
-                    HAS_OFF ? load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 1024 + 2 * col), p.s_dtype) : 0.0f;
-                sx[j] = sf[j] * (of - BASE);
+    for (int seg = 0; seg < nseg; ++seg) {
+        int t = ta, u0 = 0, u1 = nu;
+        bool head = false, tail = false;
+        if constexpr (SK) {
+            // first the lockstep rounds; then the stream-K share.  tail_first (a debug order): the tail
+            // segment first, then the head, then the whole tiles
+            const int sg = seg - dp_rounds;
+            const int hs = tail_first ? (int)has_tail : 0;                 // the head's position
+            const int ts = tail_first ? 0 : nseg - dp_rounds - 1;            // the tail's position
+            const int fs = tail_first ? (int)has_tail + (int)has_head : (int)has_head;  // the first whole tile's
+            if (sg < 0) {
+                t = seg * P + r;
+            } else if (has_head && sg == hs) {
+                t = tb;
+                u1 = ub;
+                head = true;
+            } else if (has_tail && sg == ts) {
+                u0 = ua;
+                tail = true;
+            } else {
+                t = ta + (int)has_tail + sg - fs;
             }
+        }
+        int tm, tn;
+        tile_mn(t, tm, tn);
+        const int m0 = tm * BM, n0 = tn * BN;
+        const int rows = M - m0 < BM ? M - m0 : BM;
+        // activations: rows past M read as zeros (range-checked offsets), K*2 bytes per row
+        const __amdgpu_buffer_rsrc_t rx =
+            make_rsrc(static_cast<const char*>(p.x) + (size_t)m0 * ldx, (uint32_t)(rows - 1) * ldx + ldx);
+        // the 16 NZ blocks of the column block: block i of step s at ((n0/16 + i) * kb_n + s) KB
+        const __amdgpu_buffer_rsrc_t rw =
+            make_rsrc(static_cast<const char*>(p.w) + (size_t)(n0 / 16) * kb_n * 1024, (uint32_t)(16 * kb_n * 1024));
+
+        auto issue = [&](int s) {
+            const uint32_t base = sbase + (uint32_t)(s % NSTG) * STG;
+#pragma unroll
+            for (int u = 0; u < XB / 8192; ++u) {  // the stage's activation rows, 1 KB per DMA
+                const int q = wave + 8 * u;
+                dma16(rx, base + (uint32_t)q * 1024u, vx(q), (uint32_t)s * (uint32_t)(KSW * 2));
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int i = wave + 8 * u;
+                dma16(rw, base + XB + (uint32_t)i * 1024u, (uint32_t)i * (uint32_t)kb_n * 1024u + 16u * lane,
+                      (uint32_t)s * 1024u);
+            }
+            const uint32_t g = (uint32_t)(s * KSW / G);
+            const uint32_t sdst = base + XB + W_BYTES;
+            if (wave == 0) dma16(rs, sdst, (g * (uint32_t)N + (uint32_t)n0) * 2u + l32, 0);
+            if (HAS_OFF && wave == 1) dma16(ro, sdst + 1024u, (g * (uint32_t)N + (uint32_t)n0) * 2u + l32, 0);
+            if (wave == NSC - 1) dma16(rxs, sdst + 2048u, (g * (uint32_t)M + (uint32_t)m0) * 4u + l32, 0);
         };
-        auto fold_row = [&](int i, const float (&sf)[TN], const float (&sx)[TN]) {
-            const f32x4 xs = *reinterpret_cast<const f32x4*>(sc + 2048 + 4 * (16 * i + 4 * g4));
+
+        f32x4 acc[TM][TN], ag[TM][TN];
+        const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    acc[i][j][r] = __builtin_fmaf(sf[j], ag[i][j][r], __builtin_fmaf(sx[j], xs[r], acc[i][j][r]));
-        };
-        // k-step t's operands: the activation fragments of the wave's 8 row tiles, the weight of its 2 blocks
-        auto a_frag = [&](int i, int t) {
-            const int r = 16 * i + fr;
-            if constexpr (W8) return *reinterpret_cast<const u32x4*>(As + r * 128 + 16 * ((2 * g4 + t) ^ (r & 7)));
-            else return *reinterpret_cast<const u32x4*>(As + r * 256 + 16 * ((4 * t + g4) ^ (r & 15)));
-        };
-        auto b_op = [&](int j, int t) {
-            if constexpr (W8) return nz8_operand<DT>(bw[j][2 * t], bw[j][2 * t + 1]);
-            else return nz_operand<MM::MAGIC>(bw[j][t]);
-        };
-        if constexpr (G1) {
-            float sf[TN], sx[TN];
-            col_factors(sf, sx);
+            for (int j = 0; j < TN; ++j) acc[i][j] = ag[i][j] = zero4;
+        int s0 = u0 * gsteps;
+        const int s1 = u1 * gsteps;
+        if constexpr (SK) {
+            if (tail) {
+                // continue from range r - 1's head if it has arrived (the usual case: it ran first there);
+                // otherwise run the whole tile here.  Either way the groups fold in order from zero.
+                if (splitk_last(ctr + (r - 1), 2u, tag)) {
 #pragma unroll
-            for (int t = 0; t < NKT; ++t) {
-                u32x4 af[TM], b[TN];
+                    for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int i = 0; i < TM; ++i) af[i] = a_frag(i, t);
-#pragma unroll
-                for (int j = 0; j < TN; ++j) b[j] = b_op(j, t);
-#pragma unroll
-                for (int i = 0; i < TM; ++i) {
-#pragma unroll
-                    for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], b[j], t == 0 ? zero4 : ag[i][j]);
-                    if (t == NKT - 1 && i >= 2) fold_row(i - 2, sf, sx);  // two row tiles behind the MFMAs
+                        for (int j = 0; j < TN; ++j) {
+                            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rp, part_off(r - 1, i, j), 0,
+                                                                                  kCoherent);
+                            acc[i][j] = __builtin_bit_cast(f32x4, v);
+                        }
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                } else {
+                    s0 = 0;
                 }
             }
-            fold_row(TM - 2, sf, sx);
-            fold_row(TM - 1, sf, sx);
-            continue;
         }
-#pragma unroll
-        for (int t = 0; t < NKT; ++t) {
-            u32x4 af[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = a_frag(i, t);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = b_op(j, t);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], b[j], ag[i][j]);
-        }
-        if (((s + 1) * KSW) % G == 0) {  // the group ends with this step: fold it into acc
-            float sf[TN], sx[TN];
-            col_factors(sf, sx);
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                fold_row(i, sf, sx);
-#pragma unroll
-                for (int j = 0; j < TN; ++j) ag[i][j] = zero4;
-            }
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    __syncthreads();  // every wave is past its last reads of the ring
 
-    // ---- epilogue: + bias, cast, staged through LDS for 16-byte row stores
-    float bv[TN];
+        const bool more = wave < NSC;  // this wave issues one more DMA per step
+        for (int s = s0; s < s0 + 2 && s < s1; ++s) issue(s);
+        for (int s = s0; s < s1; ++s) {
+            // stage s has landed once at most stage s+1's DMAs are outstanding
+            if (s + 1 < s1) {  // one step's DMAs: XB / 8 KB activation, 2 weight (+1 group row for waves < NSC)
+                constexpr int PER = XB / 8192 + 2;
+                if (more) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER + 1));
+                else __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();  // stage s visible to every wave; every wave is done with stage s-1
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 2 < s1) issue(s + 2);  // into the buffer of stage s-1
+            const char* As = smem + (s % NSTG) * STG;
+            const char* Bs = As + XB;
+            u32x4 bw[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-        bv[j] = p.bias_dtype ? load_scalar(p.bias, n0 + 32 * wave + 16 * j + fr, p.bias_dtype) : 0.0f;
-    uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+            for (int j = 0; j < TN; ++j)
+                bw[j] = *reinterpret_cast<const u32x4*>(Bs + (2 * wave + j) * 1024 + 16 * lane);
+            const char* sc = As + XB + W_BYTES;
+            // the group's per-column factors s and s * (offset - BASE) of this wave's columns
+            auto col_factors = [&](float (&sf)[TN], float (&sx)[TN]) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+                for (int j = 0; j < TN; ++j) {
+                    const int col = 32 * wave + 16 * j + fr;
+                    sf[j] = load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 2 * col), p.s_dtype);
+                    const float of = HAS_OFF
+                                         ? load_half_bits(*reinterpret_cast<const uint16_t*>(sc + 1024 + 2 * col),
+                                                          p.s_dtype)
+                                         : 0.0f;
+                    sx[j] = sf[j] * (of - BASE);
+                }
+            };
+            auto fold_row = [&](int i, const float (&sf)[TN], const float (&sx)[TN]) {
+                const f32x4 xs = *reinterpret_cast<const f32x4*>(sc + 2048 + 4 * (16 * i + 4 * g4));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 16 * i + 4 * g4 + r;
+                for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const float v = acc[i][j][r] + bv[j];
-                ot[row * (OROWB / 2) + 32 * wave + 16 * j + fr] =
-                    (uint16_t)(p.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+                    for (int q = 0; q < 4; ++q)
+                        acc[i][j][q] = __builtin_fmaf(sf[j], ag[i][j][q], __builtin_fmaf(sx[j], xs[q], acc[i][j][q]));
+            };
+            // k-step t's operands: the activation fragments of the wave's 8 row tiles, the weight of its 2 blocks
+            auto a_frag = [&](int i, int kt) {
+                const int rr = 16 * i + fr;
+                if constexpr (W8)
+                    return *reinterpret_cast<const u32x4*>(As + rr * 128 + 16 * ((2 * g4 + kt) ^ (rr & 7)));
+                else
+                    return *reinterpret_cast<const u32x4*>(As + rr * 256 + 16 * ((4 * kt + g4) ^ (rr & 15)));
+            };
+            auto b_op = [&](int j, int kt) {
+                if constexpr (W8) return nz8_operand<DT>(bw[j][2 * kt], bw[j][2 * kt + 1]);
+                else return nz_operand<MM::MAGIC>(bw[j][kt]);
+            };
+            if constexpr (G1) {
+                float sf[TN], sx[TN];
+                col_factors(sf, sx);
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) {
+                    u32x4 af[TM], b[TN];
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) af[i] = a_frag(i, kt);
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) b[j] = b_op(j, kt);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], b[j], kt == 0 ? zero4 : ag[i][j]);
+                        if (kt == NKT - 1 && i >= 2) fold_row(i - 2, sf, sx);  // two row tiles behind the MFMAs
+                    }
+                }
+                fold_row(TM - 2, sf, sx);
+                fold_row(TM - 1, sf, sx);
+                continue;
+            }
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+                u32x4 af[TM], b[TN];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) af[i] = a_frag(i, kt);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) b[j] = b_op(j, kt);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) ag[i][j] = MM::mma(af[i], b[j], ag[i][j]);
+            }
+            if (((s + 1) * KSW) % G == 0) {  // the group ends with this step: fold it into acc
+                float sf[TN], sx[TN];
+                col_factors(sf, sx);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    fold_row(i, sf, sx);
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) ag[i][j] = zero4;
+                }
             }
         }
-    __syncthreads();
-    constexpr int CPRO = 2 * BN / 16;  // 16-byte chunks per output row
-    for (int q = tid; q < BM * CPRO; q += NT) {
-        const int row = q / CPRO, c = q % CPRO;
-        if (row >= rows) break;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * OROWB + 16 * c);
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (size_t)(m0 + row) * N +
-                                                                n0 + 8 * c));  // written once
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __syncthreads();  // every wave is past its last reads of the ring
+
+        if constexpr (SK) {
+            if (head) {  // hand the folded groups 0 .. ub to range r + 1 (stores through the L2), then arrive
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), rp,
+                                                               part_off(r, i, j), 0, kCoherent);
+                splitk_last(ctr + r, 2u, tag);
+                continue;
+            }
+        }
+
+        // ---- epilogue: + bias, cast, staged through LDS for 16-byte row stores
+        float bv[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            bv[j] = p.bias_dtype ? load_scalar(p.bias, n0 + 32 * wave + 16 * j + fr, p.bias_dtype) : 0.0f;
+        uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int row = 16 * i + 4 * g4 + q;
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const float v = acc[i][j][q] + bv[j];
+                    ot[row * (OROWB / 2) + 32 * wave + 16 * j + fr] =
+                        (uint16_t)(p.out_dtype == QK_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+                }
+            }
+        __syncthreads();
+        constexpr int CPRO = 2 * BN / 16;  // 16-byte chunks per output row
+        for (int q = tid; q < BM * CPRO; q += NT) {
+            const int row = q / CPRO, c = q % CPRO;
+            if (row >= rows) break;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * OROWB + 16 * c);
+            __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) +
+                                                                    (size_t)(m0 + row) * N + n0 + 8 * c));  // written once
+        }
+        if constexpr (SK) __syncthreads();  // the staging is read before the next segment's DMAs land
     }
 }
 
@@ -886,29 +990,97 @@ NzGemmPlan nzg_plan(const WqbmmArgs& p) {
     return g;
 }
 
-size_t nzg_workspace(const WqbmmArgs& p) {
-    const int64_t G = p.group == 0 ? p.K : p.group;
-    return QK_SPLIT_COUNTER_BYTES + (size_t)(p.K / G) * (size_t)p.M * sizeof(float);
-}
-
-template <int DT, bool W8>
-void launch_nzg_k(const WqbmmArgs& p, const NzGemmPlan& g, const float* xsum, hipStream_t stream) {
-    const dim3 grid((uint32_t)(g.tiles_m * g.tiles_n)), block(nzg::NT);
-    if (p.group == (W8 ? nzg::KS8 : nzg::KS)) {
-        if (p.offset) w4nz_gemm<DT, true, true, W8><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
-        else w4nz_gemm<DT, false, true, W8><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
-    } else {
-        if (p.offset) w4nz_gemm<DT, true, false, W8><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
-        else w4nz_gemm<DT, false, false, W8><<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum);
+// CUs of the current device (cached per device; 0 if it cannot be read)
+int device_cus() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cache[kMaxDev];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
+        cache[dev].store(n, std::memory_order_relaxed);
     }
+    return n;
 }
 
+// Stream-K schedule of the NZ prefill GEMM: one workgroup per CU takes an equal share of all tiles' groups,
+// where whole tiles per workgroup would leave at least an eighth of the last round's CUs idle (cfg3, M = 2048:
+// 688 tiles on 256 CUs, 2.69 rounds run as 3).  Needs at least one tile per CU (so a tile has at most two
+// segments) and two groups per tile; at most 512 workgroups (one split-counter word per range boundary).
+// The result bits do not depend on it: a split tile's second segment continues from the first one's folded
+// fp32 accumulator (or runs the whole tile itself when the first has not arrived yet), so each output folds
+// its groups in order from zero exactly as with whole tiles.
+int nzg_stream_k_wgs(const WqbmmArgs& p, const NzGemmPlan& g) {
+    if (plan_override().nzg_sk == 0) return 0;
+    const int64_t G = p.group == 0 ? p.K : p.group;
+    const int64_t nu = p.K / G, T = (int64_t)g.tiles_m * g.tiles_n;
+    const int P = device_cus() < 512 ? device_cus() : 512;
+    if (P < 2 || nu < 2 || T < P || T % P == 0) return 0;
+    if ((((T + P - 1) / P) * P - T) * 8 < P) return 0;
+    return P;
+}
+
+// Whole-tile rounds run before the stream-K share (all but the last one to two rounds' worth of tiles, the
+// data-parallel + stream-K hybrid of Osama et al., "Stream-K: Work-centric Parallel Decomposition for Dense
+// Matrix Multiplication on the GPU", 2023): in lockstep, the workgroups of an XCD read the same activation
+// rows and weight blocks at about the same time (L2 hits), where stream-K ranges drift apart in K.  cfg3,
+// M = 2048 (one box, three passes, 8 rotating int4 NZ weights): 195-197 us against 199-201 for stream-K
+// throughout and 200-201 with whole tiles only.
+int nzg_dp_rounds(const NzGemmPlan& g, int wgs) {
+    const int most = (g.tiles_m * g.tiles_n) / wgs - 1;  // the stream-K share keeps a tile per workgroup
+    const int want = plan_override().nzg_sk_dp;
+    return want < 0 || want > most ? most : want;
+}
+
+// bytes of the stream-K partial slots: one folded 128 x 256 fp32 tile per range boundary
+size_t nzg_stream_k_bytes(int wgs) { return wgs > 1 ? (size_t)(wgs - 1) * nzg::BM * nzg::BN * sizeof(float) : 0; }
+
+size_t nzg_xsum_bytes(const WqbmmArgs& p) {
+    const int64_t G = p.group == 0 ? p.K : p.group;
+    return (size_t)(p.K / G) * (size_t)p.M * sizeof(float);
+}
+
+// [split counters][x group sums fp32 [K/G][M]][stream-K partial slots, when planned and stream_k]
+size_t nzg_workspace(const WqbmmArgs& p, bool stream_k) {
+    const size_t sk = stream_k ? nzg_stream_k_bytes(nzg_stream_k_wgs(p, nzg_plan(p))) : 0;
+    return QK_SPLIT_COUNTER_BYTES + (sk ? round256(nzg_xsum_bytes(p)) + sk : nzg_xsum_bytes(p));
+}
+
+template <int DT, bool W8, bool SK>
+void launch_nzg_k(const WqbmmArgs& p, const NzGemmPlan& g, const float* xsum, uint64_t* ctr, float* part, int wgs,
+                  hipStream_t stream) {
+    const dim3 grid((uint32_t)(SK ? wgs : g.tiles_m * g.tiles_n)), block(nzg::NT);
+    const uint64_t tag = SK ? next_split_tag() : 0;
+    const int tail_first = plan_override().nzg_sk == 2 ? 1 : 0;
+    const auto k = p.group == (W8 ? nzg::KS8 : nzg::KS)
+                       ? (p.offset ? w4nz_gemm<DT, true, true, W8, SK> : w4nz_gemm<DT, false, true, W8, SK>)
+                       : (p.offset ? w4nz_gemm<DT, true, false, W8, SK> : w4nz_gemm<DT, false, false, W8, SK>);
+    k<<<grid, block, 0, stream>>>(p, g.tiles_m, g.tiles_n, xsum, ctr, part, tag, tail_first,
+                                  SK ? nzg_dp_rounds(g, wgs) : 0);
+}
+
+// The x group sums, then the GEMM.  ws: the call's workspace, whose counters open it; xsum inside it; the
+// stream-K partial slots follow the group sums when ws_end leaves room for them.
 template <int DT>
-hipError_t launch_nzg_dt(const WqbmmArgs& p, const NzGemmPlan& g, float* xsum, hipStream_t stream) {
+hipError_t launch_nzg_dt(const WqbmmArgs& p, const NzGemmPlan& g, char* ws, float* xsum, const char* ws_end,
+                         hipStream_t stream) {
     hipError_t e = launch_w4_xsum(p, xsum, stream);
     if (e != hipSuccess) return e;
-    if (p.w_dtype == QK_I8_NZ) launch_nzg_k<DT, true>(p, g, xsum, stream);
-    else launch_nzg_k<DT, false>(p, g, xsum, stream);
+    int wgs = nzg_stream_k_wgs(p, g);
+    char* part = reinterpret_cast<char*>(xsum) + round256(nzg_xsum_bytes(p));
+    if (wgs && (part > ws_end || (size_t)(ws_end - part) < nzg_stream_k_bytes(wgs) ||
+                (uintptr_t)part % 16 != 0))
+        wgs = 0;
+    uint64_t* ctr = reinterpret_cast<uint64_t*>(ws);
+    float* pf = reinterpret_cast<float*>(part);
+    if (p.w_dtype == QK_I8_NZ) {
+        if (wgs) launch_nzg_k<DT, true, true>(p, g, xsum, ctr, pf, wgs, stream);
+        else launch_nzg_k<DT, true, false>(p, g, xsum, ctr, pf, 0, stream);
+    } else {
+        if (wgs) launch_nzg_k<DT, false, true>(p, g, xsum, ctr, pf, wgs, stream);
+        else launch_nzg_k<DT, false, false>(p, g, xsum, ctr, pf, 0, stream);
+    }
     return hipGetLastError();
 }
 
@@ -949,9 +1121,9 @@ hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N
 // [QK_SPLIT_COUNTER_BYTES, unused][ND weight][row-major call's workspace].
 // An int8 [N, K] weight (QK_I8_NK) takes the same decode kernel (reading it in place) or is transposed into the
 // workspace for the row-major kernels: [QK_SPLIT_COUNTER_BYTES, unused][[K, N] weight][row-major call's workspace].
-size_t w4_nz_workspace(const WqbmmArgs& p) {
+size_t w4_nz_workspace(const WqbmmArgs& p, bool stream_k) {
     if (!plan_override().w4nz_off && nz_plan(p).ok) return 0;
-    if (!plan_override().w4nz_off && nzg_plan(p).ok) return nzg_workspace(p);
+    if (!plan_override().w4nz_off && nzg_plan(p).ok) return nzg_workspace(p, stream_k);
     const int nd_dtype = p.w_dtype == QK_I4_NZ ? QK_I32 : QK_I8;
     return QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(p)) +
            weight_quant_bmm_workspace(p.M, p.N, p.K, nd_dtype, p.group, true);
@@ -963,9 +1135,12 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
         return p.x_dtype == QK_BF16 ? launch_nz_dt<QK_BF16>(p, z, stream) : launch_nz_dt<QK_F16>(p, z, stream);
     const NzGemmPlan g = plan_override().w4nz_off ? NzGemmPlan{false, 0, 0} : nzg_plan(p);
     if (g.ok) {
-        if (!workspace || ws_bytes < nzg_workspace(p) || (uintptr_t)workspace % 16 != 0) return hipErrorInvalidValue;
-        float* xs = reinterpret_cast<float*>(static_cast<char*>(workspace) + QK_SPLIT_COUNTER_BYTES);
-        return p.x_dtype == QK_BF16 ? launch_nzg_dt<QK_BF16>(p, g, xs, stream) : launch_nzg_dt<QK_F16>(p, g, xs, stream);
+        if (!workspace || ws_bytes < nzg_workspace(p, false) || (uintptr_t)workspace % 16 != 0)
+            return hipErrorInvalidValue;
+        char* ws = static_cast<char*>(workspace);
+        float* xs = reinterpret_cast<float*>(ws + QK_SPLIT_COUNTER_BYTES);
+        return p.x_dtype == QK_BF16 ? launch_nzg_dt<QK_BF16>(p, g, ws, xs, ws + ws_bytes, stream)
+                                    : launch_nzg_dt<QK_F16>(p, g, ws, xs, ws + ws_bytes, stream);
     }
     const bool w8 = p.w_dtype != QK_I4_NZ;
     const int nd_dtype = w8 ? QK_I8 : QK_I32;
@@ -996,7 +1171,7 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
 // The debug overrides that force or disable a prefill kernel switch it off.
 constexpr int64_t kCastNzMinM = 1024;
 
-size_t w4_cast_nz_workspace(const WqbmmArgs& p) {
+size_t w4_cast_nz_workspace(const WqbmmArgs& p, bool stream_k) {
     const PlanOverride& ov = plan_override();
     if (!(p.w_dtype == QK_I32 || p.w_dtype == QK_I8) || p.M < kCastNzMinM || ov.w4nz_off || ov.w4_gemm != 0)
         return 0;
@@ -1004,11 +1179,12 @@ size_t w4_cast_nz_workspace(const WqbmmArgs& p) {
     q.w = reinterpret_cast<const void*>((uintptr_t)256);  // the cast's destination: 256-byte aligned
     q.w_dtype = p.w_dtype == QK_I8 ? QK_I8_NZ : QK_I4_NZ;
     if (!nzg_plan(q).ok) return 0;
-    return round256(QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)) + (nzg_workspace(q) - QK_SPLIT_COUNTER_BYTES));
+    return round256(QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)) +
+                    (nzg_workspace(q, stream_k) - QK_SPLIT_COUNTER_BYTES));
 }
 
 bool launch_w4_cast_nz(const WqbmmArgs& p, void* workspace, size_t ws_bytes, hipStream_t stream, hipError_t* err) {
-    const size_t need = w4_cast_nz_workspace(p);
+    const size_t need = w4_cast_nz_workspace(p, false);
     if (need == 0 || !workspace || ws_bytes < need || (uintptr_t)workspace % 256 != 0) return false;
     char* ws = static_cast<char*>(workspace);
     void* nz = ws + QK_SPLIT_COUNTER_BYTES;
@@ -1024,7 +1200,8 @@ bool launch_w4_cast_nz(const WqbmmArgs& p, void* workspace, size_t ws_bytes, hip
                                           stream);
     if (e == hipSuccess) {
         float* xs = reinterpret_cast<float*>(ws + QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)));
-        e = p.x_dtype == QK_BF16 ? launch_nzg_dt<QK_BF16>(q, g, xs, stream) : launch_nzg_dt<QK_F16>(q, g, xs, stream);
+        e = p.x_dtype == QK_BF16 ? launch_nzg_dt<QK_BF16>(q, g, ws, xs, ws + ws_bytes, stream)
+                                 : launch_nzg_dt<QK_F16>(q, g, ws, xs, ws + ws_bytes, stream);
     }
     *err = e;
     return true;

@@ -1603,7 +1603,7 @@ hipError_t launch_w4_xsum(const WqbmmArgs& p, float* xsum, hipStream_t stream) {
     return hipGetLastError();
 }
 
-size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group, bool no_cast) {
+size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group, int level) {
     WqbmmArgs p{};
     p.M = M;
     p.N = N;
@@ -1614,9 +1614,9 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     p.x = p.scale = p.offset = p.out = (void*)(uintptr_t)256;
     p.w = (void*)(uintptr_t)256;
     if (p.group == 0) p.group = p.K;
-    if (w_dtype == QK_I4_NZ || w_dtype == QK_I8_NZ || w_dtype == QK_I8_NK) return w4_nz_workspace(p);
-    if (!no_cast)
-        if (const size_t c = w4_cast_nz_workspace(p)) return c;
+    if (w_dtype == QK_I4_NZ || w_dtype == QK_I8_NZ || w_dtype == QK_I8_NK) return w4_nz_workspace(p, level == kWsFull);
+    if (level != kWsNoCast)
+        if (const size_t c = w4_cast_nz_workspace(p, level == kWsFull)) return c;
     // [split-K counters][fp32 partials [nsplit][M][N]]
     const StreamPlan s = stream_plan(p);
     if (s.ok) return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);

@@ -86,6 +86,10 @@ bool parse_plan(const char* spec, PlanOverride& o) {
             r.mid_bn = std::atoi(v.c_str());
         } else if (k == "w4nz" && v == "off") {
             r.w4nz_off = true;
+        } else if (k == "nzg_sk" && (v == "0" || v == "1" || v == "tailfirst")) {
+            r.nzg_sk = v == "0" ? 0 : v == "1" ? 1 : 2;
+        } else if (k == "nzg_sk_dp" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 0 && a <= 64) {
+            r.nzg_sk_dp = a;
         } else if (k == "w4nz_wg" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 65536) {
             r.w4nz_wg = a;
         } else if (k == "w4nz_nit" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 8) {
@@ -428,11 +432,14 @@ int weight_quant_bmm_run(const char* op, const void* x, int x_dtype, const void*
     if (M == 0 || N == 0) return QK_OK;
     if (!out || (K > 0 && (!x || !weight || !antiquant_scale))) return fail(QK_ERR_ARG, "%s: null pointer", op);
     // The no-allocation scratch runs the op's own plan (so the same kernels, the same bits) wherever that
-    // plan's workspace fits in it; otherwise the plan without the cast to NZ of a row-major int4 / int8 weight,
-    // whose cast weight is what does not fit.
-    size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, false);
+    // plan's workspace fits in it; otherwise the same kernels with whole tiles per workgroup in place of the NZ
+    // prefill kernel's stream-K partials (the same bits too); otherwise the plan without the cast to NZ of a
+    // row-major int4 / int8 weight, whose cast weight is what does not fit.
+    size_t need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, qk::kWsFull);
     if (scratch && need > QK_NOALLOC_SCRATCH_BYTES)
-        need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, true);
+        need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, qk::kWsNoStreamK);
+    if (scratch && need > QK_NOALLOC_SCRATCH_BYTES)
+        need = qk::weight_quant_bmm_workspace(M, N, K, weight_dtype, group_size, qk::kWsNoCast);
     if (scratch && need > 0) {
         int rc = QK_OK;
         workspace = scratch(need, &workspace_bytes, &rc);

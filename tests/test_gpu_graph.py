@@ -125,3 +125,40 @@ def test_graph_replays_mlp_block(ops):
         again = run()
         torch.cuda.synchronize()
         assert torch.equal(again, eager), f"eager call after replay {r} differs"
+
+
+def test_graph_replays_nz_prefill_stream_k(ops):
+    """The NZ prefill kernel's stream-K schedule under capture (cfg3's width, M = 1024: 344 tiles on one
+    workgroup per CU): one tag per graph, so each replay must find the range-boundary counters cleared by the
+    previous one's last arrivals, and read only partial slots written in the same replay."""
+    from op_plugin_amd import workloads as W
+    say("HIP graph: W4A16 NZ prefill, stream-K (1024 x 11008 x 4096), 3 replays")
+    d = W.w4a16_inputs(W.W4A16Case(M=1024, N=11008, K=4096, group=128, x_dtype=torch.bfloat16, offset=True), seed=17)
+    x, sc, off = d["x"].to(DEV), d["scale"].to(DEV), d["offset"].to(DEV)
+    nz = ops.npu_format_cast(d["w_packed"].to(DEV), 29)
+
+    def run():
+        return ops.npu_weight_quant_batchmatmul(x, nz, sc, off, antiquant_group_size=128)
+
+    eager = run().clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = run()
+    torch.cuda.synchronize()
+    for r in range(3):
+        captured.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {r}: the prefill output differs from the eager call"
+        again = run()
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager), f"eager call after replay {r} differs"

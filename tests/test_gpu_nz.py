@@ -429,6 +429,79 @@ def test_w8a16_row_major_cast_to_nz(ops, oracle, plan, M, N, K, group, offset, x
     torch.testing.assert_close(out.float(), rm.float(), rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("w8,M,N,K,group,offset,x_dtype,bias", [
+    (False, 2048, 11008, 4096, 128, True, torch.bfloat16, False),   # cfg3: 688 tiles, one step per group
+    (False, 1024, 11008, 4096, 256, False, torch.float16, True),    # 344 tiles, two steps per group
+    (False, 2100, 4096, 1024, 128, True, torch.bfloat16, True),     # 272 tiles, last row tile of 52 rows
+    (True, 2048, 11008, 4096, 128, True, torch.bfloat16, False),    # int8: two 64-row steps per group
+    (True, 1100, 8192, 2048, 64, False, torch.float16, True),       # int8: one step per group, 76-row last tile
+])
+def test_nz_prefill_stream_k_bits(ops, plan, w8, M, N, K, group, offset, x_dtype, bias):
+    """Shapes whose tiles leave part of the last round of CUs idle run the NZ prefill kernel as stream-K (one
+    workgroup per CU, equal shares of all tiles' groups; the size query reports the partial slots). A split
+    tile's second segment continues from the first one's folded accumulator, or runs the whole tile when it
+    arrives first, so the output is bit for bit the kernel's with whole tiles per workgroup (debug override
+    nzg_sk=0) -- also when every tail segment runs first and so takes the whole-tile path (nzg_sk=tailfirst),
+    and with or without the whole-tile rounds the plan runs before the stream-K share (nzg_sk_dp=0: stream-K
+    throughout; shapes of two rounds and more run one round of whole tiles first by default).
+    Through the C ABI with a 0xA5-filled workspace: the partial slots were written, the output is the op's."""
+    say(f"NZ prefill stream-K {'int8' if w8 else 'int4'} M={M} N={N} K={K} group={group} offset={offset} "
+        f"{x_dtype} bias={bias}")
+    L = ops.abi()
+    if w8:
+        d = _w8(M, N, K, group, offset, x_dtype, seed=M + N + K + 11)
+        w, wdt = ops.npu_format_cast(d["w"].to(DEV), 29), ops.QK_I8_NZ
+    else:
+        d = _inputs(M, N, K, group, offset, x_dtype, seed=M + N + K + 11)
+        w, wdt = ops.npu_format_cast(d["w_packed"].to(DEV), 29), ops.QK_I4_NZ
+    b = torch.randn(N, generator=torch.Generator().manual_seed(12)).to(x_dtype).to(DEV) if bias else None
+    x, sc = d["x"].to(DEV), d["scale"].to(DEV)
+    off = None if d["offset"] is None else d["offset"].to(DEV)
+    need = ctypes.c_size_t(0)
+    assert L.qk_weight_quant_bmm_workspace_size(M, N, K, wdt, group, ctypes.byref(need)) == 0
+    base = 4096 + (K // group) * M * 4
+    assert need.value >= base + (1 << 20), "the size query reports the stream-K partial slots"
+
+    def run():
+        return ops.npu_weight_quant_batchmatmul(x, w, sc, off, bias=b, antiquant_group_size=group)
+
+    sk = run()
+    plan("nzg_sk=0")
+    whole = run()
+    plan("nzg_sk=tailfirst")
+    tails_first = run()
+    plan("nzg_sk_dp=0")
+    sk_throughout = run()
+    plan("")
+    torch.cuda.synchronize()
+    assert torch.equal(sk.view(torch.int16), whole.view(torch.int16)), "stream-K differs from whole tiles"
+    assert torch.equal(tails_first.view(torch.int16), whole.view(torch.int16)), "the whole-tile fallback differs"
+    assert torch.equal(sk_throughout.view(torch.int16), whole.view(torch.int16)), "stream-K throughout differs"
+
+    ws = torch.full((need.value,), 0xA5, dtype=torch.uint8, device=DEV)
+    out = torch.empty(M, N, dtype=x_dtype, device=DEV)
+    XD = CODE[x_dtype]
+    rc = L.qk_weight_quant_bmm(x.data_ptr(), XD, w.data_ptr(), wdt, sc.data_ptr(),
+                               None if off is None else off.data_ptr(), F16, M, N, K, group,
+                               None if b is None else b.data_ptr(), 0 if b is None else XD, out.data_ptr(), XD,
+                               ws.data_ptr(), need.value, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ops.last_error()
+    torch.cuda.synchronize()
+    slots = ws[need.value - (1 << 20):]
+    assert bool((slots != 0xA5).any()), "no stream-K partial slot was written"
+    assert torch.equal(out.view(torch.int16), whole.view(torch.int16))
+    # the no-allocation entry point: the partial slots do not fit its scratch, so whole tiles, the same bits
+    assert need.value > ops.QK_NOALLOC_SCRATCH_BYTES
+    na = torch.empty(M, N, dtype=x_dtype, device=DEV)
+    rc = L.qk_weight_quant_bmm_noalloc(x.data_ptr(), XD, w.data_ptr(), wdt, sc.data_ptr(),
+                                       None if off is None else off.data_ptr(), F16, M, N, K, group,
+                                       None if b is None else b.data_ptr(), 0 if b is None else XD, na.data_ptr(), XD,
+                                       torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ops.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(na.view(torch.int16), whole.view(torch.int16))
+
+
 def test_abi_w8_nz(ops, oracle):
     say("ABI qk_weight_quant_bmm QK_I8_NZ M=16 N=1024 K=2048")
     L = ops.abi()
