@@ -30,7 +30,9 @@
  * QK_SPLIT_COUNTER_BYTES of split-K arrival counters, followed by the partial
  * sums (split-K shapes) or by the activations' per-group sums (weight-quant
  * matmul at large M; from M = 1024 on a row-major int4 weight the weight cast
- * to NZ, K*N/2 bytes rounded to 256, comes first, then the sums).  Each arrival adds D = tag * 2^16 + 1 to its
+ * to NZ, K*N/2 bytes rounded to 256, comes first, then the sums; where the NZ
+ * prefill kernel runs stream-K, (P - 1) x 128 KB of fp32 partial slots follow
+ * the sums, P being the current device's CU count).  Each arrival adds D = tag * 2^16 + 1 to its
  * counter (a 48-bit tag drawn per call, never 0 or all ones), so a counter of
  * this call holds j * D after j arrivals; a zero word is empty (the last
  * arrival leaves zero behind), and any other word that is not such a multiple
