@@ -233,7 +233,9 @@ int qk_weight_quant_bmm(const void* x, int x_dtype,
  * array of QK_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, and
  * the call allocates nothing.  Where the workspace qk_weight_quant_bmm_workspace_size
  * reports fits in that array, the call runs exactly the kernels qk_weight_quant_bmm
- * runs (the same bits).  Otherwise, for a row-major int4 or int8 weight at
+ * runs (the same bits).  Where only the NZ prefill kernel's stream-K partial
+ * slots do not fit, it runs that kernel with whole tiles per workgroup (the
+ * same bits again).  Otherwise, for a row-major int4 or int8 weight at
  * M >= 1024 whose cast to NZ is what does not fit, it runs the row-major
  * prefill kernel without the cast (within the same 1e-2 bar; for int4 on
  * cfg3's shape, N = 11008, K = 4096, 128-row groups, the same bits); a shape whose scratch exceeds
