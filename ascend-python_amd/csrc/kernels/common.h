@@ -381,6 +381,7 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   mid_bm=<16|32|64>, mid_split=<1|2>              qmm_mid: row block and K split (where the shape allows them)
 //   mid_bn=<64|128>                                 qmm_mid: column block (128 only for a [K,N] weight)
 //   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
+//   skinny_pf=<1..3>                                W8A8 small-M stream: stages loaded ahead in registers
 //   w4nz=off                                        NZ int4 weights: unpack to ND and take the row-major kernels
 //   nzg_sk=<0|1|tailfirst>                          NZ prefill GEMM: 0 whole tiles per workgroup (no stream-K);
 //                                                   tailfirst: stream-K with each workgroup's tail segment run
@@ -400,6 +401,7 @@ struct PlanOverride {
     bool qmm_mid = true;
     int mid_bm = 0, mid_split = 0, mid_bn = 0;
     int skinny_splits = 0;
+    int skinny_pf = 0;  // W8A8 small-M stream: stages loaded ahead in registers (0: the planner's choice)
     bool w4nz_off = false;
     int nzg_sk = 1;
     int nzg_sk_dp = -1;  // whole-tile rounds before the stream-K share (-1: the planner's choice)

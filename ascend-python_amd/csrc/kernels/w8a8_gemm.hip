@@ -906,15 +906,15 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
 // Skinny kernel (decode and small M <= 128): an HBM weight stream.  A workgroup owns
 // 16*MT rows x 256 columns and one K split; its 4 waves take 64 columns
 // each.  Stages of 128 k-rows go through LDS (the weight in its natural
-// layout, B fragments by ds_read_b64_tr_b8 for [K,N]) with the next stage's
-// global loads in flight.  With several splits each writes exact int32
+// layout, B fragments by ds_read_b64_tr_b8 for [K,N]) with the next PF
+// stages' global loads in flight in registers.  With several splits each writes exact int32
 // partial sums and qmm_reduce adds them (order-free, exact) before the same
 // epilogue as every other path.
 namespace sk {
 constexpr int BN = 256, BK = 128;
 }
 
-template <bool B_KN, int MT, bool FINAL>
+template <bool B_KN, int MT, bool FINAL, int PF = 1>
 __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, int nsplit, int32_t* partial) {
     using big::rk_off;
     using big::kn_off;
@@ -936,15 +936,16 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fr = lane & 15, g = lane >> 4;
 
-    i32x4 ra[A_PER_T], rb[B_PER_T];
-    auto gload = [&](int64_t k0) {
+    // PF register slots: stage s is loaded into slot s % PF, PF stages ahead of the one in LDS
+    i32x4 ra[PF][A_PER_T], rb[PF][B_PER_T];
+    auto gload = [&](int64_t k0, int sl) {
 #pragma unroll
         for (int i = 0; i < A_PER_T; ++i) {
             const int q = tid + kThreads * i;
             const int r = q >> 3, c = q & 7;
             const int64_t m = m0 + r;
-            ra[i] = (q < A_CHUNKS && m < p.M) ? *reinterpret_cast<const i32x4*>(p.a + m * p.lda + k0 + 16 * c)
-                                              : (i32x4){0, 0, 0, 0};
+            ra[sl][i] = (q < A_CHUNKS && m < p.M) ? *reinterpret_cast<const i32x4*>(p.a + m * p.lda + k0 + 16 * c)
+                                                  : (i32x4){0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < B_PER_T; ++i) {
@@ -959,27 +960,27 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
             if (!B_KN) {
                 const int r = q >> 3, c = q & 7;
                 const int64_t n = n0 + r;
-                rb[i] = n < p.N ? wload(p.b + n * p.sbn + k0 + 16 * c) : (i32x4){0, 0, 0, 0};
+                rb[sl][i] = n < p.N ? wload(p.b + n * p.sbn + k0 + 16 * c) : (i32x4){0, 0, 0, 0};
             } else {
                 const int kr = q >> 4, c16 = q & 15;
                 const int64_t n = n0 + 16 * c16;
-                rb[i] = n < p.N ? wload(p.b + (k0 + kr) * p.sbk + n) : (i32x4){0, 0, 0, 0};
+                rb[sl][i] = n < p.N ? wload(p.b + (k0 + kr) * p.sbk + n) : (i32x4){0, 0, 0, 0};
             }
         }
     };
-    auto lstore = [&](int st) {
+    auto lstore = [&](int st, int sl) {
         int8_t* As = smem + st * STAGE;
         int8_t* Bs = As + A_BYTES;
 #pragma unroll
         for (int i = 0; i < A_PER_T; ++i) {
             const int q = tid + kThreads * i;
-            if (q < A_CHUNKS) *reinterpret_cast<i32x4*>(As + rk_off(q >> 3, q & 7)) = ra[i];
+            if (q < A_CHUNKS) *reinterpret_cast<i32x4*>(As + rk_off(q >> 3, q & 7)) = ra[sl][i];
         }
 #pragma unroll
         for (int i = 0; i < B_PER_T; ++i) {
             const int q = tid + kThreads * i;
-            if (!B_KN) *reinterpret_cast<i32x4*>(Bs + rk_off(q >> 3, q & 7)) = rb[i];
-            else *reinterpret_cast<i32x4*>(Bs + kn_off(q >> 4, q & 15)) = rb[i];
+            if (!B_KN) *reinterpret_cast<i32x4*>(Bs + rk_off(q >> 3, q & 7)) = rb[sl][i];
+            else *reinterpret_cast<i32x4*>(Bs + kn_off(q >> 4, q & 15)) = rb[sl][i];
         }
     };
 
@@ -991,10 +992,16 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
     const int tr_base = kn_off(16 * g + (fr >> 1), 0) + 8 * (fr & 1);
 
     const int64_t nk = ks / sk::BK;
-    gload(kbeg);
-    lstore(0);
-    if (nk > 1) gload(kbeg + sk::BK);
-    for (int64_t it = 0; it < nk; ++it) {
+    gload(kbeg, 0);
+    lstore(0, 0);
+#pragma unroll
+    for (int u = 1; u <= PF; ++u)
+        if (u < nk) gload(kbeg + u * sk::BK, u % PF);
+    for (int64_t it0 = 0; it0 < nk; it0 += PF)
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {  // it0 is a multiple of PF, so stage it + 1 sits in slot (u + 1) % PF
+        const int64_t it = it0 + u;
+        if (it >= nk) break;
         __syncthreads();
         const int st = (int)(it & 1);
         const int8_t* As = smem + st * STAGE;
@@ -1017,8 +1024,8 @@ __global__ __launch_bounds__(kThreads) void qmm_skinny(QmmArgs p, int tiles_n, i
             }
         }
         if (it + 1 < nk) {
-            lstore(st ^ 1);
-            if (it + 2 < nk) gload(kbeg + (it + 2) * sk::BK);
+            lstore(st ^ 1, (u + 1) % PF);
+            if (it + 1 + PF < nk) gload(kbeg + (it + 1 + PF) * sk::BK, (u + 1) % PF);
         }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
@@ -1757,7 +1764,7 @@ hipError_t launch_split128(const QmmArgs& p, const BigPlan& b, int32_t* partial,
 namespace {
 
 struct SkinnyPlan {
-    int mt = 0, nsplit = 1, tiles_n = 0, tiles_m = 0;
+    int mt = 0, nsplit = 1, tiles_n = 0, tiles_m = 0, pf = 1;
 };
 
 // Decode and small-M shapes (M <= 128, K a multiple of 128): row tiles of
@@ -1782,6 +1789,11 @@ SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K) {
     if (const int v = plan_override().skinny_splits) {
         if (v == 1 || fits(v)) s.nsplit = v;
     }
+    // stages loaded ahead in registers: two for 16-row tiles (the decode stream: cfg2 M=1/16 42.6-45.1 ->
+    // 41.4-43.6 us, N = 11008, K = 4096: 15.8-16.8 -> 15.0-15.9 us; three measured slower), one for taller
+    // tiles (M = 32: 17.1 -> 20.7 us with two)
+    s.pf = s.mt == 1 ? 2 : 1;
+    if (const int v = plan_override().skinny_pf) s.pf = v;
     if (base * s.nsplit >= ((int64_t)1 << 31)) s.mt = 0;
     if (s.mt == 8 && s.nsplit == 1) s.mt = 0;  // 128-row tiles only as a split stream (their in-place epilogue is not unrolled)
     return s;
@@ -1794,11 +1806,15 @@ hipError_t launch_skinny_t(const QmmArgs& p, const SkinnyPlan& s, int32_t* parti
         // 128-row tiles run only as a split stream (skinny_plan), so that instance is not built
         if constexpr (MT == 8) return hipErrorInvalidValue;
         else {
-            qmm_skinny<B_KN, MT, true><<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, 1, nullptr);
+            const auto k = s.pf == 3 ? qmm_skinny<B_KN, MT, true, 3>
+                           : s.pf == 2 ? qmm_skinny<B_KN, MT, true, 2> : qmm_skinny<B_KN, MT, true, 1>;
+            k<<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, 1, nullptr);
             return hipGetLastError();
         }
     }
-    qmm_skinny<B_KN, MT, false><<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, s.nsplit, partial);
+    const auto k = s.pf == 3 ? qmm_skinny<B_KN, MT, false, 3>
+                   : s.pf == 2 ? qmm_skinny<B_KN, MT, false, 2> : qmm_skinny<B_KN, MT, false, 1>;
+    k<<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, s.nsplit, partial);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     int64_t blocks = (p.M * p.N + kThreads - 1) / kThreads;

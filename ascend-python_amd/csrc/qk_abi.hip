@@ -94,6 +94,8 @@ bool parse_plan(const char* spec, PlanOverride& o) {
             r.w4nz_wg = a;
         } else if (k == "w4nz_nit" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 8) {
             r.w4nz_nit = a;
+        } else if (k == "skinny_pf" && (v == "1" || v == "2" || v == "3")) {
+            r.skinny_pf = std::atoi(v.c_str());
         } else if (k == "skinny_splits" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 64 &&
                    (a & (a - 1)) == 0) {
             r.skinny_splits = a;
