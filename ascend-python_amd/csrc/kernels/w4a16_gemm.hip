@@ -347,6 +347,9 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
 // of its K-blocks, rows 8kg..8kg+7 of one word column straight from HBM (one
 // dword per row; the 16 lanes of a k-group cover WPL consecutive words), so the
 // B operands are built in registers without any LDS transpose:
+//   WPL == 32: slot c owns words 2c and 2c+1 (one 8-byte load per row, so a
+//              k-group's 16 lanes read the whole 128-byte line) and their 16
+//              nibbles (16 MFMA tiles, columns 16c + t);
 //   WPL == 16: slot c owns word c and all 8 of its nibbles (8 MFMA tiles);
 //   WPL == 8:  slots c and c+8 share word c&7, slot c takes nibbles
 //              4(c>>3)..4(c>>3)+3 (4 tiles).
@@ -370,7 +373,8 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
     static_assert(!W8 || WPL == 16, "int8 weights use 16-dword sub-strips");
     constexpr int CPW = W8 ? 4 : 8;         // output columns per weight dword
     constexpr int SW = 256 / CPW;           // dwords per strip row (256 columns)
-    constexpr int TPL = W8 ? 4 : (WPL == 16 ? 8 : 4);  // MFMA tiles per lane
+    constexpr int LW = WPL == 32 ? 2 : 1;   // dwords per lane and row
+    constexpr int TPL = W8 ? 4 : (WPL == 32 ? 16 : WPL == 16 ? 8 : 4);  // MFMA tiles per lane
     constexpr int HALVES = SW / WPL;        // column sub-strips per workgroup
     constexpr int KW = NWAVE / HALVES;      // K ranges per workgroup
     constexpr int NCOL = CPW * WPL;         // output columns per wave
@@ -392,10 +396,12 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
 
     const int M = (int)p.M, K = (int)p.K, N = (int)p.N, G = (int)p.group;
     const int NW = W8 ? (N >> 2) : (N >> 3);  // weight dwords per row
-    const int slot = WPL == 16 ? c : (c & 7);
-    const int nh = WPL == 16 ? 0 : (c >> 3);  // nibble half (WPL == 8)
-    const int wc_raw = strip * SW + h * WPL + slot;
-    const int wc = wc_raw < NW ? wc_raw : NW - 1;  // clamped: loads stay in bounds, those columns are not stored
+    const int slot = WPL >= 16 ? c : (c & 7);
+    const int nh = WPL == 8 ? (c >> 3) : 0;  // nibble half (WPL == 8)
+    const int wc_raw = strip * SW + h * WPL + LW * slot;
+    // clamped: loads stay in bounds, those columns are not stored (LW == 2: the planner gives it an even NW,
+    // so a pair is either whole in the row or wholly past it)
+    const int wc = wc_raw <= NW - LW ? wc_raw : NW - LW;
     // rows past M read row M-1: every output row depends only on its own x row, and those rows are not stored
     const int m = rb * 16 + c < M ? rb * 16 + c : M - 1;
     const int k_wave = split * (KW * NKB * 32) + kw * (NKB * 32);
@@ -416,17 +422,22 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
     // register slots.  Loads return in order, so consuming block kb waits only
     // for it; keeping few blocks in flight per wave makes each block arrive
     // early instead of every block finishing near the end of the stream.
-    typedef typename std::conditional<TPL == 8, u32x4, u32x2>::type SV;
-    SV sv[NPIECE], ov[NPIECE];
+    typedef typename std::conditional<TPL >= 8, u32x4, u32x2>::type SV;  // 8 (or 4) halves
+    constexpr int SVN = TPL >= 8 ? TPL / 8 : 1;
+    SV sv[NPIECE][SVN], ov[NPIECE][SVN];
 #pragma unroll
     for (int pc = 0; pc < NPIECE; ++pc) {
         const uint32_t g = (uint32_t)(k_wave + pc * PIECE_KB * 32) / (uint32_t)G;
         const size_t goff = (size_t)g * (uint32_t)N * 2u;
-        sv[pc] = *reinterpret_cast<const SV*>(static_cast<const char*>(p.scale) + goff + s_lane);
-        if (HAS_OFF) ov[pc] = *reinterpret_cast<const SV*>(static_cast<const char*>(p.offset) + goff + s_lane);
+#pragma unroll
+        for (int v = 0; v < SVN; ++v) {
+            const size_t o = goff + s_lane + (size_t)v * sizeof(SV);
+            sv[pc][v] = *reinterpret_cast<const SV*>(static_cast<const char*>(p.scale) + o);
+            if (HAS_OFF) ov[pc][v] = *reinterpret_cast<const SV*>(static_cast<const char*>(p.offset) + o);
+        }
     }
     constexpr int SL = PF + 1;
-    uint32_t wv[SL][8];
+    uint32_t wv[SL][LW][8];
     u32x4 xa[SL];
     auto issue = [&](int kb) {
         // the scheduler must not interleave blocks: a later block's load moved
@@ -434,8 +445,16 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
         __builtin_amdgcn_sched_barrier(0);
         xa[kb % SL] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, x_lane, kb * 64, 0));
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
-            wv[kb % SL][r] = __builtin_amdgcn_raw_buffer_load_b32(wr, w_lane, (uint32_t)(kb * 32 + r) * rowbytes, 0);
+        for (int r = 0; r < 8; ++r) {
+            const uint32_t ro = (uint32_t)(kb * 32 + r) * rowbytes;
+            if constexpr (LW == 2) {
+                const u32x2 d = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, w_lane, ro, 0));
+                wv[kb % SL][0][r] = d[0];
+                wv[kb % SL][1][r] = d[1];
+            } else {
+                wv[kb % SL][0][r] = __builtin_amdgcn_raw_buffer_load_b32(wr, w_lane, ro, 0);
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
@@ -455,8 +474,18 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
         if (kb + PF < NKB) issue(kb + PF);
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 xk = xa[kb % SL];
-        const uint32_t* wk = wv[kb % SL];
-        if constexpr (W8) {
+        const uint32_t* wk = wv[kb % SL][0];
+        if constexpr (WPL == 32) {  // tile 8d + 2b + o: nibble 2b + o of dword d (column 16c + 8d + 2b + o)
+#pragma unroll
+            for (int d = 0; d < 2; ++d)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    ag[8 * d + 2 * b] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wv[kb % SL][d], byte_sel(b)),
+                                                ag[8 * d + 2 * b]);
+                    ag[8 * d + 2 * b + 1] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wv[kb % SL][d], byte_sel(b)),
+                                                    ag[8 * d + 2 * b + 1]);
+                }
+        } else if constexpr (W8) {
             ag[0] = MM::mma(xk, unpack_i8<DT>(wk, 0), ag[0]);
             ag[1] = MM::mma(xk, unpack_i8<DT>(wk, 1), ag[1]);
             ag[2] = MM::mma(xk, unpack_i8<DT>(wk, 2), ag[2]);
@@ -482,10 +511,10 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
             const int pc = kb / PIECE_KB;
 #pragma unroll
             for (int t = 0; t < TPL; ++t) {
-                const uint32_t sb = sv[pc][t >> 1] >> (16 * (t & 1));
+                const uint32_t sb = sv[pc][t >> 3][(t & 7) >> 1] >> (16 * (t & 1));
                 const float sf = load_half_bits(sb & 0xffffu, p.s_dtype);
                 float of = 0.0f;
-                if (HAS_OFF) of = load_half_bits((ov[pc][t >> 1] >> (16 * (t & 1))) & 0xffffu, p.s_dtype);
+                if (HAS_OFF) of = load_half_bits((ov[pc][t >> 3][(t & 7) >> 1] >> (16 * (t & 1))) & 0xffffu, p.s_dtype);
                 const float sx = sf * (of - BASE);
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
@@ -496,12 +525,13 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
         }
     }
 
-    // lane (c, kg) holds rows 4kg..4kg+3 of columns  CPW*slot + 4*nh + t
+    // lane (c, kg) holds rows 4kg..4kg+3 of columns  LW*CPW*slot + 4*nh + t
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        float* dst = &red[wave][4 * kg + r][CPW * slot + 4 * nh];
-        *reinterpret_cast<f32x4*>(dst) = (f32x4){acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-        if constexpr (TPL == 8) *reinterpret_cast<f32x4*>(dst + 4) = (f32x4){acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+        float* dst = &red[wave][4 * kg + r][LW * CPW * slot + 4 * nh];
+#pragma unroll
+        for (int t = 0; t < TPL; t += 4)
+            *reinterpret_cast<f32x4*>(dst + t) = (f32x4){acc[t][r], acc[t + 1][r], acc[t + 2][r], acc[t + 3][r]};
     }
     __syncthreads();
 
@@ -1413,8 +1443,8 @@ hipError_t launch_decode_dt(const WqbmmArgs& p, const DecodePlan& d, float* part
     }
 }
 
-// Stream kernel plan (M <= 16): a strip of `wpl` words per workgroup of
-// `nwave` waves, 128 rows of K per wave, K split into nsplit workgroup ranges.
+// Stream kernel plan (M <= 16): a strip of 256 columns per workgroup of `nwave` waves, each wave `wpl` words
+// wide, 128 rows of K per wave, K split into nsplit workgroup ranges.
 struct StreamPlan {
     bool ok;
     int wpl, nwave, nkb, pf, nsplit, nstrip, piece_kb;
@@ -1453,6 +1483,16 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
         s.nwave = 16;
         s.nkb = 4;
         s.pf = 2;
+    } else if (s.piece_kb == 4 && p.N % 16 == 0 &&
+               (ov.w4_stream_wpl == 32 || (ov.w4_stream_wpl == 0 && !ov.w4_stream_nwave && p.M > 4))) {
+        // whole 128-byte rows per wave (8-wave strips): cfg3 M=16 12.3 -> 11.8 us, K=8192 N=28672 M=16
+        // 49.2 -> 47.2 us; at M=1 10.3 -> 10.45 us, so few rows keep the 16-wave half-line strips.  An even
+        // word count per row keeps every lane's 8-byte pair inside the row (a clamped pair is all columns
+        // past N, which are not stored).
+        s.wpl = 32;
+        s.nwave = 8;
+        s.nkb = 4;
+        s.pf = ov.w4_stream_pf == 3 ? 3 : 2;
     }
     const int halves = (w8 ? 64 : 32) / s.wpl;
     int kw = s.nwave / halves;
@@ -1469,15 +1509,15 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
     return s;
 }
 
-template <int DT, int NWAVE, int NKB, int PF, int PKB, bool HAS_OFF, bool W8>
+template <int DT, int NWAVE, int NKB, int PF, int PKB, bool HAS_OFF, bool W8, int WPL = 16>
 hipError_t launch_stream_t(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint64_t* ctr,
                            hipStream_t stream) {
     const dim3 grid((uint32_t)((int64_t)s.nstrip * s.nsplit));
     if (s.nsplit == 1)
-        w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, true, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
+        w4_stream<DT, WPL, NWAVE, NKB, PF, PKB, HAS_OFF, true, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
             p, partial, s.nstrip, 1, nullptr, 0);
     else
-        w4_stream<DT, 16, NWAVE, NKB, PF, PKB, HAS_OFF, false, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
+        w4_stream<DT, WPL, NWAVE, NKB, PF, PKB, HAS_OFF, false, W8><<<grid, dim3(64 * NWAVE), 0, stream>>>(
             p, partial, s.nstrip, s.nsplit, ctr, ctr ? next_split_tag() : 0);
     return hipGetLastError();
 }
@@ -1496,6 +1536,9 @@ hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* parti
         return hipErrorInvalidValue;
     }
     if constexpr (NWAVE == 8) {  // short groups and 8-row-block waves run 8-wave strips only (16 would spill)
+        if (s.wpl == 32 && s.piece_kb == 4 && s.nkb == 4)  // whole-line rows per wave
+            return s.pf == 3 ? launch_stream_t<DT, 8, 4, 3, 4, HAS_OFF, false, 32>(p, s, partial, ctr, stream)
+                             : launch_stream_t<DT, 8, 4, 2, 4, HAS_OFF, false, 32>(p, s, partial, ctr, stream);
         switch (s.piece_kb) {
         case 1: return launch_stream_t<DT, 8, 4, 2, 1, HAS_OFF, false>(p, s, partial, ctr, stream);
         case 2: return launch_stream_t<DT, 8, 4, 2, 2, HAS_OFF, false>(p, s, partial, ctr, stream);

@@ -705,6 +705,31 @@ def test_w4a16_stream_configs(ops, oracle, plan, cfg):
         bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b))
 
 
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,bias", [
+    (16, 11008, 4096, 128, True, torch.bfloat16, False),   # cfg3 decode: 43 strips x 4 K splits
+    (5, 1104, 2048, 128, True, torch.float16, True),       # last strip of 80 columns (10 words), 2 splits
+    (9, 272, 1024, 0, False, torch.bfloat16, True),        # per channel, one split, last strip of 16 columns
+    (16, 1096, 2048, 128, True, torch.bfloat16, False),    # N % 16 != 0: the half-line strips run instead
+])
+def test_w4a16_stream_whole_line(ops, oracle, plan, M, N, K, group, offset, x_dtype, bias):
+    """The decode stream with whole 128-byte weight rows per wave (8-wave strips, each lane two adjacent
+    packed words: the plan for M > 4 and N % 16 == 0): within rtol/atol 1e-2 of the oracle, and bit for bit
+    the half-line strips' output (the same K ranges, folded in the same order)."""
+    say(f"w4a16 whole-line stream M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    case = W.W4A16Case(M=M, N=N, K=K, group=group, x_dtype=x_dtype, offset=offset)
+    d = W.w4a16_inputs(case, seed=3 * M + N)
+    if group == 0:
+        d = dict(d, scale=d["scale"].reshape(-1), offset=None if d["offset"] is None else d["offset"].reshape(-1))
+    b = torch.randn(N).to(x_dtype) if bias else None
+    out = _w4_run(ops, d, group, bias=b)
+    plan("w4_stream_wpl=16")
+    half = _w4_run(ops, d, group, bias=b)
+    plan("")
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), half.view(torch.int16))
+    bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b, x_dtype=x_dtype), dtype=x_dtype)
+
+
 @pytest.mark.parametrize("M,N,K,group,offset,x_dtype", [
     (300, 520, 512, 128, True, torch.bfloat16),     # ragged M and N
     (256, 256, 256, 64, False, torch.float16),      # full tiles
