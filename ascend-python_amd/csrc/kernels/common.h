@@ -373,7 +373,9 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 // a call agree unless the override changes between them.  Spec: a
 // comma-separated list of
 //   w4_stream=off | w4_stream=<nwave>:<nkb>:<pf>   decode stream shape (16:4:2 16:4:4 8:4:2 8:4:4 8:8:2 8:8:3)
-//   w4_stream_wpl=<16|32>                           decode stream: half-line or whole-line weight rows per wave
+//   w4_stream_wpl=<16|32|64>                        decode stream: dwords of each weight row per wave (int4: 16
+//                                                   half lines, 32 whole lines; int8: 16 quarter, 32 half, 64
+//                                                   whole 256-byte rows)
 //   w4_gemm=force | nodma | off                     prefill kernels on few tiles / register-staged only / never
 //   w4_splits=<n>                                   K splits of the 32-row-block decode kernel
 //   qmm_dma=0                                       W8A8 prefill: register-staged kernel instead of the DMA one
@@ -395,7 +397,7 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 struct PlanOverride {
     int w4_stream_nwave = 0, w4_stream_nkb = 0, w4_stream_pf = 0;  // 0: the planner's choice
     bool w4_stream_off = false;
-    int w4_stream_wpl = 0;  // W4A16 decode stream strip width per wave (0: planner, 32 for M > 4)
+    int w4_stream_wpl = 0;  // decode stream: weight-row dwords per wave (0: the planner's choice)
     int w4_gemm = 0;  // 0 planner, 1 force, 2 nodma, 3 off
     int w4_splits = 0;
     bool qmm_dma = true;

@@ -370,11 +370,11 @@ template <int DT, int WPL, int NWAVE, int NKB, int PF, int PIECE_KB, bool HAS_OF
 __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __restrict__ partial, int nstrip,
                                                         int nsplit, uint64_t* __restrict__ ctr, uint64_t tag) {
     typedef Mfma<DT> MM;
-    static_assert(!W8 || WPL == 16, "int8 weights use 16-dword sub-strips");
+    static_assert(!W8 || WPL == 16 || WPL == 32 || WPL == 64, "int8 weights use 16-, 32- or 64-dword sub-strips");
     constexpr int CPW = W8 ? 4 : 8;         // output columns per weight dword
     constexpr int SW = 256 / CPW;           // dwords per strip row (256 columns)
-    constexpr int LW = WPL == 32 ? 2 : 1;   // dwords per lane and row
-    constexpr int TPL = W8 ? 4 : (WPL == 32 ? 16 : WPL == 16 ? 8 : 4);  // MFMA tiles per lane
+    constexpr int LW = W8 ? WPL / 16 : (WPL == 32 ? 2 : 1);  // dwords per lane and row
+    constexpr int TPL = W8 ? 4 * LW : (WPL == 32 ? 16 : WPL == 16 ? 8 : 4);  // MFMA tiles per lane
     constexpr int HALVES = SW / WPL;        // column sub-strips per workgroup
     constexpr int KW = NWAVE / HALVES;      // K ranges per workgroup
     constexpr int NCOL = CPW * WPL;         // output columns per wave
@@ -447,7 +447,11 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const uint32_t ro = (uint32_t)(kb * 32 + r) * rowbytes;
-            if constexpr (LW == 2) {
+            if constexpr (LW == 4) {
+                const u32x4 d = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, w_lane, ro, 0));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) wv[kb % SL][e][r] = d[e];
+            } else if constexpr (LW == 2) {
                 const u32x2 d = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, w_lane, ro, 0));
                 wv[kb % SL][0][r] = d[0];
                 wv[kb % SL][1][r] = d[1];
@@ -475,7 +479,13 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 xk = xa[kb % SL];
         const uint32_t* wk = wv[kb % SL][0];
-        if constexpr (WPL == 32) {  // tile 8d + 2b + o: nibble 2b + o of dword d (column 16c + 8d + 2b + o)
+        if constexpr (W8) {  // tile 4d + t: byte t of dword d (column 4 * LW * c + 4d + t)
+#pragma unroll
+            for (int d = 0; d < LW; ++d)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    ag[4 * d + t] = MM::mma(xk, unpack_i8<DT>(wv[kb % SL][d], t), ag[4 * d + t]);
+        } else if constexpr (WPL == 32) {  // tile 8d + 2b + o: nibble 2b + o of dword d (column 16c + 8d + 2b + o)
 #pragma unroll
             for (int d = 0; d < 2; ++d)
 #pragma unroll
@@ -485,11 +495,6 @@ __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __re
                     ag[8 * d + 2 * b + 1] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wv[kb % SL][d], byte_sel(b)),
                                                     ag[8 * d + 2 * b + 1]);
                 }
-        } else if constexpr (W8) {
-            ag[0] = MM::mma(xk, unpack_i8<DT>(wk, 0), ag[0]);
-            ag[1] = MM::mma(xk, unpack_i8<DT>(wk, 1), ag[1]);
-            ag[2] = MM::mma(xk, unpack_i8<DT>(wk, 2), ag[2]);
-            ag[3] = MM::mma(xk, unpack_i8<DT>(wk, 3), ag[3]);
         } else if constexpr (WPL == 16) {
             ag[0] = MM::mma(xk, unpack_raw<MM::MAGIC, false>(wk, byte_sel(0)), ag[0]);
             ag[1] = MM::mma(xk, unpack_raw<MM::MAGIC, true>(wk, byte_sel(0)), ag[1]);
@@ -1479,10 +1484,25 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
         s.nkb = 4;
         s.pf = 2;
     }
-    if (w8) {  // int8 weights: one instantiated shape
+    if (w8) {
+        // int8 weights: 8-wave strips in which each lane loads 4 (whole 256-byte rows per wave) or 2 (half
+        // rows) adjacent dwords, where groups are whole 128-row pieces; else 16-wave quarter-row strips.
+        // cfg3's shape with int8 weights, M = 16 / 1: 19.9 / 17.4 us quarter rows, 18.5 / 16.2 half rows,
+        // 14.8 / 13.5 whole rows; K = 8192, N = 28672, M = 16 / 1: 81 / 65.5, 66 / 51.5, 66 / 58.4 us.  Whole
+        // rows (1024 K rows per workgroup, one workgroup per CU by its LDS) while at most 512 workgroups run.
         s.nwave = 16;
         s.nkb = 4;
         s.pf = 2;
+        int wpl = ov.w4_stream_wpl;
+        if (wpl == 0 && s.piece_kb == 4) {
+            const int64_t strips = (p.N + 255) / 256;
+            if (p.N % 16 == 0 && p.K % 1024 == 0 && strips * (p.K / 1024) <= 512) wpl = 64;
+            else if (p.N % 8 == 0 && p.K % 512 == 0) wpl = 32;
+        }
+        if (s.piece_kb == 4 && (wpl == 32 || wpl == 64) && p.N % (wpl / 4) == 0) {
+            s.wpl = wpl;
+            s.nwave = 8;
+        }
     } else if (s.piece_kb == 4 && p.N % 16 == 0 &&
                (ov.w4_stream_wpl == 32 || (ov.w4_stream_wpl == 0 && !ov.w4_stream_nwave && p.M > 4))) {
         // whole 128-byte rows per wave (8-wave strips): cfg3 M=16 12.3 -> 11.8 us, K=8192 N=28672 M=16
@@ -1501,7 +1521,7 @@ StreamPlan stream_plan(const WqbmmArgs& p) {
     if (p.K % (kw * rows) != 0) return s;
     s.nwave = kw * halves;
     if (s.nwave != 8 && s.nwave != 16) return s;  // the instantiated shapes
-    if (w8 && s.nwave != 16) return s;
+    if (w8 && s.nwave != (s.wpl == 16 ? 16 : 8)) return s;
     s.nsplit = (int)(p.K / (kw * rows));
     s.nstrip = (int)((p.N + 255) / 256);
     if (s.nsplit > 1 && (int64_t)s.nsplit * p.M * p.N * 4 > ((int64_t)256 << 20)) return s;
@@ -1525,13 +1545,16 @@ hipError_t launch_stream_t(const WqbmmArgs& p, const StreamPlan& s, float* parti
 template <int DT, int NWAVE, bool HAS_OFF>
 hipError_t launch_stream_w(const WqbmmArgs& p, const StreamPlan& s, float* partial, uint64_t* ctr,
                            hipStream_t stream) {
-    if (p.w_dtype == QK_I8) {  // int8 weights: the default shape only
+    if (p.w_dtype == QK_I8) {  // int8 weights: the default shape, or 8-wave strips of wider rows per wave
         if constexpr (NWAVE == 16) {
             switch (s.piece_kb) {
             case 1: return launch_stream_t<DT, 16, 4, 2, 1, HAS_OFF, true>(p, s, partial, ctr, stream);
             case 2: return launch_stream_t<DT, 16, 4, 2, 2, HAS_OFF, true>(p, s, partial, ctr, stream);
             default: return launch_stream_t<DT, 16, 4, 2, 4, HAS_OFF, true>(p, s, partial, ctr, stream);
             }
+        } else {
+            if (s.piece_kb == 4 && s.wpl == 64) return launch_stream_t<DT, 8, 4, 2, 4, HAS_OFF, true, 64>(p, s, partial, ctr, stream);
+            if (s.piece_kb == 4 && s.wpl == 32) return launch_stream_t<DT, 8, 4, 2, 4, HAS_OFF, true, 32>(p, s, partial, ctr, stream);
         }
         return hipErrorInvalidValue;
     }

@@ -65,7 +65,7 @@ bool parse_plan(const char* spec, PlanOverride& o) {
                 r.w4_stream_nkb = b;
                 r.w4_stream_pf = c;
             } else return false;
-        } else if (k == "w4_stream_wpl" && (v == "16" || v == "32")) {
+        } else if (k == "w4_stream_wpl" && (v == "16" || v == "32" || v == "64")) {
             r.w4_stream_wpl = std::atoi(v.c_str());
         } else if (k == "w4_gemm") {
             if (v == "force") r.w4_gemm = 1;

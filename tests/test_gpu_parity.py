@@ -730,6 +730,36 @@ def test_w4a16_stream_whole_line(ops, oracle, plan, M, N, K, group, offset, x_dt
     bf16_close(to_bits(out), _w4_ref(oracle, d, group, bias=b, x_dtype=x_dtype), dtype=x_dtype)
 
 
+@pytest.mark.parametrize("M,N,K,group,offset,x_dtype,bias", [
+    (16, 11008, 4096, 128, True, torch.bfloat16, False),   # cfg3's shape: whole rows, 43 strips x 4 K splits
+    (1, 1040, 2048, 128, True, torch.float16, True),       # whole rows, last strip of 16 columns, 2 splits
+    (7, 1032, 1024, 128, False, torch.bfloat16, True),     # N % 16 == 8: half rows, last strip of 8 columns
+    (4, 24576, 8192, 128, True, torch.bfloat16, False),    # 768 workgroups of whole rows: half rows instead
+    (5, 1036, 2048, 128, True, torch.bfloat16, False),     # N % 8 == 4: quarter rows (16-wave strips)
+])
+def test_w8a16_stream_row_widths(ops, oracle, plan, M, N, K, group, offset, x_dtype, bias):
+    """The int8 decode stream on a row-major [K, N] weight with 4 (whole 256-byte rows per wave), 2 (half rows)
+    or 1 (quarter rows) dwords per lane, as planned for the shape: within rtol/atol 1e-2 of the oracle; and every
+    row width forced on the shape (where it applies) within the same bar."""
+    say(f"w8a16 stream row widths M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn((M, K), generator=g).to(x_dtype)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    sc = (5e-4 + 2.5e-3 * torch.rand((K // group, N), generator=g)).to(torch.float16)
+    off = (8 * torch.rand((K // group, N), generator=g) - 4).to(torch.float16) if offset else None
+    b = torch.randn(N, generator=g).to(x_dtype) if bias else None
+    ref = oracle.weight_quant_bmm(W.bits(x), CODE[x_dtype], w.numpy(), W.bits(sc),
+                                  None if off is None else W.bits(off), F16, group,
+                                  bias=None if b is None else W.bits(b), bias_dtype=CODE[x_dtype],
+                                  out_dtype=CODE[x_dtype])
+    args = (x.to(DEV), w.to(DEV), sc.to(DEV), None if off is None else off.to(DEV))
+    for spec in ("", "w4_stream_wpl=16", "w4_stream_wpl=32", "w4_stream_wpl=64"):
+        plan(spec)
+        out = ops.npu_weight_quant_batchmatmul(*args, bias=None if b is None else b.to(DEV), antiquant_group_size=group)
+        bf16_close(to_bits(out), ref, dtype=x_dtype)
+    plan("")
+
+
 @pytest.mark.parametrize("M,N,K,group,offset,x_dtype", [
     (300, 520, 512, 128, True, torch.bfloat16),     # ragged M and N
     (256, 256, 256, 64, False, torch.float16),      # full tiles
