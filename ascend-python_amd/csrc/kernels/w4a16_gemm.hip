@@ -363,9 +363,11 @@ __global__ __launch_bounds__(kThreads) void w4_decode(WqbmmArgs p, float* __rest
 // and the strip's last split to arrive adds them in split order, adds bias
 // and casts (one kernel); without one, w4_reduce finishes.
 // W8 (int8 weights [K, N], W8A16): a strip is 64 dwords (256 columns, two
-// lines per row), slot c owns dword c of its sub-strip and its 4 bytes (4
-// MFMA tiles, columns 4c + t), and the operands are the exact 16-bit values
-// of the bytes (no magic offset: BASE = 0).
+// lines per row) and WPL is 16, 32 or 64 (a quarter, half or whole row per
+// wave): slot c owns LW = WPL/16 adjacent dwords of its sub-strip (one 4-,
+// 8- or 16-byte load per row) and their 4*LW bytes (MFMA tiles, columns
+// 4*LW*c + t), and the operands are the exact 16-bit values of the bytes (no
+// magic offset: BASE = 0).
 template <int DT, int WPL, int NWAVE, int NKB, int PF, int PIECE_KB, bool HAS_OFF, bool FINAL, bool W8>
 __global__ __launch_bounds__(64 * NWAVE) void w4_stream(WqbmmArgs p, float* __restrict__ partial, int nstrip,
                                                         int nsplit, uint64_t* __restrict__ ctr, uint64_t tag) {
