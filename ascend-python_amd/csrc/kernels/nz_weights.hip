@@ -571,11 +571,12 @@ __global__ __launch_bounds__(nzg::NT) void w4nz_gemm(WqbmmArgs p, int tiles_m, i
     };
 
     // The workgroup's segments, in the order it runs them.  Whole tiles: one, the workgroup's own.  Stream-K
-    // (one workgroup per CU): range r of the ntiles * nu groups, tile-major, is r * U / P .. (r+1) * U / P; it
-    // runs first the head of the tile its range ends in (groups 0 .. ub of tile tb, handed on to range r + 1
-    // through partial slot r), then its whole tiles, then the tail of the tile its range starts in (groups
-    // ua .. nu of tile ta), which continues from range r - 1's head.  Each tile has at most two segments (a
-    // range holds at least one tile's groups).
+    // (P workgroups, one per CU, workgroup r = the XCD-swizzled block index): first dp_rounds whole tiles in
+    // lockstep (tile seg * P + r), then range r of the other tiles' U = (ntiles - D) * nu groups, tile-major,
+    // r * U / P .. (r+1) * U / P.  A range runs first the head of the tile it ends in (groups 0 .. ub of tile
+    // tb, handed on to range r + 1 through partial slot r), then its whole tiles, then the tail of the tile it
+    // starts in (groups ua .. nu of tile ta), which continues from range r - 1's head.  Each tile has at most
+    // two segments (a range holds at least one tile's groups).
     int r = 0, ta = 0, ua = 0, tb = 0, ub = 0, nseg = 1;
     bool has_head = false, has_tail = false;
     const int P = (int)gridDim.x;
