@@ -380,6 +380,8 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   w4_splits=<n>                                   K splits of the 32-row-block decode kernel
 //   qmm_dma=0                                       W8A8 prefill: register-staged kernel instead of the DMA one
 //   qmm_bm128=0                                     W8A8 K splits: 256-row tiles only (no 128-row split tiles)
+//   qmm_rev=0                                       W8A8 DMA kernel: every round walks K forwards (by default
+//                                                   every other round of one workgroup per CU walks it backwards)
 //   qmm_mid=0                                       W8A8 M <= 256: split stream / tiled kernels instead of qmm_mid
 //   mid_bm=<16|32|64>, mid_split=<1|2>              qmm_mid: row block and K split (where the shape allows them)
 //   mid_bn=<64|128>                                 qmm_mid: column block (128 only for a [K,N] weight)
@@ -409,9 +411,12 @@ struct PlanOverride {
     bool w4nz_off = false;
     int nzg_sk = 1;
     int nzg_sk_dp = -1;  // whole-tile rounds before the stream-K share (-1: the planner's choice)
+    int qmm_rev = 1;
     int w4nz_wg = 0, w4nz_nit = 0;
 };
 const PlanOverride& plan_override();
+// CUs of the current device (cached per device; 0 if it cannot be read)
+int device_cus();
 bool set_plan_override(const char* spec);  // false: spec not understood (override unchanged)
 
 // ---------------------------------------------------------------- launchers

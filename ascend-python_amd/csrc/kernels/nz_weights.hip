@@ -35,6 +35,21 @@
 #include "common.h"
 
 namespace qk {
+
+// CUs of the current device (cached per device; 0 if it cannot be read)
+int device_cus() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cache[kMaxDev];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 namespace {
 
 constexpr int kNzThreads = 256;
@@ -989,20 +1004,6 @@ NzGemmPlan nzg_plan(const WqbmmArgs& p) {
     if ((int64_t)g.tiles_m * g.tiles_n < 64) return g;
     g.ok = true;
     return g;
-}
-
-// CUs of the current device (cached per device; 0 if it cannot be read)
-int device_cus() {
-    constexpr int kMaxDev = 64;
-    static std::atomic<int> cache[kMaxDev];
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
-    int n = cache[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
-        cache[dev].store(n, std::memory_order_relaxed);
-    }
-    return n;
 }
 
 // Stream-K schedule of the NZ prefill GEMM: one workgroup per CU takes an equal share of all tiles' groups,

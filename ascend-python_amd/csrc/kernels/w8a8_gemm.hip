@@ -12,6 +12,8 @@
 // registers while the current one is multiplied.  A weight given as
 // [K,N]-contiguous is transposed 4x4 bytes at a time with v_perm_b32 on its
 // way into LDS, so both storage orders feed the same MFMA fragments.
+#include <climits>
+
 #include "common.h"
 
 namespace qk {
@@ -655,9 +657,12 @@ constexpr int SMEM = RING > OUT_BYTES ? RING : OUT_BYTES;
 // N = 2I columns, gate then up; tile tn covers outputs 128 tn .. +127, its B columns the gate columns
 // 128 tn .. and the up columns I + 128 tn .. (NZ blocks or [K,N] column chunks addressed apart); no split.
 // There `partial`, when not null, receives the tiles' per-row partial absmax of h (fp32 [M][I / 128]).
+// rev_from (> 0; the CU count, or INT_MAX for none): workgroups in odd rounds of rev_from walk their K range
+// backwards.  A second-round workgroup takes the next column tiles of the same row blocks on its XCD, so it
+// starts on the K stages the first round read last, which are still in that XCD's L2.
 template <int BL, int OUT, int BMX = 256>
 __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int tiles_n, int nsplit,
-                                                  int32_t* __restrict__ partial) {
+                                                  int32_t* __restrict__ partial, int rev_from) {
     using namespace dm;
     constexpr bool B_KN = BL == kLayKN, B_NZ = BL == kLayNZ;
     constexpr bool SWI = OUT >= kOutSwiGLU;
@@ -726,10 +731,14 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
 
     const int nk = (int)(k_len / dm::BK);  // a multiple of NST (checked on the host)
     const int nr = nk / 2;                 // A slots' worth of K
+    // every other round of rev_from workgroups (the second, fourth, ...) walks K backwards: int32 sums are
+    // exact in any order
+    const bool rev = (((int)blockIdx.x / rev_from) & 1) != 0;
     // group 1 issues the weight: stage kt into buffer st, four instructions per wave (a stage past the end
     // fetches the last one again into its free buffer, so every stage issues the same number of DMAs)
     auto issue_b = [&](int kt, int st) {
-        const uint32_t k0 = k_base + (uint32_t)(kt < nk ? kt : nk - 1) * dm::BK;
+        const int ks = kt < nk ? kt : nk - 1;
+        const uint32_t k0 = k_base + (uint32_t)(rev ? nk - 1 - ks : ks) * dm::BK;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int b = 4 * gw + i;
@@ -746,7 +755,8 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
     // group 0 issues A: rows 128h..128h+127 of range r (K bytes 128r..128r+127 of this split) into slot
     // r % 3 (past the last range, the last range again)
     auto issue_a = [&](int r, int h) {
-        const int rs = r < nr ? r : nr - 1;
+        const int rs0 = r < nr ? r : nr - 1;
+        const int rs = rev ? nr - 1 - rs0 : rs0;
         const uint32_t lds = sbase + A_BASE + (uint32_t)(r % NSA) * A_SL;
         const uint32_t k0 = k_base + (uint32_t)rs * A_KB;
 #pragma unroll
@@ -768,7 +778,7 @@ __global__ __launch_bounds__(dm::NT) void qmm_dma(QmmArgs p, int tiles_m, int ti
 
     i32x4 af[TM], bfr[8];
     auto frags = [&](int kt, int st) {
-        const int ard = ((kt & 1) ? a_rd1 : a_rd0) + ((kt >> 1) % NSA) * A_SL;
+        const int ard = (((kt & 1) != 0) != rev ? a_rd1 : a_rd0) + ((kt >> 1) % NSA) * A_SL;
 #pragma unroll
         for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i32x4*>(smem + ard + i * 16 * A_KB);
 #pragma unroll
@@ -1665,6 +1675,12 @@ bool big_dma_ok(const QmmArgs& p, bool b_kn, int nsplit) {
            (b_kn ? (p.sbk % 16 == 0 && (uint64_t)p.K * (uint64_t)p.sbk < (1ull << 32)) : (p.sbn % 16 == 0));
 }
 
+// qmm_dma's round length for walking K backwards in every other round: one workgroup per CU (INT_MAX: never)
+int dma_rev_from() {
+    const int cus = plan_override().qmm_rev ? device_cus() : 0;
+    return cus > 0 ? cus : INT_MAX;
+}
+
 template <int OUT>
 hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, int nsplit, int32_t* partial,
                       hipStream_t stream) {
@@ -1673,8 +1689,8 @@ hipError_t launch_big(const QmmArgs& p, bool b_kn, int tiles_m, int tiles_n, int
     const bool dma = big_dma_ok(p, b_kn, nsplit);
     if (nsplit > 1 && !full && !dma) return hipErrorInvalidValue;  // not planned (launch_quant_matmul unsplits)
     if (dma) {
-        if (b_kn) qmm_dma<kLayKN, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
-        else qmm_dma<kLayNK, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
+        if (b_kn) qmm_dma<kLayKN, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial, dma_rev_from());
+        else qmm_dma<kLayNK, OUT><<<grid, dim3(dm::NT), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial, dma_rev_from());
     } else if (full) {
         if (b_kn) qmm_big<true, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
         else qmm_big<false, OUT, 8, true><<<grid, dim3(512), 0, stream>>>(p, tiles_m, tiles_n, nsplit, partial);
@@ -1743,7 +1759,7 @@ size_t big_split_workspace(const BigPlan& b, int64_t M, int64_t N) {
 template <int BL>
 hipError_t launch_split128(const QmmArgs& p, const BigPlan& b, int32_t* partial, hipStream_t stream) {
     const dim3 sgrid((uint32_t)((int64_t)b.tiles_m * b.tiles_n * b.nsplit)), sblock(dm::NT);
-    qmm_dma<BL, QK_I32, 128><<<sgrid, sblock, 0, stream>>>(p, b.tiles_m, b.tiles_n, b.nsplit, partial);
+    qmm_dma<BL, QK_I32, 128><<<sgrid, sblock, 0, stream>>>(p, b.tiles_m, b.tiles_n, b.nsplit, partial, dma_rev_from());
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     int64_t blocks = ((int64_t)b.tiles_m * b.tiles_n * 8 * 16 * 64 + kThreads - 1) / kThreads;
@@ -2092,7 +2108,7 @@ bool nz_dma_ok(const BigPlan& b, int64_t M, int64_t N, int64_t K) {
 template <int OUT>
 hipError_t launch_dma_nz(const QmmArgs& p, const BigPlan& b, int32_t* partial, hipStream_t stream) {
     qmm_dma<kLayNZ, OUT><<<dim3((uint32_t)(b.tiles_m * b.tiles_n * b.nsplit)), dim3(dm::NT), 0, stream>>>(
-        p, b.tiles_m, b.tiles_n, b.nsplit, partial);
+        p, b.tiles_m, b.tiles_n, b.nsplit, partial, dma_rev_from());
     return hipGetLastError();
 }
 
@@ -2169,11 +2185,11 @@ hipError_t launch_quant_matmul_swiglu(const QmmArgs& p, bool nz, float* amax_par
     constexpr int S = kOutSwiGLU;
     int32_t* ap = reinterpret_cast<int32_t*>(amax_part);
     if (nz) {
-        if (e.out_dtype == QK_BF16) qmm_dma<kLayNZ, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap);
-        else qmm_dma<kLayNZ, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap);
+        if (e.out_dtype == QK_BF16) qmm_dma<kLayNZ, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap, dma_rev_from());
+        else qmm_dma<kLayNZ, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap, dma_rev_from());
     } else {
-        if (e.out_dtype == QK_BF16) qmm_dma<kLayKN, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap);
-        else qmm_dma<kLayKN, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap);
+        if (e.out_dtype == QK_BF16) qmm_dma<kLayKN, S + QK_BF16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap, dma_rev_from());
+        else qmm_dma<kLayKN, S + QK_F16><<<grid, block, 0, stream>>>(p, tm, tn, 1, ap, dma_rev_from());
     }
     return hipGetLastError();
 }

@@ -513,6 +513,38 @@ def test_quant_matmul_prefill_ragged_m_register_staged(ops, plan):
     assert torch.equal(dma.view(torch.int16), reg.view(torch.int16))
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 8192, 512), (2304, 8192, 1024)])
+@pytest.mark.parametrize("layout", ["kn", "nk", "nz"])
+def test_quant_matmul_prefill_reverse_rounds(ops, plan, M, N, K, layout):
+    """The direct-to-LDS prefill kernel walks K backwards in every other round of one workgroup per CU (1024
+    tiles: four rounds; 288 tiles: one and a bit).  Every int32 accumulator passes exact row and column
+    checksums, and the int32 and bf16 outputs equal those of the run with every round forwards (qmm_rev=0)."""
+    say(f"quant_matmul M={M} N={N} K={K} {layout}, K backwards in odd rounds vs forwards")
+    g = torch.Generator().manual_seed(M + K)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    wd = w.to(DEV)
+    if layout == "nk":
+        wd = w.t().contiguous().to(DEV).t()
+    elif layout == "nz":
+        wd = ops.npu_format_cast(wd, ops.ACL_FORMAT_FRACTAL_NZ)
+    ad = a.to(DEV)
+    s = (1e-3 + 9e-3 * torch.rand(N, generator=g)).to(DEV)
+    pt = (1e-2 * torch.rand(M, generator=g)).to(DEV)
+    outs = []
+    for spec in ("", "qmm_rev=0"):
+        plan(spec)
+        acc = ops.npu_quant_matmul(ad, wd, torch.ones(1, device=DEV), output_dtype=torch.int32)
+        out = ops.npu_quant_matmul(ad, wd, s, pertoken_scale=pt, output_dtype=torch.bfloat16)
+        outs.append((acc, out))
+    acc64 = outs[0][0].to(torch.int64)
+    a64, w64 = a.to(torch.int64), w.to(torch.int64)
+    assert torch.equal(acc64.sum(0).cpu(), a64.sum(0) @ w64)
+    assert torch.equal(acc64.sum(1).cpu(), a64 @ w64.sum(1))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1].view(torch.int16), outs[1][1].view(torch.int16))
+
+
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32, torch.int32])
 @pytest.mark.parametrize("per_tensor", [False, True])

@@ -37,10 +37,12 @@ def test_debug_plan_override_parsing():
     for spec in ("", "w4_stream=16:4:4", "w4_stream=off", "w4_gemm=force,skinny_splits=4", "qmm_dma=0", "qmm_mid=0",
                  "mid_bm=32,mid_split=2", "mid_bn=64", "qmm_bm128=0",
                  "w4_splits=8,w4_gemm=nodma", "w4nz=off", "w4nz_wg=172", "w4nz_nit=4", "nzg_sk=0",
-                 "nzg_sk=tailfirst", "nzg_sk=1,nzg_sk_dp=0", "skinny_pf=2", "w4_stream_wpl=32", "w4_stream_wpl=64"):
+                 "nzg_sk=tailfirst", "nzg_sk=1,nzg_sk_dp=0", "skinny_pf=2", "w4_stream_wpl=32", "w4_stream_wpl=64",
+                 "qmm_rev=0", "qmm_rev=1"):
         q.debug_set_plan(spec)
     for bad in ("w4_stream=12:4:2", "w4_gemm=maybe", "skinny_splits=3", "nonsense", "qmm_dma=2", "w4nz=on",
-                "w4nz_wg=0", "qmm_bm128=2", "nzg_sk=2", "nzg_sk_dp=-1", "skinny_pf=4", "w4_stream_wpl=8"):
+                "w4nz_wg=0", "qmm_bm128=2", "nzg_sk=2", "nzg_sk_dp=-1", "skinny_pf=4", "w4_stream_wpl=8",
+                "qmm_rev=2"):
         with pytest.raises(ValueError, match="not understood"):
             q.debug_set_plan(bad)
     q.debug_set_plan("")
