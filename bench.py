@@ -101,7 +101,7 @@ def cpu_model() -> str:
 
 
 def cpu_baseline(target_s: float) -> dict:
-    """The CPU reference path of BASELINE.md section 3 on cfg1, on all host cores.
+    """The reference's CPU path on cfg1 (the first of BASELINE.json's configs), on all host cores.
 
     One step = npu_dynamic_quant (torch CPU fp32: absmax / 127, IEEE division, round-half-even, clamp)
     + the exact int32 GEMM (float64 BLAS on int8-valued operands) + the fused epilogue and bf16 cast
@@ -411,7 +411,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU sharding plan is described in DESIGN.md, not measured", file=sys.stderr)
+              "the multi-GPU sharding plan is a design, not a measured path", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
