@@ -513,11 +513,11 @@ def test_quant_matmul_prefill_ragged_m_register_staged(ops, plan):
     assert torch.equal(dma.view(torch.int16), reg.view(torch.int16))
 
 
-@pytest.mark.parametrize("M,N,K", [(8192, 8192, 512), (2304, 8192, 1024)])
+@pytest.mark.parametrize("M,N,K", [(8192, 8192, 512), (2304, 8192, 1024), (4000, 8192, 512)])
 @pytest.mark.parametrize("layout", ["kn", "nk", "nz"])
 def test_quant_matmul_prefill_reverse_rounds(ops, plan, M, N, K, layout):
     """The direct-to-LDS prefill kernel walks K backwards in every other round of one workgroup per CU (1024
-    tiles: four rounds; 288 tiles: one and a bit).  Every int32 accumulator passes exact row and column
+    tiles: four rounds; 288 tiles: one and a bit; M = 4000: two rounds, the last row tile 160 rows).  Every int32 accumulator passes exact row and column
     checksums, and the int32 and bf16 outputs equal those of the run with every round forwards (qmm_rev=0)."""
     say(f"quant_matmul M={M} N={N} K={K} {layout}, K backwards in odd rounds vs forwards")
     g = torch.Generator().manual_seed(M + K)
