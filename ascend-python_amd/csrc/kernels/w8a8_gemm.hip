@@ -1833,7 +1833,8 @@ hipError_t launch_skinny_t(const QmmArgs& p, const SkinnyPlan& s, int32_t* parti
     k<<<grid, dim3(kThreads), 0, stream>>>(p, s.tiles_n, s.nsplit, partial);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    int64_t blocks = (p.M * p.N + kThreads - 1) / kThreads;
+    // qmm_reduce takes 4 outputs per thread where N % 4 == 0 (grid-stride loops either way)
+    int64_t blocks = ((p.N % 4 == 0 ? p.M * p.N / 4 : p.M * p.N) + kThreads - 1) / kThreads;
     if (blocks > 65536) blocks = 65536;
     qmm_reduce<<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(p, s.nsplit, partial);
     return hipGetLastError();
