@@ -383,6 +383,8 @@ __device__ __forceinline__ void qmm_store(const QmmEpilogue& e, int64_t m, int64
 //   qmm_rev=0                                       W8A8 DMA kernel: every round walks K forwards (by default
 //                                                   every other round of one workgroup per CU walks it backwards)
 //   qmm_mid=0                                       W8A8 M <= 256: split stream / tiled kernels instead of qmm_mid
+//   qmm_small=<0|2|4|8>                             W8A8 [K,N], 32 < M <= 128: 0 always qmm_mid; n 128-row tiles
+//                                                   with n K splits where the shape allows (default: cost model)
 //   mid_bm=<16|32|64>, mid_split=<1|2>              qmm_mid: row block and K split (where the shape allows them)
 //   mid_bn=<64|128>                                 qmm_mid: column block (128 only for a [K,N] weight)
 //   skinny_splits=<n>                               W8A8 small-M stream: K splits (power of two, same bounds)
@@ -412,6 +414,7 @@ struct PlanOverride {
     int nzg_sk = 1;
     int nzg_sk_dp = -1;  // whole-tile rounds before the stream-K share (-1: the planner's choice)
     int qmm_rev = 1;
+    int qmm_small = -1;
     int w4nz_wg = 0, w4nz_nit = 0;
 };
 const PlanOverride& plan_override();

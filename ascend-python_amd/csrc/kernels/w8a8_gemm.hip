@@ -1917,6 +1917,52 @@ size_t mid_workspace(const MidPlan& m) {
     return m.nsplit > 1 ? QK_SPLIT_COUNTER_BYTES + (size_t)m.tiles * m.nsplit * m.bm * m.bn * sizeof(int32_t) : 0;
 }
 
+// [K,N] weights with 32 < M <= 128: qmm_mid reads the weight once per row block and fills LDS at ~45 GB/s per
+// CU, so on wide or deep weights the 128-row K splits of the direct-to-LDS kernel (one row tile: every weight
+// byte read once; exact int32 partials, then qmm_reduce_tiled) finish sooner.  A cost model in microseconds
+// from measured rates (a CU's LDS fill ~45 GB/s; one HBM stream ~5 TB/s, and ~3.1 TB/s for qmm_mid's weight
+// reads; the reduce ~4 TB/s plus ~3 us):
+//   qmm_mid: the larger of its plan's rounds x (BM + BN) x K / nsplit bytes per CU at the fill rate and its
+//            weight at its HBM rate;
+//   split:   the larger of its fill time (the M rows of A: rows past M read as zeros without a fetch) and its
+//            HBM time (the weight and the partials written), plus the reduce of the partials.
+// The split count with the lowest estimate is taken when it is below 0.9 of qmm_mid's.  The sums are exact, so
+// the bits equal qmm_mid's.  Returns the split count, or 0 for qmm_mid.
+int small_split(int64_t M, int64_t N, int64_t K, const MidPlan& mp) {
+    const PlanOverride& ov = plan_override();  // debug override: qmm_small=0 never, =<n> that split count
+    if (ov.qmm_small == 0 || mp.bm == 0 || M <= 32 || M > 128 || N % 256 != 0 || K <= 0) return 0;
+    auto rounds = [](int64_t wgs) { return (double)((wgs + 255) / 256); };
+    constexpr double kFill = 45e3, kHbm = 5e6, kMidHbm = 3.1e6, kReduce = 4e6, kReduceFixed = 3.0;  // bytes/us; us
+    const double w_bytes = (double)K * (double)N;
+    const double t_mid_fill = rounds((int64_t)mp.tiles * mp.nsplit) * (mp.bm + mp.bn) * (double)(K / mp.nsplit) / kFill;
+    const double t_mid = t_mid_fill > w_bytes / kMidHbm ? t_mid_fill : w_bytes / kMidHbm;
+    int best = 0;
+    double t_best = 0.9 * t_mid;
+    for (int ns : {2, 4, 8}) {
+        if (ov.qmm_small > 0 && ns != ov.qmm_small) continue;
+        if (K % ((int64_t)ns * dm::BK * dm::NST) != 0) continue;
+        const double part = (double)ns * 128.0 * (double)N * 4.0;
+        const double t_fill = rounds(N / 256 * ns) * (double)(M + 256) * (double)(K / ns) / kFill;
+        const double t_hbm = (w_bytes + part) / kHbm;
+        const double t = (t_fill > t_hbm ? t_fill : t_hbm) + part / kReduce + kReduceFixed;
+        if (ov.qmm_small > 0 || t < t_best) {
+            best = ns;
+            t_best = t;
+        }
+    }
+    return best;
+}
+
+BigPlan small_split_plan(int64_t M, int64_t N, int ns) {
+    BigPlan b;
+    b.ok = true;
+    b.bm = 128;
+    b.tiles_m = (int)((M + 127) / 128);
+    b.tiles_n = (int)(N / 256);
+    b.nsplit = ns;
+    return b;
+}
+
 template <int BL, int BM, int BN, int OUT>
 hipError_t launch_mid_o(const QmmArgs& p, const MidPlan& mp, int32_t* partial, uint64_t* ctr, hipStream_t stream) {
     // 8 waves; a prefetch wave 12 stages ahead for a [K,N] weight (measured: it shortens the [K,N]
@@ -1972,8 +2018,15 @@ hipError_t launch_qmm_fallback(const QmmArgs& p, bool a_ok, bool b_kn, bool b_nk
 
 // A split workspace is [split-K counters][int32 partials [nsplit][M][N]].
 size_t quant_matmul_workspace(int64_t M, int64_t N, int64_t K) {
-    if (mid_plan(M, N, K, false).bm != 0 && M > 32)  // eligibility does not depend on the layout; the
-        return mid_workspace(mid_plan(M, N, K, true));  // [K,N] plan's split needs a workspace
+    if (mid_plan(M, N, K, false).bm != 0 && M > 32) {  // eligibility does not depend on the layout; the
+        const MidPlan mk = mid_plan(M, N, K, true);     // [K,N] plan's splits need a workspace
+        size_t need = mid_workspace(mk);
+        if (const int ns = small_split(M, N, K, mk)) {
+            const size_t alt = big_split_workspace(small_split_plan(M, N, ns), M, N);
+            if (alt > need) need = alt;
+        }
+        return need;
+    }
     const SkinnyPlan s = skinny_plan(M, N, K);
     if (s.mt != 0)
         return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(int32_t);
@@ -1998,6 +2051,14 @@ hipError_t launch_quant_matmul(const QmmArgs& p, void* workspace, size_t ws_byte
     int32_t* partial = ws ? reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES) : nullptr;
     MidPlan mp = mid_plan(p.M, p.N, p.K, b_kn16);
     if (mp.bm != 0 && (p.M > 32 || !b_kn16)) {
+        if (b_kn16) {  // wide or deep [K,N] weights: 128-row K splits where the cost model favours them
+            if (const int ns = small_split(p.M, p.N, p.K, mp)) {
+                const BigPlan sb = small_split_plan(p.M, p.N, ns);
+                if (big_dma_ok(p, true, ns) && partial && ws_bytes >= big_split_workspace(sb, p.M, p.N) &&
+                    (uintptr_t)partial % 16 == 0)
+                    return launch_split128<kLayKN>(p, sb, partial, stream);
+            }
+        }
         // a split plan needs its partials and counters; with less workspace the same blocks run unsplit
         const size_t need = mid_workspace(mp);
         if (need && (!ws || ws_bytes < need || (uintptr_t)ws % 16 != 0)) mp.nsplit = 1;

@@ -94,6 +94,8 @@ bool parse_plan(const char* spec, PlanOverride& o) {
             r.nzg_sk_dp = a;
         } else if (k == "qmm_rev" && (v == "0" || v == "1")) {
             r.qmm_rev = std::atoi(v.c_str());
+        } else if (k == "qmm_small" && (v == "0" || v == "2" || v == "4" || v == "8")) {
+            r.qmm_small = std::atoi(v.c_str());
         } else if (k == "w4nz_wg" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 65536) {
             r.w4nz_wg = a;
         } else if (k == "w4nz_nit" && std::sscanf(v.c_str(), "%d", &a) == 1 && a >= 1 && a <= 8) {

@@ -513,6 +513,44 @@ def test_quant_matmul_prefill_ragged_m_register_staged(ops, plan):
     assert torch.equal(dma.view(torch.int16), reg.view(torch.int16))
 
 
+@pytest.mark.parametrize("M,N,K,spec", [
+    (128, 11008, 4096, ""),           # the cost model's 128-row K splits (4)
+    (100, 11008, 4096, ""),           # the same with a ragged row tile (28 rows past M)
+    (128, 4096, 14336, ""),           # a deep weight
+    (64, 4096, 4096, "qmm_small=2"),  # forced: 2 splits, half a row tile
+    (48, 4096, 8192, "qmm_small=8"),  # forced: 8 splits
+])
+def test_quant_matmul_small_m_split_tiles(ops, oracle, plan, M, N, K, spec):
+    """[K,N] weights with 32 < M <= 128 on 128-row tiles with K splits (exact int32 partials, then the tiled
+    reduce) where the cost model favours them over the mid-M kernel: every int32 accumulator passes exact row and
+    column checksums, a row subset of the bf16 output (per-token and per-channel scales, bf16 bias) equals the
+    oracle bit for bit, and both outputs equal the mid-M kernel's (qmm_small=0)."""
+    say(f"quant_matmul small M on split tiles M={M} N={N} K={K} {spec or 'planner'}")
+    g = torch.Generator().manual_seed(M + N + K + 1)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    ad, wd = a.to(DEV), w.to(DEV)
+    s = 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    pt = 1e-2 * torch.rand(M, generator=g)
+    b = torch.randn(N, generator=g).to(torch.bfloat16)
+    outs = []
+    for sp in (spec, "qmm_small=0"):
+        plan(sp)
+        acc = ops.npu_quant_matmul(ad, wd, torch.ones(1, device=DEV), output_dtype=torch.int32)
+        out = ops.npu_quant_matmul(ad, wd, s.to(DEV), pertoken_scale=pt.to(DEV), bias=b.to(DEV),
+                                   output_dtype=torch.bfloat16)
+        outs.append((acc, out))
+    a64, w64, acc64 = a.to(torch.int64), w.to(torch.int64), outs[0][0].cpu().to(torch.int64)
+    assert torch.equal(acc64.sum(0), a64.sum(0) @ w64)
+    assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
+    rows = np.r_[0:8, M - 8:M]
+    ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(), pertoken=pt[rows].numpy(), bias=W.bits(b),
+                              bias_dtype=BF16, out_dtype=BF16)
+    assert np.array_equal(to_bits(outs[0][1])[rows], ref)
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1].view(torch.int16), outs[1][1].view(torch.int16))
+
+
 @pytest.mark.parametrize("M,N,K", [(8192, 8192, 512), (2304, 8192, 1024), (4000, 8192, 512)])
 @pytest.mark.parametrize("layout", ["kn", "nk", "nz"])
 def test_quant_matmul_prefill_reverse_rounds(ops, plan, M, N, K, layout):

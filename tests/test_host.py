@@ -38,11 +38,11 @@ def test_debug_plan_override_parsing():
                  "mid_bm=32,mid_split=2", "mid_bn=64", "qmm_bm128=0",
                  "w4_splits=8,w4_gemm=nodma", "w4nz=off", "w4nz_wg=172", "w4nz_nit=4", "nzg_sk=0",
                  "nzg_sk=tailfirst", "nzg_sk=1,nzg_sk_dp=0", "skinny_pf=2", "w4_stream_wpl=32", "w4_stream_wpl=64",
-                 "qmm_rev=0", "qmm_rev=1"):
+                 "qmm_rev=0", "qmm_rev=1", "qmm_small=0", "qmm_small=8"):
         q.debug_set_plan(spec)
     for bad in ("w4_stream=12:4:2", "w4_gemm=maybe", "skinny_splits=3", "nonsense", "qmm_dma=2", "w4nz=on",
                 "w4nz_wg=0", "qmm_bm128=2", "nzg_sk=2", "nzg_sk_dp=-1", "skinny_pf=4", "w4_stream_wpl=8",
-                "qmm_rev=2"):
+                "qmm_rev=2", "qmm_small=3"):
         with pytest.raises(ValueError, match="not understood"):
             q.debug_set_plan(bad)
     q.debug_set_plan("")
@@ -65,6 +65,15 @@ def test_w8a8_split_plan_workspace_sizes():
         # a ragged M pads the 128-row tiles' partials to whole tiles: 300 rows -> 3 tiles, 4 splits
         assert L.qk_quant_matmul_nz_workspace_size(300, 4096, 8192, BF16, ctypes.byref(ws)) == 0
         assert ws.value == ctr + 4 * 384 * 4096 * 4
+        # M = 128 on a wide [K,N] weight (11008 x 4096) runs 128-row tiles with 4 K splits (the cost model's
+        # choice over qmm_mid); cfg1 (4096 x 4096) stays on qmm_mid, which needs no workspace
+        assert L.qk_quant_matmul_workspace_size(128, 11008, 4096, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == ctr + 4 * 128 * 11008 * 4
+        assert L.qk_quant_matmul_workspace_size(128, 4096, 4096, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == 0
+        q.debug_set_plan("qmm_small=0")
+        assert L.qk_quant_matmul_workspace_size(128, 11008, 4096, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == 0
         q.debug_set_plan("qmm_bm128=0")
         assert L.qk_quant_matmul_nz_workspace_size(M, N, K, BF16, ctypes.byref(ws)) == 0
         assert ws.value == ctr + 8 * M * N * 4
