@@ -1917,25 +1917,27 @@ size_t mid_workspace(const MidPlan& m) {
     return m.nsplit > 1 ? QK_SPLIT_COUNTER_BYTES + (size_t)m.tiles * m.nsplit * m.bm * m.bn * sizeof(int32_t) : 0;
 }
 
-// [K,N] weights with 32 < M <= 128: qmm_mid reads the weight once per row block and fills LDS at ~45 GB/s per
-// CU, so on wide or deep weights the 128-row K splits of the direct-to-LDS kernel (one row tile: every weight
-// byte read once; exact int32 partials, then qmm_reduce_tiled) finish sooner.  A cost model in microseconds
-// from measured rates (a CU's LDS fill ~45 GB/s; one HBM stream ~5 TB/s, and ~3.1 TB/s for qmm_mid's weight
-// reads; the reduce ~4 TB/s plus ~3 us):
+// [K,N] and int8 NZ weights with 32 < M <= 128: qmm_mid reads the weight once per row block and fills LDS at
+// ~45 GB/s per CU, so on wide or deep weights the 128-row K splits of the direct-to-LDS kernel (one row tile:
+// every weight byte read once; exact int32 partials, then qmm_reduce_tiled) finish sooner.  A cost model in
+// microseconds from measured rates (a CU's LDS fill ~45 GB/s; one HBM stream ~5 TB/s, and for qmm_mid's weight
+// reads ~3.1 TB/s on [K,N] rows, ~4.6 TB/s on NZ blocks; the reduce ~4 TB/s plus ~3 us):
 //   qmm_mid: the larger of its plan's rounds x (BM + BN) x K / nsplit bytes per CU at the fill rate and its
 //            weight at its HBM rate;
 //   split:   the larger of its fill time (the M rows of A: rows past M read as zeros without a fetch) and its
 //            HBM time (the weight and the partials written), plus the reduce of the partials.
 // The split count with the lowest estimate is taken when it is below 0.9 of qmm_mid's.  The sums are exact, so
 // the bits equal qmm_mid's.  Returns the split count, or 0 for qmm_mid.
-int small_split(int64_t M, int64_t N, int64_t K, const MidPlan& mp) {
+constexpr double kMidHbmKn = 3.1e6, kMidHbmNz = 4.6e6;  // qmm_mid's weight read rate, bytes per us
+
+int small_split(int64_t M, int64_t N, int64_t K, const MidPlan& mp, double mid_hbm = kMidHbmKn) {
     const PlanOverride& ov = plan_override();  // debug override: qmm_small=0 never, =<n> that split count
     if (ov.qmm_small == 0 || mp.bm == 0 || M <= 32 || M > 128 || N % 256 != 0 || K <= 0) return 0;
     auto rounds = [](int64_t wgs) { return (double)((wgs + 255) / 256); };
-    constexpr double kFill = 45e3, kHbm = 5e6, kMidHbm = 3.1e6, kReduce = 4e6, kReduceFixed = 3.0;  // bytes/us; us
+    constexpr double kFill = 45e3, kHbm = 5e6, kReduce = 4e6, kReduceFixed = 3.0;  // bytes per us; us
     const double w_bytes = (double)K * (double)N;
     const double t_mid_fill = rounds((int64_t)mp.tiles * mp.nsplit) * (mp.bm + mp.bn) * (double)(K / mp.nsplit) / kFill;
-    const double t_mid = t_mid_fill > w_bytes / kMidHbm ? t_mid_fill : w_bytes / kMidHbm;
+    const double t_mid = t_mid_fill > w_bytes / mid_hbm ? t_mid_fill : w_bytes / mid_hbm;
     int best = 0;
     double t_best = 0.9 * t_mid;
     for (int ns : {2, 4, 8}) {
@@ -2181,7 +2183,10 @@ size_t round_up256(size_t v) { return (v + 255) & ~(size_t)255; }
 size_t quant_matmul_nz_workspace(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     if (nzd_plan(M, N, K).nb) return 0;
-    if (mid_plan(M, N, K, false).bm) return 0;
+    if (mid_plan(M, N, K, false).bm) {  // the mid-M shapes: qmm_mid on NZ blocks (no workspace) or split tiles
+        const int ns = small_split(M, N, K, mid_plan(M, N, K, false), kMidHbmNz);
+        return ns ? big_split_workspace(small_split_plan(M, N, ns), M, N) : 0;
+    }
     const BigPlan b = big_plan(M, N, K);
     if (nz_dma_ok(b, M, N, K)) return b.nsplit > 1 ? big_split_workspace(b, M, N) : 0;
     return round_up256((size_t)K * (size_t)N) + quant_matmul_workspace(M, N, K);
@@ -2192,9 +2197,20 @@ hipError_t launch_quant_matmul_nz(const QmmArgs& p, void* workspace, size_t ws_b
     if (p.K == 0) return launch_qmm_fallback(p, false, false, false, stream);  // reads no weight
     const NzdPlan z = nzd_plan(p.M, p.N, p.K);
     if (z.nb) return launch_nzd(p, z, stream);
-    const MidPlan mp = mid_plan(p.M, p.N, p.K, false);
-    if (mp.bm) return launch_mid<kLayNZ>(p, mp, nullptr, nullptr, stream);
     char* ws = static_cast<char*>(workspace);
+    const MidPlan mp = mid_plan(p.M, p.N, p.K, false);
+    if (mp.bm) {
+        // wide or deep weights: 128-row K-split tiles where the cost model favours them (a workspace smaller
+        // than the query's runs qmm_mid, the same bits)
+        if (const int ns = small_split(p.M, p.N, p.K, mp, kMidHbmNz)) {
+            const BigPlan sb = small_split_plan(p.M, p.N, ns);
+            if (plan_override().qmm_dma && ws && ws_bytes >= big_split_workspace(sb, p.M, p.N) &&
+                (uintptr_t)ws % 16 == 0)
+                return launch_split128<kLayNZ>(p, sb, reinterpret_cast<int32_t*>(ws + QK_SPLIT_COUNTER_BYTES),
+                                               stream);
+        }
+        return launch_mid<kLayNZ>(p, mp, nullptr, nullptr, stream);
+    }
     const BigPlan b = big_plan(p.M, p.N, p.K);
     if (nz_dma_ok(b, p.M, p.N, p.K)) {
         if (b.nsplit == 1) {

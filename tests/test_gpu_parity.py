@@ -513,23 +513,27 @@ def test_quant_matmul_prefill_ragged_m_register_staged(ops, plan):
     assert torch.equal(dma.view(torch.int16), reg.view(torch.int16))
 
 
-@pytest.mark.parametrize("M,N,K,spec", [
-    (128, 11008, 4096, ""),           # the cost model's 128-row K splits (4)
-    (100, 11008, 4096, ""),           # the same with a ragged row tile (28 rows past M)
-    (128, 4096, 14336, ""),           # a deep weight
-    (64, 4096, 4096, "qmm_small=2"),  # forced: 2 splits, half a row tile
-    (48, 4096, 8192, "qmm_small=8"),  # forced: 8 splits
+@pytest.mark.parametrize("M,N,K,nz,spec", [
+    (128, 11008, 4096, False, ""),           # the cost model's 128-row K splits (4)
+    (100, 11008, 4096, False, ""),           # the same with a ragged row tile (28 rows past M)
+    (128, 4096, 14336, False, ""),           # a deep weight (8 splits)
+    (64, 4096, 4096, False, "qmm_small=2"),  # forced: 2 splits, half a row tile
+    (48, 4096, 8192, False, "qmm_small=8"),  # forced: 8 splits
+    (128, 4096, 14336, True, ""),            # NZ blocks: the cost model's 8 splits
+    (100, 11008, 4096, True, "qmm_small=4"), # NZ blocks, forced: 4 splits, a ragged row tile
 ])
-def test_quant_matmul_small_m_split_tiles(ops, oracle, plan, M, N, K, spec):
-    """[K,N] weights with 32 < M <= 128 on 128-row tiles with K splits (exact int32 partials, then the tiled
-    reduce) where the cost model favours them over the mid-M kernel: every int32 accumulator passes exact row and
-    column checksums, a row subset of the bf16 output (per-token and per-channel scales, bf16 bias) equals the
-    oracle bit for bit, and both outputs equal the mid-M kernel's (qmm_small=0)."""
-    say(f"quant_matmul small M on split tiles M={M} N={N} K={K} {spec or 'planner'}")
+def test_quant_matmul_small_m_split_tiles(ops, oracle, plan, M, N, K, nz, spec):
+    """[K,N] and int8 NZ weights with 32 < M <= 128 on 128-row tiles with K splits (exact int32 partials, then
+    the tiled reduce) where the cost model favours them over the mid-M kernel: every int32 accumulator passes
+    exact row and column checksums, a row subset of the bf16 output (per-token and per-channel scales, bf16 bias)
+    equals the oracle bit for bit, and both outputs equal the mid-M kernel's (qmm_small=0)."""
+    say(f"quant_matmul small M on split tiles M={M} N={N} K={K} {'NZ' if nz else '[K,N]'} {spec or 'planner'}")
     g = torch.Generator().manual_seed(M + N + K + 1)
     a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
     w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
     ad, wd = a.to(DEV), w.to(DEV)
+    if nz:
+        wd = ops.npu_format_cast(wd, ops.ACL_FORMAT_FRACTAL_NZ)
     s = 1e-3 + 9e-3 * torch.rand(N, generator=g)
     pt = 1e-2 * torch.rand(M, generator=g)
     b = torch.randn(N, generator=g).to(torch.bfloat16)

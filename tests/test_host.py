@@ -71,8 +71,16 @@ def test_w8a8_split_plan_workspace_sizes():
         assert ws.value == ctr + 4 * 128 * 11008 * 4
         assert L.qk_quant_matmul_workspace_size(128, 4096, 4096, BF16, ctypes.byref(ws)) == 0
         assert ws.value == 0
+        # on NZ blocks (whose mid-M kernel streams better) 128 x 4096 x 14336 takes 8 splits, 128 x 11008 x 4096
+        # stays on the mid-M kernel
+        assert L.qk_quant_matmul_nz_workspace_size(128, 4096, 14336, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == ctr + 8 * 128 * 4096 * 4
+        assert L.qk_quant_matmul_nz_workspace_size(128, 11008, 4096, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == 0
         q.debug_set_plan("qmm_small=0")
         assert L.qk_quant_matmul_workspace_size(128, 11008, 4096, BF16, ctypes.byref(ws)) == 0
+        assert ws.value == 0
+        assert L.qk_quant_matmul_nz_workspace_size(128, 4096, 14336, BF16, ctypes.byref(ws)) == 0
         assert ws.value == 0
         q.debug_set_plan("qmm_bm128=0")
         assert L.qk_quant_matmul_nz_workspace_size(M, N, K, BF16, ctypes.byref(ws)) == 0
