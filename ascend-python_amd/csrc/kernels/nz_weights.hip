@@ -1166,16 +1166,21 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
     return launch_weight_quant_bmm(q, rest ? ws + QK_SPLIT_COUNTER_BYTES + nd_bytes : nullptr, rest, stream);
 }
 
-// Row-major int4 [K, N/8] and int8 [K, N] weights at large M: the call casts the weight into its workspace
-// ([QK_SPLIT_COUNTER_BYTES, unused][NZ weight][x group sums fp32 [K/G][M]]) and runs the NZ prefill GEMM on
-// it.  The cast reads and writes the weight once; from M = 1024 the NZ GEMM saves more than that costs (cfg3's
-// 4096 x 11008 weight: int4 cast ~15 us, NZ GEMM ~195 us against ~250 us for the row-major prefill kernel).
-// The debug overrides that force or disable a prefill kernel switch it off.
-constexpr int64_t kCastNzMinM = 1024;
+// Row-major int4 [K, N/8] and int8 [K, N] weights past the decode rows: the call casts the weight into its
+// workspace ([QK_SPLIT_COUNTER_BYTES, unused][NZ weight][x group sums fp32 [K/G][M]]) and runs the NZ prefill
+// GEMM on it.  The cast reads and writes the weight once (cfg3's 4096 x 11008 weight: int4 ~10 us, int8
+// ~25 us).  Measured per call at that shape (one box, 6 rotating weights), cast + NZ GEMM against the row-major
+// kernels: int4 M = 257 / 384 / 512 / 640 / 896 86 / 79 / 80 / 84 / 111 us against 126 / 120 / 87 / 228 / 234 us
+// (the row-major prefill kernel's register-staged form takes a ragged M), while at M = 200 / 256 the decode
+// kernels are faster (67 / 72 against 77 us); int8 M = 200 / 256 / 384 / 640 116 / 117 / 116 / 120 us against
+// 6450 / 7927 / 126 / 246 us.  So int4 casts from M = 257 and int8 from M = 129.  The debug overrides that
+// force or disable a prefill kernel switch it off.
+int64_t cast_nz_min_m(int w_dtype) { return w_dtype == QK_I8 ? 129 : 257; }
 
 size_t w4_cast_nz_workspace(const WqbmmArgs& p, bool stream_k) {
     const PlanOverride& ov = plan_override();
-    if (!(p.w_dtype == QK_I32 || p.w_dtype == QK_I8) || p.M < kCastNzMinM || ov.w4nz_off || ov.w4_gemm != 0)
+    if (!(p.w_dtype == QK_I32 || p.w_dtype == QK_I8) || p.M < cast_nz_min_m(p.w_dtype) || ov.w4nz_off ||
+        ov.w4_gemm != 0)
         return 0;
     WqbmmArgs q = p;
     q.w = reinterpret_cast<const void*>((uintptr_t)256);  // the cast's destination: 256-byte aligned

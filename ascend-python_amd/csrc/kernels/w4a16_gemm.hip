@@ -1614,8 +1614,8 @@ GemmPlan gemm_plan(const WqbmmArgs& p) {
     const int force = plan_override().w4_gemm;
     if (force == 3) return g;
     const bool forced = force == 1;
-    // too few tiles: the decode kernels stream the weight better
-    if (!forced && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
+    // too few tiles: the decode kernels stream an int4 weight better (they take no int8 weight)
+    if (!forced && !w8 && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
     g.full = p.M % 256 == 0 && p.N % 128 == 0;
     // the DMA pipeline: whole tiles, whole 64-row stages per group, 16-byte aligned scale / offset rows
     g.dma = g.full && G % 64 == 0 && ((uintptr_t)p.scale | (uintptr_t)(p.offset ? p.offset : p.scale)) % 16 == 0 &&
@@ -1671,6 +1671,34 @@ hipError_t launch_w4_xsum(const WqbmmArgs& p, float* xsum, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// An int8 row-major weight with 16 < M <= 128 (where no cast plan runs): the decode stream on slices of 16 rows,
+// one launch each (cfg3's shape: ~16 us per slice, against ~130 us for the register-staged prefill kernel on one
+// 256-row tile).  The slice of row r0 is the call with x and out advanced by r0 rows.  Returns the workspace the
+// slices need (the larger of the full and the last slice's plan), or -1 where the slices do not apply.
+constexpr int64_t kW8SliceRows = 16, kW8SliceMaxM = 128;
+
+WqbmmArgs w8_slice(const WqbmmArgs& p, int64_t r0) {
+    WqbmmArgs q = p;
+    const int xs = 2, os = 2;  // 16-bit activations and outputs
+    q.x = static_cast<const char*>(p.x) + r0 * p.K * xs;
+    q.out = static_cast<char*>(p.out) + r0 * p.N * os;
+    q.M = p.M - r0 < kW8SliceRows ? p.M - r0 : kW8SliceRows;
+    return q;
+}
+
+int64_t w8_slices_workspace(const WqbmmArgs& p) {
+    if (p.w_dtype != QK_I8 || p.M <= kW8SliceRows || p.M > kW8SliceMaxM || plan_override().w4_gemm != 0) return -1;
+    int64_t need = 0;
+    for (int64_t r0 : {(int64_t)0, (p.M - 1) / kW8SliceRows * kW8SliceRows}) {
+        const StreamPlan s = stream_plan(w8_slice(p, r0));
+        if (!s.ok) return -1;
+        const int64_t rows = w8_slice(p, r0).M;
+        const int64_t w = s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (int64_t)s.nsplit * rows * p.N * (int64_t)sizeof(float);
+        if (w > need) need = w;
+    }
+    return need;
+}
+
 size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, int64_t group, int level) {
     WqbmmArgs p{};
     p.M = M;
@@ -1685,6 +1713,7 @@ size_t weight_quant_bmm_workspace(int64_t M, int64_t N, int64_t K, int w_dtype, 
     if (w_dtype == QK_I4_NZ || w_dtype == QK_I8_NZ || w_dtype == QK_I8_NK) return w4_nz_workspace(p, level == kWsFull);
     if (level != kWsNoCast)
         if (const size_t c = w4_cast_nz_workspace(p, level == kWsFull)) return c;
+    if (const int64_t sl = w8_slices_workspace(p); sl >= 0) return (size_t)sl;
     // [split-K counters][fp32 partials [nsplit][M][N]]
     const StreamPlan s = stream_plan(p);
     if (s.ok) return s.nsplit == 1 ? 0 : QK_SPLIT_COUNTER_BYTES + (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
@@ -1722,8 +1751,26 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
                                       : launch_reduce<QK_F16>(p, sp.nsplit, partial, stream);
     }
     if (!sp.ok) {
-        hipError_t ce = hipSuccess;  // large M on an int4 weight: cast to NZ in the workspace, NZ prefill GEMM
+        hipError_t ce = hipSuccess;  // large M: cast to NZ in the workspace, NZ prefill GEMM
         if (launch_w4_cast_nz(p, workspace, ws_bytes, stream, &ce)) return ce;
+        const int64_t sl = w8_slices_workspace(p);  // int8, 16 < M <= 128: the decode stream per 16 rows
+        if (sl >= 0 && (sl == 0 || (ws && ws_bytes >= (size_t)sl && (uintptr_t)ws % 256 == 0))) {
+            for (int64_t r0 = 0; r0 < p.M; r0 += kW8SliceRows) {
+                const WqbmmArgs q = w8_slice(p, r0);
+                const StreamPlan s = stream_plan(q);
+                if (!s.ok) return hipErrorInvalidValue;  // checked for both slice sizes above
+                uint64_t* ctr = (s.nsplit > 1 && (size_t)s.nstrip * 8 <= QK_SPLIT_COUNTER_BYTES &&
+                                 s.nsplit < (1 << kSplitCountBits))
+                                    ? reinterpret_cast<uint64_t*>(ws) : nullptr;
+                hipError_t e = q.x_dtype == QK_BF16 ? launch_stream_dt<QK_BF16>(q, s, partial, ctr, stream)
+                                                    : launch_stream_dt<QK_F16>(q, s, partial, ctr, stream);
+                if (e == hipSuccess && s.nsplit > 1 && !ctr)
+                    e = q.out_dtype == QK_BF16 ? launch_reduce<QK_BF16>(q, s.nsplit, partial, stream)
+                                               : launch_reduce<QK_F16>(q, s.nsplit, partial, stream);
+                if (e != hipSuccess) return e;
+            }
+            return hipSuccess;
+        }
         GemmPlan gp = gemm_plan(p);
         if (gp.ok) {
             // without the workspace the size query asked for, the register-staged kernel runs

@@ -708,6 +708,8 @@ def test_w4a16_cfg3_prefill(ops, oracle):
     (2, 8, 512, 128, False, torch.float16),
     (1, 11008, 4096, 128, True, torch.bfloat16),
     (13, 2056, 1536, 256, True, torch.float16),
+    # past 256 rows a row-major weight is cast to NZ in the workspace when the NZ prefill kernel takes the shape
+    (300, 8192, 1024, 128, True, torch.bfloat16),
 ])
 def test_w4a16_shapes(ops, oracle, M, N, K, group, offset, x_dtype):
     say(f"w4a16 M={M} N={N} K={K} group={group} offset={offset} {x_dtype}")
@@ -938,6 +940,10 @@ def _w8_inputs(M, N, K, group, offset, x_dtype, seed):
     (256, 384, 256, 64, False, torch.float16, "force"),
     (2048, 11008, 4096, 128, True, torch.bfloat16, None),  # prefill at the cfg3 shape (row subset)
     (5, 24, 96, 0, True, torch.bfloat16, None),            # generic kernel
+    (40, 4096, 2048, 128, True, torch.bfloat16, None),     # 16 < M <= 128: the decode stream on 16-row slices
+    (128, 2048, 1024, 64, False, torch.float16, None),     # eight slices
+    (200, 8192, 1024, 128, True, torch.bfloat16, None),    # M > 128: cast to NZ, NZ prefill kernel
+    (200, 2048, 1024, 128, True, torch.bfloat16, None),    # too few NZ tiles: the register-staged prefill kernel
 ])
 def test_w8a16(ops, oracle, plan, M, N, K, group, offset, x_dtype, force):
     """npu_weight_quant_batchmatmul with int8 weights [K, N] (W8A16) against the float64 oracle."""
