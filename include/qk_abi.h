@@ -29,8 +29,9 @@
  * contents -- uninitialised memory is fine.  A non-empty workspace begins with
  * QK_SPLIT_COUNTER_BYTES of split-K arrival counters, followed by the partial
  * sums (split-K shapes) or by the activations' per-group sums (weight-quant
- * matmul at large M; from M = 1024 on a row-major int4 weight the weight cast
- * to NZ, K*N/2 bytes rounded to 256, comes first, then the sums; where the NZ
+ * matmul at large M; from M = 257 on a row-major int4 weight, and from M = 129
+ * on a row-major int8 weight, the weight cast to NZ, K*N/2 (int4) or K*N
+ * (int8) bytes rounded to 256, comes first, then the sums; where the NZ
  * prefill kernel runs stream-K, (P - 1) x 128 KB of fp32 partial slots follow
  * the sums, P being the current device's CU count).  Each arrival adds D = tag * 2^16 + 1 to its
  * counter (a 48-bit tag drawn per call, never 0 or all ones), so a counter of
@@ -235,10 +236,11 @@ int qk_weight_quant_bmm(const void* x, int x_dtype,
  * reports fits in that array, the call runs exactly the kernels qk_weight_quant_bmm
  * runs (the same bits).  Where only the NZ prefill kernel's stream-K partial
  * slots do not fit, it runs that kernel with whole tiles per workgroup (the
- * same bits again).  Otherwise, for a row-major int4 or int8 weight at
- * M >= 1024 whose cast to NZ is what does not fit, it runs the row-major
- * prefill kernel without the cast (within the same 1e-2 bar; for int4 on
- * cfg3's shape, N = 11008, K = 4096, 128-row groups, the same bits); a shape whose scratch exceeds
+ * same bits again).  Otherwise, for a row-major int4 weight at M >= 257 or int8
+ * weight at M >= 129 whose cast to NZ is what does not fit, it runs the
+ * row-major kernels without the cast (within the same 1e-2 bar; for int4 on
+ * cfg3's shape, N = 11008, K = 4096, 128-row groups, at M = 1024 and 2048 the
+ * same bits); a shape whose scratch exceeds
  * QK_NOALLOC_SCRATCH_BYTES even so is refused with QK_ERR_UNSUPPORTED.  The call uses the array of the current device, so
  * `stream` must belong to it.  All calls on one GPU share that array: calls
  * that may run at the same time on one GPU (several streams or threads) race
