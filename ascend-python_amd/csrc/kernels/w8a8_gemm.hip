@@ -1739,9 +1739,11 @@ BigPlan big_plan(int64_t M, int64_t N, int64_t K, bool allow128 = true) {
     if (ns == 1 || tm * tn * ns < 64 || (int64_t)ns * M * N * 4 > ((int64_t)512 << 20)) return b;
     b.nsplit = ns;
     b.ok = true;
+    // 128-row tiles run only as K splits (their kernel writes int32 partials): where the 128-row tiles alone
+    // already fill the CUs (ns2 == 1) the 256-row split stays
     const int64_t tm2 = (M + 127) / 128;
     const int ns2 = big_splits(tm2 * tn, K);
-    if (allow128 && plan_override().qmm_bm128 && ns2 < ns && tm2 * tn * ns2 >= 64 &&
+    if (allow128 && plan_override().qmm_bm128 && ns2 > 1 && ns2 < ns && tm2 * tn * ns2 >= 64 &&
         K % ((int64_t)ns2 * dm::BK * dm::NST) == 0) {
         b.bm = 128;
         b.tiles_m = (int)tm2;
@@ -2171,6 +2173,7 @@ bool nz_dma_ok(const BigPlan& b, int64_t M, int64_t N, int64_t K) {
 
 template <int OUT>
 hipError_t launch_dma_nz(const QmmArgs& p, const BigPlan& b, int32_t* partial, hipStream_t stream) {
+    if (b.bm != 256) return hipErrorInvalidValue;  // 256-row tiles: tiles_m counts them
     qmm_dma<kLayNZ, OUT><<<dim3((uint32_t)(b.tiles_m * b.tiles_n * b.nsplit)), dim3(dm::NT), 0, stream>>>(
         p, b.tiles_m, b.tiles_n, b.nsplit, partial, dma_rev_from());
     return hipGetLastError();

@@ -513,6 +513,36 @@ def test_quant_matmul_prefill_ragged_m_register_staged(ops, plan):
     assert torch.equal(dma.view(torch.int16), reg.view(torch.int16))
 
 
+@pytest.mark.parametrize("M", [1500, 2000])
+@pytest.mark.parametrize("layout", ["kn", "nk", "nz"])
+def test_quant_matmul_split_where_128_row_tiles_fill_the_cus(ops, oracle, M, layout):
+    """N = K = 4096 with M = 1500 / 2000: 96 / 128 tiles of 256 rows (split in two), while 128-row tiles alone
+    (192 / 256) would fill the CUs unsplit, which their split-only kernel does not run.  The 256-row split runs:
+    exact int32 row and column checksums, a bf16 row subset bit-exact against the oracle, and no read past
+    x's last row (the NZ launch once sized its 256-row grid by the 128-row tile count)."""
+    N = K = 4096
+    say(f"quant_matmul M={M} N={N} K={K} {layout}: 256-row split where 128-row tiles fill the CUs")
+    g = torch.Generator().manual_seed(M + 17)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    wd = w.to(DEV)
+    if layout == "nk":
+        wd = w.t().contiguous().to(DEV).t()
+    elif layout == "nz":
+        wd = ops.npu_format_cast(wd, ops.ACL_FORMAT_FRACTAL_NZ)
+    ad = a.to(DEV)
+    acc = ops.npu_quant_matmul(ad, wd, torch.ones(1, device=DEV), output_dtype=torch.int32)
+    a64, w64, acc64 = a.to(torch.int64), w.to(torch.int64), acc.cpu().to(torch.int64)
+    assert torch.equal(acc64.sum(0), a64.sum(0) @ w64)
+    assert torch.equal(acc64.sum(1), a64 @ w64.sum(1))
+    s = 1e-3 + 9e-3 * torch.rand(N, generator=g)
+    pt = 1e-2 * torch.rand(M, generator=g)
+    out = ops.npu_quant_matmul(ad, wd, s.to(DEV), pertoken_scale=pt.to(DEV), output_dtype=torch.bfloat16)
+    rows = np.r_[0:8, M - 8:M]
+    ref = oracle.quant_matmul(a[rows].numpy(), w.numpy(), s.numpy(), pertoken=pt[rows].numpy(), out_dtype=BF16)
+    assert np.array_equal(to_bits(out)[rows], ref)
+
+
 @pytest.mark.parametrize("M,N,K,nz,spec", [
     (128, 11008, 4096, False, ""),           # the cost model's 128-row K splits (4)
     (100, 11008, 4096, False, ""),           # the same with a ragged row tile (28 rows past M)
