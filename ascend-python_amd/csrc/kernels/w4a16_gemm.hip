@@ -1597,7 +1597,7 @@ struct GemmPlan {
     int tiles_m, tiles_n;
 };
 
-GemmPlan gemm_plan(const WqbmmArgs& p) {
+GemmPlan gemm_plan(const WqbmmArgs& p, bool any_tiles = false) {
     GemmPlan g{false, false, false, 0, 0};
     const int64_t G = p.group == 0 ? p.K : p.group;
     const bool w8 = p.w_dtype == QK_I8;
@@ -1615,7 +1615,7 @@ GemmPlan gemm_plan(const WqbmmArgs& p) {
     if (force == 3) return g;
     const bool forced = force == 1;
     // too few tiles: the decode kernels stream an int4 weight better (they take no int8 weight)
-    if (!forced && !w8 && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
+    if (!forced && !any_tiles && !w8 && (int64_t)g.tiles_m * g.tiles_n < 128) return g;
     g.full = p.M % 256 == 0 && p.N % 128 == 0;
     // the DMA pipeline: whole tiles, whole 64-row stages per group, 16-byte aligned scale / offset rows
     g.dma = g.full && G % 64 == 0 && ((uintptr_t)p.scale | (uintptr_t)(p.offset ? p.offset : p.scale)) % 16 == 0 &&
@@ -1801,6 +1801,13 @@ hipError_t launch_weight_quant_bmm(const WqbmmArgs& a, void* workspace, size_t w
             w4_reduce<QK_F16><<<dim3((uint32_t)blocks), dim3(kThreads), 0, stream>>>(partial, d.nsplit, p.M, p.N, p.bias,
                                                                                     p.bias_dtype, p.out);
         return hipGetLastError();
+    }
+    // shapes the decode kernels do not take (K not a multiple of 256, say): the register-staged prefill kernel
+    // whatever its tile count (one round of tiles), which needs no workspace, before the generic kernel
+    if (GemmPlan gf = gemm_plan(p, true); gf.ok) {
+        gf.dma = false;
+        return p.x_dtype == QK_BF16 ? launch_gemm_dt<QK_BF16>(p, gf, nullptr, stream)
+                                    : launch_gemm_dt<QK_F16>(p, gf, nullptr, stream);
     }
     const int64_t total = p.M * p.N;
     int64_t blocks = (total + kThreads - 1) / kThreads;

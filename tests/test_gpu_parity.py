@@ -731,6 +731,8 @@ def test_w4a16_cfg3_prefill(ops, oracle):
     (40, 200, 256, 0, True, torch.bfloat16),
     (5, 24, 96, 0, False, torch.float16),
     (2, 16, 100, 0, True, torch.bfloat16),       # K % 32 != 0: generic kernel
+    (16, 1024, 4160, 64, True, torch.bfloat16),  # K % 256 != 0: no decode kernel; the register-staged prefill kernel
+    (3, 512, 320, 64, False, torch.float16),
     # stream kernel (M <= 16, K a multiple of 512): ragged strips, clamped rows, every group size
     (7, 1000, 1024, 32, True, torch.float16),
     (16, 520, 2048, 64, True, torch.bfloat16),
