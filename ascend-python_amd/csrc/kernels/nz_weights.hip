@@ -1123,8 +1123,27 @@ hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N
 // [QK_SPLIT_COUNTER_BYTES, unused][ND weight][row-major call's workspace].
 // An int8 [N, K] weight (QK_I8_NK) takes the same decode kernel (reading it in place) or is transposed into the
 // workspace for the row-major kernels: [QK_SPLIT_COUNTER_BYTES, unused][[K, N] weight][row-major call's workspace].
+// int8 NZ / [N,K] weights with 64 < M <= 128 (below the NZ prefill kernel's 64 tiles at most widths): the decode
+// kernel on two row chunks of at most 64, no workspace.  The alternative unpacks the weight and runs the
+// row-major int8 kernels (N = 4096, K = 4096: M = 65 / 128 68 / 103 us, against ~2 x 21 us).  int4 keeps the
+// unpack, which is faster there (28-35 us against ~2 x 19 us).
+constexpr int64_t kNzChunkRows = 64;
+
+bool nz_chunks_ok(const WqbmmArgs& p) {
+    if (plan_override().w4nz_off || p.w_dtype == QK_I4_NZ || p.M <= kNzChunkRows || p.M > 2 * kNzChunkRows)
+        return false;
+    WqbmmArgs c = p;
+    c.M = kNzChunkRows;
+    if (!nz_plan(c).ok) return false;
+    c.x = static_cast<const char*>(p.x) + kNzChunkRows * p.K * 2;  // 16-bit activations and outputs
+    c.out = static_cast<char*>(p.out) + kNzChunkRows * p.N * 2;
+    c.M = p.M - kNzChunkRows;
+    return nz_plan(c).ok;
+}
+
 size_t w4_nz_workspace(const WqbmmArgs& p, bool stream_k) {
     if (!plan_override().w4nz_off && nz_plan(p).ok) return 0;
+    if (nz_chunks_ok(p)) return 0;
     if (!plan_override().w4nz_off && nzg_plan(p).ok) return nzg_workspace(p, stream_k);
     const int nd_dtype = p.w_dtype == QK_I4_NZ ? QK_I32 : QK_I8;
     return QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(p)) +
@@ -1135,6 +1154,20 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
     const NzPlan z = plan_override().w4nz_off ? NzPlan{false, 0, 0, 0, 0, 0} : nz_plan(p);
     if (z.ok)
         return p.x_dtype == QK_BF16 ? launch_nz_dt<QK_BF16>(p, z, stream) : launch_nz_dt<QK_F16>(p, z, stream);
+    if (nz_chunks_ok(p)) {
+        for (int64_t r0 = 0; r0 < p.M; r0 += kNzChunkRows) {
+            WqbmmArgs c = p;
+            c.x = static_cast<const char*>(p.x) + r0 * p.K * 2;
+            c.out = static_cast<char*>(p.out) + r0 * p.N * 2;
+            c.M = p.M - r0 < kNzChunkRows ? p.M - r0 : kNzChunkRows;
+            const NzPlan zc = nz_plan(c);
+            if (!zc.ok) return hipErrorInvalidValue;  // both chunk shapes checked above
+            const hipError_t e = p.x_dtype == QK_BF16 ? launch_nz_dt<QK_BF16>(c, zc, stream)
+                                                      : launch_nz_dt<QK_F16>(c, zc, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     const NzGemmPlan g = plan_override().w4nz_off ? NzGemmPlan{false, 0, 0} : nzg_plan(p);
     if (g.ok) {
         if (!workspace || ws_bytes < nzg_workspace(p, false) || (uintptr_t)workspace % 16 != 0)

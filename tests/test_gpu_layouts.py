@@ -102,6 +102,7 @@ def test_nz_format_is_recorded_with_the_storage(ops, oracle):
     (40, 768, 1024, 0, True, torch.bfloat16, True),        # decode, per channel, three row blocks
     (300, 1024, 2048, 128, True, torch.bfloat16, False),   # prefill: transposed into the workspace
     (8, 80, 192, 64, False, torch.float16, False),         # K % 128 != 0: transposed, row-major decode kernels
+    (100, 1024, 2048, 128, True, torch.bfloat16, True),    # 64 < M <= 128: the decode kernel on two row chunks
 ])
 def test_w8a16_nk_view(ops, oracle, M, N, K, group, offset, x_dtype, bias):
     """The transposed view of an int8 [N, K] weight against the oracle, and bit for bit against the same call on
@@ -119,7 +120,8 @@ def test_w8a16_nk_view(ops, oracle, M, N, K, group, offset, x_dtype, bias):
     L = ops.abi()
     ws = ctypes.c_size_t(1)
     assert L.qk_weight_quant_bmm_workspace_size(M, N, K, ops.QK_I8_NK, group, ctypes.byref(ws)) == 0
-    decode = M <= 64 and K % 128 == 0 and N % 16 == 0 and (group == 0 or group % 128 == 0)
+    # the decode kernel (M <= 64, or two row chunks up to 128) reads the rows in place
+    decode = M <= 128 and K % 128 == 0 and N % 16 == 0 and (group == 0 or group % 128 == 0)
     if decode:
         assert ws.value == 0, "the decode kernel reads the [N, K] rows in place: no workspace, no copy"
         same = _wq(ops, x, ops.npu_format_cast(d["w"].to(DEV), 29), d, group, b)
