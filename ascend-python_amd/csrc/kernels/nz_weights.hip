@@ -1210,15 +1210,27 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
 // force or disable a prefill kernel switch it off.
 int64_t cast_nz_min_m(int w_dtype) { return w_dtype == QK_I8 ? 129 : 257; }
 
+// An int8 row-major weight with 32 < M <= 128 is cast too, for the NZ decode kernel (on two row chunks past 64
+// rows): N = 4096, K = 4096, M = 65 / 128 41 / 53 us against 68 / 90 us for the row-major decode stream on
+// 16-row slices; at N = 11008 60 / 80 against 68 / 107 us.  The call's workspace then holds the NZ weight alone.
+bool nz_decode_ok(const WqbmmArgs& q) { return q.M <= kNzChunkRows ? nz_plan(q).ok : nz_chunks_ok(q); }
+
+bool cast_nz_decode(const WqbmmArgs& p) {
+    if (p.w_dtype != QK_I8 || p.M <= 32 || p.M > 2 * kNzChunkRows) return false;
+    WqbmmArgs q = p;
+    q.w = reinterpret_cast<const void*>((uintptr_t)256);
+    q.w_dtype = QK_I8_NZ;
+    return nz_decode_ok(q);
+}
+
 size_t w4_cast_nz_workspace(const WqbmmArgs& p, bool stream_k) {
     const PlanOverride& ov = plan_override();
-    if (!(p.w_dtype == QK_I32 || p.w_dtype == QK_I8) || p.M < cast_nz_min_m(p.w_dtype) || ov.w4nz_off ||
-        ov.w4_gemm != 0)
-        return 0;
+    if (!(p.w_dtype == QK_I32 || p.w_dtype == QK_I8) || ov.w4nz_off || ov.w4_gemm != 0) return 0;
     WqbmmArgs q = p;
     q.w = reinterpret_cast<const void*>((uintptr_t)256);  // the cast's destination: 256-byte aligned
     q.w_dtype = p.w_dtype == QK_I8 ? QK_I8_NZ : QK_I4_NZ;
-    if (!nzg_plan(q).ok) return 0;
+    if (cast_nz_decode(p)) return round256(QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)));
+    if (p.M < cast_nz_min_m(p.w_dtype) || !nzg_plan(q).ok) return 0;
     return round256(QK_SPLIT_COUNTER_BYTES + round256(nd_weight_bytes(q)) +
                     (nzg_workspace(q, stream_k) - QK_SPLIT_COUNTER_BYTES));
 }
@@ -1232,6 +1244,14 @@ bool launch_w4_cast_nz(const WqbmmArgs& p, void* workspace, size_t ws_bytes, hip
     WqbmmArgs q = p;
     q.w = nz;
     q.w_dtype = w8 ? QK_I8_NZ : QK_I4_NZ;
+    if (cast_nz_decode(p)) {
+        if (!nz_decode_ok(q)) return false;  // with the call's own operands (their alignment)
+        hipError_t e = launch_w8_nz_cast(static_cast<const int8_t*>(p.w), true, p.K, p.N, static_cast<int8_t*>(nz),
+                                         stream);
+        if (e == hipSuccess) e = launch_w4_nz_bmm(q, nullptr, 0, stream);
+        *err = e;
+        return true;
+    }
     const NzGemmPlan g = nzg_plan(q);  // with the call's own operands (their alignment)
     if (!g.ok) return false;
     hipError_t e = w8 ? launch_w8_nz_cast(static_cast<const int8_t*>(p.w), true, p.K, p.N, static_cast<int8_t*>(nz),

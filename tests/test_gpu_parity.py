@@ -973,7 +973,8 @@ def _w8_inputs(M, N, K, group, offset, x_dtype, seed):
     (2048, 11008, 4096, 128, True, torch.bfloat16, None),  # prefill at the cfg3 shape (row subset)
     (5, 24, 96, 0, True, torch.bfloat16, None),            # generic kernel
     (40, 4096, 2048, 128, True, torch.bfloat16, None),     # 16 < M <= 128: the decode stream on 16-row slices
-    (128, 2048, 1024, 64, False, torch.float16, None),     # eight slices
+    (128, 2048, 1024, 64, False, torch.float16, None),     # eight slices (64-row groups: no NZ decode plan)
+    (100, 4096, 2048, 128, True, torch.bfloat16, None),    # 64 < M <= 128: cast to NZ, NZ decode on two row chunks
     (200, 8192, 1024, 128, True, torch.bfloat16, None),    # M > 128: cast to NZ, NZ prefill kernel
     (200, 2048, 1024, 128, True, torch.bfloat16, None),    # too few NZ tiles: the register-staged prefill kernel
 ])
