@@ -29,9 +29,10 @@
  * contents -- uninitialised memory is fine.  A non-empty workspace begins with
  * QK_SPLIT_COUNTER_BYTES of split-K arrival counters, followed by the partial
  * sums (split-K shapes) or by the activations' per-group sums (weight-quant
- * matmul at large M; from M = 257 on a row-major int4 weight, and from M = 129
+ * matmul at large M; from M = 257 on a row-major int4 weight, and from M = 33
  * on a row-major int8 weight, the weight cast to NZ, K*N/2 (int4) or K*N
- * (int8) bytes rounded to 256, comes first, then the sums; where the NZ
+ * (int8) bytes rounded to 256, comes first, then the sums (none up to M = 128
+ * on int8, where the NZ decode kernel runs); where the NZ
  * prefill kernel runs stream-K, (P - 1) x 128 KB of fp32 partial slots follow
  * the sums, P being the current device's CU count).  Each arrival adds D = tag * 2^16 + 1 to its
  * counter (a 48-bit tag drawn per call, never 0 or all ones), so a counter of
