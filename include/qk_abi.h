@@ -238,7 +238,7 @@ int qk_weight_quant_bmm(const void* x, int x_dtype,
  * runs (the same bits).  Where only the NZ prefill kernel's stream-K partial
  * slots do not fit, it runs that kernel with whole tiles per workgroup (the
  * same bits again).  Otherwise, for a row-major int4 weight at M >= 257 or int8
- * weight at M >= 129 whose cast to NZ is what does not fit, it runs the
+ * weight at M >= 33 whose cast to NZ is what does not fit, it runs the
  * row-major kernels without the cast (within the same 1e-2 bar; for int4 on
  * cfg3's shape, N = 11008, K = 4096, 128-row groups, at M = 1024 and 2048 the
  * same bits); a shape whose scratch exceeds
