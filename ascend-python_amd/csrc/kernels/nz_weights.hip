@@ -1123,21 +1123,24 @@ hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N
 // [QK_SPLIT_COUNTER_BYTES, unused][ND weight][row-major call's workspace].
 // An int8 [N, K] weight (QK_I8_NK) takes the same decode kernel (reading it in place) or is transposed into the
 // workspace for the row-major kernels: [QK_SPLIT_COUNTER_BYTES, unused][[K, N] weight][row-major call's workspace].
-// int8 NZ / [N,K] weights with 64 < M <= 128 (below the NZ prefill kernel's 64 tiles at most widths): the decode
-// kernel on two row chunks of at most 64, no workspace.  The alternative unpacks the weight and runs the
-// row-major int8 kernels (N = 4096, K = 4096: M = 65 / 128 68 / 103 us, against ~2 x 21 us).  int4 keeps the
-// unpack, which is faster there (28-35 us against ~2 x 19 us).
+// int8 NZ / [N,K] weights with 64 < M <= 128, or up to 256 where the NZ prefill kernel does not take the shape
+// (it needs 64 tiles): the decode kernel on row chunks of at most 64, no workspace.  The alternative unpacks the
+// weight and runs the row-major int8 kernels (N = 4096, K = 4096: M = 65 / 128 68 / 103 us, against ~2 x 21 us;
+// M = 129-256 ~130 us against 3-4 x 21 us).  int4 keeps the unpack, which is faster there (28-35 us against
+// ~2 x 19 us).
 constexpr int64_t kNzChunkRows = 64;
 
 bool nz_chunks_ok(const WqbmmArgs& p) {
-    if (plan_override().w4nz_off || p.w_dtype == QK_I4_NZ || p.M <= kNzChunkRows || p.M > 2 * kNzChunkRows)
+    if (plan_override().w4nz_off || p.w_dtype == QK_I4_NZ || p.M <= kNzChunkRows || p.M > 4 * kNzChunkRows)
         return false;
+    if (p.M > 2 * kNzChunkRows && nzg_plan(p).ok) return false;
     WqbmmArgs c = p;
     c.M = kNzChunkRows;
     if (!nz_plan(c).ok) return false;
-    c.x = static_cast<const char*>(p.x) + kNzChunkRows * p.K * 2;  // 16-bit activations and outputs
-    c.out = static_cast<char*>(p.out) + kNzChunkRows * p.N * 2;
-    c.M = p.M - kNzChunkRows;
+    const int64_t last = (p.M - 1) / kNzChunkRows * kNzChunkRows;  // the last chunk's first row
+    c.x = static_cast<const char*>(p.x) + last * p.K * 2;  // 16-bit activations and outputs
+    c.out = static_cast<char*>(p.out) + last * p.N * 2;
+    c.M = p.M - last;
     return nz_plan(c).ok;
 }
 
@@ -1210,13 +1213,14 @@ hipError_t launch_w4_nz_bmm(const WqbmmArgs& p, void* workspace, size_t ws_bytes
 // force or disable a prefill kernel switch it off.
 int64_t cast_nz_min_m(int w_dtype) { return w_dtype == QK_I8 ? 129 : 257; }
 
-// An int8 row-major weight with 32 < M <= 128 is cast too, for the NZ decode kernel (on two row chunks past 64
-// rows): N = 4096, K = 4096, M = 65 / 128 41 / 53 us against 68 / 90 us for the row-major decode stream on
-// 16-row slices; at N = 11008 60 / 80 against 68 / 107 us.  The call's workspace then holds the NZ weight alone.
+// An int8 row-major weight with 32 < M <= 128 (or up to 256 where the NZ prefill kernel does not take the shape)
+// is cast too, for the NZ decode kernel (on row chunks past 64 rows): N = 4096, K = 4096, M = 65 / 128 41 / 53 us
+// against 68 / 90 us for the row-major decode stream on 16-row slices; at N = 11008 60 / 80 against 68 / 107 us.
+// The call's workspace then holds the NZ weight alone.
 bool nz_decode_ok(const WqbmmArgs& q) { return q.M <= kNzChunkRows ? nz_plan(q).ok : nz_chunks_ok(q); }
 
 bool cast_nz_decode(const WqbmmArgs& p) {
-    if (p.w_dtype != QK_I8 || p.M <= 32 || p.M > 2 * kNzChunkRows) return false;
+    if (p.w_dtype != QK_I8 || p.M <= 32 || p.M > 4 * kNzChunkRows) return false;
     WqbmmArgs q = p;
     q.w = reinterpret_cast<const void*>((uintptr_t)256);
     q.w_dtype = QK_I8_NZ;

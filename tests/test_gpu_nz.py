@@ -369,7 +369,8 @@ def test_format_cast_int8_device_matches_oracle(ops, oracle):
     (7, 2048, 1024, 64, False, torch.bfloat16, False),     # 64-row groups
     (80, 256, 512, 128, True, torch.float16, False),       # M > 64: the decode kernel on two row chunks
     (128, 2048, 1024, 128, True, torch.bfloat16, True),    # two full 64-row chunks
-    (200, 256, 512, 128, True, torch.float16, False),      # M > 128: unpacked to ND
+    (200, 256, 512, 128, True, torch.float16, False),      # 128 < M <= 256, too few prefill tiles: four row chunks
+    (300, 256, 512, 128, True, torch.bfloat16, False),     # M > 256: unpacked to ND
 ])
 def test_w8a16_nz_shapes(ops, oracle, M, N, K, group, offset, x_dtype, bias):
     say(f"w8a16 NZ M={M} N={N} K={K} group={group} offset={offset} {x_dtype} bias={bias}")

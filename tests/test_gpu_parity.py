@@ -976,7 +976,8 @@ def _w8_inputs(M, N, K, group, offset, x_dtype, seed):
     (128, 2048, 1024, 64, False, torch.float16, None),     # eight slices (64-row groups: no NZ decode plan)
     (100, 4096, 2048, 128, True, torch.bfloat16, None),    # 64 < M <= 128: cast to NZ, NZ decode on two row chunks
     (200, 8192, 1024, 128, True, torch.bfloat16, None),    # M > 128: cast to NZ, NZ prefill kernel
-    (200, 2048, 1024, 128, True, torch.bfloat16, None),    # too few NZ tiles: the register-staged prefill kernel
+    (200, 2048, 1024, 128, True, torch.bfloat16, None),    # too few NZ prefill tiles: cast, NZ decode on row chunks
+    (300, 2048, 1024, 128, True, torch.bfloat16, None),    # M > 256 with too few NZ tiles: the register-staged kernel
 ])
 def test_w8a16(ops, oracle, plan, M, N, K, group, offset, x_dtype, force):
     """npu_weight_quant_batchmatmul with int8 weights [K, N] (W8A16) against the float64 oracle."""
