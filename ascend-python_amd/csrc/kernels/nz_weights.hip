@@ -1123,7 +1123,7 @@ hipError_t launch_w8_nz_cast(const int8_t* src, bool to_nz, int64_t K, int64_t N
 // [QK_SPLIT_COUNTER_BYTES, unused][ND weight][row-major call's workspace].
 // An int8 [N, K] weight (QK_I8_NK) takes the same decode kernel (reading it in place) or is transposed into the
 // workspace for the row-major kernels: [QK_SPLIT_COUNTER_BYTES, unused][[K, N] weight][row-major call's workspace].
-// int8 NZ / [N,K] weights with 64 < M <= 128, or up to 256 where the NZ prefill kernel does not take the shape
+// int8 NZ / [N,K] weights with 64 < M <= 192, or up to 256 where the NZ prefill kernel does not take the shape
 // (it needs 64 tiles): the decode kernel on row chunks of at most 64, no workspace.  The alternative unpacks the
 // weight and runs the row-major int8 kernels (N = 4096, K = 4096: M = 65 / 128 68 / 103 us, against ~2 x 21 us;
 // M = 129-256 ~130 us against 3-4 x 21 us).  int4 keeps the unpack, which is faster there (28-35 us against
@@ -1133,7 +1133,11 @@ constexpr int64_t kNzChunkRows = 64;
 bool nz_chunks_ok(const WqbmmArgs& p) {
     if (plan_override().w4nz_off || p.w_dtype == QK_I4_NZ || p.M <= kNzChunkRows || p.M > 4 * kNzChunkRows)
         return false;
-    if (p.M > 2 * kNzChunkRows && nzg_plan(p).ok) return false;
+    if (p.M > 3 * kNzChunkRows) {  // four chunks only where the NZ prefill kernel does not take the shape as NZ
+        WqbmmArgs z = p;           // (an [N,K] weight gets there by its transpose and cast: N = 11008, M = 256
+        z.w_dtype = QK_I8_NZ;      // 135 us against 169 us for four chunks; three chunks, M = 129 / 192, 97 / 124
+        if (nzg_plan(z).ok) return false;  // us against 136 / 135 us)
+    }
     WqbmmArgs c = p;
     c.M = kNzChunkRows;
     if (!nz_plan(c).ok) return false;
